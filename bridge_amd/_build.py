@@ -1,0 +1,77 @@
+"""Build libtpr_attn.so in-tree with hipcc for gfx950 (no JIT, no torch extension).
+
+``python -m bridge_amd._build`` or ``bridge_amd._build.build()`` compiles every
+source under ``bridge_amd/csrc`` and links ``bridge_amd/libtpr_attn.so``.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(PKG_DIR, "csrc")
+BUILD_DIR = os.path.join(PKG_DIR, "_build")
+LIB_PATH = os.path.join(PKG_DIR, "libtpr_attn.so")
+ARCH = os.environ.get("TPR_OFFLOAD_ARCH", "gfx950")
+
+HIP_SOURCES = ["tpr_abi.hip", "tpr_simt.hip", "tpr_mfma.hip"]
+CXX_SOURCES = ["tpr_plan.cpp"]
+
+
+def _hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found; set HIPCC or install ROCm")
+
+
+def _hip_flags():
+    return [
+        f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall",
+        "-Wno-unused-function", "-Wno-unused-variable",
+        # packed fp32 VALU forms are kept out of every kernel
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-I", os.path.join(PKG_DIR, "..", "include"),
+    ]
+
+
+def _run(cmd):
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    lines = [ln for ln in proc.stdout.splitlines() if "packed-fp32-ops" not in ln]
+    return proc.returncode, "\n".join(lines)
+
+
+def build(verbose: bool = False, extra_flags=()) -> str:
+    """Compile all sources and link the shared library; returns its path."""
+    os.makedirs(BUILD_DIR, exist_ok=True)
+    hipcc = _hipcc()
+    jobs = []
+    for src in HIP_SOURCES:
+        obj = os.path.join(BUILD_DIR, src.rsplit(".", 1)[0] + ".o")
+        jobs.append((obj, [hipcc, *_hip_flags(), *extra_flags, "-c", os.path.join(CSRC, src), "-o", obj]))
+    for src in CXX_SOURCES:
+        obj = os.path.join(BUILD_DIR, src.rsplit(".", 1)[0] + ".o")
+        jobs.append((obj, ["g++", "-O2", "-std=c++17", "-fPIC", "-Wall", "-I",
+                           os.path.join(PKG_DIR, "..", "include"), "-c", os.path.join(CSRC, src), "-o", obj]))
+    with ThreadPoolExecutor(max_workers=min(8, len(jobs))) as pool:
+        results = list(pool.map(lambda job: _run(job[1]), jobs))
+    for (obj, cmd), (rc, out) in zip(jobs, results):
+        if verbose and out:
+            print(out)
+        if rc != 0:
+            raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{out}")
+    tmp = LIB_PATH + ".tmp"
+    rc, out = _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp,
+                    *[obj for obj, _ in jobs]])
+    if rc != 0:
+        raise RuntimeError(f"link failed:\n{out}")
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

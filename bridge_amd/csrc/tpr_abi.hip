@@ -1,0 +1,178 @@
+// tpr_abi.hip -- extern "C" entry points of libtpr_attn.so: argument checks,
+// plan-header decoding and kernel dispatch. Host code only.
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "../../include/tpr_attn.h"
+#include "tpr_device.h"
+#include "tpr_host.h"
+
+namespace tpr {
+
+int launch_simt_fwd(const KernelArgs& a, bool fp32, hipStream_t s);
+int launch_delta(const KernelArgs& a, bool fp32, hipStream_t s);
+int launch_simt_bwd(const KernelArgs& a, int n_fwd, int n_dkdv, bool fp32, hipStream_t s);
+int launch_mfma_fwd(const KernelArgs& a, hipStream_t s);
+int launch_mfma_bwd(const KernelArgs& a, int n_fwd, int n_dkdv, hipStream_t s);
+
+namespace {
+thread_local char g_error[512] = "";
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_plan(const int32_t* plan_host, const int32_t* plan_device) {
+  if (!plan_host || !plan_device) return fail(TPR_ERR_INVALID_ARGUMENT, "plan_host and plan_device must not be NULL");
+  if (plan_host[PF_MAGIC] != kPlanMagic || plan_host[PF_VERSION] != kPlanVersion)
+    return fail(TPR_ERR_INVALID_ARGUMENT, "plan_host is not a plan blob written by tpr_attn_plan (version %d)",
+                kPlanVersion);
+  return TPR_OK;
+}
+
+int check_scale(float scale) {
+  if (!std::isfinite(scale) || scale <= 0.f)
+    return fail(TPR_ERR_INVALID_ARGUMENT, "softmax_scale must be finite and positive, got %g", scale);
+  return TPR_OK;
+}
+
+KernelArgs args_from_plan(const int32_t* ph, const int32_t* pd, float scale) {
+  KernelArgs a;
+  std::memset(&a, 0, sizeof(a));
+  a.plan = pd;
+  a.scale = scale;
+  a.hq = ph[PF_HQ];
+  a.hkv = ph[PF_HKV];
+  a.d = ph[PF_D];
+  a.group = a.hq / a.hkv;
+  a.hpw = 1;
+  for (int g = kFwdWaves; g >= 1; g--)
+    if (a.group % g == 0 && kFwdWaves % g == 0) { a.hpw = g; break; }
+  a.total_q = ph[PF_TOTAL_Q];
+  a.total_prefix = ph[PF_TOTAL_PREFIX];
+  a.max_depth = ph[PF_MAX_DEPTH];
+  a.off_cu = ph[PF_OFF_CU];
+  a.off_node_off = ph[PF_OFF_NODE_OFF];
+  a.off_anc = ph[PF_OFF_ANC];
+  a.off_node_leaf = ph[PF_OFF_NODE_LEAF];
+  a.off_qblk = ph[PF_OFF_QBLK];
+  a.off_leaf_qblk = ph[PF_OFF_LEAF_QBLK];
+  a.off_fwd = ph[PF_OFF_FWD];
+  a.off_dkdv = ph[PF_OFF_DKDV];
+  return a;
+}
+
+int check_tensor(const void* p, const char* name, bool needed, bool mfma) {
+  if (!needed) return TPR_OK;
+  if (!p) return fail(TPR_ERR_INVALID_ARGUMENT, "%s must not be NULL", name);
+  if (mfma && !aligned16(p)) return fail(TPR_ERR_INVALID_ARGUMENT, "%s must be 16-byte aligned", name);
+  return TPR_OK;
+}
+}  // namespace
+
+int fail(int status, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(g_error, sizeof(g_error), fmt, ap);
+  va_end(ap);
+  return status;
+}
+
+void clear_error() { g_error[0] = '\0'; }
+
+}  // namespace tpr
+
+using namespace tpr;
+
+extern "C" int tpr_attn_abi_version(void) { return TPR_ATTN_ABI_VERSION; }
+
+extern "C" const char* tpr_attn_last_error(void) { return g_error; }
+
+extern "C" size_t tpr_attn_bwd_workspace_bytes(const int32_t* plan_host) {
+  if (!plan_host || plan_host[PF_MAGIC] != kPlanMagic) return 0;
+  const size_t slots = static_cast<size_t>(plan_host[PF_N_SLOTS]);
+  return slots * static_cast<size_t>(kDkdvKeys) * static_cast<size_t>(plan_host[PF_D]) * 2 * sizeof(float);
+}
+
+extern "C" int tpr_attn_fwd(const TprFwdParams* p, void* stream) {
+  clear_error();
+  if (!p) return fail(TPR_ERR_INVALID_ARGUMENT, "params must not be NULL");
+  if (p->abi_version != TPR_ATTN_ABI_VERSION)
+    return fail(TPR_ERR_INVALID_ARGUMENT, "abi_version %d does not match library version %d", p->abi_version,
+                TPR_ATTN_ABI_VERSION);
+  int rc = check_plan(p->plan_host, p->plan_device);
+  if (rc) return rc;
+  if ((rc = check_scale(p->softmax_scale))) return rc;
+  const int32_t* ph = p->plan_host;
+  const bool mfma = ph[PF_PATH] == PATH_MFMA;
+  const bool any_q = ph[PF_TOTAL_Q] > 0, any_p = ph[PF_TOTAL_PREFIX] > 0;
+  if ((rc = check_tensor(p->q, "q", any_q, mfma)) || (rc = check_tensor(p->k, "k", any_q, mfma)) ||
+      (rc = check_tensor(p->v, "v", any_q, mfma)) || (rc = check_tensor(p->out, "out", any_q, mfma)) ||
+      (rc = check_tensor(p->lse, "lse", any_q, false)) ||
+      (rc = check_tensor(p->prefix_k, "prefix_k", any_p, mfma)) ||
+      (rc = check_tensor(p->prefix_v, "prefix_v", any_p, mfma)))
+    return rc;
+  KernelArgs a = args_from_plan(ph, p->plan_device, p->softmax_scale);
+  a.q = p->q;
+  a.k = p->k;
+  a.v = p->v;
+  a.pk = p->prefix_k;
+  a.pv = p->prefix_v;
+  a.out = p->out;
+  a.lse = p->lse;
+  a.n_items = ph[PF_N_FWD];
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  rc = mfma ? launch_mfma_fwd(a, s) : launch_simt_fwd(a, ph[PF_DTYPE] == TPR_DTYPE_FP32, s);
+  if (rc) return fail(TPR_ERR_LAUNCH, "forward launch failed: %s", hipGetErrorString(hipGetLastError()));
+  return TPR_OK;
+}
+
+extern "C" int tpr_attn_bwd(const TprBwdParams* p, void* stream) {
+  clear_error();
+  if (!p) return fail(TPR_ERR_INVALID_ARGUMENT, "params must not be NULL");
+  if (p->abi_version != TPR_ATTN_ABI_VERSION)
+    return fail(TPR_ERR_INVALID_ARGUMENT, "abi_version %d does not match library version %d", p->abi_version,
+                TPR_ATTN_ABI_VERSION);
+  int rc = check_plan(p->plan_host, p->plan_device);
+  if (rc) return rc;
+  if ((rc = check_scale(p->softmax_scale))) return rc;
+  const int32_t* ph = p->plan_host;
+  const bool mfma = ph[PF_PATH] == PATH_MFMA;
+  const bool any_q = ph[PF_TOTAL_Q] > 0, any_p = ph[PF_TOTAL_PREFIX] > 0;
+  if ((rc = check_tensor(p->q, "q", any_q, mfma)) || (rc = check_tensor(p->k, "k", any_q, mfma)) ||
+      (rc = check_tensor(p->v, "v", any_q, mfma)) || (rc = check_tensor(p->out, "out", any_q, mfma)) ||
+      (rc = check_tensor(p->dout, "dout", any_q, mfma)) || (rc = check_tensor(p->lse, "lse", any_q, false)) ||
+      (rc = check_tensor(p->delta, "delta", any_q, false)) || (rc = check_tensor(p->dq, "dq", any_q, mfma)) ||
+      (rc = check_tensor(p->dk, "dk", any_q, mfma)) || (rc = check_tensor(p->dv, "dv", any_q, mfma)) ||
+      (rc = check_tensor(p->prefix_k, "prefix_k", any_p, mfma)) ||
+      (rc = check_tensor(p->prefix_v, "prefix_v", any_p, mfma)) ||
+      (rc = check_tensor(p->dprefix_k, "dprefix_k", any_p, mfma)) ||
+      (rc = check_tensor(p->dprefix_v, "dprefix_v", any_p, mfma)))
+    return rc;
+  const size_t need = tpr_attn_bwd_workspace_bytes(ph);
+  if (need > 0 && (!p->workspace || p->workspace_bytes < need))
+    return fail(TPR_ERR_BUFFER_TOO_SMALL, "backward workspace needs %zu bytes, got %zu", need, p->workspace_bytes);
+  KernelArgs a = args_from_plan(ph, p->plan_device, p->softmax_scale);
+  a.q = p->q;
+  a.k = p->k;
+  a.v = p->v;
+  a.pk = p->prefix_k;
+  a.pv = p->prefix_v;
+  a.out_in = p->out;
+  a.dout = p->dout;
+  a.lse_in = p->lse;
+  a.delta = p->delta;
+  a.dq = p->dq;
+  a.dk = p->dk;
+  a.dv = p->dv;
+  a.dpk = p->dprefix_k;
+  a.dpv = p->dprefix_v;
+  const bool fp32 = ph[PF_DTYPE] == TPR_DTYPE_FP32;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  rc = launch_delta(a, fp32, s);
+  if (!rc) rc = mfma ? launch_mfma_bwd(a, ph[PF_N_FWD], ph[PF_N_DKDV], s)
+                     : launch_simt_bwd(a, ph[PF_N_FWD], ph[PF_N_DKDV], fp32, s);
+  if (rc) return fail(TPR_ERR_LAUNCH, "backward launch failed: %s", hipGetErrorString(hipGetLastError()));
+  return TPR_OK;
+}

@@ -1,0 +1,80 @@
+// tpr_common.h -- layout of the launch-plan blob shared by the host planner
+// (tpr_plan.cpp) and the kernels, plus the tile shapes each kernel family
+// uses. The plan is a flat int32 array: a fixed header of offsets/counts,
+// the tree metadata and the per-kernel work lists.
+#pragma once
+
+#include <stdint.h>
+
+namespace tpr {
+
+constexpr int32_t kPlanMagic = 0x31525054;  // "TPR1"
+constexpr int32_t kPlanVersion = 1;
+
+// Header word indices.
+enum PlanField : int {
+  PF_MAGIC = 0,
+  PF_VERSION,
+  PF_NUM_LEAVES,
+  PF_NUM_NODES,
+  PF_MAX_DEPTH,
+  PF_TOTAL_Q,
+  PF_TOTAL_PREFIX,
+  PF_HQ,
+  PF_HKV,
+  PF_D,
+  PF_DTYPE,
+  PF_PATH,           // KernelPath
+  PF_OFF_CU,         // cu_seqlens_q [N+1]
+  PF_OFF_NODE_OFF,   // node_offsets [M+1]
+  PF_OFF_ANC,        // leaf_ancestors [N*max_depth]
+  PF_OFF_NODE_LEAF,  // node leaf range [M][2] = {first leaf, last leaf + 1}
+  PF_N_QBLK,         // number of query blocks (dK/dV kernel granularity)
+  PF_OFF_QBLK,       // query blocks [n][2] = {leaf, token start within leaf}
+  PF_OFF_LEAF_QBLK,  // first query block of each leaf [N+1]
+  PF_N_FWD,          // forward / dQ work items
+  PF_OFF_FWD,        // [n][4] = {leaf, token start, first q head, kv head}; leaf < 0 = empty
+  PF_N_DKDV,         // dK/dV work items
+  PF_OFF_DKDV,       // [n][8] = DkdvItem
+  PF_N_RED,          // split-reduction items
+  PF_OFF_RED,        // [n][4] = {node, key start, kv head, first slot}
+  PF_N_SLOTS,        // fp32 partial slots (each kDkdvKeys x D x 2 floats)
+  PF_SPLIT,          // partials per split prefix tile
+  PF_TOTAL_WORDS,
+  PF_HEADER_WORDS = 32
+};
+
+enum KernelPath : int32_t {
+  PATH_SIMT = 0,  // portable fp32-accumulate SIMT kernels (fp32, or any head_dim)
+  PATH_MFMA = 1   // bf16 MFMA kernels, head_dim 128
+};
+
+// dK/dV work item: one (KV segment tile, KV head) and the query blocks that see it.
+enum DkdvField : int {
+  DK_SRC = 0,   // 0 = prefix node (fully visible), 1 = leaf suffix (causal)
+  DK_SEG,       // node id or leaf id
+  DK_KEY0,      // first key of the tile, relative to the segment
+  DK_KVH,       // KV head
+  DK_QB_LO,     // query-block range [lo, hi) in the global query-block list
+  DK_QB_HI,
+  DK_SLOT,      // -1: write dK/dV directly; else fp32 partial slot
+  DK_PAD,
+  DK_WORDS = 8
+};
+
+// ---- tile shapes -----------------------------------------------------------
+// SIMT family (any dtype / head_dim <= 128)
+constexpr int kSimtQ = 64;      // queries per forward / dQ block (one head)
+constexpr int kSimtKeys = 64;   // keys per dK/dV block
+constexpr int kSimtTile = 32;   // keys (fwd/dQ) or queries (dK/dV) staged per LDS tile
+
+// MFMA family (bf16, head_dim 128)
+constexpr int kMfmaD = 128;
+constexpr int kFwdWaves = 4;          // waves per forward / dQ workgroup
+constexpr int kFwdTokens = 32;        // tokens per wave (one query head per wave)
+constexpr int kFwdKeys = 64;          // keys per LDS tile
+constexpr int kDkdvWaves = 4;         // waves per dK/dV workgroup
+constexpr int kDkdvKeys = 32 * kDkdvWaves;  // keys per dK/dV workgroup (32 per wave)
+constexpr int kDkdvQ = 64;            // queries per staged query block
+
+}  // namespace tpr

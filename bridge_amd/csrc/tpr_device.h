@@ -1,0 +1,84 @@
+// tpr_device.h -- device helpers shared by the HIP kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "tpr_common.h"
+
+namespace tpr {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// Arguments every kernel receives by value. Plan offsets are copied from the
+// host header so kernels do not chase them through memory.
+struct KernelArgs {
+  const int32_t* plan;
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* pk;
+  const void* pv;
+  const void* out_in;   // forward output (backward input)
+  const void* dout;
+  void* out;            // forward output
+  float* lse;           // [Hq, Tq]
+  float* delta;         // [Hq, Tq]
+  const float* lse_in;  // backward input
+  void* dq;
+  void* dk;
+  void* dv;
+  void* dpk;
+  void* dpv;
+  float scale;
+  int32_t hq, hkv, d, group;
+  int32_t hpw;  // query heads per forward/dQ workgroup (MFMA path)
+  int32_t total_q, total_prefix, max_depth;
+  int32_t off_cu, off_node_off, off_anc, off_node_leaf;
+  int32_t off_qblk, off_leaf_qblk, off_fwd, off_dkdv;
+  int32_t n_items;
+};
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(bf16 x) { return static_cast<float>(x); }
+template <typename T> __device__ __forceinline__ T from_f32(float x);
+template <> __device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <> __device__ __forceinline__ bf16 from_f32<bf16>(float x) { return static_cast<bf16>(x); }
+
+// 16-byte chunk swizzle of a [rows][128 bf16] LDS tile (256 B rows):
+// physical chunk = logical chunk ^ f(row), with f swapping the two 2-bit
+// fields of row % 16. Rows r..r+15 at one logical chunk land in 16 distinct
+// chunks (conflict-free ds_read_b128 over 16 lanes), and 4 consecutive rows
+// (r % 4 == 0) x 4 consecutive chunks land in 16 distinct chunks
+// (conflict-free ds_read_tr16_b64 over 32 lanes).
+__device__ __forceinline__ int swz_chunk(int row, int chunk) {
+  return chunk ^ (((row & 3) << 2) | ((row >> 2) & 3));
+}
+// byte offset of element (row, col) in a swizzled 256-byte-row tile
+__device__ __forceinline__ int swz_off(int row, int col) {
+  return row * 256 + (swz_chunk(row, col >> 3) << 4) + ((col & 7) << 1);
+}
+
+// Key permutation sigma applied to the A-operand rows of a 32x32x16 MFMA so
+// that accumulator register r of lane-half h holds key 16*(r/8) + 8*h + r%8:
+// the 8 registers of one 16-key chunk are then 8 consecutive keys, which is
+// the k-slot order of the next MFMA's operand.
+__device__ __forceinline__ int sigma32(int m) {
+  const int a = m >> 3, h = (m >> 2) & 1, b = m & 3;
+  return ((a >> 1) << 4) + (h << 3) + ((a & 1) << 2) + b;
+}
+
+__device__ __forceinline__ float wave_max32(float x) {  // max over lanes l and l^32
+  return fmaxf(x, __shfl_xor(x, 32));
+}
+__device__ __forceinline__ float wave_sum32(float x) { return x + __shfl_xor(x, 32); }
+
+}  // namespace tpr

@@ -1,0 +1,583 @@
+// tpr_mfma.hip -- gfx950 bf16 MFMA prefix-reuse attention kernels (head_dim 128).
+//
+// Forward and dQ: one workgroup = 4 waves sharing one KV head; wave w owns 32
+// tokens of one query head of the GQA group, so every K/V tile staged in LDS
+// feeds all query heads of the group. The key loop runs over the ancestor
+// prefix nodes (fully visible, root first) and then the leaf's own suffix
+// (right-down causal), keeping one online-softmax state (max, sum, O) in
+// registers across both phases: the fp32 (out, max, sum) merge of the
+// reference's prefix FULL and suffix CAUSAL blocks
+// (verl/models/mcore/tpr/parallel/ring_attention.py:588-636) happens in the
+// loop instead of between kernel calls.
+//
+// dK/dV: one workgroup = 4 waves x 32 keys of one KV segment tile and KV head;
+// it streams every query block that sees those keys (for a prefix node: all
+// descendant leaves, every query head of the group) in the plan's fixed
+// order, so a prefix node's gradient is summed over siblings in registers,
+// without atomics (the deterministic counterpart of
+// verl/models/mcore/tpr/prefix_state.py:565-573).
+//
+// MFMA layout (v_mfma_f32_32x32x16_bf16): A lane l holds row l%32, k-slots
+// 8*(l/32)+i; B lane l holds column l%32, same k-slots; accumulator register r
+// of lane l holds (row 8*(r/4) + 4*(l/32) + r%4, column l%32). Scores are
+// computed transposed (S^T = K Q^T) with the key rows permuted by sigma32, so
+// a lane holds one query and 8-key runs; P^T then feeds the P.V MFMA as its B
+// operand straight from registers, and V is read column-wise from its
+// row-major LDS tile with ds_read_tr16_b64.
+
+#include "tpr_device.h"
+
+namespace tpr {
+namespace {
+
+constexpr int kTileRows = 64;                 // rows per staged K/V/Q/dO tile
+constexpr int kTileBytes = kTileRows * 256;   // 64 rows x 128 bf16
+
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+__device__ __forceinline__ f32x16 mfma(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ bf16x8 lds_read_b128(const char* tile, int row, int col) {
+  return *reinterpret_cast<const bf16x8*>(tile + swz_off(row, col));
+}
+
+// Transposed operand read: lane l gets rows r0 + 0..7 (two ds_read_tr16_b64)
+// of column c0 + (l % 32) -- i.e. 8 consecutive rows of one column of a
+// row-major swizzled tile. r0 must be a multiple of 8 plus 8*(l/32) handled by
+// the caller; c0 a multiple of 32.
+__device__ __forceinline__ bf16x8 lds_read_col8(const char* tile, int r0, int c0, int lane) {
+  const int g = lane >> 4, i = lane & 15;
+  const int row = r0 + (i >> 2);
+  const int col = c0 + ((g & 1) << 4) + ((i & 3) << 2);
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_s16x4*)(tile + swz_off(row, col)));
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_s16x4*)(tile + swz_off(row + 4, col)));
+  bf16x8 r;
+  const bf16x4 l4 = __builtin_bit_cast(bf16x4, lo);
+  const bf16x4 h4 = __builtin_bit_cast(bf16x4, hi);
+  r[0] = l4[0]; r[1] = l4[1]; r[2] = l4[2]; r[3] = l4[3];
+  r[4] = h4[0]; r[5] = h4[1]; r[6] = h4[2]; r[7] = h4[3];
+  return r;
+}
+
+__device__ __forceinline__ bf16x8 to_bf16x8(const f32x16& x, int base) {
+  bf16x8 r;
+#pragma unroll
+  for (int i = 0; i < 8; i++) r[i] = static_cast<bf16>(x[base + i]);
+  return r;
+}
+
+// Locate tile `idx` of a forward/dQ key stream: ancestors (full) then suffix
+// (causal). Returns the row offset into the segment's tensor and fills the
+// tile's key count, the key position of its first row and the causal flag.
+struct TileLoc {
+  int64_t row;   // absolute row in prefix_k/v (prefix) or k/v (suffix)
+  int len;       // valid rows in this tile (<= 64)
+  int pos0;      // position of the first key (suffix tiles: within the leaf)
+  bool suffix;
+};
+
+__device__ __forceinline__ TileLoc locate_tile(const KernelArgs& a, int leaf, int suffix_keys, int idx) {
+  const int32_t* no = a.plan + a.off_node_off;
+  const int32_t* anc = a.plan + a.off_anc + leaf * a.max_depth;
+  for (int dd = 0; dd < a.max_depth; dd++) {
+    const int n = anc[dd];
+    if (n < 0) break;
+    const int len = no[n + 1] - no[n];
+    const int tiles = (len + kTileRows - 1) / kTileRows;
+    if (idx < tiles) return TileLoc{static_cast<int64_t>(no[n]) + idx * kTileRows,
+                                    min(kTileRows, len - idx * kTileRows), idx * kTileRows, false};
+    idx -= tiles;
+  }
+  const int32_t* cu = a.plan + a.off_cu;
+  return TileLoc{static_cast<int64_t>(cu[leaf]) + idx * kTileRows, min(kTileRows, suffix_keys - idx * kTileRows),
+                 idx * kTileRows, true};
+}
+
+__device__ __forceinline__ int count_tiles(const KernelArgs& a, int leaf, int suffix_keys) {
+  const int32_t* no = a.plan + a.off_node_off;
+  const int32_t* anc = a.plan + a.off_anc + leaf * a.max_depth;
+  int tiles = 0;
+  for (int dd = 0; dd < a.max_depth; dd++) {
+    const int n = anc[dd];
+    if (n < 0) break;
+    tiles += (no[n + 1] - no[n] + kTileRows - 1) / kTileRows;
+  }
+  return tiles + (suffix_keys + kTileRows - 1) / kTileRows;
+}
+
+// Global -> register staging of one 64x128 bf16 tile pair (4 chunks of 16 B
+// per thread per tensor), and register -> swizzled LDS store.
+struct Stage2 {
+  bf16x8 x[4];
+  bf16x8 y[4];
+};
+
+__device__ __forceinline__ void stage_load(Stage2& st, const bf16* xb, const bf16* yb, int64_t stride,
+                                           int64_t row0, int len) {
+#pragma unroll
+  for (int u = 0; u < 4; u++) {
+    const int idx = threadIdx.x + 256 * u;
+    const int r = min(idx >> 4, len - 1);
+    const int64_t off = (row0 + r) * stride + ((idx & 15) << 3);
+    st.x[u] = *reinterpret_cast<const bf16x8*>(xb + off);
+    st.y[u] = *reinterpret_cast<const bf16x8*>(yb + off);
+  }
+}
+
+__device__ __forceinline__ void stage_store(const Stage2& st, char* xt, char* yt) {
+#pragma unroll
+  for (int u = 0; u < 4; u++) {
+    const int idx = threadIdx.x + 256 * u;
+    const int off = swz_off(idx >> 4, (idx & 15) << 3);
+    *reinterpret_cast<bf16x8*>(xt + off) = st.x[u];
+    *reinterpret_cast<bf16x8*>(yt + off) = st.y[u];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Forward
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256, 2) void mfma_fwd(KernelArgs a) {
+  const int32_t* item = a.plan + a.off_fwd + 4 * blockIdx.x;
+  const int leaf = item[0];
+  if (leaf < 0) return;
+  const int tok0 = item[1], qh0 = item[2], kvh = item[3];
+  const int32_t* cu = a.plan + a.off_cu;
+  const int row0 = cu[leaf], len = cu[leaf + 1] - cu[leaf];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int hpw = a.hpw;  // query heads per workgroup
+  const int head = qh0 + wave % hpw;
+  const int tw0 = tok0 + kFwdTokens * (wave / hpw);  // first token of this wave
+  const int tpw = kFwdTokens * (kFwdWaves / hpw);    // tokens per workgroup
+  const int suffix_keys = min(len, tok0 + tpw);
+  const int n = lane & 31, h = lane >> 5;
+  const int t = tw0 + n;                            // this lane's query token
+  const bool wave_active = tw0 < len;
+
+  const int64_t qstride = static_cast<int64_t>(a.hq) * kMfmaD;
+  const int64_t kstride = static_cast<int64_t>(a.hkv) * kMfmaD;
+
+  __shared__ __attribute__((aligned(16))) char smem[4 * kTileBytes];  // K0 V0 K1 V1
+
+  // Q as the B operand of S^T = K Q^T: lane holds Q[t][16c + 8h .. +7]
+  bf16x8 qv[8];
+  {
+    const bf16* qp = static_cast<const bf16*>(a.q) + static_cast<int64_t>(row0 + min(t, len - 1)) * qstride +
+                     head * kMfmaD + 8 * h;
+#pragma unroll
+    for (int c = 0; c < 8; c++) qv[c] = *reinterpret_cast<const bf16x8*>(qp + 16 * c);
+  }
+
+  f32x16 o[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) o[i] = f32x16{};
+  float m = -1e30f, l = 0.f;
+  const float c2 = a.scale * kLog2e;
+
+  const bf16* kbase = static_cast<const bf16*>(a.k) + kvh * kMfmaD;
+  const bf16* vbase = static_cast<const bf16*>(a.v) + kvh * kMfmaD;
+  const bf16* pkbase = static_cast<const bf16*>(a.pk) + kvh * kMfmaD;
+  const bf16* pvbase = static_cast<const bf16*>(a.pv) + kvh * kMfmaD;
+
+  const int ntiles = count_tiles(a, leaf, suffix_keys);
+  Stage2 st;
+  {
+    const TileLoc tl = locate_tile(a, leaf, suffix_keys, 0);
+    stage_load(st, tl.suffix ? kbase : pkbase, tl.suffix ? vbase : pvbase, kstride, tl.row, tl.len);
+    stage_store(st, smem, smem + kTileBytes);
+  }
+  __syncthreads();
+
+  for (int it = 0; it < ntiles; it++) {
+    const char* kt = smem + (it & 1) * 2 * kTileBytes;
+    const char* vt = kt + kTileBytes;
+    const TileLoc tl = locate_tile(a, leaf, suffix_keys, it);
+    if (it + 1 < ntiles) {
+      const TileLoc nx = locate_tile(a, leaf, suffix_keys, it + 1);
+      stage_load(st, nx.suffix ? kbase : pkbase, nx.suffix ? vbase : pvbase, kstride, nx.row, nx.len);
+    }
+    // a wave skips tiles whose keys are all in its future
+    const bool skip = !wave_active || (tl.suffix && tl.pos0 > tw0 + kFwdTokens - 1);
+    if (!skip) {
+      f32x16 s[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++) {
+        s[kb] = f32x16{};
+        const int krow = kb * 32 + sigma32(n);
+#pragma unroll
+        for (int c = 0; c < 8; c++) s[kb] = mfma(lds_read_b128(kt, krow, 16 * c + 8 * h), qv[c], s[kb]);
+      }
+      const bool need_mask = tl.len < kTileRows || (tl.suffix && tl.pos0 + kTileRows - 1 > tw0);
+      if (need_mask) {
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+          for (int r = 0; r < 16; r++) {
+            const int j = kb * 32 + 16 * (r >> 3) + 8 * h + (r & 7);
+            const bool vis = j < tl.len && (!tl.suffix || tl.pos0 + j <= t);
+            if (!vis) s[kb][r] = -INFINITY;
+          }
+      }
+      float mt = m;
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) mt = fmaxf(mt, s[kb][r]);
+      mt = wave_max32(mt);
+      const float alpha = exp2f((m - mt) * c2);
+      const float mc = mt * c2;
+      m = mt;
+      float ls = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const float p = exp2f(fmaf(s[kb][r], c2, -mc));
+          s[kb][r] = p;
+          ls += p;
+        }
+      l = l * alpha + ls;
+#pragma unroll
+      for (int db = 0; db < 4; db++) o[db] *= alpha;
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+        for (int cc = 0; cc < 2; cc++) {
+          const bf16x8 pb = to_bf16x8(s[kb], 8 * cc);
+          const int r0 = kb * 32 + 16 * cc + 8 * h;
+#pragma unroll
+          for (int db = 0; db < 4; db++) o[db] = mfma(lds_read_col8(vt, r0, 32 * db, lane), pb, o[db]);
+        }
+    }
+    if (it + 1 < ntiles) {
+      char* nk = smem + ((it + 1) & 1) * 2 * kTileBytes;
+      stage_store(st, nk, nk + kTileBytes);
+    }
+    __syncthreads();
+  }
+
+  const float lt = wave_sum32(l);  // all 64 lanes take part in the exchange
+  if (!wave_active || t >= len) return;
+  const float inv = 1.f / lt;
+  bf16* op = static_cast<bf16*>(a.out) + static_cast<int64_t>(row0 + t) * qstride + head * kMfmaD;
+#pragma unroll
+  for (int db = 0; db < 4; db++)
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      bf16x4 v4;
+#pragma unroll
+      for (int b = 0; b < 4; b++) v4[b] = static_cast<bf16>(o[db][4 * g + b] * inv);
+      *reinterpret_cast<bf16x4*>(op + 32 * db + 8 * g + 4 * h) = v4;
+    }
+  if (h == 0) a.lse[static_cast<int64_t>(head) * a.total_q + row0 + t] = m * a.scale + logf(lt);
+}
+
+// ---------------------------------------------------------------------------
+// dQ: same workgroup shape and key stream as the forward.
+//   S^T = K Q^T, P^T = exp(scale S^T - lse), dP^T = V dO^T,
+//   dS^T = P^T (dP^T - delta), dQ^T += K^T dS^T, dQ = scale * dQ.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256, 2) void mfma_dq(KernelArgs a) {
+  const int32_t* item = a.plan + a.off_fwd + 4 * blockIdx.x;
+  const int leaf = item[0];
+  if (leaf < 0) return;
+  const int tok0 = item[1], qh0 = item[2], kvh = item[3];
+  const int32_t* cu = a.plan + a.off_cu;
+  const int row0 = cu[leaf], len = cu[leaf + 1] - cu[leaf];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int hpw = a.hpw;
+  const int head = qh0 + wave % hpw;
+  const int tw0 = tok0 + kFwdTokens * (wave / hpw);
+  const int tpw = kFwdTokens * (kFwdWaves / hpw);
+  const int suffix_keys = min(len, tok0 + tpw);
+  const int n = lane & 31, h = lane >> 5;
+  const int t = tw0 + n;
+  const int tc = min(t, len - 1);
+  const bool wave_active = tw0 < len;
+
+  const int64_t qstride = static_cast<int64_t>(a.hq) * kMfmaD;
+  const int64_t kstride = static_cast<int64_t>(a.hkv) * kMfmaD;
+
+  __shared__ __attribute__((aligned(16))) char smem[4 * kTileBytes];
+
+  bf16x8 qv[8], gv[8];
+  {
+    const int64_t off = static_cast<int64_t>(row0 + tc) * qstride + head * kMfmaD + 8 * h;
+    const bf16* qp = static_cast<const bf16*>(a.q) + off;
+    const bf16* gp = static_cast<const bf16*>(a.dout) + off;
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+      qv[c] = *reinterpret_cast<const bf16x8*>(qp + 16 * c);
+      gv[c] = *reinterpret_cast<const bf16x8*>(gp + 16 * c);
+    }
+  }
+  const int64_t stat = static_cast<int64_t>(head) * a.total_q + row0 + tc;
+  const float c2 = a.scale * kLog2e;
+  const float lse2 = a.lse_in[stat] * kLog2e;
+  const float delta = a.delta[stat];
+
+  f32x16 dq[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) dq[i] = f32x16{};
+
+  const bf16* kbase = static_cast<const bf16*>(a.k) + kvh * kMfmaD;
+  const bf16* vbase = static_cast<const bf16*>(a.v) + kvh * kMfmaD;
+  const bf16* pkbase = static_cast<const bf16*>(a.pk) + kvh * kMfmaD;
+  const bf16* pvbase = static_cast<const bf16*>(a.pv) + kvh * kMfmaD;
+
+  const int ntiles = count_tiles(a, leaf, suffix_keys);
+  Stage2 st;
+  {
+    const TileLoc tl = locate_tile(a, leaf, suffix_keys, 0);
+    stage_load(st, tl.suffix ? kbase : pkbase, tl.suffix ? vbase : pvbase, kstride, tl.row, tl.len);
+    stage_store(st, smem, smem + kTileBytes);
+  }
+  __syncthreads();
+
+  for (int it = 0; it < ntiles; it++) {
+    const char* kt = smem + (it & 1) * 2 * kTileBytes;
+    const char* vt = kt + kTileBytes;
+    const TileLoc tl = locate_tile(a, leaf, suffix_keys, it);
+    if (it + 1 < ntiles) {
+      const TileLoc nx = locate_tile(a, leaf, suffix_keys, it + 1);
+      stage_load(st, nx.suffix ? kbase : pkbase, nx.suffix ? vbase : pvbase, kstride, nx.row, nx.len);
+    }
+    const bool skip = !wave_active || (tl.suffix && tl.pos0 > tw0 + kFwdTokens - 1);
+    if (!skip) {
+      f32x16 s[2], dp[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++) {
+        s[kb] = f32x16{};
+        dp[kb] = f32x16{};
+        const int krow = kb * 32 + sigma32(n);
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+          s[kb] = mfma(lds_read_b128(kt, krow, 16 * c + 8 * h), qv[c], s[kb]);
+          dp[kb] = mfma(lds_read_b128(vt, krow, 16 * c + 8 * h), gv[c], dp[kb]);
+        }
+      }
+      const bool need_mask = tl.len < kTileRows || (tl.suffix && tl.pos0 + kTileRows - 1 > tw0);
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          float p = exp2f(fmaf(s[kb][r], c2, -lse2));
+          if (need_mask) {
+            const int j = kb * 32 + 16 * (r >> 3) + 8 * h + (r & 7);
+            if (!(j < tl.len && (!tl.suffix || tl.pos0 + j <= t))) p = 0.f;
+          }
+          s[kb][r] = p * (dp[kb][r] - delta);  // dS^T
+        }
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+        for (int cc = 0; cc < 2; cc++) {
+          const bf16x8 dsb = to_bf16x8(s[kb], 8 * cc);
+          const int r0 = kb * 32 + 16 * cc + 8 * h;
+#pragma unroll
+          for (int db = 0; db < 4; db++) dq[db] = mfma(lds_read_col8(kt, r0, 32 * db, lane), dsb, dq[db]);
+        }
+    }
+    if (it + 1 < ntiles) {
+      char* nk = smem + ((it + 1) & 1) * 2 * kTileBytes;
+      stage_store(st, nk, nk + kTileBytes);
+    }
+    __syncthreads();
+  }
+
+  if (!wave_active || t >= len) return;
+  bf16* dst = static_cast<bf16*>(a.dq) + static_cast<int64_t>(row0 + t) * qstride + head * kMfmaD;
+#pragma unroll
+  for (int db = 0; db < 4; db++)
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      bf16x4 v4;
+#pragma unroll
+      for (int b = 0; b < 4; b++) v4[b] = static_cast<bf16>(dq[db][4 * g + b] * a.scale);
+      *reinterpret_cast<bf16x4*>(dst + 32 * db + 8 * g + 4 * h) = v4;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// dK/dV
+//   S = Q K^T (query rows permuted by sigma32), P = exp(scale S - lse),
+//   dP = dO V^T, dS = P (dP - delta), dV += P^T dO, dK += dS^T Q, dK *= scale.
+// K/V of the wave's 32 keys are B operands held in registers; Q/dO blocks of
+// 64 queries are staged in LDS and read row-wise (A operands) and
+// column-wise (B operands of dV/dK, ds_read_tr16_b64).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
+  const int32_t* item = a.plan + a.off_dkdv + DK_WORDS * blockIdx.x;
+  if (item[DK_SRC] < 0) return;
+  const bool prefix = item[DK_SRC] == 0;
+  const int seg = item[DK_SEG], key0 = item[DK_KEY0], kvh = item[DK_KVH];
+  const int qb_lo = item[DK_QB_LO], qb_hi = item[DK_QB_HI];
+  const int32_t* cu = a.plan + a.off_cu;
+  const int32_t* no = a.plan + a.off_node_off;
+  const int32_t* qblk = a.plan + a.off_qblk;
+  const int seg_row0 = prefix ? no[seg] : cu[seg];
+  const int seg_len = prefix ? no[seg + 1] - no[seg] : cu[seg + 1] - cu[seg];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n = lane & 31, h = lane >> 5;
+  const int kw0 = key0 + 32 * wave;          // first key position of this wave
+  const int kp = kw0 + n;                     // this lane's key position (B-operand column)
+  const bool wave_active = kw0 < seg_len;
+
+  const int64_t qstride = static_cast<int64_t>(a.hq) * kMfmaD;
+  const int64_t kstride = static_cast<int64_t>(a.hkv) * kMfmaD;
+
+  __shared__ __attribute__((aligned(16))) char smem[4 * kTileBytes];   // Q0 G0 Q1 G1
+  __shared__ __attribute__((aligned(16))) float stats[2][2][kTileRows];  // [buf][lse2|delta][row]
+
+  bf16x8 kv[8], vv[8];
+  {
+    const bf16* kb = static_cast<const bf16*>(prefix ? a.pk : a.k);
+    const bf16* vb = static_cast<const bf16*>(prefix ? a.pv : a.v);
+    const int64_t off = static_cast<int64_t>(seg_row0 + min(kp, seg_len - 1)) * kstride + kvh * kMfmaD + 8 * h;
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+      kv[c] = *reinterpret_cast<const bf16x8*>(kb + off + 16 * c);
+      vv[c] = *reinterpret_cast<const bf16x8*>(vb + off + 16 * c);
+    }
+  }
+  f32x16 dk[4], dv[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    dk[i] = f32x16{};
+    dv[i] = f32x16{};
+  }
+  const float c2 = a.scale * kLog2e;
+  const int nstage = (qb_hi - qb_lo) * a.group;
+  const bf16* qbase = static_cast<const bf16*>(a.q);
+  const bf16* gbase = static_cast<const bf16*>(a.dout);
+
+  auto stage_info = [&](int sidx, int& row0, int& tok0, int& nq, int& qh) {
+    const int qb = qb_lo + sidx / a.group;
+    qh = kvh * a.group + sidx % a.group;
+    const int lf = qblk[2 * qb];
+    tok0 = qblk[2 * qb + 1];
+    row0 = cu[lf];
+    nq = min(kTileRows, cu[lf + 1] - row0 - tok0);
+  };
+  auto load_stats = [&](int buf, int row0, int tok0, int nq, int qh) {
+    if (threadIdx.x < 2 * kTileRows) {
+      const int r = threadIdx.x & (kTileRows - 1);
+      const int64_t at = static_cast<int64_t>(qh) * a.total_q + row0 + tok0 + min(r, nq - 1);
+      if (threadIdx.x < kTileRows)
+        stats[buf][0][r] = r < nq ? a.lse_in[at] * kLog2e : INFINITY;  // invalid query: P = 0
+      else
+        stats[buf][1][r] = r < nq ? a.delta[at] : 0.f;
+    }
+  };
+
+  Stage2 st;
+  if (nstage > 0) {
+    int row0, tok0, nq, qh;
+    stage_info(0, row0, tok0, nq, qh);
+    stage_load(st, qbase + qh * kMfmaD, gbase + qh * kMfmaD, qstride, row0 + tok0, nq);
+    stage_store(st, smem, smem + kTileBytes);
+    load_stats(0, row0, tok0, nq, qh);
+  }
+  __syncthreads();
+
+  for (int sidx = 0; sidx < nstage; sidx++) {
+    const int buf = sidx & 1;
+    const char* qt = smem + buf * 2 * kTileBytes;
+    const char* gt = qt + kTileBytes;
+    int row0, tok0, nq, qh;
+    stage_info(sidx, row0, tok0, nq, qh);
+    int nrow0 = 0, ntok0 = 0, nnq = 0, nqh = 0;
+    if (sidx + 1 < nstage) {
+      stage_info(sidx + 1, nrow0, ntok0, nnq, nqh);
+      stage_load(st, qbase + nqh * kMfmaD, gbase + nqh * kMfmaD, qstride, nrow0 + ntok0, nnq);
+    }
+    if (wave_active) {
+#pragma unroll
+      for (int qs = 0; qs < 2; qs++) {
+        const int qpos0 = tok0 + 32 * qs;  // first query position of the sub-block
+        // skip sub-blocks past the leaf end, or (suffix) entirely before the wave's keys
+        if (32 * qs >= nq || (!prefix && qpos0 + 31 < kw0)) continue;
+        f32x16 s = f32x16{}, dp = f32x16{};
+        const int qrow = 32 * qs + sigma32(n);
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+          s = mfma(lds_read_b128(qt, qrow, 16 * c + 8 * h), kv[c], s);
+          dp = mfma(lds_read_b128(gt, qrow, 16 * c + 8 * h), vv[c], dp);
+        }
+        // register r holds query 32*qs + 16*(r/8) + 8*h + r%8 of the block
+        const float* l2 = &stats[buf][0][32 * qs + 8 * h];
+        const float* dl = &stats[buf][1][32 * qs + 8 * h];
+        const bool need_mask = !prefix && qpos0 < kw0 + 31;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const int qi = 16 * (r >> 3) + (r & 7);
+          float p = exp2f(fmaf(s[r], c2, -l2[qi]));
+          if (need_mask && kp > qpos0 + 8 * h + qi) p = 0.f;
+          s[r] = p;
+          dp[r] = p * (dp[r] - dl[qi]);
+        }
+#pragma unroll
+        for (int cc = 0; cc < 2; cc++) {
+          const bf16x8 pb = to_bf16x8(s, 8 * cc);
+          const bf16x8 db8 = to_bf16x8(dp, 8 * cc);
+          const int r0 = 32 * qs + 16 * cc + 8 * h;
+#pragma unroll
+          for (int db = 0; db < 4; db++) {
+            dv[db] = mfma(pb, lds_read_col8(gt, r0, 32 * db, lane), dv[db]);
+            dk[db] = mfma(db8, lds_read_col8(qt, r0, 32 * db, lane), dk[db]);
+          }
+        }
+      }
+    }
+    if (sidx + 1 < nstage) {
+      char* nt = smem + (buf ^ 1) * 2 * kTileBytes;
+      stage_store(st, nt, nt + kTileBytes);
+      load_stats(buf ^ 1, nrow0, ntok0, nnq, nqh);
+    }
+    __syncthreads();
+  }
+
+  if (!wave_active) return;
+  // accumulator register r of lane l: key 8*(r/4) + 4*h + r%4 of the wave, d = 32*db + n
+  bf16* dkd = static_cast<bf16*>(prefix ? a.dpk : a.dk);
+  bf16* dvd = static_cast<bf16*>(prefix ? a.dpv : a.dv);
+#pragma unroll
+  for (int r = 0; r < 16; r++) {
+    const int key = kw0 + 8 * (r >> 2) + 4 * h + (r & 3);
+    if (key >= seg_len) continue;
+    const int64_t off = static_cast<int64_t>(seg_row0 + key) * kstride + kvh * kMfmaD + n;
+#pragma unroll
+    for (int db = 0; db < 4; db++) {
+      dkd[off + 32 * db] = static_cast<bf16>(dk[db][r] * a.scale);
+      dvd[off + 32 * db] = static_cast<bf16>(dv[db][r]);
+    }
+  }
+}
+
+}  // namespace
+
+int launch_mfma_fwd(const KernelArgs& a, hipStream_t s) {
+  if (a.n_items > 0) hipLaunchKernelGGL(mfma_fwd, dim3(a.n_items), dim3(256), 0, s, a);
+  return hipGetLastError() == hipSuccess ? 0 : 4;
+}
+
+int launch_mfma_bwd(const KernelArgs& a, int n_fwd, int n_dkdv, hipStream_t s) {
+  if (n_dkdv > 0) {
+    hipLaunchKernelGGL(mfma_dkdv, dim3(n_dkdv), dim3(256), 0, s, a);
+    if (hipGetLastError() != hipSuccess) return 4;
+  }
+  if (n_fwd > 0) {
+    hipLaunchKernelGGL(mfma_dq, dim3(n_fwd), dim3(256), 0, s, a);
+    if (hipGetLastError() != hipSuccess) return 4;
+  }
+  return 0;
+}
+
+}  // namespace tpr

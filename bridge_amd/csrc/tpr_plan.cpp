@@ -1,0 +1,277 @@
+// tpr_plan.cpp -- host planner: validates the prefix tree and lowers it to the
+// flat int32 plan blob the kernels consume (tree metadata + work lists).
+//
+// The tree contract follows the reference's SegmentPlan
+// (verl/models/mcore/tpr/segment_plan.py:153-313: one parent per segment,
+// children start at the parent's end) after lowering to packed offsets, and
+// the prefix path order of KVStack.build_past_key_values (kv_stack.py:139-154).
+//
+// Work lists are ordered for the MI355X dispatcher: workgroup i runs on XCD
+// i % 8, so items are dealt into 8 per-XCD queues (all items of one KV head
+// on the same XCD when the head count allows it, so that head's prefix K/V
+// tiles are fetched into one L2), each queue in decreasing-work order, and
+// interleaved back into one array.
+
+#include <algorithm>
+#include <cstring>
+#include <numeric>
+#include <vector>
+
+#include "../../include/tpr_attn.h"
+#include "tpr_common.h"
+#include "tpr_host.h"
+
+namespace tpr {
+namespace {
+
+constexpr int kXcds = 8;
+
+struct Item {
+  std::vector<int32_t> words;
+  int64_t work;
+  int32_t kvh;
+};
+
+int gcd_int(int a, int b) { return b == 0 ? a : gcd_int(b, a % b); }
+
+// Deal items into per-XCD queues and interleave; pads with empty items
+// (first word -1) so every queue has the same length.
+std::vector<int32_t> order_for_xcds(std::vector<Item>& items, int hkv, int words_per_item, int32_t* count) {
+  std::stable_sort(items.begin(), items.end(), [](const Item& a, const Item& b) { return a.work > b.work; });
+  std::vector<std::vector<const Item*>> queue(kXcds);
+  std::vector<int64_t> load(kXcds, 0);
+  for (const Item& it : items) {
+    int best = -1;
+    if (hkv % kXcds == 0) {
+      best = it.kvh % kXcds;
+    } else if (kXcds % hkv == 0) {
+      // head h owns XCDs {h, h + hkv, h + 2*hkv, ...}
+      for (int x = it.kvh; x < kXcds; x += hkv)
+        if (best < 0 || load[x] < load[best]) best = x;
+    } else {
+      for (int x = 0; x < kXcds; x++)
+        if (best < 0 || load[x] < load[best]) best = x;
+    }
+    queue[best].push_back(&it);
+    load[best] += it.work;
+  }
+  size_t depth = 0;
+  for (auto& q : queue) depth = std::max(depth, q.size());
+  std::vector<int32_t> out;
+  out.reserve(depth * kXcds * words_per_item);
+  for (size_t i = 0; i < depth; i++) {
+    for (int x = 0; x < kXcds; x++) {
+      if (i < queue[x].size()) {
+        out.insert(out.end(), queue[x][i]->words.begin(), queue[x][i]->words.end());
+      } else {
+        std::vector<int32_t> empty(words_per_item, 0);
+        empty[0] = -1;
+        out.insert(out.end(), empty.begin(), empty.end());
+      }
+    }
+  }
+  // drop trailing all-empty rows (cannot happen: the first row is full when any item exists)
+  *count = static_cast<int32_t>(depth * kXcds);
+  if (items.empty()) {
+    out.clear();
+    *count = 0;
+  }
+  return out;
+}
+
+}  // namespace
+
+static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
+  if (!t) return fail(TPR_ERR_INVALID_ARGUMENT, "tree descriptor is NULL");
+  const int N = t->num_leaves, M = t->num_nodes, depth = t->max_depth;
+  const int Hq = t->num_q_heads, Hkv = t->num_kv_heads, D = t->head_dim;
+  if (N <= 0) return fail(TPR_ERR_INVALID_ARGUMENT, "num_leaves must be positive, got %d", N);
+  if (M < 0) return fail(TPR_ERR_INVALID_ARGUMENT, "num_nodes must be non-negative, got %d", M);
+  if (depth < 0) return fail(TPR_ERR_INVALID_ARGUMENT, "max_depth must be non-negative, got %d", depth);
+  if (M > 0 && depth == 0) return fail(TPR_ERR_INVALID_ARGUMENT, "max_depth must be positive when nodes exist");
+  if (Hq <= 0 || Hkv <= 0 || D <= 0)
+    return fail(TPR_ERR_INVALID_ARGUMENT, "head counts and head_dim must be positive, got Hq=%d Hkv=%d D=%d", Hq, Hkv, D);
+  if (Hq % Hkv != 0)
+    return fail(TPR_ERR_INVALID_ARGUMENT, "query head count must be divisible by KV head count, got Q=%d, KV=%d", Hq, Hkv);
+  if (D > 128 || D % 8 != 0)
+    return fail(TPR_ERR_UNSUPPORTED, "head_dim must be a multiple of 8 and at most 128, got %d", D);
+  if (t->dtype != TPR_DTYPE_BF16 && t->dtype != TPR_DTYPE_FP32)
+    return fail(TPR_ERR_INVALID_ARGUMENT, "unknown dtype %d", t->dtype);
+  if (!t->cu_seqlens_q || !t->node_offsets || (N * depth > 0 && !t->leaf_ancestors))
+    return fail(TPR_ERR_INVALID_ARGUMENT, "tree metadata pointers must not be NULL");
+
+  const int32_t* cu = t->cu_seqlens_q;
+  const int32_t* no = t->node_offsets;
+  const int32_t* anc = t->leaf_ancestors;
+  if (cu[0] != 0) return fail(TPR_ERR_INVALID_ARGUMENT, "cu_seqlens_q[0] must be 0, got %d", cu[0]);
+  for (int s = 0; s < N; s++)
+    if (cu[s + 1] < cu[s]) return fail(TPR_ERR_INVALID_ARGUMENT, "cu_seqlens_q must be non-decreasing (leaf %d)", s);
+  if (no[0] != 0) return fail(TPR_ERR_INVALID_ARGUMENT, "node_offsets[0] must be 0, got %d", no[0]);
+  for (int n = 0; n < M; n++)
+    if (no[n + 1] < no[n]) return fail(TPR_ERR_INVALID_ARGUMENT, "node_offsets must be non-decreasing (node %d)", n);
+
+  // ancestor paths: ids in [0, M), -1 padding only at the end, no repeats,
+  // each node at one depth with one identical path above it.
+  std::vector<int> node_depth(M, -1), leaf_lo(M, -1), leaf_hi(M, -1), leaf_count(M, 0);
+  std::vector<int> node_parent(M, -2);
+  for (int s = 0; s < N; s++) {
+    bool ended = false;
+    for (int d = 0; d < depth; d++) {
+      int n = anc[s * depth + d];
+      if (n == -1) { ended = true; continue; }
+      if (ended) return fail(TPR_ERR_INVALID_ARGUMENT, "leaf %d ancestor list has a node after -1 padding", s);
+      if (n < 0 || n >= M) return fail(TPR_ERR_INVALID_ARGUMENT, "leaf %d ancestor %d out of range [0, %d)", s, n, M);
+      int parent = d == 0 ? -1 : anc[s * depth + d - 1];
+      if (node_depth[n] == -1) {
+        node_depth[n] = d;
+        node_parent[n] = parent;
+        leaf_lo[n] = s;
+      } else if (node_depth[n] != d || node_parent[n] != parent) {
+        return fail(TPR_ERR_INVALID_ARGUMENT, "node %d has inconsistent paths (leaf %d): not a tree", n, s);
+      }
+      leaf_hi[n] = s + 1;
+      leaf_count[n]++;
+    }
+  }
+  for (int n = 0; n < M; n++) {
+    if (leaf_count[n] == 0) { leaf_lo[n] = 0; leaf_hi[n] = 0; continue; }
+    if (leaf_hi[n] - leaf_lo[n] != leaf_count[n])
+      return fail(TPR_ERR_INVALID_ARGUMENT,
+                  "descendant leaves of node %d are not contiguous; number leaves in DFS order", n);
+  }
+
+  const int path = (t->dtype == TPR_DTYPE_BF16 && D == kMfmaD) ? PATH_MFMA : PATH_SIMT;
+  const int G = Hq / Hkv;
+  std::vector<int64_t> prefix_len(N, 0);
+  for (int s = 0; s < N; s++)
+    for (int d = 0; d < depth; d++) {
+      int n = anc[s * depth + d];
+      if (n >= 0) prefix_len[s] += no[n + 1] - no[n];
+    }
+
+  // ---- query-block list (dK/dV granularity) --------------------------------
+  const int BQ = path == PATH_MFMA ? kDkdvQ : kSimtTile;
+  std::vector<int32_t> qblk, leaf_qblk(N + 1, 0);
+  for (int s = 0; s < N; s++) {
+    leaf_qblk[s] = static_cast<int32_t>(qblk.size() / 2);
+    for (int tok = 0; tok < cu[s + 1] - cu[s]; tok += BQ) {
+      qblk.push_back(s);
+      qblk.push_back(tok);
+    }
+  }
+  leaf_qblk[N] = static_cast<int32_t>(qblk.size() / 2);
+  const int32_t n_qblk = leaf_qblk[N];
+
+  // ---- forward / dQ items -----------------------------------------------------
+  int heads_per_wg, tokens_per_wg;
+  if (path == PATH_MFMA) {
+    heads_per_wg = gcd_int(G, kFwdWaves);
+    tokens_per_wg = kFwdTokens * (kFwdWaves / heads_per_wg);
+  } else {
+    heads_per_wg = 1;
+    tokens_per_wg = kSimtQ;
+  }
+  std::vector<Item> fwd;
+  for (int s = 0; s < N; s++) {
+    const int len = cu[s + 1] - cu[s];
+    for (int tok = 0; tok < len; tok += tokens_per_wg) {
+      const int64_t keys = prefix_len[s] + std::min(tok + tokens_per_wg, len);
+      for (int qh = 0; qh < Hq; qh += heads_per_wg) {
+        Item it;
+        it.words = {s, tok, qh, qh / G};
+        it.work = keys;
+        it.kvh = qh / G;
+        fwd.push_back(std::move(it));
+      }
+    }
+  }
+  int32_t n_fwd = 0;
+  std::vector<int32_t> fwd_words = order_for_xcds(fwd, Hkv, 4, &n_fwd);
+
+  // ---- dK/dV items ---------------------------------------------------------
+  const int KT = path == PATH_MFMA ? kDkdvKeys : kSimtKeys;
+  std::vector<Item> dkdv;
+  for (int n = 0; n < M; n++) {
+    const int len = no[n + 1] - no[n];
+    // a node no leaf descends from gets an empty query range: its items write zeros
+    const int32_t lo = leaf_qblk[leaf_lo[n]], hi = leaf_qblk[leaf_hi[n]];
+    const int64_t queries = cu[leaf_hi[n]] - cu[leaf_lo[n]];
+    for (int k0 = 0; k0 < len; k0 += KT)
+      for (int h = 0; h < Hkv; h++) {
+        Item it;
+        it.words = {0, n, k0, h, lo, hi, -1, 0};
+        it.work = queries * G + 1;
+        it.kvh = h;
+        dkdv.push_back(std::move(it));
+      }
+  }
+  for (int s = 0; s < N; s++) {
+    const int len = cu[s + 1] - cu[s];
+    for (int k0 = 0; k0 < len; k0 += KT)
+      for (int h = 0; h < Hkv; h++) {
+        Item it;
+        it.words = {1, s, k0, h, leaf_qblk[s] + k0 / BQ, leaf_qblk[s + 1], -1, 0};
+        it.work = static_cast<int64_t>(len - k0) * G;
+        it.kvh = h;
+        dkdv.push_back(std::move(it));
+      }
+  }
+  int32_t n_dkdv = 0;
+  std::vector<int32_t> dkdv_words = order_for_xcds(dkdv, Hkv, DK_WORDS, &n_dkdv);
+
+  // ---- assemble ----------------------------------------------------------------
+  plan.assign(PF_HEADER_WORDS, 0);
+  auto append = [&](const int32_t* src, size_t count) {
+    int32_t off = static_cast<int32_t>(plan.size());
+    plan.insert(plan.end(), src, src + count);
+    return off;
+  };
+  plan[PF_MAGIC] = kPlanMagic;
+  plan[PF_VERSION] = kPlanVersion;
+  plan[PF_NUM_LEAVES] = N;
+  plan[PF_NUM_NODES] = M;
+  plan[PF_MAX_DEPTH] = depth;
+  plan[PF_TOTAL_Q] = cu[N];
+  plan[PF_TOTAL_PREFIX] = no[M];
+  plan[PF_HQ] = Hq;
+  plan[PF_HKV] = Hkv;
+  plan[PF_D] = D;
+  plan[PF_DTYPE] = t->dtype;
+  plan[PF_PATH] = path;
+  plan[PF_OFF_CU] = append(cu, N + 1);
+  plan[PF_OFF_NODE_OFF] = append(no, M + 1);
+  plan[PF_OFF_ANC] = append(anc ? anc : cu, static_cast<size_t>(N) * depth);
+  std::vector<int32_t> nl(2 * M);
+  for (int n = 0; n < M; n++) { nl[2 * n] = leaf_lo[n]; nl[2 * n + 1] = leaf_hi[n]; }
+  plan[PF_OFF_NODE_LEAF] = append(nl.data(), nl.size());
+  plan[PF_N_QBLK] = n_qblk;
+  plan[PF_OFF_QBLK] = append(qblk.data(), qblk.size());
+  plan[PF_OFF_LEAF_QBLK] = append(leaf_qblk.data(), leaf_qblk.size());
+  plan[PF_N_FWD] = n_fwd;
+  plan[PF_OFF_FWD] = append(fwd_words.data(), fwd_words.size());
+  plan[PF_N_DKDV] = n_dkdv;
+  plan[PF_OFF_DKDV] = append(dkdv_words.data(), dkdv_words.size());
+  plan[PF_N_RED] = 0;
+  plan[PF_OFF_RED] = static_cast<int32_t>(plan.size());
+  plan[PF_N_SLOTS] = 0;
+  plan[PF_SPLIT] = 1;
+  plan[PF_TOTAL_WORDS] = static_cast<int32_t>(plan.size());
+  return TPR_OK;
+}
+
+}  // namespace tpr
+
+extern "C" int tpr_attn_plan(const TprTreeDesc* tree, int32_t* plan, int64_t capacity_words,
+                             int64_t* words_needed) {
+  tpr::clear_error();
+  std::vector<int32_t> blob;
+  int rc = tpr::build_plan(tree, blob);
+  if (rc != TPR_OK) return rc;
+  if (words_needed) *words_needed = static_cast<int64_t>(blob.size());
+  if (!plan) return TPR_OK;
+  if (capacity_words < static_cast<int64_t>(blob.size()))
+    return tpr::fail(TPR_ERR_BUFFER_TOO_SMALL, "plan needs %zu words, capacity is %lld", blob.size(),
+                     static_cast<long long>(capacity_words));
+  std::memcpy(plan, blob.data(), blob.size() * sizeof(int32_t));
+  return TPR_OK;
+}

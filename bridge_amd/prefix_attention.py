@@ -1,0 +1,179 @@
+"""Sibling-batched prefix-reuse attention as a torch.autograd.Function.
+
+``TPRPrefixAttention.apply(q, k, v, prefix_k, prefix_v, meta, softmax_scale)``
+returns ``(out, lse)``:
+
+* q ``[Tq, Hq, D]``, k/v ``[Tq, Hkv, D]``: the N leaf suffixes packed by
+  ``meta.cu_seqlens_q`` (TND, rectangular_attention.py:179-181);
+* prefix_k/prefix_v ``[Tp, Hkv, D]``: the shared prefix nodes packed by
+  ``meta.node_offsets``;
+* out ``[Tq, Hq, D]`` (input dtype) and lse ``[Hq, Tq]`` float32 (natural log of
+  the scaled-score normaliser, the quantity max + log(sum) of
+  _ring_merge_probe.py:25-27; it is not differentiable).
+
+Backward returns dq, dk, dv and dprefix_k/dprefix_v, where each node's
+gradient is the sum over all its descendant leaves in leaf order -- the
+sibling relay of kv_stack.py:175-203 / prefix_state.py:546-573, reduced on the
+GPU without atomics.
+
+For one leaf under one node this equals the reference's
+rectangular_causal_attention(q, cat(prefix_k, k), cat(prefix_v, v))
+(rectangular_attention.py:125-209); see ``bridge_amd.rectangular_attention``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Optional
+
+import torch
+
+from . import _lib
+from .meta import TPRPrefixMeta
+
+__all__ = ["TPRPrefixAttention", "tpr_prefix_attention"]
+
+_SUPPORTED = (torch.bfloat16, torch.float32)
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    if t is None or t.numel() == 0:
+        return None
+    return t.data_ptr()
+
+
+def _stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def validate(q, k, v, prefix_k, prefix_v, meta: TPRPrefixMeta, softmax_scale):
+    """Contract checks with the reference's exception types and wording
+    (rectangular_attention.py:51-83, 165-172). Returns the resolved scale."""
+    for name, t in (("query", q), ("key", k), ("value", v), ("prefix_key", prefix_k), ("prefix_value", prefix_v)):
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
+        if t.ndim != 3:
+            raise ValueError(f"{name} must have shape [tokens, heads, head_dim], got {tuple(t.shape)}")
+    if not isinstance(meta, TPRPrefixMeta):
+        raise TypeError(f"meta must be a TPRPrefixMeta, got {type(meta).__name__}")
+    tq, hq, d = q.shape
+    if k.shape != v.shape:
+        raise ValueError(f"key and value must have identical shapes, got key={tuple(k.shape)}, value={tuple(v.shape)}")
+    if prefix_k.shape != prefix_v.shape:
+        raise ValueError("prefix key and value must have identical shapes, "
+                         f"got key={tuple(prefix_k.shape)}, value={tuple(prefix_v.shape)}")
+    hkv = k.shape[1]
+    if k.shape[0] != tq:
+        raise ValueError(f"suffix key length must equal query length, got Q={tq}, KV={k.shape[0]}")
+    if k.shape[2] != d or prefix_k.shape[2] != d:
+        raise ValueError(f"Q and KV head dimensions must match, got Q={d}, KV={k.shape[2]}, prefix={prefix_k.shape[2]}")
+    if prefix_k.shape[1] != hkv:
+        raise ValueError(f"prefix KV head count must match suffix KV heads, got {prefix_k.shape[1]} vs {hkv}")
+    if hq <= 0 or hkv <= 0 or d <= 0:
+        raise ValueError(f"head counts and head_dim must be positive, got Q={tuple(q.shape)}, KV={tuple(k.shape)}")
+    if hq % hkv != 0:
+        raise ValueError(f"query head count must be divisible by KV head count, got Q={hq}, KV={hkv}")
+    dtypes = {q.dtype, k.dtype, v.dtype, prefix_k.dtype, prefix_v.dtype}
+    if len(dtypes) != 1:
+        raise ValueError(f"Q, K, and V dtypes must match, got Q={q.dtype}, K={k.dtype}, V={v.dtype}, "
+                         f"prefix K={prefix_k.dtype}, prefix V={prefix_v.dtype}")
+    devices = {q.device, k.device, v.device, prefix_k.device, prefix_v.device}
+    if len(devices) != 1:
+        raise ValueError(f"Q, K, and V devices must match, got {sorted(str(x) for x in devices)}")
+    if not q.is_floating_point():
+        raise ValueError(f"Q, K, and V must use a floating-point dtype, got {q.dtype}")
+    if q.dtype not in _SUPPORTED:
+        raise ValueError(f"prefix attention supports torch.bfloat16 and torch.float32, got {q.dtype}")
+    if tq != meta.total_q:
+        raise ValueError(f"query rows ({tq}) must equal meta.total_q ({meta.total_q})")
+    if prefix_k.shape[0] != meta.total_prefix:
+        raise ValueError(f"prefix rows ({prefix_k.shape[0]}) must equal meta.total_prefix ({meta.total_prefix})")
+    if q.device.type != "cuda":
+        raise RuntimeError(f"tpr_prefix_attention requires a ROCm GPU (cuda) tensor, got device {q.device}")
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(d)
+    softmax_scale = float(softmax_scale)
+    if not math.isfinite(softmax_scale) or softmax_scale <= 0:
+        raise ValueError(f"softmax_scale must be finite and positive, got {softmax_scale}")
+    return softmax_scale
+
+
+def _forward(q, k, v, prefix_k, prefix_v, meta, scale):
+    plan = meta.plan(q.shape[1], k.shape[1], q.shape[2], q.dtype, q.device)
+    out = torch.empty_like(q)
+    lse = torch.empty((q.shape[1], q.shape[0]), dtype=torch.float32, device=q.device)
+    if q.shape[0] == 0:
+        return out, lse
+    lib = _lib.load()
+    params = _lib.TprFwdParams(
+        _lib.ABI_VERSION, 0, scale, 0.0,
+        plan.host.data_ptr(), plan.device.data_ptr(),
+        _ptr(q), _ptr(k), _ptr(v), _ptr(prefix_k), _ptr(prefix_v), _ptr(out), _ptr(lse))
+    _lib.check(lib.tpr_attn_fwd(ctypes.byref(params), ctypes.c_void_p(_stream_handle(q.device))), "tpr_attn_fwd")
+    return out, lse
+
+
+def _backward(q, k, v, prefix_k, prefix_v, out, lse, dout, meta, scale):
+    plan = meta.plan(q.shape[1], k.shape[1], q.shape[2], q.dtype, q.device)
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    dpk = torch.empty_like(prefix_k)
+    dpv = torch.empty_like(prefix_v)
+    if q.shape[0] == 0:
+        return dq, dk, dv, dpk.zero_(), dpv.zero_()
+    delta = torch.empty_like(lse)
+    ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=q.device) if plan.workspace_bytes else None
+    lib = _lib.load()
+    params = _lib.TprBwdParams(
+        _lib.ABI_VERSION, 0, scale, 0.0,
+        plan.host.data_ptr(), plan.device.data_ptr(),
+        _ptr(q), _ptr(k), _ptr(v), _ptr(prefix_k), _ptr(prefix_v), _ptr(out), _ptr(dout), _ptr(lse),
+        _ptr(delta), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dpk), _ptr(dpv), _ptr(ws), plan.workspace_bytes)
+    _lib.check(lib.tpr_attn_bwd(ctypes.byref(params), ctypes.c_void_p(_stream_handle(q.device))), "tpr_attn_bwd")
+    return dq, dk, dv, dpk, dpv
+
+
+class TPRPrefixAttention(torch.autograd.Function):
+    """(q, k, v, prefix_k, prefix_v, meta, softmax_scale) -> (out, lse)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, prefix_k, prefix_v, meta, softmax_scale=None):
+        scale = validate(q, k, v, prefix_k, prefix_v, meta, softmax_scale)
+        q, k, v, prefix_k, prefix_v = (t.contiguous() for t in (q, k, v, prefix_k, prefix_v))
+        out, lse = _forward(q, k, v, prefix_k, prefix_v, meta, scale)
+        ctx.save_for_backward(q, k, v, prefix_k, prefix_v, out, lse)
+        ctx.meta = meta
+        ctx.scale = scale
+        ctx.mark_non_differentiable(lse)
+        return out, lse
+
+    @staticmethod
+    def backward(ctx, dout, _dlse):
+        q, k, v, prefix_k, prefix_v, out, lse = ctx.saved_tensors
+        if dout is None:
+            dout = torch.zeros_like(out)
+        dout = dout.contiguous()
+        dq, dk, dv, dpk, dpv = _backward(q, k, v, prefix_k, prefix_v, out, lse, dout, ctx.meta, ctx.scale)
+        return dq, dk, dv, dpk, dpv, None, None
+
+
+def tpr_prefix_attention(q, k, v, prefix_k, prefix_v, meta: TPRPrefixMeta, softmax_scale=None):
+    """Functional form of TPRPrefixAttention; returns (out, lse)."""
+    return TPRPrefixAttention.apply(q, k, v, prefix_k, prefix_v, meta, softmax_scale)
+
+
+def prefix_attention_forward(q, k, v, prefix_k, prefix_v, meta: TPRPrefixMeta, softmax_scale=None):
+    """Forward only, no autograd graph: (out, lse)."""
+    scale = validate(q, k, v, prefix_k, prefix_v, meta, softmax_scale)
+    q, k, v, prefix_k, prefix_v = (t.contiguous() for t in (q, k, v, prefix_k, prefix_v))
+    return _forward(q, k, v, prefix_k, prefix_v, meta, scale)
+
+
+def prefix_attention_backward(q, k, v, prefix_k, prefix_v, out, lse, dout, meta: TPRPrefixMeta,
+                              softmax_scale=None):
+    """Backward only: (dq, dk, dv, dprefix_k, dprefix_v) from saved out/lse."""
+    scale = validate(q, k, v, prefix_k, prefix_v, meta, softmax_scale)
+    tensors = [t.contiguous() for t in (q, k, v, prefix_k, prefix_v, out, lse, dout)]
+    return _backward(*tensors[:7], tensors[7], meta, scale)

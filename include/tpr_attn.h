@@ -1,0 +1,162 @@
+/*
+ * tpr_attn.h -- C ABI of libtpr_attn.so, the gfx950 (MI355X) prefix-reuse
+ * attention library.
+ *
+ * One call attends N sibling suffixes ("leaves") to the shared K/V of their
+ * ancestor prefix segments ("nodes") plus their own causal suffix K/V:
+ *
+ *   query token i of leaf s sees every token of every ancestor node of s
+ *   (root -> parent order) and suffix tokens j <= i of leaf s.
+ *
+ * With one leaf and one node this is exactly the reference's single-sequence
+ * operator rectangular_causal_attention(q, cat(pk, k), cat(pv, v))
+ * (verl/models/mcore/tpr/rectangular_attention.py:125-209, right-down causal
+ * mask "key j visible to query i iff j <= P + i", sparse mode 3 at :30,118;
+ * the same mask is stated by tests/models/mcore/tpr/parallel/_fa_fp32_reference.py:24-25).
+ * The sibling-summed prefix gradient replaces the per-sibling anchor relay of
+ * verl/models/mcore/tpr/kv_stack.py:175-203 and prefix_state.py:546-573.
+ *
+ * Layouts (all row-major, head_dim contiguous, "TND" as in
+ * rectangular_attention.py:179-181):
+ *   q, out, dq, dout : [total_q, num_q_heads, head_dim]       (leaves packed by cu_seqlens_q)
+ *   k, v, dk, dv     : [total_q, num_kv_heads, head_dim]
+ *   prefix_k/v, dprefix_k/v : [total_prefix, num_kv_heads, head_dim] (nodes packed by node_offsets)
+ *   lse, delta       : float32 [num_q_heads, total_q]  (natural-log LSE of the scaled scores)
+ * GQA: query head h reads KV head h / (num_q_heads / num_kv_heads)
+ * (_fa_fp32_reference.py:20-21, contiguous query-head groups).
+ *
+ * Ownership: the caller allocates every buffer, including the plan blob and
+ * the backward workspace. The library never allocates or frees device memory,
+ * keeps no pointer after a call returns, holds no mutable global state except
+ * the thread-local error string, and never synchronises the stream.
+ * Launches are enqueued on the stream given; results are deterministic
+ * (no floating-point atomics; every output element has one writer or a
+ * fixed-order reduction).
+ *
+ * Errors: every entry point returns TPR_OK (0) or a TprStatus; the message of
+ * the last failure on the calling thread is returned by tpr_attn_last_error().
+ */
+#ifndef TPR_ATTN_H
+#define TPR_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TPR_ATTN_ABI_VERSION 1
+
+typedef enum TprStatus {
+  TPR_OK = 0,
+  TPR_ERR_INVALID_ARGUMENT = 1, /* bad shape / metadata / pointer */
+  TPR_ERR_UNSUPPORTED = 2,      /* valid request this build has no kernel for */
+  TPR_ERR_BUFFER_TOO_SMALL = 3, /* plan or workspace capacity too small */
+  TPR_ERR_LAUNCH = 4            /* the HIP runtime rejected a launch */
+} TprStatus;
+
+typedef enum TprDtype {
+  TPR_DTYPE_BF16 = 0, /* bf16 in/out, fp32 accumulation (MFMA path) */
+  TPR_DTYPE_FP32 = 1  /* fp32 in/out, fp32 accumulation */
+} TprDtype;
+
+/* Host-side description of the prefix tree, input of the planner.
+ * Mirrors the reference's tree metadata: SegmentSpec/SegmentPlan
+ * (verl/models/mcore/tpr/segment_plan.py:67-313) lowered to packed offsets.
+ *   cu_seqlens_q[num_leaves+1]   leaf suffix offsets into q/k/v rows
+ *   node_offsets[num_nodes+1]    node offsets into prefix_k/prefix_v rows
+ *   leaf_ancestors[num_leaves*max_depth]  node ids of each leaf's path,
+ *       root first, padded with -1 at the end (kv_stack.py:139-154 order).
+ * Every node must be the ancestor of a contiguous range of leaves (true when
+ * leaves are numbered in DFS order, segment_plan.py:266-275), and a node that
+ * appears in a path must appear at the same depth in every path. */
+typedef struct TprTreeDesc {
+  int32_t num_leaves;
+  int32_t num_nodes;
+  int32_t max_depth;
+  int32_t num_q_heads;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int32_t dtype; /* TprDtype */
+  int32_t reserved;
+  const int32_t* cu_seqlens_q;
+  const int32_t* node_offsets;
+  const int32_t* leaf_ancestors;
+} TprTreeDesc;
+
+/* Forward: out = softmax(scale * q [prefix_k; k]^T + mask) [prefix_v; v], and
+ * lse. Replaces one npu_fusion_attention call per sibling
+ * (rectangular_attention.py:187-204) by one launch over all siblings. */
+typedef struct TprFwdParams {
+  int32_t abi_version; /* must be TPR_ATTN_ABI_VERSION */
+  int32_t reserved;
+  float softmax_scale; /* finite, > 0 (rectangular_attention.py:169-172) */
+  float reserved_f;
+  const int32_t* plan_host;   /* plan blob written by tpr_attn_plan (host copy) */
+  const int32_t* plan_device; /* identical blob in device memory */
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* prefix_k;
+  const void* prefix_v;
+  void* out;
+  float* lse;
+} TprFwdParams;
+
+/* Backward: dq, dk, dv for the suffix tokens, and dprefix_k/dprefix_v summed
+ * over every descendant leaf of each node in leaf order (fixed-order
+ * reduction, the deterministic counterpart of prefix_state.py:565-573).
+ * delta is caller-provided scratch of lse's shape; workspace is caller-provided
+ * scratch of tpr_attn_bwd_workspace_bytes() bytes (may be NULL when that is 0). */
+typedef struct TprBwdParams {
+  int32_t abi_version;
+  int32_t reserved;
+  float softmax_scale;
+  float reserved_f;
+  const int32_t* plan_host;
+  const int32_t* plan_device;
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* prefix_k;
+  const void* prefix_v;
+  const void* out;
+  const void* dout;
+  const float* lse;
+  float* delta;
+  void* dq;
+  void* dk;
+  void* dv;
+  void* dprefix_k;
+  void* dprefix_v;
+  void* workspace;
+  size_t workspace_bytes;
+} TprBwdParams;
+
+/* ABI version compiled into the library (TPR_ATTN_ABI_VERSION). */
+int tpr_attn_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* tpr_attn_last_error(void);
+
+/* Build the launch plan (metadata + work lists) for a tree on the host.
+ * With plan == NULL only *words_needed is written. The blob is position
+ * independent: copy it unchanged to device memory for plan_device. */
+int tpr_attn_plan(const TprTreeDesc* tree, int32_t* plan, int64_t capacity_words,
+                  int64_t* words_needed);
+
+/* Bytes of fp32 workspace the backward needs for this plan. */
+size_t tpr_attn_bwd_workspace_bytes(const int32_t* plan_host);
+
+/* Enqueue the forward on `stream` (a hipStream_t; NULL = default stream). */
+int tpr_attn_fwd(const TprFwdParams* params, void* stream);
+
+/* Enqueue the backward on `stream`. */
+int tpr_attn_bwd(const TprBwdParams* params, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TPR_ATTN_H */

@@ -1,0 +1,59 @@
+"""Shared helpers for the parity tests: seeded inputs, the oracle call, metrics."""
+
+from __future__ import annotations
+
+import torch
+
+from oracle.tpr_oracle import Tree, tree_backward, tree_forward
+
+# north-star tolerances
+BF16_FWD_MAX_ABS = 2e-2
+BF16_FWD_COS = 0.9999
+BF16_GRAD_COS = 0.999
+BF16_PREFIX_GRAD_REL_L2 = 1e-2
+FP32_TOL = 1e-4
+
+
+def tree_of(meta) -> Tree:
+    return Tree(list(meta.cu_seqlens_q), list(meta.node_offsets), [list(a) for a in meta.leaf_ancestors])
+
+
+def make_inputs(meta, hq, hkv, d, dtype, seed, device):
+    """N(0,1) q, k, v, prefix_k, prefix_v, dout from a CPU generator, cast, then moved."""
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    tq, tp = meta.total_q, meta.total_prefix
+    shapes = [(tq, hq, d), (tq, hkv, d), (tq, hkv, d), (tp, hkv, d), (tp, hkv, d), (tq, hq, d)]
+    return [torch.randn(s, generator=gen).to(dtype).to(device) for s in shapes]
+
+
+def oracle(meta, q, k, v, pk, pv, dout, scale, compute_dtype=torch.float64, device="cpu"):
+    tree = tree_of(meta)
+    args = [t.detach().to(device) for t in (q, k, v, pk, pv)]
+    out, lse = tree_forward(*args, tree, scale, compute_dtype=compute_dtype)
+    grads = tree_backward(*args, tree, dout.detach().to(device), scale, compute_dtype=compute_dtype, out=out, lse=lse)
+    return out, lse, grads
+
+
+def max_abs(a, b) -> float:
+    if a.numel() == 0:
+        return 0.0
+    return (a.double().cpu() - b.double().cpu()).abs().max().item()
+
+
+def cosine(a, b) -> float:
+    a = a.double().flatten().cpu()
+    b = b.double().flatten().cpu()
+    if a.numel() == 0:
+        return 1.0
+    na, nb = a.norm(), b.norm()
+    if na == 0 and nb == 0:
+        return 1.0
+    return (a @ b / (na * nb).clamp_min(1e-300)).item()
+
+
+def rel_l2(a, b) -> float:
+    a = a.double().flatten().cpu()
+    b = b.double().flatten().cpu()
+    if b.norm() == 0:
+        return a.norm().item()
+    return ((a - b).norm() / b.norm()).item()

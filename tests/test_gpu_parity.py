@@ -1,0 +1,151 @@
+"""GPU parity of the HIP kernels (through the C ABI) against the fp64 CPU oracle."""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from _helpers import (
+    BF16_FWD_COS,
+    BF16_FWD_MAX_ABS,
+    BF16_GRAD_COS,
+    BF16_PREFIX_GRAD_REL_L2,
+    FP32_TOL,
+    cosine,
+    make_inputs,
+    max_abs,
+    oracle,
+    rel_l2,
+)
+
+pytestmark = pytest.mark.gpu
+
+
+def _meta_cases():
+    from bridge_amd import TPRPrefixMeta as M
+    return {
+        # name: (meta, hq, hkv)
+        "shared_prefix_gqa4": (M.shared_prefix(200, [100, 37]), 8, 2),
+        "no_prefix": (M.shared_prefix(0, [70, 33]), 4, 1),
+        "tile_aligned": (M.shared_prefix(128, [64, 64, 128]), 8, 2),
+        "mha": (M.shared_prefix(96, [80]), 2, 2),
+        "gqa2": (M.shared_prefix(64, [90]), 4, 2),
+        "gqa3": (M.shared_prefix(70, [45, 20]), 6, 2),
+        "depth3_tree": (M(cu_seqlens_q=(0, 33, 98, 138, 155), node_offsets=(0, 130, 200, 270),
+                          leaf_ancestors=((0, 1), (0, 1), (0, 2), (0, 2))), 8, 2),
+        "unused_node": (M(cu_seqlens_q=(0, 40), node_offsets=(0, 10, 30), leaf_ancestors=((0,),)), 4, 1),
+        "empty_leaf": (M.shared_prefix(50, [0, 60, 0]), 4, 1),
+    }
+
+
+CASES = ["shared_prefix_gqa4", "no_prefix", "tile_aligned", "mha", "gqa2", "gqa3", "depth3_tree",
+         "unused_node", "empty_leaf"]
+
+
+def _run(meta, q, k, v, pk, pv, dout, scale):
+    from bridge_amd import TPRPrefixAttention
+    tensors = [t.clone().requires_grad_(True) for t in (q, k, v, pk, pv)]
+    out, lse = TPRPrefixAttention.apply(*tensors, meta, scale)
+    out.backward(dout)
+    torch.cuda.synchronize()
+    return out.detach(), lse.detach(), [t.grad for t in tensors]
+
+
+def _report(name, out, lse, grads, ref):
+    ro, rl, rg = ref
+    lines = [f"[{name}] out max_abs={max_abs(out, ro):.3e} cos={cosine(out, ro):.6f} "
+             f"lse max_abs={max_abs(lse, rl):.3e}"]
+    for label, g, r in zip(("dq", "dk", "dv", "dpk", "dpv"), grads, rg):
+        lines.append(f"  {label}: cos={cosine(g, r):.6f} rel_l2={rel_l2(g, r):.3e} max_abs={max_abs(g, r):.3e}")
+    print("\n".join(lines), flush=True)
+
+
+@pytest.mark.parametrize("name", CASES)
+def test_mfma_bf16_matches_oracle(name, cuda_device):
+    meta, hq, hkv = _meta_cases()[name]
+    d = 128
+    scale = 1.0 / math.sqrt(d)
+    q, k, v, pk, pv, dout = make_inputs(meta, hq, hkv, d, torch.bfloat16, seed=1234, device=cuda_device)
+    assert meta.plan(hq, hkv, d, torch.bfloat16, cuda_device).path == "mfma"
+    out, lse, grads = _run(meta, q, k, v, pk, pv, dout, scale)
+    ref = oracle(meta, q, k, v, pk, pv, dout, scale)
+    _report(name, out, lse, grads, ref)
+    ro, rl, rg = ref
+    assert max_abs(out, ro) <= BF16_FWD_MAX_ABS
+    assert cosine(out, ro) >= BF16_FWD_COS
+    assert max_abs(lse, rl) <= 1e-3
+    for g, r in zip(grads, rg):
+        assert cosine(g, r) >= BF16_GRAD_COS
+    for g, r in zip(grads[3:], rg[3:]):
+        assert rel_l2(g, r) <= BF16_PREFIX_GRAD_REL_L2
+    if name == "unused_node":
+        assert torch.count_nonzero(grads[3][10:]) == 0 and torch.count_nonzero(grads[4][10:]) == 0
+
+
+def test_fp32_plumbing_config_matches_oracle(cuda_device):
+    """P=512, 2 sibling suffixes of 512, 4 heads MHA, D=64, fp32 (tolerance 1e-4)."""
+    from bridge_amd import TPRPrefixMeta
+    meta = TPRPrefixMeta.shared_prefix(512, [512, 512])
+    hq = hkv = 4
+    d = 64
+    scale = 1.0 / math.sqrt(d)
+    q, k, v, pk, pv, dout = make_inputs(meta, hq, hkv, d, torch.float32, seed=7, device=cuda_device)
+    assert meta.plan(hq, hkv, d, torch.float32, cuda_device).path == "simt"
+    out, lse, grads = _run(meta, q, k, v, pk, pv, dout, scale)
+    ref = oracle(meta, q, k, v, pk, pv, dout, scale)
+    _report("fp32_config1", out, lse, grads, ref)
+    ro, rl, rg = ref
+    assert max_abs(out, ro) <= FP32_TOL
+    assert max_abs(lse, rl) <= FP32_TOL
+    for g, r in zip(grads, rg):
+        assert max_abs(g, r) <= FP32_TOL
+
+
+def test_simt_bf16_head_dim_64_matches_oracle(cuda_device):
+    from bridge_amd import TPRPrefixMeta
+    meta = TPRPrefixMeta.shared_prefix(100, [70, 40])
+    hq, hkv, d = 8, 2, 64
+    scale = 1.0 / math.sqrt(d)
+    q, k, v, pk, pv, dout = make_inputs(meta, hq, hkv, d, torch.bfloat16, seed=3, device=cuda_device)
+    assert meta.plan(hq, hkv, d, torch.bfloat16, cuda_device).path == "simt"
+    out, lse, grads = _run(meta, q, k, v, pk, pv, dout, scale)
+    ref = oracle(meta, q, k, v, pk, pv, dout, scale)
+    _report("simt_bf16_d64", out, lse, grads, ref)
+    ro, _, rg = ref
+    assert max_abs(out, ro) <= BF16_FWD_MAX_ABS and cosine(out, ro) >= BF16_FWD_COS
+    for g, r in zip(grads, rg):
+        assert cosine(g, r) >= BF16_GRAD_COS
+
+
+def test_mfma_is_deterministic(cuda_device):
+    meta, hq, hkv = _meta_cases()["depth3_tree"]
+    q, k, v, pk, pv, dout = make_inputs(meta, hq, hkv, 128, torch.bfloat16, seed=99, device=cuda_device)
+    first = _run(meta, q, k, v, pk, pv, dout, None)
+    second = _run(meta, q, k, v, pk, pv, dout, None)
+    assert torch.equal(first[0], second[0]) and torch.equal(first[1], second[1])
+    for a, b in zip(first[2], second[2]):
+        assert torch.equal(a, b)
+
+
+def test_rectangular_shim_matches_reference_oracle(cuda_device):
+    from bridge_amd import rectangular_causal_attention
+    from oracle.tpr_oracle import prefix_attention
+    gen = torch.Generator().manual_seed(44)
+    sq, skv, hq, hkv, d = 40, 100, 8, 2, 128
+    q = torch.randn(sq, 1, hq, d, generator=gen).bfloat16()
+    k = torch.randn(skv, 1, hkv, d, generator=gen).bfloat16()
+    v = torch.randn(skv, 1, hkv, d, generator=gen).bfloat16()
+    g = torch.randn(sq, 1, hq * d, generator=gen).bfloat16()
+    qd, kd, vd = (t.to(cuda_device).requires_grad_(True) for t in (q, k, v))
+    out = rectangular_causal_attention(qd, kd, vd)
+    assert out.shape == (sq, 1, hq * d) and out.dtype == torch.bfloat16
+    out.backward(g.to(cuda_device))
+    qc, kc, vc = (t.double().requires_grad_(True) for t in (q, k, v))
+    p = skv - sq
+    ref = prefix_attention(qc, kc[p:], vc[p:], kc[:p], vc[:p], None)
+    ref.backward(g.double())
+    assert max_abs(out, ref) <= BF16_FWD_MAX_ABS and cosine(out, ref) >= BF16_FWD_COS
+    for mine, theirs in ((qd.grad, qc.grad), (kd.grad, kc.grad), (vd.grad, vc.grad)):
+        assert cosine(mine, theirs) >= BF16_GRAD_COS
