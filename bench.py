@@ -1,0 +1,246 @@
+#!/usr/bin/env python3
+"""Prefix-reuse (TPR) attention benchmark on one MI355X.
+
+A step is one forward + backward pass of sibling-batched prefix attention
+over the whole workload (inputs already resident in HBM). Default workload:
+the Qwen3-4B attention-layer shape -- GQA 32/8, head_dim 128, bf16, one
+shared prefix of 4096 tokens and 4 sibling suffixes of 4096 tokens, N(0,1)
+synthetic inputs, scale 1/sqrt(128).
+
+Throughput is algorithmic: only visible (query, key) pairs count,
+V_i = S_i * P_i + S_i (S_i + 1) / 2 per query head, and
+fwd = 4 Hq D sum(V_i), fwd+bwd = 14 Hq D sum(V_i) FLOP.
+
+Prints one JSON line (rank 0). ``--gpus N`` with N > 1 exits: this build
+runs on one GPU.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import statistics
+import sys
+import time
+
+import torch
+
+BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+FP32_PEAK_TFLOPS = 157.3    # MI355X dense fp32 MFMA
+HBM_PEAK_GBS = 8000.0
+
+
+def workload(name: str):
+    """(description, meta, hq, hkv, d, dtype) for a named workload."""
+    from bridge_amd import TPRPrefixMeta
+    if name == "qwen3-4b":
+        return ("Qwen3-4B attention layer: prefix 4096 + 4 x 4096 sibling suffixes, GQA 32/8, d128, bf16",
+                TPRPrefixMeta.shared_prefix(4096, [4096] * 4), 32, 8, 128, torch.bfloat16)
+    if name == "plumbing-fp32":
+        return ("plumbing: prefix 512 + 2 x 512 suffixes, 4 heads MHA, d64, fp32",
+                TPRPrefixMeta.shared_prefix(512, [512] * 2), 4, 4, 64, torch.float32)
+    if name == "long-session":
+        return ("long agent session: prefix 32768 + 8 x 2048 suffixes, GQA 32/8, d128, bf16",
+                TPRPrefixMeta.shared_prefix(32768, [2048] * 8), 32, 8, 128, torch.bfloat16)
+    if name == "ragged":
+        g = torch.Generator(device="cpu").manual_seed(0)
+        lens = torch.randint(256, 8193, (16,), generator=g).tolist()
+        return (f"ragged varlen: prefix 8192 + 16 suffixes U[256,8192] (seed 0), GQA 32/8, d128, bf16",
+                TPRPrefixMeta.shared_prefix(8192, lens), 32, 8, 128, torch.bfloat16)
+    if name == "turn-tree":
+        anc = tuple((0, 1 + i // 4) for i in range(16))
+        meta = TPRPrefixMeta(tuple(1024 * i for i in range(17)), (0, 2048, 3072, 4096, 5120, 6144), anc)
+        return ("turn-boundary tree depth 3: root 2048 -> 4 x 1024 -> 16 leaves x 1024, GQA 32/8, d128, bf16",
+                meta, 32, 8, 128, torch.bfloat16)
+    raise SystemExit(f"unknown workload {name!r}")
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(prefix_len: int, suffix_len: int, hq_sample: int, hkv: int, hq: int, d: int, reps: int = 3):
+    """The reference's CPU fp32 path (dense prefix attention + autograd), timed
+    on a bounded sample: one sibling and one KV-head group."""
+    from oracle.tpr_oracle import prefix_attention
+    g = torch.Generator(device="cpu").manual_seed(0)
+    group = hq // hkv
+    heads = max(1, min(hq_sample, group))
+    q = torch.randn(suffix_len, 1, heads, d, generator=g)
+    k = torch.randn(suffix_len, 1, 1, d, generator=g)
+    v = torch.randn(suffix_len, 1, 1, d, generator=g)
+    pk = torch.randn(prefix_len, 1, 1, d, generator=g)
+    pv = torch.randn(prefix_len, 1, 1, d, generator=g)
+    dout = torch.randn(suffix_len, 1, heads * d, generator=g)
+    times = []
+    for i in range(reps + 1):
+        tensors = [t.clone().requires_grad_(True) for t in (q, k, v, pk, pv)]
+        t0 = time.perf_counter()
+        out = prefix_attention(*tensors, 1.0 / math.sqrt(d))
+        torch.autograd.grad(out, tensors, grad_outputs=dout)
+        dt = time.perf_counter() - t0
+        if i > 0:
+            times.append(dt)
+    pairs = suffix_len * prefix_len + suffix_len * (suffix_len + 1) // 2
+    flops = 14.0 * heads * d * pairs
+    med = statistics.median(times)
+    return {
+        "value": round(flops / med / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"1 sibling (prefix {prefix_len} + suffix {suffix_len}) x {heads} query heads of one KV group, "
+                   f"fp32 dense prefix attention + autograd on the host CPU ({cpu_model()}), "
+                   f"median of {reps} after 1 warmup, {med:.2f} s per rep"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="qwen3-4b",
+                    choices=["qwen3-4b", "plumbing-fp32", "long-session", "ragged", "turn-tree"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(sharding by KV-head group or by sibling is described in DESIGN.md)", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs an MI355X GPU", file=sys.stderr)
+        return 2
+
+    from bridge_amd import _lib
+    from bridge_amd.prefix_attention import prefix_attention_backward, prefix_attention_forward
+
+    device = torch.device("cuda", 0)
+    desc, meta, hq, hkv, d, dtype = workload(args.workload)
+    scale = 1.0 / math.sqrt(d)
+    gen = torch.Generator(device=device).manual_seed(1234)
+    tq, tp = meta.total_q, meta.total_prefix
+    q = torch.randn(tq, hq, d, device=device, generator=gen).to(dtype)
+    k = torch.randn(tq, hkv, d, device=device, generator=gen).to(dtype)
+    v = torch.randn(tq, hkv, d, device=device, generator=gen).to(dtype)
+    pk = torch.randn(tp, hkv, d, device=device, generator=gen).to(dtype)
+    pv = torch.randn(tp, hkv, d, device=device, generator=gen).to(dtype)
+    dout = torch.randn(tq, hq, d, device=device, generator=gen).to(dtype)
+    plan = meta.plan(hq, hkv, d, dtype, device)
+
+    buffers = {"dq": torch.empty_like(q), "dk": torch.empty_like(k), "dv": torch.empty_like(v),
+               "dprefix_k": torch.empty_like(pk), "dprefix_v": torch.empty_like(pv),
+               "delta": torch.empty((hq, tq), dtype=torch.float32, device=device)}
+    stream = torch.cuda.current_stream(device)
+
+    def step(events=None):
+        if events:
+            events[0].record(stream)
+        out, lse = prefix_attention_forward(q, k, v, pk, pv, meta, scale)
+        if events:
+            events[1].record(stream)
+        prefix_attention_backward(q, k, v, pk, pv, out, lse, dout, meta, scale,
+                                  phases=_lib.TPR_BWD_DELTA, buffers=buffers)
+        if events:
+            events[2].record(stream)
+        prefix_attention_backward(q, k, v, pk, pv, out, lse, dout, meta, scale,
+                                  phases=_lib.TPR_BWD_DKDV, buffers=buffers)
+        if events:
+            events[3].record(stream)
+        prefix_attention_backward(q, k, v, pk, pv, out, lse, dout, meta, scale,
+                                  phases=_lib.TPR_BWD_DQ, buffers=buffers)
+        if events:
+            events[4].record(stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(events[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall * 1e3 / args.steps
+
+    def avg(a, b):
+        return statistics.mean(e[a].elapsed_time(e[b]) for e in events)
+
+    fwd_ms, delta_ms, dkdv_ms, dq_ms = avg(0, 1), avg(1, 2), avg(2, 3), avg(3, 4)
+    pairs = meta.visible_pairs()
+    unit = 2.0 * hq * d * pairs          # FLOP of one GEMM over the visible pairs
+    total_flops = 7.0 * unit            # fwd (2 GEMMs) + bwd (5 GEMMs)
+    value = total_flops / (ms_per_step * 1e-3) / 1e12
+    peak = BF16_PEAK_TFLOPS if dtype == torch.bfloat16 else FP32_PEAK_TFLOPS
+    kernels = {
+        "fwd": (fwd_ms, 2.0 * unit, "tpr::mfma_fwd" if plan.path == "mfma" else "tpr::simt_fwd"),
+        "dkdv": (dkdv_ms, 4.0 * unit, "tpr::mfma_dkdv" if plan.path == "mfma" else "tpr::simt_dkdv"),
+        "dq": (dq_ms, 3.0 * unit, "tpr::mfma_dq" if plan.path == "mfma" else "tpr::simt_dq"),
+    }
+    dom = max(kernels, key=lambda n: kernels[n][0])
+    dom_ms, dom_flops, dom_name = kernels[dom]
+    achieved = dom_flops / (dom_ms * 1e-3) / 1e12
+
+    result = {
+        "metric": "prefix-attn fwd+bwd TFLOP/s & % bf16 MFMA peak, Qwen3-4B shape, 1 GPU",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if dtype == torch.bfloat16 else "fp32",
+        "data": "synthetic N(0,1) inputs, seeded",
+        "config": {
+            "workload": desc,
+            "prefix_tokens": tp,
+            "suffix_tokens": tq,
+            "siblings": meta.num_leaves,
+            "q_heads": hq,
+            "kv_heads": hkv,
+            "head_dim": d,
+            "visible_pairs_per_head": pairs,
+            "fwd_bwd_flop": total_flops,
+        },
+        "fraction_of_peak": round(value / peak, 4),
+        "fwd_tflops": round(2.0 * unit / (fwd_ms * 1e-3) / 1e12, 2),
+        "tokens_per_s": round(tq / (ms_per_step * 1e-3), 1),
+        "kernel_ms": {"fwd": round(fwd_ms, 4), "delta": round(delta_ms, 4), "dkdv": round(dkdv_ms, 4),
+                      "dq": round(dq_ms, 4)},
+        "roofline": {
+            "kernel": dom_name,
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": peak,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / peak, 4),
+            "traffic": None,
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        p0 = meta.prefix_length(0)
+        s0 = meta.suffix_lengths()[0]
+        result["cpu_baseline"] = cpu_baseline(p0, s0, hq // hkv, hkv, hq, d)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -30,7 +30,12 @@ EXPORTED_SYMBOLS = (
     "tpr_attn_bwd_workspace_bytes",
     "tpr_attn_fwd",
     "tpr_attn_bwd",
+    "tpr_attn_bwd_phases",
 )
+
+TPR_BWD_DELTA = 1
+TPR_BWD_DKDV = 2
+TPR_BWD_DQ = 4
 
 _p = ctypes.c_void_p
 _i32p = ctypes.POINTER(ctypes.c_int32)
@@ -130,6 +135,8 @@ def load():
         lib.tpr_attn_fwd.argtypes = [ctypes.POINTER(TprFwdParams), _p]
         lib.tpr_attn_bwd.restype = ctypes.c_int
         lib.tpr_attn_bwd.argtypes = [ctypes.POINTER(TprBwdParams), _p]
+        lib.tpr_attn_bwd_phases.restype = ctypes.c_int
+        lib.tpr_attn_bwd_phases.argtypes = [ctypes.POINTER(TprBwdParams), ctypes.c_int, _p]
         version = lib.tpr_attn_abi_version()
         if version != ABI_VERSION:
             raise RuntimeError(f"{path} has ABI version {version}, expected {ABI_VERSION}; rebuild it")

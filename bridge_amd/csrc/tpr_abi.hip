@@ -129,7 +129,13 @@ extern "C" int tpr_attn_fwd(const TprFwdParams* p, void* stream) {
 }
 
 extern "C" int tpr_attn_bwd(const TprBwdParams* p, void* stream) {
+  return tpr_attn_bwd_phases(p, TPR_BWD_DELTA | TPR_BWD_DKDV | TPR_BWD_DQ, stream);
+}
+
+extern "C" int tpr_attn_bwd_phases(const TprBwdParams* p, int phases, void* stream) {
   clear_error();
+  if (phases <= 0 || (phases & ~(TPR_BWD_DELTA | TPR_BWD_DKDV | TPR_BWD_DQ)))
+    return fail(TPR_ERR_INVALID_ARGUMENT, "phases must be a non-empty mask of TPR_BWD_* bits, got %d", phases);
   if (!p) return fail(TPR_ERR_INVALID_ARGUMENT, "params must not be NULL");
   if (p->abi_version != TPR_ATTN_ABI_VERSION)
     return fail(TPR_ERR_INVALID_ARGUMENT, "abi_version %d does not match library version %d", p->abi_version,
@@ -170,9 +176,11 @@ extern "C" int tpr_attn_bwd(const TprBwdParams* p, void* stream) {
   a.dpv = p->dprefix_v;
   const bool fp32 = ph[PF_DTYPE] == TPR_DTYPE_FP32;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  rc = launch_delta(a, fp32, s);
-  if (!rc) rc = mfma ? launch_mfma_bwd(a, ph[PF_N_FWD], ph[PF_N_DKDV], s)
-                     : launch_simt_bwd(a, ph[PF_N_FWD], ph[PF_N_DKDV], fp32, s);
+  const int n_dkdv = (phases & TPR_BWD_DKDV) ? ph[PF_N_DKDV] : 0;
+  const int n_dq = (phases & TPR_BWD_DQ) ? ph[PF_N_FWD] : 0;
+  rc = (phases & TPR_BWD_DELTA) ? launch_delta(a, fp32, s) : 0;
+  if (!rc && (n_dkdv || n_dq))
+    rc = mfma ? launch_mfma_bwd(a, n_dq, n_dkdv, s) : launch_simt_bwd(a, n_dq, n_dkdv, fp32, s);
   if (rc) return fail(TPR_ERR_LAUNCH, "backward launch failed: %s", hipGetErrorString(hipGetLastError()));
   return TPR_OK;
 }

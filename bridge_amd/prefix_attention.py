@@ -114,24 +114,32 @@ def _forward(q, k, v, prefix_k, prefix_v, meta, scale):
     return out, lse
 
 
-def _backward(q, k, v, prefix_k, prefix_v, out, lse, dout, meta, scale):
+def _backward(q, k, v, prefix_k, prefix_v, out, lse, dout, meta, scale, *, phases=None, buffers=None):
+    """Enqueue the backward. ``buffers`` may supply preallocated dq, dk, dv,
+    dprefix_k, dprefix_v and delta tensors; ``phases`` is a mask of
+    _lib.TPR_BWD_* bits (default: all)."""
     plan = meta.plan(q.shape[1], k.shape[1], q.shape[2], q.dtype, q.device)
-    dq = torch.empty_like(q)
-    dk = torch.empty_like(k)
-    dv = torch.empty_like(v)
-    dpk = torch.empty_like(prefix_k)
-    dpv = torch.empty_like(prefix_v)
+    b = dict(buffers or {})
+    dq = b.get("dq") if b.get("dq") is not None else torch.empty_like(q)
+    dk = b.get("dk") if b.get("dk") is not None else torch.empty_like(k)
+    dv = b.get("dv") if b.get("dv") is not None else torch.empty_like(v)
+    dpk = b.get("dprefix_k") if b.get("dprefix_k") is not None else torch.empty_like(prefix_k)
+    dpv = b.get("dprefix_v") if b.get("dprefix_v") is not None else torch.empty_like(prefix_v)
     if q.shape[0] == 0:
         return dq, dk, dv, dpk.zero_(), dpv.zero_()
-    delta = torch.empty_like(lse)
-    ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=q.device) if plan.workspace_bytes else None
+    delta = b.get("delta") if b.get("delta") is not None else torch.empty_like(lse)
+    ws = b.get("workspace")
+    if ws is None and plan.workspace_bytes:
+        ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=q.device)
     lib = _lib.load()
     params = _lib.TprBwdParams(
         _lib.ABI_VERSION, 0, scale, 0.0,
         plan.host.data_ptr(), plan.device.data_ptr(),
         _ptr(q), _ptr(k), _ptr(v), _ptr(prefix_k), _ptr(prefix_v), _ptr(out), _ptr(dout), _ptr(lse),
         _ptr(delta), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dpk), _ptr(dpv), _ptr(ws), plan.workspace_bytes)
-    _lib.check(lib.tpr_attn_bwd(ctypes.byref(params), ctypes.c_void_p(_stream_handle(q.device))), "tpr_attn_bwd")
+    mask = phases if phases is not None else (_lib.TPR_BWD_DELTA | _lib.TPR_BWD_DKDV | _lib.TPR_BWD_DQ)
+    _lib.check(lib.tpr_attn_bwd_phases(ctypes.byref(params), int(mask), ctypes.c_void_p(_stream_handle(q.device))),
+               "tpr_attn_bwd")
     return dq, dk, dv, dpk, dpv
 
 
@@ -172,8 +180,12 @@ def prefix_attention_forward(q, k, v, prefix_k, prefix_v, meta: TPRPrefixMeta, s
 
 
 def prefix_attention_backward(q, k, v, prefix_k, prefix_v, out, lse, dout, meta: TPRPrefixMeta,
-                              softmax_scale=None):
-    """Backward only: (dq, dk, dv, dprefix_k, dprefix_v) from saved out/lse."""
+                              softmax_scale=None, *, phases=None, buffers=None):
+    """Backward only: (dq, dk, dv, dprefix_k, dprefix_v) from saved out/lse.
+
+    ``phases`` selects backward phases (mask of TPR_BWD_DELTA / _DKDV / _DQ;
+    the delta phase must have run before the other two); ``buffers`` may hold
+    preallocated outputs and the fp32 ``delta`` scratch, keyed by name."""
     scale = validate(q, k, v, prefix_k, prefix_v, meta, softmax_scale)
     tensors = [t.contiguous() for t in (q, k, v, prefix_k, prefix_v, out, lse, dout)]
-    return _backward(*tensors[:7], tensors[7], meta, scale)
+    return _backward(*tensors[:7], tensors[7], meta, scale, phases=phases, buffers=buffers)

@@ -152,8 +152,16 @@ size_t tpr_attn_bwd_workspace_bytes(const int32_t* plan_host);
 /* Enqueue the forward on `stream` (a hipStream_t; NULL = default stream). */
 int tpr_attn_fwd(const TprFwdParams* params, void* stream);
 
-/* Enqueue the backward on `stream`. */
+/* Enqueue the backward on `stream` (all phases, in order). */
 int tpr_attn_bwd(const TprBwdParams* params, void* stream);
+
+/* Backward phases, for callers that time them separately or run dK/dV and dQ
+ * on two streams: TPR_BWD_DELTA must complete before the other two, which
+ * are independent of each other. tpr_attn_bwd == all three in this order. */
+#define TPR_BWD_DELTA 1 /* delta = rowsum(dout * out), fp32 [Hq, Tq] */
+#define TPR_BWD_DKDV 2  /* dk, dv, dprefix_k, dprefix_v */
+#define TPR_BWD_DQ 4    /* dq */
+int tpr_attn_bwd_phases(const TprBwdParams* params, int phases, void* stream);
 
 #ifdef __cplusplus
 }
