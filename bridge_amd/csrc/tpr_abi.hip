@@ -17,6 +17,7 @@ int launch_delta(const KernelArgs& a, bool fp32, hipStream_t s);
 int launch_simt_bwd(const KernelArgs& a, int n_fwd, int n_dkdv, bool fp32, hipStream_t s);
 int launch_mfma_fwd(const KernelArgs& a, hipStream_t s);
 int launch_mfma_bwd(const KernelArgs& a, int n_fwd, int n_dkdv, hipStream_t s);
+int launch_mfma_delta(const KernelArgs& a, hipStream_t s);
 
 namespace {
 thread_local char g_error[512] = "";
@@ -178,7 +179,7 @@ extern "C" int tpr_attn_bwd_phases(const TprBwdParams* p, int phases, void* stre
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int n_dkdv = (phases & TPR_BWD_DKDV) ? ph[PF_N_DKDV] : 0;
   const int n_dq = (phases & TPR_BWD_DQ) ? ph[PF_N_FWD] : 0;
-  rc = (phases & TPR_BWD_DELTA) ? launch_delta(a, fp32, s) : 0;
+  rc = (phases & TPR_BWD_DELTA) ? (mfma ? launch_mfma_delta(a, s) : launch_delta(a, fp32, s)) : 0;
   if (!rc && (n_dkdv || n_dq))
     rc = mfma ? launch_mfma_bwd(a, n_dq, n_dkdv, s) : launch_simt_bwd(a, n_dq, n_dkdv, fp32, s);
   if (rc) return fail(TPR_ERR_LAUNCH, "backward launch failed: %s", hipGetErrorString(hipGetLastError()));

@@ -109,34 +109,33 @@ __device__ __forceinline__ int count_tiles(const KernelArgs& a, int leaf, int su
   return tiles + (suffix_keys + kTileRows - 1) / kTileRows;
 }
 
-// Global -> register staging of one 64x128 bf16 tile pair (4 chunks of 16 B
-// per thread per tensor), and register -> swizzled LDS store.
-struct Stage2 {
-  bf16x8 x[4];
-  bf16x8 y[4];
-};
+// Direct global -> LDS copy (gfx950 global_load_lds_dwordx4) of the 64 rows
+// [row0, row0 + 64) of a bf16 tensor (128 columns at `base`, row stride
+// `stride` elements) into a swizzled 64 x 256 B tile; rows at or beyond `len`
+// re-read row len - 1. Each wave issues 16 / kWaves DMA blocks of 1 KiB: lane
+// l of a block lands at block + 16*l, i.e. at (row 4*blk + l/16, physical
+// chunk l%16), so the lane fetches the logical chunk that swizzles there. No
+// registers hold the data, and the wave's vmcnt covers the copy.
+typedef __attribute__((address_space(3))) void lds_void;
 
-__device__ __forceinline__ void stage_load(Stage2& st, const bf16* xb, const bf16* yb, int64_t stride,
-                                           int64_t row0, int len) {
+template <int kWaves>
+__device__ __forceinline__ void dma_tile(const bf16* base, int64_t stride, int64_t row0, int len, char* tile,
+                                         int wave, int lane) {
+  constexpr int kBlocks = 16 / kWaves;
 #pragma unroll
-  for (int u = 0; u < 4; u++) {
-    const int idx = threadIdx.x + 256 * u;
-    const int r = min(idx >> 4, len - 1);
-    const int64_t off = (row0 + r) * stride + ((idx & 15) << 3);
-    st.x[u] = *reinterpret_cast<const bf16x8*>(xb + off);
-    st.y[u] = *reinterpret_cast<const bf16x8*>(yb + off);
+  for (int j = 0; j < kBlocks; j++) {
+    const int blk = wave * kBlocks + j;
+    const int row = 4 * blk + (lane >> 4);
+    const int chunk = swz_chunk(row, lane & 15);
+    const bf16* src = base + (row0 + min(row, len - 1)) * stride + chunk * 8;
+    __builtin_amdgcn_global_load_lds(src, (lds_void*)(tile + blk * 1024), 16, 0, 0);
   }
 }
 
-__device__ __forceinline__ void stage_store(const Stage2& st, char* xt, char* yt) {
-#pragma unroll
-  for (int u = 0; u < 4; u++) {
-    const int idx = threadIdx.x + 256 * u;
-    const int off = swz_off(idx >> 4, (idx & 15) << 3);
-    *reinterpret_cast<bf16x8*>(xt + off) = st.x[u];
-    *reinterpret_cast<bf16x8*>(yt + off) = st.y[u];
-  }
-}
+// Wait until this wave's outstanding global->LDS copies have landed.
+__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // ---------------------------------------------------------------------------
 // Forward
@@ -150,19 +149,31 @@ __global__ __launch_bounds__(256, 2) void mfma_fwd(KernelArgs a) {
   const int row0 = cu[leaf], len = cu[leaf + 1] - cu[leaf];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int hpw = a.hpw;  // query heads per workgroup
+  const int hpw = a.hpw;                             // query heads per workgroup
   const int head = qh0 + wave % hpw;
   const int tw0 = tok0 + kFwdTokens * (wave / hpw);  // first token of this wave
   const int tpw = kFwdTokens * (kFwdWaves / hpw);    // tokens per workgroup
   const int suffix_keys = min(len, tok0 + tpw);
   const int n = lane & 31, h = lane >> 5;
-  const int t = tw0 + n;                            // this lane's query token
+  const int t = tw0 + n;                             // this lane's query token
   const bool wave_active = tw0 < len;
 
   const int64_t qstride = static_cast<int64_t>(a.hq) * kMfmaD;
   const int64_t kstride = static_cast<int64_t>(a.hkv) * kMfmaD;
 
-  __shared__ __attribute__((aligned(16))) char smem[4 * kTileBytes];  // K0 V0 K1 V1
+  __shared__ __attribute__((aligned(1024))) char smem[4 * kTileBytes];  // K0 V0 K1 V1
+
+  const bf16* kbase = static_cast<const bf16*>(a.k) + kvh * kMfmaD;
+  const bf16* vbase = static_cast<const bf16*>(a.v) + kvh * kMfmaD;
+  const bf16* pkbase = static_cast<const bf16*>(a.pk) + kvh * kMfmaD;
+  const bf16* pvbase = static_cast<const bf16*>(a.pv) + kvh * kMfmaD;
+
+  const int ntiles = count_tiles(a, leaf, suffix_keys);
+  {
+    const TileLoc tl = locate_tile(a, leaf, suffix_keys, 0);
+    dma_tile<kFwdWaves>(tl.suffix ? kbase : pkbase, kstride, tl.row, tl.len, smem, wave, lane);
+    dma_tile<kFwdWaves>(tl.suffix ? vbase : pvbase, kstride, tl.row, tl.len, smem + kTileBytes, wave, lane);
+  }
 
   // Q as the B operand of S^T = K Q^T: lane holds Q[t][16c + 8h .. +7]
   bf16x8 qv[8];
@@ -179,18 +190,7 @@ __global__ __launch_bounds__(256, 2) void mfma_fwd(KernelArgs a) {
   float m = -1e30f, l = 0.f;
   const float c2 = a.scale * kLog2e;
 
-  const bf16* kbase = static_cast<const bf16*>(a.k) + kvh * kMfmaD;
-  const bf16* vbase = static_cast<const bf16*>(a.v) + kvh * kMfmaD;
-  const bf16* pkbase = static_cast<const bf16*>(a.pk) + kvh * kMfmaD;
-  const bf16* pvbase = static_cast<const bf16*>(a.pv) + kvh * kMfmaD;
-
-  const int ntiles = count_tiles(a, leaf, suffix_keys);
-  Stage2 st;
-  {
-    const TileLoc tl = locate_tile(a, leaf, suffix_keys, 0);
-    stage_load(st, tl.suffix ? kbase : pkbase, tl.suffix ? vbase : pvbase, kstride, tl.row, tl.len);
-    stage_store(st, smem, smem + kTileBytes);
-  }
+  wait_dma();
   __syncthreads();
 
   for (int it = 0; it < ntiles; it++) {
@@ -199,7 +199,9 @@ __global__ __launch_bounds__(256, 2) void mfma_fwd(KernelArgs a) {
     const TileLoc tl = locate_tile(a, leaf, suffix_keys, it);
     if (it + 1 < ntiles) {
       const TileLoc nx = locate_tile(a, leaf, suffix_keys, it + 1);
-      stage_load(st, nx.suffix ? kbase : pkbase, nx.suffix ? vbase : pvbase, kstride, nx.row, nx.len);
+      char* nk = smem + ((it + 1) & 1) * 2 * kTileBytes;
+      dma_tile<kFwdWaves>(nx.suffix ? kbase : pkbase, kstride, nx.row, nx.len, nk, wave, lane);
+      dma_tile<kFwdWaves>(nx.suffix ? vbase : pvbase, kstride, nx.row, nx.len, nk + kTileBytes, wave, lane);
     }
     // a wave skips tiles whose keys are all in its future
     const bool skip = !wave_active || (tl.suffix && tl.pos0 > tw0 + kFwdTokens - 1);
@@ -212,38 +214,39 @@ __global__ __launch_bounds__(256, 2) void mfma_fwd(KernelArgs a) {
 #pragma unroll
         for (int c = 0; c < 8; c++) s[kb] = mfma(lds_read_b128(kt, krow, 16 * c + 8 * h), qv[c], s[kb]);
       }
-      const bool need_mask = tl.len < kTileRows || (tl.suffix && tl.pos0 + kTileRows - 1 > tw0);
-      if (need_mask) {
+      if (tl.len < kTileRows || (tl.suffix && tl.pos0 + kTileRows - 1 > tw0)) {
+        // register r of key block kb holds tile key kb*32 + 16*(r/8) + 8*h + r%8
+        int lim = tl.len - 1 - 8 * h;
+        if (tl.suffix) lim = min(lim, t - tl.pos0 - 8 * h);
 #pragma unroll
         for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-          for (int r = 0; r < 16; r++) {
-            const int j = kb * 32 + 16 * (r >> 3) + 8 * h + (r & 7);
-            const bool vis = j < tl.len && (!tl.suffix || tl.pos0 + j <= t);
-            if (!vis) s[kb][r] = -INFINITY;
-          }
+          for (int r = 0; r < 16; r++) s[kb][r] = (kb * 32 + 16 * (r >> 3) + (r & 7) <= lim) ? s[kb][r] : -INFINITY;
       }
-      float mt = m;
+      float mt = s[0][0];
 #pragma unroll
       for (int kb = 0; kb < 2; kb++)
 #pragma unroll
         for (int r = 0; r < 16; r++) mt = fmaxf(mt, s[kb][r]);
-      mt = wave_max32(mt);
-      const float alpha = exp2f((m - mt) * c2);
-      const float mc = mt * c2;
-      m = mt;
+      const float m_new = fmaxf(m, wave_max32(mt));
+      if (__any(m_new > m)) {  // rescale only when some row's running max grew
+        const float alpha = fast_exp2((m - m_new) * c2);
+        m = m_new;
+        l *= alpha;
+#pragma unroll
+        for (int db = 0; db < 4; db++) o[db] *= alpha;
+      }
+      const float mc = m * c2;
       float ls = 0.f;
 #pragma unroll
       for (int kb = 0; kb < 2; kb++)
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-          const float p = exp2f(fmaf(s[kb][r], c2, -mc));
+          const float p = fast_exp2(fmaf(s[kb][r], c2, -mc));
           s[kb][r] = p;
           ls += p;
         }
-      l = l * alpha + ls;
-#pragma unroll
-      for (int db = 0; db < 4; db++) o[db] *= alpha;
+      l += ls;
 #pragma unroll
       for (int kb = 0; kb < 2; kb++)
 #pragma unroll
@@ -254,10 +257,7 @@ __global__ __launch_bounds__(256, 2) void mfma_fwd(KernelArgs a) {
           for (int db = 0; db < 4; db++) o[db] = mfma(lds_read_col8(vt, r0, 32 * db, lane), pb, o[db]);
         }
     }
-    if (it + 1 < ntiles) {
-      char* nk = smem + ((it + 1) & 1) * 2 * kTileBytes;
-      stage_store(st, nk, nk + kTileBytes);
-    }
+    wait_dma();
     __syncthreads();
   }
 
@@ -275,6 +275,28 @@ __global__ __launch_bounds__(256, 2) void mfma_fwd(KernelArgs a) {
       *reinterpret_cast<bf16x4*>(op + 32 * db + 8 * g + 4 * h) = v4;
     }
   if (h == 0) a.lse[static_cast<int64_t>(head) * a.total_q + row0 + t] = m * a.scale + logf(lt);
+}
+
+// ---------------------------------------------------------------------------
+// delta[h][t] = sum_d dout[t][h][d] * out[t][h][d] (head_dim 128): 16 lanes per
+// (t, h) row, one 16-byte load of each tensor per lane.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void mfma_delta(KernelArgs a) {
+  const int64_t rows = static_cast<int64_t>(a.total_q) * a.hq;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 16 + (threadIdx.x >> 4);
+  const int c = threadIdx.x & 15;
+  float s = 0.f;
+  if (row < rows) {
+    const bf16x8 o = *reinterpret_cast<const bf16x8*>(static_cast<const bf16*>(a.out_in) + row * kMfmaD + 8 * c);
+    const bf16x8 g = *reinterpret_cast<const bf16x8*>(static_cast<const bf16*>(a.dout) + row * kMfmaD + 8 * c);
+#pragma unroll
+    for (int i = 0; i < 8; i++) s = fmaf(static_cast<float>(o[i]), static_cast<float>(g[i]), s);
+  }
+  s += __shfl_xor(s, 8);
+  s += __shfl_xor(s, 4);
+  s += __shfl_xor(s, 2);
+  s += __shfl_xor(s, 1);
+  if (c == 0 && row < rows) a.delta[(row % a.hq) * a.total_q + row / a.hq] = s;
 }
 
 // ---------------------------------------------------------------------------
@@ -304,7 +326,19 @@ __global__ __launch_bounds__(256, 2) void mfma_dq(KernelArgs a) {
   const int64_t qstride = static_cast<int64_t>(a.hq) * kMfmaD;
   const int64_t kstride = static_cast<int64_t>(a.hkv) * kMfmaD;
 
-  __shared__ __attribute__((aligned(16))) char smem[4 * kTileBytes];
+  __shared__ __attribute__((aligned(1024))) char smem[4 * kTileBytes];
+
+  const bf16* kbase = static_cast<const bf16*>(a.k) + kvh * kMfmaD;
+  const bf16* vbase = static_cast<const bf16*>(a.v) + kvh * kMfmaD;
+  const bf16* pkbase = static_cast<const bf16*>(a.pk) + kvh * kMfmaD;
+  const bf16* pvbase = static_cast<const bf16*>(a.pv) + kvh * kMfmaD;
+
+  const int ntiles = count_tiles(a, leaf, suffix_keys);
+  {
+    const TileLoc tl = locate_tile(a, leaf, suffix_keys, 0);
+    dma_tile<kFwdWaves>(tl.suffix ? kbase : pkbase, kstride, tl.row, tl.len, smem, wave, lane);
+    dma_tile<kFwdWaves>(tl.suffix ? vbase : pvbase, kstride, tl.row, tl.len, smem + kTileBytes, wave, lane);
+  }
 
   bf16x8 qv[8], gv[8];
   {
@@ -326,18 +360,7 @@ __global__ __launch_bounds__(256, 2) void mfma_dq(KernelArgs a) {
 #pragma unroll
   for (int i = 0; i < 4; i++) dq[i] = f32x16{};
 
-  const bf16* kbase = static_cast<const bf16*>(a.k) + kvh * kMfmaD;
-  const bf16* vbase = static_cast<const bf16*>(a.v) + kvh * kMfmaD;
-  const bf16* pkbase = static_cast<const bf16*>(a.pk) + kvh * kMfmaD;
-  const bf16* pvbase = static_cast<const bf16*>(a.pv) + kvh * kMfmaD;
-
-  const int ntiles = count_tiles(a, leaf, suffix_keys);
-  Stage2 st;
-  {
-    const TileLoc tl = locate_tile(a, leaf, suffix_keys, 0);
-    stage_load(st, tl.suffix ? kbase : pkbase, tl.suffix ? vbase : pvbase, kstride, tl.row, tl.len);
-    stage_store(st, smem, smem + kTileBytes);
-  }
+  wait_dma();
   __syncthreads();
 
   for (int it = 0; it < ntiles; it++) {
@@ -346,7 +369,9 @@ __global__ __launch_bounds__(256, 2) void mfma_dq(KernelArgs a) {
     const TileLoc tl = locate_tile(a, leaf, suffix_keys, it);
     if (it + 1 < ntiles) {
       const TileLoc nx = locate_tile(a, leaf, suffix_keys, it + 1);
-      stage_load(st, nx.suffix ? kbase : pkbase, nx.suffix ? vbase : pvbase, kstride, nx.row, nx.len);
+      char* nk = smem + ((it + 1) & 1) * 2 * kTileBytes;
+      dma_tile<kFwdWaves>(nx.suffix ? kbase : pkbase, kstride, nx.row, nx.len, nk, wave, lane);
+      dma_tile<kFwdWaves>(nx.suffix ? vbase : pvbase, kstride, nx.row, nx.len, nk + kTileBytes, wave, lane);
     }
     const bool skip = !wave_active || (tl.suffix && tl.pos0 > tw0 + kFwdTokens - 1);
     if (!skip) {
@@ -362,16 +387,17 @@ __global__ __launch_bounds__(256, 2) void mfma_dq(KernelArgs a) {
           dp[kb] = mfma(lds_read_b128(vt, krow, 16 * c + 8 * h), gv[c], dp[kb]);
         }
       }
-      const bool need_mask = tl.len < kTileRows || (tl.suffix && tl.pos0 + kTileRows - 1 > tw0);
+      int lim = 1 << 30;
+      if (tl.len < kTileRows || (tl.suffix && tl.pos0 + kTileRows - 1 > tw0)) {
+        lim = tl.len - 1 - 8 * h;
+        if (tl.suffix) lim = min(lim, t - tl.pos0 - 8 * h);
+      }
 #pragma unroll
       for (int kb = 0; kb < 2; kb++)
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-          float p = exp2f(fmaf(s[kb][r], c2, -lse2));
-          if (need_mask) {
-            const int j = kb * 32 + 16 * (r >> 3) + 8 * h + (r & 7);
-            if (!(j < tl.len && (!tl.suffix || tl.pos0 + j <= t))) p = 0.f;
-          }
+          float p = fast_exp2(fmaf(s[kb][r], c2, -lse2));
+          p = (kb * 32 + 16 * (r >> 3) + (r & 7) <= lim) ? p : 0.f;
           s[kb][r] = p * (dp[kb][r] - delta);  // dS^T
         }
 #pragma unroll
@@ -384,10 +410,7 @@ __global__ __launch_bounds__(256, 2) void mfma_dq(KernelArgs a) {
           for (int db = 0; db < 4; db++) dq[db] = mfma(lds_read_col8(kt, r0, 32 * db, lane), dsb, dq[db]);
         }
     }
-    if (it + 1 < ntiles) {
-      char* nk = smem + ((it + 1) & 1) * 2 * kTileBytes;
-      stage_store(st, nk, nk + kTileBytes);
-    }
+    wait_dma();
     __syncthreads();
   }
 
@@ -409,7 +432,7 @@ __global__ __launch_bounds__(256, 2) void mfma_dq(KernelArgs a) {
 //   S = Q K^T (query rows permuted by sigma32), P = exp(scale S - lse),
 //   dP = dO V^T, dS = P (dP - delta), dV += P^T dO, dK += dS^T Q, dK *= scale.
 // K/V of the wave's 32 keys are B operands held in registers; Q/dO blocks of
-// 64 queries are staged in LDS and read row-wise (A operands) and
+// 64 queries are copied to LDS and read row-wise (A operands) and
 // column-wise (B operands of dV/dK, ds_read_tr16_b64).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
@@ -433,27 +456,9 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
   const int64_t qstride = static_cast<int64_t>(a.hq) * kMfmaD;
   const int64_t kstride = static_cast<int64_t>(a.hkv) * kMfmaD;
 
-  __shared__ __attribute__((aligned(16))) char smem[4 * kTileBytes];   // Q0 G0 Q1 G1
-  __shared__ __attribute__((aligned(16))) float stats[2][2][kTileRows];  // [buf][lse2|delta][row]
+  __shared__ __attribute__((aligned(1024))) char smem[4 * kTileBytes];   // Q0 G0 Q1 G1
+  __shared__ __attribute__((aligned(16))) float stats[2][2][kTileRows];  // [buf][lse*log2e | delta][row]
 
-  bf16x8 kv[8], vv[8];
-  {
-    const bf16* kb = static_cast<const bf16*>(prefix ? a.pk : a.k);
-    const bf16* vb = static_cast<const bf16*>(prefix ? a.pv : a.v);
-    const int64_t off = static_cast<int64_t>(seg_row0 + min(kp, seg_len - 1)) * kstride + kvh * kMfmaD + 8 * h;
-#pragma unroll
-    for (int c = 0; c < 8; c++) {
-      kv[c] = *reinterpret_cast<const bf16x8*>(kb + off + 16 * c);
-      vv[c] = *reinterpret_cast<const bf16x8*>(vb + off + 16 * c);
-    }
-  }
-  f32x16 dk[4], dv[4];
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    dk[i] = f32x16{};
-    dv[i] = f32x16{};
-  }
-  const float c2 = a.scale * kLog2e;
   const int nstage = (qb_hi - qb_lo) * a.group;
   const bf16* qbase = static_cast<const bf16*>(a.q);
   const bf16* gbase = static_cast<const bf16*>(a.dout);
@@ -477,14 +482,34 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
     }
   };
 
-  Stage2 st;
   if (nstage > 0) {
     int row0, tok0, nq, qh;
     stage_info(0, row0, tok0, nq, qh);
-    stage_load(st, qbase + qh * kMfmaD, gbase + qh * kMfmaD, qstride, row0 + tok0, nq);
-    stage_store(st, smem, smem + kTileBytes);
+    dma_tile<kDkdvWaves>(qbase + qh * kMfmaD, qstride, row0 + tok0, nq, smem, wave, lane);
+    dma_tile<kDkdvWaves>(gbase + qh * kMfmaD, qstride, row0 + tok0, nq, smem + kTileBytes, wave, lane);
     load_stats(0, row0, tok0, nq, qh);
   }
+
+  bf16x8 kv[8], vv[8];
+  {
+    const bf16* kb = static_cast<const bf16*>(prefix ? a.pk : a.k);
+    const bf16* vb = static_cast<const bf16*>(prefix ? a.pv : a.v);
+    const int64_t off = static_cast<int64_t>(seg_row0 + min(kp, seg_len - 1)) * kstride + kvh * kMfmaD + 8 * h;
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+      kv[c] = *reinterpret_cast<const bf16x8*>(kb + off + 16 * c);
+      vv[c] = *reinterpret_cast<const bf16x8*>(vb + off + 16 * c);
+    }
+  }
+  f32x16 dk[4], dv[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    dk[i] = f32x16{};
+    dv[i] = f32x16{};
+  }
+  const float c2 = a.scale * kLog2e;
+
+  wait_dma();
   __syncthreads();
 
   for (int sidx = 0; sidx < nstage; sidx++) {
@@ -496,7 +521,10 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
     int nrow0 = 0, ntok0 = 0, nnq = 0, nqh = 0;
     if (sidx + 1 < nstage) {
       stage_info(sidx + 1, nrow0, ntok0, nnq, nqh);
-      stage_load(st, qbase + nqh * kMfmaD, gbase + nqh * kMfmaD, qstride, nrow0 + ntok0, nnq);
+      char* nt = smem + (buf ^ 1) * 2 * kTileBytes;
+      dma_tile<kDkdvWaves>(qbase + nqh * kMfmaD, qstride, nrow0 + ntok0, nnq, nt, wave, lane);
+      dma_tile<kDkdvWaves>(gbase + nqh * kMfmaD, qstride, nrow0 + ntok0, nnq, nt + kTileBytes, wave, lane);
+      load_stats(buf ^ 1, nrow0, ntok0, nnq, nqh);
     }
     if (wave_active) {
 #pragma unroll
@@ -511,15 +539,16 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
           s = mfma(lds_read_b128(qt, qrow, 16 * c + 8 * h), kv[c], s);
           dp = mfma(lds_read_b128(gt, qrow, 16 * c + 8 * h), vv[c], dp);
         }
-        // register r holds query 32*qs + 16*(r/8) + 8*h + r%8 of the block
+        // register r holds query 32*qs + 16*(r/8) + 8*h + r%8 of the block;
+        // causal (suffix): key kp visible iff kp <= query position
         const float* l2 = &stats[buf][0][32 * qs + 8 * h];
         const float* dl = &stats[buf][1][32 * qs + 8 * h];
-        const bool need_mask = !prefix && qpos0 < kw0 + 31;
+        const int lim = (!prefix && qpos0 < kw0 + 31) ? kp - qpos0 - 8 * h : -(1 << 30);
 #pragma unroll
         for (int r = 0; r < 16; r++) {
           const int qi = 16 * (r >> 3) + (r & 7);
-          float p = exp2f(fmaf(s[r], c2, -l2[qi]));
-          if (need_mask && kp > qpos0 + 8 * h + qi) p = 0.f;
+          float p = fast_exp2(fmaf(s[r], c2, -l2[qi]));
+          p = (qi >= lim) ? p : 0.f;
           s[r] = p;
           dp[r] = p * (dp[r] - dl[qi]);
         }
@@ -536,11 +565,7 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
         }
       }
     }
-    if (sidx + 1 < nstage) {
-      char* nt = smem + (buf ^ 1) * 2 * kTileBytes;
-      stage_store(st, nt, nt + kTileBytes);
-      load_stats(buf ^ 1, nrow0, ntok0, nnq, nqh);
-    }
+    wait_dma();
     __syncthreads();
   }
 
@@ -565,6 +590,13 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
 
 int launch_mfma_fwd(const KernelArgs& a, hipStream_t s) {
   if (a.n_items > 0) hipLaunchKernelGGL(mfma_fwd, dim3(a.n_items), dim3(256), 0, s, a);
+  return hipGetLastError() == hipSuccess ? 0 : 4;
+}
+
+int launch_mfma_delta(const KernelArgs& a, hipStream_t s) {
+  const int64_t rows = static_cast<int64_t>(a.total_q) * a.hq;
+  const int blocks = static_cast<int>((rows + 15) / 16);
+  if (blocks > 0) hipLaunchKernelGGL(mfma_delta, dim3(blocks), dim3(256), 0, s, a);
   return hipGetLastError() == hipSuccess ? 0 : 4;
 }
 

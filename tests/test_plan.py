@@ -1,0 +1,177 @@
+"""CPU tests of the native planner (tpr_attn_plan): tree validation, work-list
+coverage, XCD-aware ordering and the segment-tree lowering. Host code only."""
+
+from collections import Counter
+
+import pytest
+import torch
+
+from bridge_amd import TPRPrefixMeta
+
+CPU = torch.device("cpu")
+
+# header word indices (bridge_amd/csrc/tpr_common.h)
+PF = dict(MAGIC=0, NUM_LEAVES=2, NUM_NODES=3, MAX_DEPTH=4, TOTAL_Q=5, TOTAL_PREFIX=6, HQ=7, HKV=8, D=9,
+          PATH=11, OFF_CU=12, OFF_NODE_OFF=13, OFF_ANC=14, OFF_NODE_LEAF=15, N_QBLK=16, OFF_QBLK=17,
+          OFF_LEAF_QBLK=18, N_FWD=19, OFF_FWD=20, N_DKDV=21, OFF_DKDV=22, N_RED=23, TOTAL_WORDS=27)
+
+
+def decode(plan):
+    w = plan.host.tolist()
+    assert w[PF["MAGIC"]] == 0x31525054 and w[PF["TOTAL_WORDS"]] == len(w)
+    fwd = [tuple(w[w[PF["OFF_FWD"]] + 4 * i: w[PF["OFF_FWD"]] + 4 * i + 4]) for i in range(w[PF["N_FWD"]])]
+    dkdv = [tuple(w[w[PF["OFF_DKDV"]] + 8 * i: w[PF["OFF_DKDV"]] + 8 * i + 8]) for i in range(w[PF["N_DKDV"]])]
+    qblk = [tuple(w[w[PF["OFF_QBLK"]] + 2 * i: w[PF["OFF_QBLK"]] + 2 * i + 2]) for i in range(w[PF["N_QBLK"]])]
+    return w, fwd, dkdv, qblk
+
+
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (8, 2), (4, 4), (6, 2), (4, 2)])
+def test_forward_items_cover_every_query_row_once(hq, hkv):
+    meta = TPRPrefixMeta(cu_seqlens_q=(0, 100, 100, 357), node_offsets=(0, 64, 200),
+                         leaf_ancestors=((0, 1), (0,), (0,)))
+    plan = meta.plan(hq, hkv, 128, torch.bfloat16, CPU)
+    assert plan.path == "mfma"
+    _, fwd, _, _ = decode(plan)
+    g = hq // hkv
+    hpw = max(x for x in (4, 2, 1) if g % x == 0)
+    tpw = 32 * (4 // hpw)
+    covered = Counter()
+    for leaf, tok0, qh0, kvh in fwd:
+        if leaf < 0:
+            continue
+        assert kvh == qh0 // g and qh0 % hpw == 0
+        length = meta.cu_seqlens_q[leaf + 1] - meta.cu_seqlens_q[leaf]
+        for h in range(qh0, qh0 + hpw):
+            for t in range(tok0, min(tok0 + tpw, length)):
+                covered[(leaf, t, h)] += 1
+    expected = {(s, t, h) for s in range(3) for t in range(meta.cu_seqlens_q[s + 1] - meta.cu_seqlens_q[s])
+                for h in range(hq)}
+    assert set(covered) == expected and set(covered.values()) == {1}
+
+
+def test_xcd_ordering_pins_kv_heads_and_is_lpt_per_xcd():
+    meta = TPRPrefixMeta.shared_prefix(4096, [4096] * 4)
+    plan = meta.plan(32, 8, 128, torch.bfloat16, CPU)
+    _, fwd, dkdv, _ = decode(plan)
+    assert len(fwd) == 4 * 128 * 8 and len(dkdv) == (32 + 4 * 32) * 8
+    for i, (leaf, tok0, qh0, kvh) in enumerate(fwd):
+        assert leaf >= 0 and kvh == i % 8
+    for i, item in enumerate(dkdv):
+        assert item[3] == i % 8
+    # decreasing causal work (prefix + tokens seen) within each XCD queue
+    for x in range(8):
+        work = [4096 + min(tok0 + 32, 4096) for (_, tok0, _, _) in fwd[x::8]]
+        assert work == sorted(work, reverse=True)
+
+
+def test_dkdv_items_cover_every_key_tile_and_query_block():
+    meta = TPRPrefixMeta(cu_seqlens_q=(0, 33, 98, 138, 155), node_offsets=(0, 130, 200, 270, 290),
+                         leaf_ancestors=((0, 1), (0, 1), (0, 2), (0, 2)))   # node 3 is unused
+    plan = meta.plan(8, 2, 128, torch.bfloat16, CPU)
+    w, _, dkdv, qblk = decode(plan)
+    leaf_qblk = w[w[PF["OFF_LEAF_QBLK"]]: w[PF["OFF_LEAF_QBLK"]] + 5]
+    seen = Counter()
+    for src, seg, key0, kvh, lo, hi, slot, _ in dkdv:
+        if src < 0:
+            continue
+        assert slot == -1
+        seen[(src, seg, key0, kvh)] += 1
+        leaves = {qblk[i][0] for i in range(lo, hi)}
+        if src == 0:
+            expected = {s for s, a in enumerate(meta.leaf_ancestors) if seg in a}
+            assert leaves == expected
+            assert (lo, hi) == ((leaf_qblk[min(expected)], leaf_qblk[max(expected) + 1]) if expected else (lo, lo))
+        else:
+            assert leaves <= {seg} and hi == leaf_qblk[seg + 1]
+            assert all(qblk[i][1] + 64 > key0 for i in range(lo, hi))
+    for n in range(4):
+        length = meta.node_offsets[n + 1] - meta.node_offsets[n]
+        for k0 in range(0, length, 128):
+            for h in range(2):
+                assert seen[(0, n, k0, h)] == 1
+    for s in range(4):
+        length = meta.cu_seqlens_q[s + 1] - meta.cu_seqlens_q[s]
+        for k0 in range(0, length, 128):
+            for h in range(2):
+                assert seen[(1, s, k0, h)] == 1
+
+
+def test_simt_path_for_fp32_and_small_head_dim():
+    meta = TPRPrefixMeta.shared_prefix(512, [512, 512])
+    assert meta.plan(4, 4, 64, torch.float32, CPU).path == "simt"
+    assert meta.plan(4, 4, 64, torch.bfloat16, CPU).path == "simt"
+    assert meta.plan(4, 4, 128, torch.float32, CPU).path == "simt"
+    assert meta.plan(4, 4, 128, torch.bfloat16, CPU).path == "mfma"
+
+
+def test_plan_is_cached_per_configuration():
+    meta = TPRPrefixMeta.shared_prefix(8, [4])
+    a = meta.plan(4, 2, 128, torch.bfloat16, CPU)
+    assert meta.plan(4, 2, 128, torch.bfloat16, CPU) is a
+    assert meta.plan(4, 2, 64, torch.bfloat16, CPU) is not a
+
+
+@pytest.mark.parametrize(
+    ("kwargs", "exc", "match"),
+    [
+        (dict(cu_seqlens_q=(0, 4, 8), node_offsets=(0, 4, 8), leaf_ancestors=((0, 1), (1,))), ValueError,
+         "inconsistent paths"),
+        (dict(cu_seqlens_q=(0, 4, 8, 12), node_offsets=(0, 4, 8), leaf_ancestors=((0,), (1,), (0,))), ValueError,
+         "not contiguous"),
+        (dict(cu_seqlens_q=(0, 4), node_offsets=(0, 4), leaf_ancestors=((3,),)), ValueError, "out of range"),
+        (dict(cu_seqlens_q=(0, 4), node_offsets=(0, 4, 6), leaf_ancestors=((-1, 0),)), ValueError, "padding"),
+        (dict(cu_seqlens_q=(0, 4, 2), node_offsets=(0, 4), leaf_ancestors=((0,), (0,))), ValueError,
+         "non-decreasing"),
+        (dict(cu_seqlens_q=(1, 4), node_offsets=(0, 4), leaf_ancestors=((0,),)), ValueError, r"cu_seqlens_q\[0\]"),
+        (dict(cu_seqlens_q=(0, 4), node_offsets=(0, 5, 3), leaf_ancestors=((0,),)), ValueError, "node_offsets"),
+        (dict(cu_seqlens_q=(0, 4), node_offsets=(0, 4), leaf_ancestors=((0, 0),)), ValueError, "inconsistent"),
+    ],
+)
+def test_planner_rejects_invalid_trees(kwargs, exc, match):
+    meta = TPRPrefixMeta(**kwargs)
+    with pytest.raises(exc, match=match):
+        meta.plan(4, 2, 128, torch.bfloat16, CPU)
+
+
+@pytest.mark.parametrize(("hq", "hkv", "d", "exc", "match"),
+                         [(6, 4, 128, ValueError, "divisible"), (4, 2, 256, NotImplementedError, "head_dim"),
+                          (4, 2, 60, NotImplementedError, "multiple of 8")])
+def test_planner_rejects_unsupported_heads(hq, hkv, d, exc, match):
+    with pytest.raises(exc, match=match):
+        TPRPrefixMeta.shared_prefix(8, [4]).plan(hq, hkv, d, torch.bfloat16, CPU)
+
+
+def test_planner_rejects_other_dtypes():
+    with pytest.raises(ValueError, match="bfloat16 and torch.float32"):
+        TPRPrefixMeta.shared_prefix(8, [4]).plan(4, 2, 128, torch.float16, CPU)
+
+
+def test_segment_tree_lowering_turn_tree():
+    # root 2048 -> 4 branches x 1024 -> 4 leaves x 1024 each (turn-boundary tree, depth 3)
+    parents = {0: None}
+    lengths = {0: 2048}
+    for b in range(4):
+        parents[1 + b] = 0
+        lengths[1 + b] = 1024
+    for i in range(16):
+        parents[100 + i] = 1 + i // 4
+        lengths[100 + i] = 1024
+    meta, nodes, leaves = TPRPrefixMeta.from_segment_tree(parents, lengths)
+    assert nodes == (0, 1, 2, 3, 4) and leaves == tuple(range(100, 116))
+    assert meta.node_offsets == (0, 2048, 3072, 4096, 5120, 6144)
+    assert meta.leaf_ancestors == tuple((0, 1 + i // 4) for i in range(16))
+    assert meta.visible_pairs() == 58728448
+    meta.plan(32, 8, 128, torch.bfloat16, CPU)  # valid for the planner
+
+
+def test_segment_tree_lowering_rejects_two_roots():
+    with pytest.raises(ValueError, match="exactly one root"):
+        TPRPrefixMeta.from_segment_tree({0: None, 1: None}, {0: 1, 1: 1})
+
+
+def test_empty_leaves_and_prefixless_trees_plan():
+    meta = TPRPrefixMeta.shared_prefix(0, [0, 5, 0])
+    plan = meta.plan(4, 1, 128, torch.bfloat16, CPU)
+    _, fwd, dkdv, _ = decode(plan)
+    assert {item[0] for item in fwd if item[0] >= 0} == {1}
+    assert all(item[0] == 1 for item in dkdv if item[0] >= 0)
