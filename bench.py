@@ -141,7 +141,9 @@ def main() -> int:
 
     buffers = {"dq": torch.empty_like(q), "dk": torch.empty_like(k), "dv": torch.empty_like(v),
                "dprefix_k": torch.empty_like(pk), "dprefix_v": torch.empty_like(pv),
-               "delta": torch.empty((hq, tq), dtype=torch.float32, device=device)}
+               "delta": torch.empty((hq, tq), dtype=torch.float32, device=device),
+               "workspace": (torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=device)
+                             if plan.workspace_bytes else None)}
     stream = torch.cuda.current_stream(device)
 
     def step(events=None):

@@ -16,7 +16,7 @@ int launch_simt_fwd(const KernelArgs& a, bool fp32, hipStream_t s);
 int launch_delta(const KernelArgs& a, bool fp32, hipStream_t s);
 int launch_simt_bwd(const KernelArgs& a, int n_fwd, int n_dkdv, bool fp32, hipStream_t s);
 int launch_mfma_fwd(const KernelArgs& a, hipStream_t s);
-int launch_mfma_bwd(const KernelArgs& a, int n_fwd, int n_dkdv, hipStream_t s);
+int launch_mfma_bwd(const KernelArgs& a, int n_fwd, int n_dkdv, int n_red, hipStream_t s);
 int launch_mfma_delta(const KernelArgs& a, hipStream_t s);
 
 namespace {
@@ -61,6 +61,7 @@ KernelArgs args_from_plan(const int32_t* ph, const int32_t* pd, float scale) {
   a.off_leaf_qblk = ph[PF_OFF_LEAF_QBLK];
   a.off_fwd = ph[PF_OFF_FWD];
   a.off_dkdv = ph[PF_OFF_DKDV];
+  a.off_red = ph[PF_OFF_RED];
   return a;
 }
 
@@ -175,13 +176,15 @@ extern "C" int tpr_attn_bwd_phases(const TprBwdParams* p, int phases, void* stre
   a.dv = p->dv;
   a.dpk = p->dprefix_k;
   a.dpv = p->dprefix_v;
+  a.ws = static_cast<float*>(p->workspace);
   const bool fp32 = ph[PF_DTYPE] == TPR_DTYPE_FP32;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int n_dkdv = (phases & TPR_BWD_DKDV) ? ph[PF_N_DKDV] : 0;
   const int n_dq = (phases & TPR_BWD_DQ) ? ph[PF_N_FWD] : 0;
   rc = (phases & TPR_BWD_DELTA) ? (mfma ? launch_mfma_delta(a, s) : launch_delta(a, fp32, s)) : 0;
   if (!rc && (n_dkdv || n_dq))
-    rc = mfma ? launch_mfma_bwd(a, n_dq, n_dkdv, s) : launch_simt_bwd(a, n_dq, n_dkdv, fp32, s);
+    rc = mfma ? launch_mfma_bwd(a, n_dq, n_dkdv, (phases & TPR_BWD_DKDV) ? ph[PF_N_RED] : 0, s)
+              : launch_simt_bwd(a, n_dq, n_dkdv, fp32, s);
   if (rc) return fail(TPR_ERR_LAUNCH, "backward launch failed: %s", hipGetErrorString(hipGetLastError()));
   return TPR_OK;
 }

@@ -37,9 +37,9 @@ enum PlanField : int {
   PF_N_DKDV,         // dK/dV work items
   PF_OFF_DKDV,       // [n][8] = DkdvItem
   PF_N_RED,          // split-reduction items
-  PF_OFF_RED,        // [n][4] = {node, key start, kv head, first slot}
+  PF_OFF_RED,        // [n][RED_WORDS] = RedItem
   PF_N_SLOTS,        // fp32 partial slots (each kDkdvKeys x D x 2 floats)
-  PF_SPLIT,          // partials per split prefix tile
+  PF_MAX_SPLIT,      // most partial slots reduced into one tile
   PF_TOTAL_WORDS,
   PF_HEADER_WORDS = 32
 };
@@ -62,6 +62,20 @@ enum DkdvField : int {
   DK_WORDS = 8
 };
 
+// Split-reduction item: sum fp32 partial slots [slot0, slot0 + nslots) of one
+// (KV segment tile, KV head) in slot order and write dK/dV in the I/O dtype.
+enum RedField : int {
+  RD_SRC = 0,   // 0 = prefix node, 1 = leaf suffix
+  RD_SEG,
+  RD_KEY0,
+  RD_KVH,
+  RD_SLOT0,
+  RD_NSLOTS,
+  RD_PAD0,
+  RD_PAD1,
+  RD_WORDS = 8
+};
+
 // ---- tile shapes -----------------------------------------------------------
 // SIMT family (any dtype / head_dim <= 128)
 constexpr int kSimtQ = 64;      // queries per forward / dQ block (one head)
@@ -76,5 +90,8 @@ constexpr int kFwdKeys = 64;          // keys per LDS tile
 constexpr int kDkdvWaves = 4;         // waves per dK/dV workgroup
 constexpr int kDkdvKeys = 32 * kDkdvWaves;  // keys per dK/dV workgroup (32 per wave)
 constexpr int kDkdvQ = 64;            // queries per staged query block
+constexpr int kDkdvMaxBlocks = 128;   // query blocks one dK/dV item may stream (LDS table size)
+constexpr int kDkdvPrefixChunk = 64;  // query blocks per item when a prefix tile is split
+constexpr int kMfmaMaxDepth = 8;      // ancestor nodes per leaf handled by the MFMA path
 
 }  // namespace tpr

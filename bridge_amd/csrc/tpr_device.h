@@ -43,8 +43,9 @@ struct KernelArgs {
   int32_t hpw;  // query heads per forward/dQ workgroup (MFMA path)
   int32_t total_q, total_prefix, max_depth;
   int32_t off_cu, off_node_off, off_anc, off_node_leaf;
-  int32_t off_qblk, off_leaf_qblk, off_fwd, off_dkdv;
+  int32_t off_qblk, off_leaf_qblk, off_fwd, off_dkdv, off_red;
   int32_t n_items;
+  float* ws;  // fp32 partial dK/dV slots of split tiles
 };
 
 __device__ __forceinline__ float to_f32(float x) { return x; }

@@ -70,43 +70,63 @@ __device__ __forceinline__ bf16x8 to_bf16x8(const f32x16& x, int base) {
   return r;
 }
 
-// Locate tile `idx` of a forward/dQ key stream: ancestors (full) then suffix
-// (causal). Returns the row offset into the segment's tensor and fills the
-// tile's key count, the key position of its first row and the causal flag.
+// Key stream of a forward/dQ workgroup: the leaf's ancestor nodes (fully
+// visible, root first) then its own suffix (right-down causal), cut into
+// 64-row tiles. The segment table is read from the plan once, before the
+// tile loop, and stays in (uniform) registers.
+struct SegTable {
+  int row[kMfmaMaxDepth];   // first row of node d in prefix_k/v
+  int len[kMfmaMaxDepth];   // rows of node d (0 past the leaf's depth)
+  int end[kMfmaMaxDepth];   // tiles in nodes 0..d
+  int suffix_row;           // first row of the leaf in k/v
+  int suffix_keys;          // suffix keys the workgroup needs
+  int ntiles;
+};
+
 struct TileLoc {
   int64_t row;   // absolute row in prefix_k/v (prefix) or k/v (suffix)
   int len;       // valid rows in this tile (<= 64)
-  int pos0;      // position of the first key (suffix tiles: within the leaf)
+  int pos0;      // position of the first key within its segment
   bool suffix;
 };
 
-__device__ __forceinline__ TileLoc locate_tile(const KernelArgs& a, int leaf, int suffix_keys, int idx) {
+__device__ __forceinline__ SegTable load_segments(const KernelArgs& a, int leaf, int suffix_keys) {
   const int32_t* no = a.plan + a.off_node_off;
   const int32_t* anc = a.plan + a.off_anc + leaf * a.max_depth;
-  for (int dd = 0; dd < a.max_depth; dd++) {
-    const int n = anc[dd];
-    if (n < 0) break;
-    const int len = no[n + 1] - no[n];
-    const int tiles = (len + kTileRows - 1) / kTileRows;
-    if (idx < tiles) return TileLoc{static_cast<int64_t>(no[n]) + idx * kTileRows,
-                                    min(kTileRows, len - idx * kTileRows), idx * kTileRows, false};
-    idx -= tiles;
+  SegTable t;
+  int tiles = 0;
+#pragma unroll
+  for (int d = 0; d < kMfmaMaxDepth; d++) {
+    const int n = d < a.max_depth ? anc[d] : -1;
+    const int r = n >= 0 ? no[n] : 0;
+    const int l = n >= 0 ? no[n + 1] - r : 0;
+    t.row[d] = r;
+    t.len[d] = l;
+    tiles += (l + kTileRows - 1) / kTileRows;
+    t.end[d] = tiles;
   }
-  const int32_t* cu = a.plan + a.off_cu;
-  return TileLoc{static_cast<int64_t>(cu[leaf]) + idx * kTileRows, min(kTileRows, suffix_keys - idx * kTileRows),
-                 idx * kTileRows, true};
+  t.suffix_row = a.plan[a.off_cu + leaf];
+  t.suffix_keys = suffix_keys;
+  t.ntiles = tiles + (suffix_keys + kTileRows - 1) / kTileRows;
+  return t;
 }
 
-__device__ __forceinline__ int count_tiles(const KernelArgs& a, int leaf, int suffix_keys) {
-  const int32_t* no = a.plan + a.off_node_off;
-  const int32_t* anc = a.plan + a.off_anc + leaf * a.max_depth;
-  int tiles = 0;
-  for (int dd = 0; dd < a.max_depth; dd++) {
-    const int n = anc[dd];
-    if (n < 0) break;
-    tiles += (no[n + 1] - no[n] + kTileRows - 1) / kTileRows;
+__device__ __forceinline__ TileLoc locate_tile(const SegTable& t, int idx) {
+  const int prefix_tiles = t.end[kMfmaMaxDepth - 1];
+  int lt = idx - prefix_tiles;
+  TileLoc r{static_cast<int64_t>(t.suffix_row) + lt * kTileRows, min(kTileRows, t.suffix_keys - lt * kTileRows),
+            lt * kTileRows, true};
+  int start = 0;
+#pragma unroll
+  for (int d = 0; d < kMfmaMaxDepth; d++) {
+    if (idx >= start && idx < t.end[d]) {
+      lt = idx - start;
+      r = TileLoc{static_cast<int64_t>(t.row[d]) + lt * kTileRows, min(kTileRows, t.len[d] - lt * kTileRows),
+                  lt * kTileRows, false};
+    }
+    start = t.end[d];
   }
-  return tiles + (suffix_keys + kTileRows - 1) / kTileRows;
+  return r;
 }
 
 // Direct global -> LDS copy (gfx950 global_load_lds_dwordx4) of the 64 rows
@@ -116,26 +136,60 @@ __device__ __forceinline__ int count_tiles(const KernelArgs& a, int leaf, int su
 // l of a block lands at block + 16*l, i.e. at (row 4*blk + l/16, physical
 // chunk l%16), so the lane fetches the logical chunk that swizzles there. No
 // registers hold the data, and the wave's vmcnt covers the copy.
-typedef __attribute__((address_space(3))) void lds_void;
+// The copy is issued from inline asm (M0 = wave-uniform LDS destination,
+// restored afterwards):
+// the compiler does not track it, so it does not serialise the next tile's
+// copy against the current tile's LDS reads; wait_dma() before the barrier
+// that publishes the tile is the only wait it needs. vmcnt retires in
+// order, so the compiler's own waits on its loads stay correct (they can
+// only become stricter). The asm needs no memory clobber: the kernel never
+// writes the global data it reads, and the LDS it writes is read only after
+// wait_dma() and a barrier.
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)(p)));
+}
+
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds_dst) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(src), "s"(lds_dst));
+}
 
 template <int kWaves>
 __device__ __forceinline__ void dma_tile(const bf16* base, int64_t stride, int64_t row0, int len, char* tile,
                                          int wave, int lane) {
   constexpr int kBlocks = 16 / kWaves;
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(tile));
 #pragma unroll
   for (int j = 0; j < kBlocks; j++) {
     const int blk = wave * kBlocks + j;
     const int row = 4 * blk + (lane >> 4);
     const int chunk = swz_chunk(row, lane & 15);
     const bf16* src = base + (row0 + min(row, len - 1)) * stride + chunk * 8;
-    __builtin_amdgcn_global_load_lds(src, (lds_void*)(tile + blk * 1024), 16, 0, 0);
+    dma16(src, __builtin_amdgcn_readfirstlane(lds0 + blk * 1024));
   }
 }
 
 // Wait until this wave's outstanding global->LDS copies have landed.
-__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Ordered before the __syncthreads() that follows it (both have side effects);
+// the barrier is what orders the LDS reads of the copied tile.
+__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)"); }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Make the compiler complete the load of `x` here. Operands loaded before a
+// tile loop are waited for once, before it, instead of at their first use
+// inside it -- a wait there would also drain the in-flight tile copies.
+template <typename T>
+__device__ __forceinline__ void settle(const T& x) {
+  asm volatile("" ::"v"(x));
+}
 
 // ---------------------------------------------------------------------------
 // Forward
@@ -168,9 +222,10 @@ __global__ __launch_bounds__(256, 2) void mfma_fwd(KernelArgs a) {
   const bf16* pkbase = static_cast<const bf16*>(a.pk) + kvh * kMfmaD;
   const bf16* pvbase = static_cast<const bf16*>(a.pv) + kvh * kMfmaD;
 
-  const int ntiles = count_tiles(a, leaf, suffix_keys);
+  const SegTable seg = load_segments(a, leaf, suffix_keys);
+  const int ntiles = seg.ntiles;
   {
-    const TileLoc tl = locate_tile(a, leaf, suffix_keys, 0);
+    const TileLoc tl = locate_tile(seg, 0);
     dma_tile<kFwdWaves>(tl.suffix ? kbase : pkbase, kstride, tl.row, tl.len, smem, wave, lane);
     dma_tile<kFwdWaves>(tl.suffix ? vbase : pvbase, kstride, tl.row, tl.len, smem + kTileBytes, wave, lane);
   }
@@ -190,15 +245,17 @@ __global__ __launch_bounds__(256, 2) void mfma_fwd(KernelArgs a) {
   float m = -1e30f, l = 0.f;
   const float c2 = a.scale * kLog2e;
 
+#pragma unroll
+  for (int c = 0; c < 8; c++) settle(qv[c]);
   wait_dma();
   __syncthreads();
 
   for (int it = 0; it < ntiles; it++) {
     const char* kt = smem + (it & 1) * 2 * kTileBytes;
     const char* vt = kt + kTileBytes;
-    const TileLoc tl = locate_tile(a, leaf, suffix_keys, it);
+    const TileLoc tl = locate_tile(seg, it);
     if (it + 1 < ntiles) {
-      const TileLoc nx = locate_tile(a, leaf, suffix_keys, it + 1);
+      const TileLoc nx = locate_tile(seg, it + 1);
       char* nk = smem + ((it + 1) & 1) * 2 * kTileBytes;
       dma_tile<kFwdWaves>(nx.suffix ? kbase : pkbase, kstride, nx.row, nx.len, nk, wave, lane);
       dma_tile<kFwdWaves>(nx.suffix ? vbase : pvbase, kstride, nx.row, nx.len, nk + kTileBytes, wave, lane);
@@ -333,9 +390,10 @@ __global__ __launch_bounds__(256, 2) void mfma_dq(KernelArgs a) {
   const bf16* pkbase = static_cast<const bf16*>(a.pk) + kvh * kMfmaD;
   const bf16* pvbase = static_cast<const bf16*>(a.pv) + kvh * kMfmaD;
 
-  const int ntiles = count_tiles(a, leaf, suffix_keys);
+  const SegTable seg = load_segments(a, leaf, suffix_keys);
+  const int ntiles = seg.ntiles;
   {
-    const TileLoc tl = locate_tile(a, leaf, suffix_keys, 0);
+    const TileLoc tl = locate_tile(seg, 0);
     dma_tile<kFwdWaves>(tl.suffix ? kbase : pkbase, kstride, tl.row, tl.len, smem, wave, lane);
     dma_tile<kFwdWaves>(tl.suffix ? vbase : pvbase, kstride, tl.row, tl.len, smem + kTileBytes, wave, lane);
   }
@@ -360,15 +418,22 @@ __global__ __launch_bounds__(256, 2) void mfma_dq(KernelArgs a) {
 #pragma unroll
   for (int i = 0; i < 4; i++) dq[i] = f32x16{};
 
+#pragma unroll
+  for (int c = 0; c < 8; c++) {
+    settle(qv[c]);
+    settle(gv[c]);
+  }
+  settle(lse2);
+  settle(delta);
   wait_dma();
   __syncthreads();
 
   for (int it = 0; it < ntiles; it++) {
     const char* kt = smem + (it & 1) * 2 * kTileBytes;
     const char* vt = kt + kTileBytes;
-    const TileLoc tl = locate_tile(a, leaf, suffix_keys, it);
+    const TileLoc tl = locate_tile(seg, it);
     if (it + 1 < ntiles) {
-      const TileLoc nx = locate_tile(a, leaf, suffix_keys, it + 1);
+      const TileLoc nx = locate_tile(seg, it + 1);
       char* nk = smem + ((it + 1) & 1) * 2 * kTileBytes;
       dma_tile<kFwdWaves>(nx.suffix ? kbase : pkbase, kstride, nx.row, nx.len, nk, wave, lane);
       dma_tile<kFwdWaves>(nx.suffix ? vbase : pvbase, kstride, nx.row, nx.len, nk + kTileBytes, wave, lane);
@@ -463,31 +528,57 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
   const bf16* qbase = static_cast<const bf16*>(a.q);
   const bf16* gbase = static_cast<const bf16*>(a.dout);
 
+  // Query-block table of this item (planner guarantees <= kDkdvMaxBlocks):
+  // {first packed row, token start within the leaf, valid rows}. Read from the
+  // plan once, so the stage loop touches no plan memory.
+  __shared__ int4 qtab[kDkdvMaxBlocks];
+  for (int i = threadIdx.x; i < qb_hi - qb_lo; i += blockDim.x) {
+    const int qb = qb_lo + i;
+    const int lf = qblk[2 * qb], tok = qblk[2 * qb + 1];
+    const int r0 = cu[lf];
+    qtab[i] = int4{r0 + tok, tok, min(kTileRows, cu[lf + 1] - r0 - tok), 0};
+  }
+  __syncthreads();
+
   auto stage_info = [&](int sidx, int& row0, int& tok0, int& nq, int& qh) {
-    const int qb = qb_lo + sidx / a.group;
+    const int4 e = qtab[sidx / a.group];
     qh = kvh * a.group + sidx % a.group;
-    const int lf = qblk[2 * qb];
-    tok0 = qblk[2 * qb + 1];
-    row0 = cu[lf];
-    nq = min(kTileRows, cu[lf + 1] - row0 - tok0);
+    row0 = e.x - e.y;
+    tok0 = e.y;
+    nq = e.z;
   };
-  auto load_stats = [&](int buf, int row0, int tok0, int nq, int qh) {
+  // lse and delta of one query block: thread r < 64 fetches lse row r, thread
+  // 64 + r delta row r. The raw value is fetched into a register before the
+  // tile copies are issued and only converted and stored to LDS after the
+  // compute, so the load's latency hides behind the stage.
+  struct Stat {
+    float x;
+    bool valid;
+  };
+  auto fetch_stat = [&](int row0, int tok0, int nq, int qh) -> Stat {
+    Stat st{0.f, false};
     if (threadIdx.x < 2 * kTileRows) {
       const int r = threadIdx.x & (kTileRows - 1);
       const int64_t at = static_cast<int64_t>(qh) * a.total_q + row0 + tok0 + min(r, nq - 1);
-      if (threadIdx.x < kTileRows)
-        stats[buf][0][r] = r < nq ? a.lse_in[at] * kLog2e : INFINITY;  // invalid query: P = 0
-      else
-        stats[buf][1][r] = r < nq ? a.delta[at] : 0.f;
+      st.x = threadIdx.x < kTileRows ? a.lse_in[at] : a.delta[at];
+      st.valid = r < nq;
     }
+    return st;
+  };
+  auto store_stat = [&](int buf, Stat st) {
+    if (threadIdx.x < kTileRows)
+      stats[buf][0][threadIdx.x] = st.valid ? st.x * kLog2e : INFINITY;  // invalid query: P = 0
+    else if (threadIdx.x < 2 * kTileRows)
+      stats[buf][1][threadIdx.x - kTileRows] = st.valid ? st.x : 0.f;
   };
 
   if (nstage > 0) {
     int row0, tok0, nq, qh;
     stage_info(0, row0, tok0, nq, qh);
+    const Stat x = fetch_stat(row0, tok0, nq, qh);
     dma_tile<kDkdvWaves>(qbase + qh * kMfmaD, qstride, row0 + tok0, nq, smem, wave, lane);
     dma_tile<kDkdvWaves>(gbase + qh * kMfmaD, qstride, row0 + tok0, nq, smem + kTileBytes, wave, lane);
-    load_stats(0, row0, tok0, nq, qh);
+    store_stat(0, x);
   }
 
   bf16x8 kv[8], vv[8];
@@ -509,6 +600,11 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
   }
   const float c2 = a.scale * kLog2e;
 
+#pragma unroll
+  for (int c = 0; c < 8; c++) {
+    settle(kv[c]);
+    settle(vv[c]);
+  }
   wait_dma();
   __syncthreads();
 
@@ -518,13 +614,15 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
     const char* gt = qt + kTileBytes;
     int row0, tok0, nq, qh;
     stage_info(sidx, row0, tok0, nq, qh);
-    int nrow0 = 0, ntok0 = 0, nnq = 0, nqh = 0;
-    if (sidx + 1 < nstage) {
+    const bool more = sidx + 1 < nstage;
+    Stat next_stat{0.f, false};
+    if (more) {
+      int nrow0, ntok0, nnq, nqh;
       stage_info(sidx + 1, nrow0, ntok0, nnq, nqh);
+      next_stat = fetch_stat(nrow0, ntok0, nnq, nqh);
       char* nt = smem + (buf ^ 1) * 2 * kTileBytes;
       dma_tile<kDkdvWaves>(qbase + nqh * kMfmaD, qstride, nrow0 + ntok0, nnq, nt, wave, lane);
       dma_tile<kDkdvWaves>(gbase + nqh * kMfmaD, qstride, nrow0 + ntok0, nnq, nt + kTileBytes, wave, lane);
-      load_stats(buf ^ 1, nrow0, ntok0, nnq, nqh);
     }
     if (wave_active) {
 #pragma unroll
@@ -565,12 +663,29 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
         }
       }
     }
+    if (more) store_stat(buf ^ 1, next_stat);
     wait_dma();
     __syncthreads();
   }
 
   if (!wave_active) return;
   // accumulator register r of lane l: key 8*(r/4) + 4*h + r%4 of the wave, d = 32*db + n
+  const int slot = item[DK_SLOT];
+  if (slot >= 0) {
+    // split tile: fp32 partial [kDkdvKeys][128] for dK (already scaled) then dV
+    float* pk = a.ws + static_cast<int64_t>(slot) * 2 * kDkdvKeys * kMfmaD;
+    float* pv = pk + kDkdvKeys * kMfmaD;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int key = 32 * wave + 8 * (r >> 2) + 4 * h + (r & 3);
+#pragma unroll
+      for (int db = 0; db < 4; db++) {
+        pk[key * kMfmaD + 32 * db + n] = dk[db][r] * a.scale;
+        pv[key * kMfmaD + 32 * db + n] = dv[db][r];
+      }
+    }
+    return;
+  }
   bf16* dkd = static_cast<bf16*>(prefix ? a.dpk : a.dk);
   bf16* dvd = static_cast<bf16*>(prefix ? a.dpv : a.dv);
 #pragma unroll
@@ -583,6 +698,42 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
       dkd[off + 32 * db] = static_cast<bf16>(dk[db][r] * a.scale);
       dvd[off + 32 * db] = static_cast<bf16>(dv[db][r]);
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Second pass of split dK/dV tiles: sum the fp32 partial slots of one
+// (segment tile, KV head) in slot order -- slot order is query-block order,
+// i.e. leaf order -- and write dK/dV. Deterministic: fixed summation order,
+// one writer per element.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void mfma_reduce(KernelArgs a) {
+  const int32_t* item = a.plan + a.off_red + RD_WORDS * blockIdx.x;
+  const bool prefix = item[RD_SRC] == 0;
+  const int seg = item[RD_SEG], key0 = item[RD_KEY0], kvh = item[RD_KVH];
+  const int slot0 = item[RD_SLOT0], nslots = item[RD_NSLOTS];
+  const int32_t* cu = a.plan + a.off_cu;
+  const int32_t* no = a.plan + a.off_node_off;
+  const int seg_row0 = prefix ? no[seg] : cu[seg];
+  const int keys = min(kDkdvKeys, (prefix ? no[seg + 1] - no[seg] : cu[seg + 1] - cu[seg]) - key0);
+  const int64_t kstride = static_cast<int64_t>(a.hkv) * kMfmaD;
+  bf16* dkd = static_cast<bf16*>(prefix ? a.dpk : a.dk);
+  bf16* dvd = static_cast<bf16*>(prefix ? a.dpv : a.dv);
+  const int64_t slot_floats = 2 * kDkdvKeys * kMfmaD;
+  // 4 consecutive d per thread: 32 threads per key row, 8 key rows per pass
+  for (int e = threadIdx.x; e < 2 * keys * (kMfmaD / 4); e += blockDim.x) {
+    const int which = e / (keys * (kMfmaD / 4));   // 0 = dK, 1 = dV
+    const int rem = e % (keys * (kMfmaD / 4));
+    const int key = rem / (kMfmaD / 4), d4 = rem % (kMfmaD / 4);
+    const float* src = a.ws + static_cast<int64_t>(slot0) * slot_floats + which * kDkdvKeys * kMfmaD +
+                       key * kMfmaD + 4 * d4;
+    f32x4 acc = *reinterpret_cast<const f32x4*>(src);
+    for (int j = 1; j < nslots; j++) acc += *reinterpret_cast<const f32x4*>(src + j * slot_floats);
+    bf16x4 o;
+#pragma unroll
+    for (int i = 0; i < 4; i++) o[i] = static_cast<bf16>(acc[i]);
+    bf16* dst = (which ? dvd : dkd) + static_cast<int64_t>(seg_row0 + key0 + key) * kstride + kvh * kMfmaD + 4 * d4;
+    *reinterpret_cast<bf16x4*>(dst) = o;
   }
 }
 
@@ -600,9 +751,13 @@ int launch_mfma_delta(const KernelArgs& a, hipStream_t s) {
   return hipGetLastError() == hipSuccess ? 0 : 4;
 }
 
-int launch_mfma_bwd(const KernelArgs& a, int n_fwd, int n_dkdv, hipStream_t s) {
+int launch_mfma_bwd(const KernelArgs& a, int n_fwd, int n_dkdv, int n_red, hipStream_t s) {
   if (n_dkdv > 0) {
     hipLaunchKernelGGL(mfma_dkdv, dim3(n_dkdv), dim3(256), 0, s, a);
+    if (hipGetLastError() != hipSuccess) return 4;
+  }
+  if (n_red > 0) {
+    hipLaunchKernelGGL(mfma_reduce, dim3(n_red), dim3(256), 0, s, a);
     if (hipGetLastError() != hipSuccess) return 4;
   }
   if (n_fwd > 0) {

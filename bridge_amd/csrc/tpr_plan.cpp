@@ -140,7 +140,7 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
                   "descendant leaves of node %d are not contiguous; number leaves in DFS order", n);
   }
 
-  const int path = (t->dtype == TPR_DTYPE_BF16 && D == kMfmaD) ? PATH_MFMA : PATH_SIMT;
+  const int path = (t->dtype == TPR_DTYPE_BF16 && D == kMfmaD && depth <= kMfmaMaxDepth) ? PATH_MFMA : PATH_SIMT;
   const int G = Hq / Hkv;
   std::vector<int64_t> prefix_len(N, 0);
   for (int s = 0; s < N; s++)
@@ -189,32 +189,58 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
   std::vector<int32_t> fwd_words = order_for_xcds(fwd, Hkv, 4, &n_fwd);
 
   // ---- dK/dV items ---------------------------------------------------------
+  // One item per (KV segment tile, KV head). On the MFMA path an item streams
+  // at most kDkdvMaxBlocks query blocks (its block table lives in LDS); a
+  // prefix tile whose query range is longer than kDkdvPrefixChunk blocks --
+  // the tile every sibling reads -- is split into chunks that each write an
+  // fp32 partial, summed afterwards in chunk (= leaf) order by a reduction
+  // item. The split also balances the dK/dV launch: an unsplit prefix tile
+  // carries N siblings' work.
   const int KT = path == PATH_MFMA ? kDkdvKeys : kSimtKeys;
   std::vector<Item> dkdv;
+  std::vector<int32_t> red;
+  int32_t n_slots = 0, max_split = 1;
+  auto add_tile = [&](int src, int seg, int k0, int h, int32_t lo, int32_t hi) {
+    const int32_t range = hi - lo;
+    int chunk = range;
+    if (path == PATH_MFMA) {
+      const int cap = src == 0 ? kDkdvPrefixChunk : kDkdvMaxBlocks;
+      if (range > cap) {
+        const int pieces = (range + cap - 1) / cap;
+        chunk = (range + pieces - 1) / pieces;
+      }
+    }
+    if (chunk >= range || range == 0) {
+      Item it;
+      it.words = {src, seg, k0, h, lo, hi, -1, 0};
+      it.work = static_cast<int64_t>(range) * G + 1;
+      it.kvh = h;
+      dkdv.push_back(std::move(it));
+      return;
+    }
+    const int32_t slot0 = n_slots;
+    int pieces = 0;
+    for (int32_t b = lo; b < hi; b += chunk, pieces++) {
+      Item it;
+      it.words = {src, seg, k0, h, b, std::min(hi, b + chunk), n_slots++, 0};
+      it.work = static_cast<int64_t>(std::min(hi, b + chunk) - b) * G + 1;
+      it.kvh = h;
+      dkdv.push_back(std::move(it));
+    }
+    red.insert(red.end(), {src, seg, k0, h, slot0, pieces, 0, 0});
+    max_split = std::max(max_split, pieces);
+  };
   for (int n = 0; n < M; n++) {
     const int len = no[n + 1] - no[n];
     // a node no leaf descends from gets an empty query range: its items write zeros
     const int32_t lo = leaf_qblk[leaf_lo[n]], hi = leaf_qblk[leaf_hi[n]];
-    const int64_t queries = cu[leaf_hi[n]] - cu[leaf_lo[n]];
     for (int k0 = 0; k0 < len; k0 += KT)
-      for (int h = 0; h < Hkv; h++) {
-        Item it;
-        it.words = {0, n, k0, h, lo, hi, -1, 0};
-        it.work = queries * G + 1;
-        it.kvh = h;
-        dkdv.push_back(std::move(it));
-      }
+      for (int h = 0; h < Hkv; h++) add_tile(0, n, k0, h, lo, hi);
   }
   for (int s = 0; s < N; s++) {
     const int len = cu[s + 1] - cu[s];
     for (int k0 = 0; k0 < len; k0 += KT)
-      for (int h = 0; h < Hkv; h++) {
-        Item it;
-        it.words = {1, s, k0, h, leaf_qblk[s] + k0 / BQ, leaf_qblk[s + 1], -1, 0};
-        it.work = static_cast<int64_t>(len - k0) * G;
-        it.kvh = h;
-        dkdv.push_back(std::move(it));
-      }
+      for (int h = 0; h < Hkv; h++) add_tile(1, s, k0, h, leaf_qblk[s] + k0 / BQ, leaf_qblk[s + 1]);
   }
   int32_t n_dkdv = 0;
   std::vector<int32_t> dkdv_words = order_for_xcds(dkdv, Hkv, DK_WORDS, &n_dkdv);
@@ -251,10 +277,10 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
   plan[PF_OFF_FWD] = append(fwd_words.data(), fwd_words.size());
   plan[PF_N_DKDV] = n_dkdv;
   plan[PF_OFF_DKDV] = append(dkdv_words.data(), dkdv_words.size());
-  plan[PF_N_RED] = 0;
-  plan[PF_OFF_RED] = static_cast<int32_t>(plan.size());
-  plan[PF_N_SLOTS] = 0;
-  plan[PF_SPLIT] = 1;
+  plan[PF_N_RED] = static_cast<int32_t>(red.size() / RD_WORDS);
+  plan[PF_OFF_RED] = append(red.data(), red.size());
+  plan[PF_N_SLOTS] = n_slots;
+  plan[PF_MAX_SPLIT] = max_split;
   plan[PF_TOTAL_WORDS] = static_cast<int32_t>(plan.size());
   return TPR_OK;
 }

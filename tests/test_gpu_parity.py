@@ -149,3 +149,28 @@ def test_rectangular_shim_matches_reference_oracle(cuda_device):
     assert max_abs(out, ref) <= BF16_FWD_MAX_ABS and cosine(out, ref) >= BF16_FWD_COS
     for mine, theirs in ((qd.grad, qc.grad), (kd.grad, kc.grad), (vd.grad, vc.grad)):
         assert cosine(mine, theirs) >= BF16_GRAD_COS
+
+
+@pytest.mark.parametrize("name,prefix,suffixes,hq,hkv", [
+    ("split_prefix_tiles", 300, [4100, 4100, 100, 4200], 8, 2),
+    ("split_suffix_tile", 64, [8300], 4, 1),
+])
+def test_mfma_split_tiles_match_oracle(name, prefix, suffixes, hq, hkv, cuda_device):
+    """dK/dV tiles whose query range is split into fp32 partials + ordered reduction."""
+    from bridge_amd import TPRPrefixMeta
+    meta = TPRPrefixMeta.shared_prefix(prefix, suffixes)
+    d = 128
+    scale = 1.0 / math.sqrt(d)
+    plan = meta.plan(hq, hkv, d, torch.bfloat16, cuda_device)
+    assert plan.path == "mfma" and plan.workspace_bytes > 0
+    q, k, v, pk, pv, dout = make_inputs(meta, hq, hkv, d, torch.bfloat16, seed=5, device=cuda_device)
+    out, lse, grads = _run(meta, q, k, v, pk, pv, dout, scale)
+    # larger shapes: the oracle runs in fp32 on the GPU
+    ref = oracle(meta, q, k, v, pk, pv, dout, scale, compute_dtype=torch.float32, device=cuda_device)
+    _report(name, out, lse, grads, ref)
+    ro, rl, rg = ref
+    assert max_abs(out, ro) <= BF16_FWD_MAX_ABS and cosine(out, ro) >= BF16_FWD_COS
+    for g, r in zip(grads, rg):
+        assert cosine(g, r) >= BF16_GRAD_COS
+    for g, r in zip(grads[3:], rg[3:]):
+        assert rel_l2(g, r) <= BF16_PREFIX_GRAD_REL_L2

@@ -53,7 +53,8 @@ def test_xcd_ordering_pins_kv_heads_and_is_lpt_per_xcd():
     meta = TPRPrefixMeta.shared_prefix(4096, [4096] * 4)
     plan = meta.plan(32, 8, 128, torch.bfloat16, CPU)
     _, fwd, dkdv, _ = decode(plan)
-    assert len(fwd) == 4 * 128 * 8 and len(dkdv) == (32 + 4 * 32) * 8
+    # prefix tiles (4 siblings x 64 query blocks each) split into 4 chunks of 64 blocks
+    assert len(fwd) == 4 * 128 * 8 and len(dkdv) == (32 * 4 + 4 * 32) * 8
     for i, (leaf, tok0, qh0, kvh) in enumerate(fwd):
         assert leaf >= 0 and kvh == i % 8
     for i, item in enumerate(dkdv):
@@ -94,6 +95,38 @@ def test_dkdv_items_cover_every_key_tile_and_query_block():
         for k0 in range(0, length, 128):
             for h in range(2):
                 assert seen[(1, s, k0, h)] == 1
+
+
+def test_split_prefix_tiles_have_ordered_partials_and_reductions():
+    meta = TPRPrefixMeta.shared_prefix(300, [4096, 4096, 100, 4096])
+    plan = meta.plan(8, 2, 128, torch.bfloat16, CPU)
+    w, _, dkdv, qblk = decode(plan)
+    reds = [tuple(w[w[24] + 8 * i: w[24] + 8 * i + 8]) for i in range(w[PF["N_RED"]])]
+    n_slots = w[25]
+    assert n_slots > 0 and plan.workspace_bytes == n_slots * 2 * 128 * 128 * 4
+    by_slot = {item[6]: item for item in dkdv if item[0] >= 0 and item[6] >= 0}
+    assert sorted(by_slot) == list(range(n_slots))
+    for src, seg, key0, kvh, slot0, nslots, _, _ in reds:
+        parts = [by_slot[slot0 + j] for j in range(nslots)]
+        assert all(p[:4] == (src, seg, key0, kvh) for p in parts)
+        # chunks tile the query range contiguously, in order
+        for a, b in zip(parts, parts[1:]):
+            assert a[5] == b[4]
+        assert all(p[5] - p[4] <= (64 if src == 0 else 128) for p in parts)
+    # every direct item streams at most 128 query blocks (its LDS table)
+    assert all(item[5] - item[4] <= 128 for item in dkdv if item[0] >= 0)
+    # each (tile, head) is either direct or reduced, never both
+    direct = {item[:4] for item in dkdv if item[0] >= 0 and item[6] < 0}
+    reduced = {r[:4] for r in reds}
+    assert not direct & reduced
+
+
+def test_deep_trees_use_the_simt_path():
+    depth = 9
+    meta = TPRPrefixMeta(cu_seqlens_q=(0, 5), node_offsets=tuple(range(0, 4 * depth + 1, 4)),
+                         leaf_ancestors=(tuple(range(depth)),))
+    assert meta.plan(4, 2, 128, torch.bfloat16, CPU).path == "simt"
+    assert meta.plan(4, 2, 128, torch.bfloat16, CPU).workspace_bytes == 0
 
 
 def test_simt_path_for_fp32_and_small_head_dim():
