@@ -113,6 +113,9 @@ def main() -> int:
     ap.add_argument("--workload", default="qwen3-4b",
                     choices=["qwen3-4b", "plumbing-fp32", "long-session", "ragged", "turn-tree"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="before the timed steps, run one plain device copy of MIB MiB (read MIB, write MIB): "
+                         "the calibration dispatch for rocprofv3 FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -164,6 +167,13 @@ def main() -> int:
                                   phases=_lib.TPR_BWD_DQ, buffers=buffers)
         if events:
             events[4].record(stream)
+
+    if args.copy_probe:
+        src = torch.ones(args.copy_probe * (1 << 20) // 2, dtype=torch.bfloat16, device=device)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     for _ in range(args.warmup):
         step()
