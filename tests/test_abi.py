@@ -1,0 +1,108 @@
+"""CPU checks of the C ABI: libtpr_attn.so loads, exports every function
+include/tpr_attn.h declares, the ctypes mirrors match the C struct layouts,
+and argument errors come back as status codes with messages (host code only,
+no GPU work is launched)."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+from bridge_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "tpr_attn.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(tpr_attn_\w+)\s*\(", text, re.M)))
+
+
+def test_library_loads_and_reports_abi_version():
+    lib = _lib.load()
+    assert lib.tpr_attn_abi_version() == _lib.ABI_VERSION == 1
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    declared = _declared_functions()
+    assert declared == sorted(_lib.EXPORTED_SYMBOLS)
+    lib = ctypes.CDLL(_lib.library_path())
+    for name in declared:
+        assert hasattr(lib, name), name
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="needs gcc")
+def test_ctypes_structs_match_c_layout(tmp_path):
+    structs = {"TprTreeDesc": _lib.TprTreeDesc, "TprFwdParams": _lib.TprFwdParams,
+               "TprBwdParams": _lib.TprBwdParams}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
+    for sname, cls in structs.items():
+        lines.append(f'  printf("{sname} size %zu\\n", sizeof({sname}));')
+        for fname, _ in cls._fields_:
+            lines.append(f'  printf("{sname}.{fname} %zu\\n", offsetof({sname}, {fname}));')
+    lines.append("  return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-Wall", "-o", str(exe), str(src)], check=True)
+    got = dict(line.rsplit(" ", 1) for line in subprocess.run([str(exe)], check=True, stdout=subprocess.PIPE,
+                                                                 text=True).stdout.splitlines())
+    for sname, cls in structs.items():
+        assert int(got[f"{sname} size"]) == ctypes.sizeof(cls), sname
+        for fname, _ in cls._fields_:
+            assert int(got[f"{sname}.{fname}"]) == getattr(cls, fname).offset, f"{sname}.{fname}"
+
+
+def test_null_params_and_bad_version_fail_with_messages():
+    lib = _lib.load()
+    assert lib.tpr_attn_fwd(None, None) == _lib.TPR_ERR_INVALID_ARGUMENT
+    assert b"must not be NULL" in lib.tpr_attn_last_error()
+    p = _lib.TprFwdParams()
+    p.abi_version = 99
+    assert lib.tpr_attn_fwd(ctypes.byref(p), None) == _lib.TPR_ERR_INVALID_ARGUMENT
+    assert b"abi_version" in lib.tpr_attn_last_error()
+    b = _lib.TprBwdParams()
+    b.abi_version = _lib.ABI_VERSION
+    assert lib.tpr_attn_bwd(ctypes.byref(b), None) == _lib.TPR_ERR_INVALID_ARGUMENT
+    assert b"plan" in lib.tpr_attn_last_error()
+    assert lib.tpr_attn_bwd_phases(ctypes.byref(b), 8, None) == _lib.TPR_ERR_INVALID_ARGUMENT
+    assert b"phases" in lib.tpr_attn_last_error()
+
+
+def test_bad_scale_is_rejected_before_any_launch():
+    import torch
+
+    from bridge_amd import TPRPrefixMeta
+    lib = _lib.load()
+    plan = TPRPrefixMeta.shared_prefix(8, [4]).plan(4, 2, 128, torch.bfloat16, torch.device("cpu"))
+    for scale in (0.0, -1.0, float("inf"), float("nan")):
+        p = _lib.TprFwdParams(_lib.ABI_VERSION, 0, scale, 0.0, plan.host.data_ptr(), plan.host.data_ptr())
+        assert lib.tpr_attn_fwd(ctypes.byref(p), None) == _lib.TPR_ERR_INVALID_ARGUMENT
+        assert b"softmax_scale" in lib.tpr_attn_last_error()
+
+
+def test_missing_tensor_pointer_is_rejected():
+    import torch
+
+    from bridge_amd import TPRPrefixMeta
+    lib = _lib.load()
+    plan = TPRPrefixMeta.shared_prefix(8, [4]).plan(4, 2, 128, torch.bfloat16, torch.device("cpu"))
+    p = _lib.TprFwdParams(_lib.ABI_VERSION, 0, 0.1, 0.0, plan.host.data_ptr(), plan.host.data_ptr())
+    assert lib.tpr_attn_fwd(ctypes.byref(p), None) == _lib.TPR_ERR_INVALID_ARGUMENT
+    assert b"q must not be NULL" in lib.tpr_attn_last_error()
+
+
+def test_plan_capacity_and_workspace_queries():
+    import torch
+
+    from bridge_amd import TPRPrefixMeta
+    plan = TPRPrefixMeta.shared_prefix(4096, [4096] * 4).plan(32, 8, 128, torch.bfloat16, torch.device("cpu"))
+    lib = _lib.load()
+    assert lib.tpr_attn_bwd_workspace_bytes(ctypes.c_void_p(plan.host.data_ptr())) == plan.workspace_bytes > 0
+    assert lib.tpr_attn_bwd_workspace_bytes(None) == 0
