@@ -25,6 +25,8 @@
 // operand straight from registers, and V is read column-wise from its
 // row-major LDS tile with ds_read_tr16_b64.
 
+#include <type_traits>
+
 #include "tpr_device.h"
 
 namespace tpr {
@@ -111,22 +113,23 @@ __device__ __forceinline__ SegTable load_segments(const KernelArgs& a, int leaf,
   return t;
 }
 
+// Branch-free: at most one segment contains tile `idx`; the suffix is the default.
 __device__ __forceinline__ TileLoc locate_tile(const SegTable& t, int idx) {
-  const int prefix_tiles = t.end[kMfmaMaxDepth - 1];
-  int lt = idx - prefix_tiles;
-  TileLoc r{static_cast<int64_t>(t.suffix_row) + lt * kTileRows, min(kTileRows, t.suffix_keys - lt * kTileRows),
-            lt * kTileRows, true};
+  int seg_row = t.suffix_row, seg_len = t.suffix_keys, first = t.end[kMfmaMaxDepth - 1];
+  bool suffix = true;
   int start = 0;
 #pragma unroll
   for (int d = 0; d < kMfmaMaxDepth; d++) {
-    if (idx >= start && idx < t.end[d]) {
-      lt = idx - start;
-      r = TileLoc{static_cast<int64_t>(t.row[d]) + lt * kTileRows, min(kTileRows, t.len[d] - lt * kTileRows),
-                  lt * kTileRows, false};
-    }
+    const bool in = (idx >= start) & (idx < t.end[d]);
+    seg_row = in ? t.row[d] : seg_row;
+    seg_len = in ? t.len[d] : seg_len;
+    first = in ? start : first;
+    suffix = in ? false : suffix;
     start = t.end[d];
   }
-  return r;
+  const int lt = idx - first;
+  return TileLoc{static_cast<int64_t>(seg_row) + lt * kTileRows, min(kTileRows, seg_len - lt * kTileRows),
+                 lt * kTileRows, suffix};
 }
 
 // Direct global -> LDS copy (gfx950 global_load_lds_dwordx4) of the 64 rows
@@ -176,6 +179,115 @@ __device__ __forceinline__ void dma_tile(const bf16* base, int64_t stride, int64
   }
 }
 
+// Same copy with a uniform 64-bit source base (SGPRs) and a per-lane 32-bit
+// byte offset: no per-copy 64-bit address arithmetic in the tile loop.
+__device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, uint32_t lds_dst) {
+  // readfirstlane returns a signed int: go through uint32_t, or the low word
+  // would be sign-extended into the high word of the address.
+  const uint64_t b = reinterpret_cast<uint64_t>(sbase);
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(b >> 32)));
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(b & 0xffffffffu)));
+  const uint64_t bs = (static_cast<uint64_t>(hi) << 32) | static_cast<uint64_t>(lo);
+  sbase = reinterpret_cast<const void*>(bs);
+  lds_dst = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(lds_dst)));
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %2\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(sbase), "s"(lds_dst));
+}
+
+// Per-lane part of a 64-row tile copy: which row / chunk this lane moves in
+// each of its 16 / kWaves DMA blocks, and the resulting byte offset for a
+// full tile (row stride `row_bytes`).
+template <int kWaves>
+struct DmaLanes {
+  static constexpr int kBlocks = 16 / kWaves;
+  uint32_t voff[kBlocks];
+  int row[kBlocks];
+  uint32_t cbytes[kBlocks];
+};
+
+template <int kWaves>
+__device__ __forceinline__ DmaLanes<kWaves> make_dma_lanes(uint32_t row_bytes, int wave, int lane) {
+  DmaLanes<kWaves> p;
+#pragma unroll
+  for (int j = 0; j < DmaLanes<kWaves>::kBlocks; j++) {
+    const int row = 4 * (wave * DmaLanes<kWaves>::kBlocks + j) + (lane >> 4);
+    p.row[j] = row;
+    p.cbytes[j] = static_cast<uint32_t>(swz_chunk(row, lane & 15)) * 16u;
+    p.voff[j] = static_cast<uint32_t>(row) * row_bytes + p.cbytes[j];
+  }
+  return p;
+}
+
+// Copy rows [0, 64) of the tile starting at `src` (uniform; rows at or beyond
+// `len` re-read row len - 1) into the swizzled LDS tile at `lds_tile`.
+template <int kWaves>
+__device__ __forceinline__ void dma_tile_s(const char* src, uint32_t row_bytes, int len, uint32_t lds_tile,
+                                           const DmaLanes<kWaves>& p, int wave) {
+  constexpr int kBlocks = DmaLanes<kWaves>::kBlocks;
+  if (len >= kTileRows) {
+#pragma unroll
+    for (int j = 0; j < kBlocks; j++) dma16s(src, p.voff[j], lds_tile + (wave * kBlocks + j) * 1024);
+  } else {
+#pragma unroll
+    for (int j = 0; j < kBlocks; j++)
+      dma16s(src, static_cast<uint32_t>(min(p.row[j], len - 1)) * row_bytes + p.cbytes[j],
+             lds_tile + (wave * kBlocks + j) * 1024);
+  }
+}
+
+// Forward-only cursor over a workgroup's key stream (SegTable order). It
+// only changes segment at segment ends, so the common step is a compare.
+struct Cursor {
+  int d;     // segment: 0..kMfmaMaxDepth-1 = ancestor node, kMfmaMaxDepth = suffix
+  int lt;    // tile within the segment
+  int row;   // first row of the segment
+  int len;   // rows of the segment
+};
+
+__device__ __forceinline__ void cursor_load(const SegTable& t, Cursor& c) {
+  int row = t.suffix_row, len = t.suffix_keys;
+#pragma unroll
+  for (int e = 0; e < kMfmaMaxDepth; e++) {
+    row = c.d == e ? t.row[e] : row;
+    len = c.d == e ? t.len[e] : len;
+  }
+  c.row = row;
+  c.len = len;
+}
+
+__device__ __forceinline__ Cursor cursor_begin(const SegTable& t) {
+  Cursor c{0, 0, 0, 0};
+  cursor_load(t, c);
+  while (c.len == 0 && c.d < kMfmaMaxDepth) {
+    c.d++;
+    cursor_load(t, c);
+  }
+  return c;
+}
+
+__device__ __forceinline__ void cursor_next(const SegTable& t, Cursor& c) {
+  c.lt++;
+  if (c.lt * kTileRows >= c.len) {
+    c.lt = 0;
+    do {
+      c.d++;
+      cursor_load(t, c);
+    } while (c.len == 0 && c.d < kMfmaMaxDepth);
+  }
+}
+
+__device__ __forceinline__ TileLoc cursor_tile(const Cursor& c) {
+  return TileLoc{static_cast<int64_t>(c.row) + c.lt * kTileRows, min(kTileRows, c.len - c.lt * kTileRows),
+                 c.lt * kTileRows, c.d >= kMfmaMaxDepth};
+}
+
 // Wait until this wave's outstanding global->LDS copies have landed.
 // Ordered before the __syncthreads() that follows it (both have side effects);
 // the barrier is what orders the LDS reads of the copied tile.
@@ -193,7 +305,29 @@ __device__ __forceinline__ void settle(const T& x) {
 
 // ---------------------------------------------------------------------------
 // Forward
+//
+// Software-pipelined over 64-key tiles: iteration `it` computes the scores
+// of tile it+1 (S = K Q^T, MFMA) while it runs the softmax of tile it (VALU)
+// -- the two are independent, so the MFMA pipe and the VALU overlap -- and
+// then accumulates P V of tile it. K runs one tile ahead of V: the DMA of
+// iteration it fetches K of tile it+2 and V of tile it+1, so two K and two V
+// buffers (64 KiB) suffice and two workgroups fit on a CU.
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ void qk_tile(const char* kt, const bf16x8 (&qv)[8], int n, int h, f32x16 (&s)[2]) {
+#pragma unroll
+  for (int kb = 0; kb < 2; kb++) {
+    s[kb] = f32x16{};
+    const int krow = kb * 32 + sigma32(n);
+#pragma unroll
+    for (int c = 0; c < 8; c++) s[kb] = mfma(lds_read_b128(kt, krow, 16 * c + 8 * h), qv[c], s[kb]);
+  }
+}
+
+// Running-max slack of the lazy rescale, in log2 units: O, l are rescaled only
+// when a row's max exceeds the max they are referenced to by more than this,
+// so unscaled probabilities stay <= 2^8 (exact arithmetic, fp32/bf16 safe).
+constexpr float kRescaleSlack = 8.f;
+
 __global__ __launch_bounds__(256, 2) void mfma_fwd(KernelArgs a) {
   const int32_t* item = a.plan + a.off_fwd + 4 * blockIdx.x;
   const int leaf = item[0];
@@ -202,7 +336,7 @@ __global__ __launch_bounds__(256, 2) void mfma_fwd(KernelArgs a) {
   const int32_t* cu = a.plan + a.off_cu;
   const int row0 = cu[leaf], len = cu[leaf + 1] - cu[leaf];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int hpw = a.hpw;                             // query heads per workgroup
   const int head = qh0 + wave % hpw;
   const int tw0 = tok0 + kFwdTokens * (wave / hpw);  // first token of this wave
@@ -210,24 +344,37 @@ __global__ __launch_bounds__(256, 2) void mfma_fwd(KernelArgs a) {
   const int suffix_keys = min(len, tok0 + tpw);
   const int n = lane & 31, h = lane >> 5;
   const int t = tw0 + n;                             // this lane's query token
-  const bool wave_active = tw0 < len;
 
   const int64_t qstride = static_cast<int64_t>(a.hq) * kMfmaD;
-  const int64_t kstride = static_cast<int64_t>(a.hkv) * kMfmaD;
+  const uint32_t row_bytes = static_cast<uint32_t>(a.hkv) * kMfmaD * 2;
 
-  __shared__ __attribute__((aligned(1024))) char smem[4 * kTileBytes];  // K0 V0 K1 V1
+  __shared__ __attribute__((aligned(1024))) char smem[4 * kTileBytes];  // K0 K1 V0 V1
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(smem));
 
-  const bf16* kbase = static_cast<const bf16*>(a.k) + kvh * kMfmaD;
-  const bf16* vbase = static_cast<const bf16*>(a.v) + kvh * kMfmaD;
-  const bf16* pkbase = static_cast<const bf16*>(a.pk) + kvh * kMfmaD;
-  const bf16* pvbase = static_cast<const bf16*>(a.pv) + kvh * kMfmaD;
+  const char* kbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.k) + kvh * kMfmaD);
+  const char* vbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.v) + kvh * kMfmaD);
+  const char* pkbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.pk) + kvh * kMfmaD);
+  const char* pvbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.pv) + kvh * kMfmaD);
+  const DmaLanes<kFwdWaves> dl = make_dma_lanes<kFwdWaves>(row_bytes, wave, lane);
 
   const SegTable seg = load_segments(a, leaf, suffix_keys);
   const int ntiles = seg.ntiles;
-  {
-    const TileLoc tl = locate_tile(seg, 0);
-    dma_tile<kFwdWaves>(tl.suffix ? kbase : pkbase, kstride, tl.row, tl.len, smem, wave, lane);
-    dma_tile<kFwdWaves>(tl.suffix ? vbase : pvbase, kstride, tl.row, tl.len, smem + kTileBytes, wave, lane);
+  Cursor cur = cursor_begin(seg);
+  TileLoc tl_cur = cursor_tile(cur), tl_v = tl_cur, tl_k = tl_cur;
+  auto kv_src = [&](const TileLoc& x, bool is_k) {
+    const char* b = x.suffix ? (is_k ? kbase : vbase) : (is_k ? pkbase : pvbase);
+    return b + x.row * static_cast<int64_t>(row_bytes);
+  };
+  dma_tile_s<kFwdWaves>(kv_src(tl_cur, true), row_bytes, tl_cur.len, lds0, dl, wave);
+  dma_tile_s<kFwdWaves>(kv_src(tl_cur, false), row_bytes, tl_cur.len, lds0 + 2 * kTileBytes, dl, wave);
+  if (ntiles > 1) {
+    cursor_next(seg, cur);
+    tl_v = cursor_tile(cur);
+    dma_tile_s<kFwdWaves>(kv_src(tl_v, true), row_bytes, tl_v.len, lds0 + kTileBytes, dl, wave);
+  }
+  if (ntiles > 2) {
+    cursor_next(seg, cur);
+    tl_k = cursor_tile(cur);
   }
 
   // Q as the B operand of S^T = K Q^T: lane holds Q[t][16c + 8h .. +7]
@@ -242,84 +389,98 @@ __global__ __launch_bounds__(256, 2) void mfma_fwd(KernelArgs a) {
   f32x16 o[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) o[i] = f32x16{};
-  float m = -1e30f, l = 0.f;
+  float m = -1e30f, l = 0.f;  // running max (raw score units) the O/l are referenced to
   const float c2 = a.scale * kLog2e;
+  const float slack = kRescaleSlack / c2;
 
 #pragma unroll
   for (int c = 0; c < 8; c++) settle(qv[c]);
   wait_dma();
   __syncthreads();
+  f32x16 sa[2], sb[2];
+  qk_tile(smem, qv, n, h, sa);
+  __syncthreads();  // every wave has read K0 before iteration 0 refills its buffer
 
-  for (int it = 0; it < ntiles; it++) {
-    const char* kt = smem + (it & 1) * 2 * kTileBytes;
-    const char* vt = kt + kTileBytes;
-    const TileLoc tl = locate_tile(seg, it);
-    if (it + 1 < ntiles) {
-      const TileLoc nx = locate_tile(seg, it + 1);
-      char* nk = smem + ((it + 1) & 1) * 2 * kTileBytes;
-      dma_tile<kFwdWaves>(nx.suffix ? kbase : pkbase, kstride, nx.row, nx.len, nk, wave, lane);
-      dma_tile<kFwdWaves>(nx.suffix ? vbase : pvbase, kstride, nx.row, nx.len, nk + kTileBytes, wave, lane);
+  // One pipeline step for tile `it` (parity P = it & 1): copies K[it+2] into
+  // K buffer P and V[it+1] into V buffer 1-P, computes S[it+1] from K buffer
+  // 1-P into `sn`, and runs softmax(S[it]) + P V[it] from V buffer P.
+  auto step = [&](auto par, int it, f32x16 (&s)[2], f32x16 (&sn)[2]) {
+    constexpr int P = decltype(par)::value;
+    if (it + 2 < ntiles)
+      dma_tile_s<kFwdWaves>(kv_src(tl_k, true), row_bytes, tl_k.len, lds0 + P * kTileBytes, dl, wave);
+    if (it + 1 < ntiles)
+      dma_tile_s<kFwdWaves>(kv_src(tl_v, false), row_bytes, tl_v.len, lds0 + (3 - P) * kTileBytes, dl, wave);
+    // visibility of tile it: key kb*32 + 16*(r/8) + 8*h + r%8 <= lim. A tile
+    // entirely in this wave's future gets lim < 0 (nothing visible).
+    if (tl_cur.len < kTileRows || (tl_cur.suffix && tl_cur.pos0 + kTileRows - 1 > tw0)) {
+      int lim = tl_cur.len - 1 - 8 * h;
+      if (tl_cur.suffix) lim = min(lim, t - tl_cur.pos0 - 8 * h);
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) s[kb][r] = (kb * 32 + 16 * (r >> 3) + (r & 7) <= lim) ? s[kb][r] : -INFINITY;
     }
-    // a wave skips tiles whose keys are all in its future
-    const bool skip = !wave_active || (tl.suffix && tl.pos0 > tw0 + kFwdTokens - 1);
-    if (!skip) {
-      f32x16 s[2];
+    // scores of tile it+1 (the last step recomputes a resident tile; unused)
+    qk_tile(smem + (1 - P) * kTileBytes, qv, n, h, sn);
+
+    // softmax of tile it (independent of the MFMAs above)
+    float mt = s[0][0];
 #pragma unroll
-      for (int kb = 0; kb < 2; kb++) {
-        s[kb] = f32x16{};
-        const int krow = kb * 32 + sigma32(n);
+    for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-        for (int c = 0; c < 8; c++) s[kb] = mfma(lds_read_b128(kt, krow, 16 * c + 8 * h), qv[c], s[kb]);
-      }
-      if (tl.len < kTileRows || (tl.suffix && tl.pos0 + kTileRows - 1 > tw0)) {
-        // register r of key block kb holds tile key kb*32 + 16*(r/8) + 8*h + r%8
-        int lim = tl.len - 1 - 8 * h;
-        if (tl.suffix) lim = min(lim, t - tl.pos0 - 8 * h);
+      for (int r = 0; r < 16; r++) mt = fmaxf(mt, s[kb][r]);
+    mt = wave_max32(mt);
+    if (__any(mt > m + slack)) {  // some row outgrew its reference max: rescale
+      const float m_new = fmaxf(m, mt);
+      const float alpha = fast_exp2((m - m_new) * c2);
+      m = m_new;
+      l *= alpha;
 #pragma unroll
-        for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-          for (int r = 0; r < 16; r++) s[kb][r] = (kb * 32 + 16 * (r >> 3) + (r & 7) <= lim) ? s[kb][r] : -INFINITY;
-      }
-      float mt = s[0][0];
-#pragma unroll
-      for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) mt = fmaxf(mt, s[kb][r]);
-      const float m_new = fmaxf(m, wave_max32(mt));
-      if (__any(m_new > m)) {  // rescale only when some row's running max grew
-        const float alpha = fast_exp2((m - m_new) * c2);
-        m = m_new;
-        l *= alpha;
-#pragma unroll
-        for (int db = 0; db < 4; db++) o[db] *= alpha;
-      }
-      const float mc = m * c2;
-      float ls = 0.f;
-#pragma unroll
-      for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-          const float p = fast_exp2(fmaf(s[kb][r], c2, -mc));
-          s[kb][r] = p;
-          ls += p;
-        }
-      l += ls;
-#pragma unroll
-      for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-        for (int cc = 0; cc < 2; cc++) {
-          const bf16x8 pb = to_bf16x8(s[kb], 8 * cc);
-          const int r0 = kb * 32 + 16 * cc + 8 * h;
-#pragma unroll
-          for (int db = 0; db < 4; db++) o[db] = mfma(lds_read_col8(vt, r0, 32 * db, lane), pb, o[db]);
-        }
+      for (int db = 0; db < 4; db++) o[db] *= alpha;
     }
+    const float mc = m * c2;
+    bf16x8 pb[2][2];
+    float ls = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+      for (int cc = 0; cc < 2; cc++) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          const float p = fast_exp2(fmaf(s[kb][8 * cc + i], c2, -mc));
+          ls += p;  // fp32 row sum of the unrounded probabilities
+          pb[kb][cc][i] = static_cast<bf16>(p);
+        }
+      }
+    l += ls;
+    const char* vt = smem + (2 + P) * kTileBytes;
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+      for (int cc = 0; cc < 2; cc++) {
+        const int r0 = kb * 32 + 16 * cc + 8 * h;
+#pragma unroll
+        for (int db = 0; db < 4; db++) o[db] = mfma(lds_read_col8(vt, r0, 32 * db, lane), pb[kb][cc], o[db]);
+      }
     wait_dma();
     __syncthreads();
+    tl_cur = tl_v;
+    tl_v = tl_k;
+    if (it + 3 < ntiles) {
+      cursor_next(seg, cur);
+      tl_k = cursor_tile(cur);
+    }
+  };
+
+  int it = 0;
+  for (; it + 1 < ntiles; it += 2) {
+    step(std::integral_constant<int, 0>{}, it, sa, sb);
+    step(std::integral_constant<int, 1>{}, it + 1, sb, sa);
   }
+  if (it < ntiles) step(std::integral_constant<int, 0>{}, it, sa, sb);
 
   const float lt = wave_sum32(l);  // all 64 lanes take part in the exchange
-  if (!wave_active || t >= len) return;
+  if (tw0 >= len || t >= len) return;
   const float inv = 1.f / lt;
   bf16* op = static_cast<bf16*>(a.out) + static_cast<int64_t>(row0 + t) * qstride + head * kMfmaD;
 #pragma unroll
@@ -369,7 +530,7 @@ __global__ __launch_bounds__(256, 2) void mfma_dq(KernelArgs a) {
   const int32_t* cu = a.plan + a.off_cu;
   const int row0 = cu[leaf], len = cu[leaf + 1] - cu[leaf];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int hpw = a.hpw;
   const int head = qh0 + wave % hpw;
   const int tw0 = tok0 + kFwdTokens * (wave / hpw);
@@ -512,7 +673,7 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
   const int seg_row0 = prefix ? no[seg] : cu[seg];
   const int seg_len = prefix ? no[seg + 1] - no[seg] : cu[seg + 1] - cu[seg];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 31, h = lane >> 5;
   const int kw0 = key0 + 32 * wave;          // first key position of this wave
   const int kp = kw0 + n;                     // this lane's key position (B-operand column)
