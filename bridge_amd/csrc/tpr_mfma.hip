@@ -708,6 +708,17 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
     tok0 = e.y;
     nq = e.z;
   };
+  const uint32_t qrow_bytes = static_cast<uint32_t>(a.hq) * kMfmaD * 2;
+  const DmaLanes<kDkdvWaves> dl = make_dma_lanes<kDkdvWaves>(qrow_bytes, wave, lane);
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(smem));
+  // copy the Q and dO rows [row, row + 64) of query head qh into the stage buffer at `tile`
+  auto issue_stage = [&](int row, int nq, int qh, const char* tile) {
+    const int64_t off = static_cast<int64_t>(qh) * kMfmaD * 2 + static_cast<int64_t>(row) * qrow_bytes;
+    const uint32_t dst = lds0 + static_cast<uint32_t>(tile - smem);
+    dma_tile_s<kDkdvWaves>(reinterpret_cast<const char*>(qbase) + off, qrow_bytes, nq, dst, dl, wave);
+    dma_tile_s<kDkdvWaves>(reinterpret_cast<const char*>(gbase) + off, qrow_bytes, nq, dst + kTileBytes, dl, wave);
+  };
+
   // lse and delta of one query block: thread r < 64 fetches lse row r, thread
   // 64 + r delta row r. The raw value is fetched into a register before the
   // tile copies are issued and only converted and stored to LDS after the
@@ -737,8 +748,7 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
     int row0, tok0, nq, qh;
     stage_info(0, row0, tok0, nq, qh);
     const Stat x = fetch_stat(row0, tok0, nq, qh);
-    dma_tile<kDkdvWaves>(qbase + qh * kMfmaD, qstride, row0 + tok0, nq, smem, wave, lane);
-    dma_tile<kDkdvWaves>(gbase + qh * kMfmaD, qstride, row0 + tok0, nq, smem + kTileBytes, wave, lane);
+    issue_stage(row0 + tok0, nq, qh, smem);
     store_stat(0, x);
   }
 
@@ -782,8 +792,7 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
       stage_info(sidx + 1, nrow0, ntok0, nnq, nqh);
       next_stat = fetch_stat(nrow0, ntok0, nnq, nqh);
       char* nt = smem + (buf ^ 1) * 2 * kTileBytes;
-      dma_tile<kDkdvWaves>(qbase + nqh * kMfmaD, qstride, nrow0 + ntok0, nnq, nt, wave, lane);
-      dma_tile<kDkdvWaves>(gbase + nqh * kMfmaD, qstride, nrow0 + ntok0, nnq, nt + kTileBytes, wave, lane);
+      issue_stage(nrow0 + ntok0, nnq, nqh, nt);
     }
     if (wave_active) {
 #pragma unroll
@@ -802,14 +811,21 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
         // causal (suffix): key kp visible iff kp <= query position
         const float* l2 = &stats[buf][0][32 * qs + 8 * h];
         const float* dl = &stats[buf][1][32 * qs + 8 * h];
-        const int lim = (!prefix && qpos0 < kw0 + 31) ? kp - qpos0 - 8 * h : -(1 << 30);
 #pragma unroll
         for (int r = 0; r < 16; r++) {
           const int qi = 16 * (r >> 3) + (r & 7);
-          float p = fast_exp2(fmaf(s[r], c2, -l2[qi]));
-          p = (qi >= lim) ? p : 0.f;
+          const float p = fast_exp2(fmaf(s[r], c2, -l2[qi]));
           s[r] = p;
           dp[r] = p * (dp[r] - dl[qi]);
+        }
+        if (!prefix && qpos0 < kw0 + 31) {  // causal diagonal: key kp visible iff kp <= query position
+          const int lim = kp - qpos0 - 8 * h;
+#pragma unroll
+          for (int r = 0; r < 16; r++) {
+            const bool vis = 16 * (r >> 3) + (r & 7) >= lim;
+            s[r] = vis ? s[r] : 0.f;
+            dp[r] = vis ? dp[r] : 0.f;
+          }
         }
 #pragma unroll
         for (int cc = 0; cc < 2; cc++) {
