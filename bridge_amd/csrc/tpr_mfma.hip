@@ -302,6 +302,14 @@ template <typename T>
 __device__ __forceinline__ void settle(const T& x) {
   asm volatile("" ::"v"(x));
 }
+// Keep `x` in accumulation registers (AGPRs) at this point. Used on the
+// dK/dV accumulators at the end of each stage so that every path through the
+// stage hands them over in the registers the MFMAs write, instead of the
+// allocator parking them in VGPRs and copying them back each stage.
+template <typename T>
+__device__ __forceinline__ void settle_acc(T& x) {
+  asm volatile("" : "+a"(x));
+}
 
 // ---------------------------------------------------------------------------
 // Forward
@@ -797,9 +805,12 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
     if (wave_active) {
 #pragma unroll
       for (int qs = 0; qs < 2; qs++) {
+        // Every sub-block is computed (no data-dependent skip, which would
+        // split the schedule): queries past the block end carry lse = +inf,
+        // so P = dS = 0, and a (suffix) sub-block entirely before the wave's
+        // keys takes the diagonal mask below, which hides all of it.
+        __builtin_amdgcn_sched_barrier(0);
         const int qpos0 = tok0 + 32 * qs;  // first query position of the sub-block
-        // skip sub-blocks past the leaf end, or (suffix) entirely before the wave's keys
-        if (32 * qs >= nq || (!prefix && qpos0 + 31 < kw0)) continue;
         f32x16 s = f32x16{}, dp = f32x16{};
         const int qrow = 32 * qs + sigma32(n);
 #pragma unroll
@@ -818,6 +829,14 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
           s[r] = p;
           dp[r] = p * (dp[r] - dl[qi]);
         }
+        // row reads four MFMAs ahead of the S/dP MFMAs that consume them
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
         if (!prefix && qpos0 < kw0 + 31) {  // causal diagonal: key kp visible iff kp <= query position
           const int lim = kp - qpos0 - 8 * h;
 #pragma unroll
@@ -838,9 +857,22 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
             dk[db] = mfma(db8, lds_read_col8(qt, r0, 32 * db, lane), dk[db]);
           }
         }
+        // column reads four MFMAs ahead of the dV/dK MFMAs that consume them
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+        for (int i = 0; i < 6; i++) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
       }
     }
     if (more) store_stat(buf ^ 1, next_stat);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {  // accumulators stay in AGPRs across the stage loop
+      settle_acc(dk[i]);
+      settle_acc(dv[i]);
+    }
     wait_dma();
     __syncthreads();
   }
