@@ -91,10 +91,23 @@ extern "C" int tpr_attn_abi_version(void) { return TPR_ATTN_ABI_VERSION; }
 
 extern "C" const char* tpr_attn_last_error(void) { return g_error; }
 
+namespace tpr {
+namespace {
+// floats of the MFMA backward's stat area (constants + lse*log2e rows), a
+// multiple of 64 so the partial slots after it stay 256-byte aligned
+size_t stat_floats(const int32_t* ph) {
+  if (ph[PF_PATH] != PATH_MFMA || ph[PF_TOTAL_Q] <= 0) return 0;
+  const size_t rows = static_cast<size_t>(ph[PF_HQ]) * static_cast<size_t>(ph[PF_TOTAL_Q]);
+  return kStatRowsOffset + (rows + 63) / 64 * 64;
+}
+}  // namespace
+}  // namespace tpr
+
 extern "C" size_t tpr_attn_bwd_workspace_bytes(const int32_t* plan_host) {
   if (!plan_host || plan_host[PF_MAGIC] != kPlanMagic) return 0;
   const size_t slots = static_cast<size_t>(plan_host[PF_N_SLOTS]);
-  return slots * static_cast<size_t>(kDkdvKeys) * static_cast<size_t>(plan_host[PF_D]) * 2 * sizeof(float);
+  return (stat_floats(plan_host) +
+          slots * static_cast<size_t>(kDkdvKeys) * static_cast<size_t>(plan_host[PF_D]) * 2) * sizeof(float);
 }
 
 extern "C" int tpr_attn_fwd(const TprFwdParams* p, void* stream) {
@@ -176,7 +189,8 @@ extern "C" int tpr_attn_bwd_phases(const TprBwdParams* p, int phases, void* stre
   a.dv = p->dv;
   a.dpk = p->dprefix_k;
   a.dpv = p->dprefix_v;
-  a.ws = static_cast<float*>(p->workspace);
+  a.stat_ws = static_cast<float*>(p->workspace);
+  a.ws = a.stat_ws + stat_floats(ph);
   const bool fp32 = ph[PF_DTYPE] == TPR_DTYPE_FP32;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int n_dkdv = (phases & TPR_BWD_DKDV) ? ph[PF_N_DKDV] : 0;

@@ -92,6 +92,10 @@ constexpr int kDkdvKeys = 32 * kDkdvWaves;  // keys per dK/dV workgroup (32 per 
 constexpr int kDkdvQ = 64;            // queries per staged query block
 constexpr int kDkdvMaxBlocks = 128;   // query blocks one dK/dV item may stream (LDS table size)
 constexpr int kDkdvPrefixChunk = 64;  // query blocks per item when a prefix tile is split
+// MFMA backward workspace, ahead of the partial slots: two constants (+inf,
+// 0) that rows past a query block's end are copied from, then lse * log2e per
+// (query head, token) in the lse layout.
+constexpr int kStatRowsOffset = 64;   // floats before the lse*log2e rows
 constexpr int kMfmaMaxDepth = 8;      // ancestor nodes per leaf handled by the MFMA path
 
 }  // namespace tpr

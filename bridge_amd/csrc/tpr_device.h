@@ -45,7 +45,8 @@ struct KernelArgs {
   int32_t off_cu, off_node_off, off_anc, off_node_leaf;
   int32_t off_qblk, off_leaf_qblk, off_fwd, off_dkdv, off_red;
   int32_t n_items;
-  float* ws;  // fp32 partial dK/dV slots of split tiles
+  float* ws;       // fp32 partial dK/dV slots of split tiles
+  float* stat_ws;  // MFMA backward: [0] = +inf, [1] = 0, then lse*log2e rows from kStatRowsOffset
 };
 
 __device__ __forceinline__ float to_f32(float x) { return x; }

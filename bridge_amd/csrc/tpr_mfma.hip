@@ -164,6 +164,19 @@ __device__ __forceinline__ void dma16(const void* src, uint32_t lds_dst) {
       : "v"(src), "s"(lds_dst));
 }
 
+// One dword per lane, lane l's landing at lds_dst + 4*l (global_load_lds_dword).
+__device__ __forceinline__ void dma4(const void* src, uint32_t lds_dst) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dword %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(src), "s"(lds_dst));
+}
+
 template <int kWaves>
 __device__ __forceinline__ void dma_tile(const bf16* base, int64_t stride, int64_t row0, int len, char* tile,
                                          int wave, int lane) {
@@ -293,6 +306,7 @@ __device__ __forceinline__ TileLoc cursor_tile(const Cursor& c) {
 // the barrier is what orders the LDS reads of the copied tile.
 __device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)"); }
 
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Make the compiler complete the load of `x` here. Operands loaded before a
@@ -309,6 +323,17 @@ __device__ __forceinline__ void settle(const T& x) {
 template <typename T>
 __device__ __forceinline__ void settle_acc(T& x) {
   asm volatile("" : "+a"(x));
+}
+
+// Calls f(std::integral_constant<int, i>) for i = 0 .. N-1, unrolled at
+// compile time (array indices derived from i are constants).
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
 // ---------------------------------------------------------------------------
@@ -505,7 +530,9 @@ __global__ __launch_bounds__(256, 2) void mfma_fwd(KernelArgs a) {
 
 // ---------------------------------------------------------------------------
 // delta[h][t] = sum_d dout[t][h][d] * out[t][h][d] (head_dim 128): 16 lanes per
-// (t, h) row, one 16-byte load of each tensor per lane.
+// (t, h) row, one 16-byte load of each tensor per lane. Also fills the stat
+// area of the workspace that the dK/dV kernel copies per query block:
+// lse[h][t] * log2e and the two constants for rows past a block's end.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void mfma_delta(KernelArgs a) {
   const int64_t rows = static_cast<int64_t>(a.total_q) * a.hq;
@@ -522,7 +549,15 @@ __global__ __launch_bounds__(256) void mfma_delta(KernelArgs a) {
   s += __shfl_xor(s, 4);
   s += __shfl_xor(s, 2);
   s += __shfl_xor(s, 1);
-  if (c == 0 && row < rows) a.delta[(row % a.hq) * a.total_q + row / a.hq] = s;
+  if (c == 0 && row < rows) {
+    const int64_t at = (row % a.hq) * a.total_q + row / a.hq;
+    a.delta[at] = s;
+    a.stat_ws[kStatRowsOffset + at] = a.lse_in[at] * kLog2e;  // the dK/dV kernel copies these rows
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    a.stat_ws[0] = INFINITY;  // lse*log2e of a query past a block's end: P = 0
+    a.stat_ws[1] = 0.f;       // its delta
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -667,8 +702,11 @@ __global__ __launch_bounds__(256, 2) void mfma_dq(KernelArgs a) {
 //   dP = dO V^T, dS = P (dP - delta), dV += P^T dO, dK += dS^T Q, dK *= scale.
 // K/V of the wave's 32 keys are B operands held in registers; Q/dO blocks of
 // 64 queries are copied to LDS and read row-wise (A operands) and
-// column-wise (B operands of dV/dK, ds_read_tr16_b64).
+// column-wise (B operands of dV/dK, ds_read_tr16_b64). A stage is one query
+// block of kHeads query heads of the GQA group (2 when the group size is even:
+// half the stages, and with them half the per-stage barriers and copy waits).
 // ---------------------------------------------------------------------------
+template <int kHeads>
 __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
   const int32_t* item = a.plan + a.off_dkdv + DK_WORDS * blockIdx.x;
   if (item[DK_SRC] < 0) return;
@@ -690,10 +728,13 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
   const int64_t qstride = static_cast<int64_t>(a.hq) * kMfmaD;
   const int64_t kstride = static_cast<int64_t>(a.hkv) * kMfmaD;
 
-  __shared__ __attribute__((aligned(1024))) char smem[4 * kTileBytes];   // Q0 G0 Q1 G1
-  __shared__ __attribute__((aligned(16))) float stats[2][2][kTileRows];  // [buf][lse*log2e | delta][row]
+  // two stage buffers of kHeads (Q, dO) tile pairs: the copies of stage s + 1
+  // run during stage s
+  __shared__ __attribute__((aligned(1024))) char smem[2 * kHeads * 2 * kTileBytes];
+  __shared__ __attribute__((aligned(256))) float stats[2][kHeads][2][kTileRows];  // [buf][head][lse*log2e | delta][row]
 
-  const int nstage = (qb_hi - qb_lo) * a.group;
+  const int spb = a.group / kHeads;  // stages per query block
+  const int nstage = (qb_hi - qb_lo) * spb;
   const bf16* qbase = static_cast<const bf16*>(a.q);
   const bf16* gbase = static_cast<const bf16*>(a.dout);
 
@@ -709,9 +750,9 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
   }
   __syncthreads();
 
-  auto stage_info = [&](int sidx, int& row0, int& tok0, int& nq, int& qh) {
-    const int4 e = qtab[sidx / a.group];
-    qh = kvh * a.group + sidx % a.group;
+  auto stage_info = [&](int sidx, int& row0, int& tok0, int& nq, int& qh) {  // qh: first head of the stage
+    const int4 e = qtab[sidx / spb];
+    qh = kvh * a.group + (sidx % spb) * kHeads;
     row0 = e.x - e.y;
     tok0 = e.y;
     nq = e.z;
@@ -727,38 +768,28 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
     dma_tile_s<kDkdvWaves>(reinterpret_cast<const char*>(gbase) + off, qrow_bytes, nq, dst + kTileBytes, dl, wave);
   };
 
-  // lse and delta of one query block: thread r < 64 fetches lse row r, thread
-  // 64 + r delta row r. The raw value is fetched into a register before the
-  // tile copies are issued and only converted and stored to LDS after the
-  // compute, so the load's latency hides behind the stage.
-  struct Stat {
-    float x;
-    bool valid;
-  };
-  auto fetch_stat = [&](int row0, int tok0, int nq, int qh) -> Stat {
-    Stat st{0.f, false};
-    if (threadIdx.x < 2 * kTileRows) {
-      const int r = threadIdx.x & (kTileRows - 1);
-      const int64_t at = static_cast<int64_t>(qh) * a.total_q + row0 + tok0 + min(r, nq - 1);
-      st.x = threadIdx.x < kTileRows ? a.lse_in[at] : a.delta[at];
-      st.valid = r < nq;
+  // lse*log2e (which 0) and delta (which 1) of the stage's 64 query rows of
+  // each of its heads, copied into its stat buffer like the tiles -- wave w
+  // copies (head w / 2, which w % 2); rows past the block end copy the
+  // constants +inf / 0 of the workspace, so their P and dS are exactly 0.
+  const uint32_t stats0 = __builtin_amdgcn_readfirstlane(lds_address(stats));
+  auto issue_stats = [&](int row, int nq, int qh, int buf) {
+    const int hh = wave >> 1, which = wave & 1;
+    if (hh < kHeads) {
+      const int64_t at = static_cast<int64_t>(qh + hh) * a.total_q + row + lane;
+      const float* rows = which == 0 ? a.stat_ws + kStatRowsOffset : a.delta;
+      dma4(lane < nq ? rows + at : a.stat_ws + which, stats0 + ((buf * kHeads + hh) * 2 + which) * kTileRows * 4);
     }
-    return st;
   };
-  auto store_stat = [&](int buf, Stat st) {
-    if (threadIdx.x < kTileRows)
-      stats[buf][0][threadIdx.x] = st.valid ? st.x * kLog2e : INFINITY;  // invalid query: P = 0
-    else if (threadIdx.x < 2 * kTileRows)
-      stats[buf][1][threadIdx.x - kTileRows] = st.valid ? st.x : 0.f;
-  };
-
-  if (nstage > 0) {
+  auto issue = [&](int sidx, int buf) {
     int row0, tok0, nq, qh;
-    stage_info(0, row0, tok0, nq, qh);
-    const Stat x = fetch_stat(row0, tok0, nq, qh);
-    issue_stage(row0 + tok0, nq, qh, smem);
-    store_stat(0, x);
-  }
+    stage_info(sidx, row0, tok0, nq, qh);
+    issue_stats(row0 + tok0, nq, qh, buf);
+#pragma unroll
+    for (int hh = 0; hh < kHeads; hh++)
+      issue_stage(row0 + tok0, nq, qh + hh, smem + (buf * kHeads + hh) * 2 * kTileBytes);
+  };
+  if (nstage > 0) issue(0, 0);
 
   bf16x8 kv[8], vv[8];
   {
@@ -787,93 +818,124 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
   wait_dma();
   __syncthreads();
 
+  // One stage: 64 queries of one head against the wave's 32 keys, as two
+  // 32-query sub-blocks j of 32 MFMAs each -- S (8), dP (8), dV (8), dK (8).
+  // The stage is laid out as a fixed sequence of 64 slots, one MFMA per slot,
+  // fenced so the compiler keeps the order:
+  //  * the LDS operands of the MFMA kAhead slots later are read in each slot,
+  //    so every read has about kAhead MFMAs (4 x 32 cycles) to land;
+  //  * P = exp2(scale*S - lse) of sub-block j is computed under its dP and
+  //    first dV MFMAs, dS = P (dP - delta) under its dV and first dK MFMAs,
+  //    so the VALU work runs while the matrix core is busy.
+  // Key kp is visible from query index qi of sub-block j iff qi >= lim - 32j
+  // (lim <= -64 off the causal diagonal: all visible). Queries past the block
+  // end carry lse = +inf, so their P and dS are exactly 0.
+  constexpr int kAhead = 4;
+  auto stage = [&](const char* qt, const char* gt, const float* st, int lim) __attribute__((always_inline)) {
+    bf16x8 rq[2][8], rg[2][8], cg[2][2][4], cq[2][2][4];
+    f32x4 l2v[2][4], dlv[2][4];
+    f32x16 sc[2], dpv[2];
+    float p[2][16], dsv[2][16];
+    bf16x8 pb[2][2], d8[2][2];
+    // operands of MFMA m (sub-block m / 32, position m % 32)
+    auto read_for = [&](auto mc) __attribute__((always_inline)) {
+      constexpr int m = decltype(mc)::value, j = m >> 5, k = m & 31;
+      if constexpr (k < 8) {
+        rq[j][k] = lds_read_b128(qt, 32 * j + sigma32(n), 16 * k + 8 * h);
+      } else if constexpr (k < 16) {
+        rg[j][k - 8] = lds_read_b128(gt, 32 * j + sigma32(n), 16 * (k - 8) + 8 * h);
+      } else if constexpr (k < 24) {
+        constexpr int cc = (k - 16) >> 2, db = (k - 16) & 3;
+        cg[j][cc][db] = lds_read_col8(gt, 32 * j + 16 * cc + 8 * h, 32 * db, lane);
+      } else {
+        constexpr int cc = (k - 24) >> 2, db = (k - 24) & 3;
+        cq[j][cc][db] = lds_read_col8(qt, 32 * j + 16 * cc + 8 * h, 32 * db, lane);
+      }
+    };
+    // lse*log2e (which 0) or delta (which 1) of the lane's 16 queries of sub-block j
+    auto read_stats = [&](auto jc, auto wc) __attribute__((always_inline)) {
+      constexpr int j = decltype(jc)::value, which = decltype(wc)::value;
+      const float* src = st + which * kTileRows + 32 * j + 8 * h;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(src + 16 * (i >> 1) + 4 * (i & 1));
+        if constexpr (which) dlv[j][i] = v;
+        else l2v[j][i] = v;
+      }
+    };
+    auto mfma_at = [&](auto mc) __attribute__((always_inline)) {
+      constexpr int m = decltype(mc)::value, j = m >> 5, k = m & 31;
+      if constexpr (k < 8) {
+        sc[j] = mfma(rq[j][k], kv[k], k == 0 ? f32x16{} : sc[j]);
+      } else if constexpr (k < 16) {
+        dpv[j] = mfma(rg[j][k - 8], vv[k - 8], k == 8 ? f32x16{} : dpv[j]);
+      } else if constexpr (k < 24) {
+        constexpr int cc = (k - 16) >> 2, db = (k - 16) & 3;
+        dv[db] = mfma(pb[j][cc], cg[j][cc][db], dv[db]);
+      } else {
+        constexpr int cc = (k - 24) >> 2, db = (k - 24) & 3;
+        dk[db] = mfma(d8[j][cc], cq[j][cc][db], dk[db]);
+      }
+    };
+    // register r of a sub-block holds query 16*(r/8) + r%8 of the lane's 8-row group
+    auto p_elem = [&](auto jc, auto rc) __attribute__((always_inline)) {
+      constexpr int j = decltype(jc)::value, r = decltype(rc)::value, qi = 16 * (r >> 3) + (r & 7);
+      float x = fmaf(sc[j][r], c2, -l2v[j][r >> 2][r & 3]);
+      x = qi >= lim - 32 * j ? x : -INFINITY;
+      p[j][r] = fast_exp2(x);
+      if constexpr ((r & 7) == 7) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) pb[j][r >> 3][i] = static_cast<bf16>(p[j][(r & 8) + i]);
+      }
+    };
+    auto ds_elem = [&](auto jc, auto rc) __attribute__((always_inline)) {
+      constexpr int j = decltype(jc)::value, r = decltype(rc)::value;
+      dsv[j][r] = p[j][r] * (dpv[j][r] - dlv[j][r >> 2][r & 3]);
+      if constexpr ((r & 7) == 7) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) d8[j][r >> 3][i] = static_cast<bf16>(dsv[j][(r & 8) + i]);
+      }
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    static_for<kAhead>([&](auto mc) __attribute__((always_inline)) { read_for(mc); });
+    read_stats(I0{}, I0{});
+    static_for<64>([&](auto mc) __attribute__((always_inline)) {
+      constexpr int m = decltype(mc)::value, j = m >> 5, k = m & 31;
+      using J = std::integral_constant<int, j>;
+      if constexpr (m + kAhead < 64) read_for(std::integral_constant<int, m + kAhead>{});
+      if constexpr (j == 1 && k == 2) read_stats(I1{}, I0{});
+      if constexpr (k == 10) read_stats(J{}, I1{});
+      mfma_at(mc);
+      static_for<16>([&](auto rc) __attribute__((always_inline)) {
+        constexpr int r = decltype(rc)::value;
+        if constexpr (k == 9 + (r * 10) / 16) p_elem(J{}, rc);   // P: slots 9..18 (pb[0] by 13, pb[1] by 18)
+        if constexpr (k == 19 + (r * 9) / 16) ds_elem(J{}, rc);  // dS: slots 19..27 (d8[0] by 22, d8[1] by 27)
+      });
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+
   for (int sidx = 0; sidx < nstage; sidx++) {
     const int buf = sidx & 1;
-    const char* qt = smem + buf * 2 * kTileBytes;
-    const char* gt = qt + kTileBytes;
     int row0, tok0, nq, qh;
     stage_info(sidx, row0, tok0, nq, qh);
-    const bool more = sidx + 1 < nstage;
-    Stat next_stat{0.f, false};
-    if (more) {
-      int nrow0, ntok0, nnq, nqh;
-      stage_info(sidx + 1, nrow0, ntok0, nnq, nqh);
-      next_stat = fetch_stat(nrow0, ntok0, nnq, nqh);
-      char* nt = smem + (buf ^ 1) * 2 * kTileBytes;
-      issue_stage(nrow0 + ntok0, nnq, nqh, nt);
-    }
+    if (sidx + 1 < nstage) issue(sidx + 1, buf ^ 1);
     if (wave_active) {
+      // (suffix) a stage that crosses the wave's causal diagonal is masked
+      const int lim = (!prefix && tok0 < kw0 + 31) ? kp - tok0 - 8 * h : -64;
 #pragma unroll
-      for (int qs = 0; qs < 2; qs++) {
-        // Every sub-block is computed (no data-dependent skip, which would
-        // split the schedule): queries past the block end carry lse = +inf,
-        // so P = dS = 0, and a (suffix) sub-block entirely before the wave's
-        // keys takes the diagonal mask below, which hides all of it.
-        __builtin_amdgcn_sched_barrier(0);
-        const int qpos0 = tok0 + 32 * qs;  // first query position of the sub-block
-        f32x16 s = f32x16{}, dp = f32x16{};
-        const int qrow = 32 * qs + sigma32(n);
-#pragma unroll
-        for (int c = 0; c < 8; c++) {
-          s = mfma(lds_read_b128(qt, qrow, 16 * c + 8 * h), kv[c], s);
-          dp = mfma(lds_read_b128(gt, qrow, 16 * c + 8 * h), vv[c], dp);
-        }
-        // register r holds query 32*qs + 16*(r/8) + 8*h + r%8 of the block;
-        // causal (suffix): key kp visible iff kp <= query position
-        const float* l2 = &stats[buf][0][32 * qs + 8 * h];
-        const float* dl = &stats[buf][1][32 * qs + 8 * h];
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-          const int qi = 16 * (r >> 3) + (r & 7);
-          const float p = fast_exp2(fmaf(s[r], c2, -l2[qi]));
-          s[r] = p;
-          dp[r] = p * (dp[r] - dl[qi]);
-        }
-        // row reads four MFMAs ahead of the S/dP MFMAs that consume them
-        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-          __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-        }
-        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-        if (!prefix && qpos0 < kw0 + 31) {  // causal diagonal: key kp visible iff kp <= query position
-          const int lim = kp - qpos0 - 8 * h;
-#pragma unroll
-          for (int r = 0; r < 16; r++) {
-            const bool vis = 16 * (r >> 3) + (r & 7) >= lim;
-            s[r] = vis ? s[r] : 0.f;
-            dp[r] = vis ? dp[r] : 0.f;
-          }
-        }
-#pragma unroll
-        for (int cc = 0; cc < 2; cc++) {
-          const bf16x8 pb = to_bf16x8(s, 8 * cc);
-          const bf16x8 db8 = to_bf16x8(dp, 8 * cc);
-          const int r0 = 32 * qs + 16 * cc + 8 * h;
-#pragma unroll
-          for (int db = 0; db < 4; db++) {
-            dv[db] = mfma(pb, lds_read_col8(gt, r0, 32 * db, lane), dv[db]);
-            dk[db] = mfma(db8, lds_read_col8(qt, r0, 32 * db, lane), dk[db]);
-          }
-        }
-        // column reads four MFMAs ahead of the dV/dK MFMAs that consume them
-        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-#pragma unroll
-        for (int i = 0; i < 6; i++) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-          __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-        }
-        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+      for (int hh = 0; hh < kHeads; hh++) {
+        const char* qt = smem + (buf * kHeads + hh) * 2 * kTileBytes;
+        stage(qt, qt + kTileBytes, &stats[buf][hh][0][0], lim);
       }
     }
-    if (more) store_stat(buf ^ 1, next_stat);
 #pragma unroll
     for (int i = 0; i < 4; i++) {  // accumulators stay in AGPRs across the stage loop
       settle_acc(dk[i]);
       settle_acc(dv[i]);
     }
-    wait_dma();
+    wait_dma();  // stage sidx + 1 has landed
     __syncthreads();
   }
 
@@ -962,7 +1024,10 @@ int launch_mfma_delta(const KernelArgs& a, hipStream_t s) {
 
 int launch_mfma_bwd(const KernelArgs& a, int n_fwd, int n_dkdv, int n_red, hipStream_t s) {
   if (n_dkdv > 0) {
-    hipLaunchKernelGGL(mfma_dkdv, dim3(n_dkdv), dim3(256), 0, s, a);
+    if (a.group % 2 == 0)
+      hipLaunchKernelGGL(mfma_dkdv<2>, dim3(n_dkdv), dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL(mfma_dkdv<1>, dim3(n_dkdv), dim3(256), 0, s, a);
     if (hipGetLastError() != hipSuccess) return 4;
   }
   if (n_red > 0) {
