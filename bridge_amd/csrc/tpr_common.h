@@ -84,7 +84,7 @@ constexpr int kSimtTile = 32;   // keys (fwd/dQ) or queries (dK/dV) staged per L
 
 // MFMA family (bf16, head_dim 128)
 constexpr int kMfmaD = 128;
-constexpr int kFwdWaves = 4;          // waves per forward / dQ workgroup
+constexpr int kFwdWaves = 8;          // waves per forward / dQ workgroup
 constexpr int kFwdTokens = 32;        // tokens per wave (one query head per wave)
 constexpr int kFwdKeys = 64;          // keys per LDS tile
 constexpr int kDkdvWaves = 4;         // waves per dK/dV workgroup

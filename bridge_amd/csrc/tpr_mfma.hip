@@ -361,7 +361,7 @@ __device__ __forceinline__ void qk_tile(const char* kt, const bf16x8 (&qv)[8], i
 // so unscaled probabilities stay <= 2^8 (exact arithmetic, fp32/bf16 safe).
 constexpr float kRescaleSlack = 8.f;
 
-__global__ __launch_bounds__(256, 2) void mfma_fwd(KernelArgs a) {
+__global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
   const int32_t* item = a.plan + a.off_fwd + 4 * blockIdx.x;
   const int leaf = item[0];
   if (leaf < 0) return;
@@ -565,7 +565,7 @@ __global__ __launch_bounds__(256) void mfma_delta(KernelArgs a) {
 //   S^T = K Q^T, P^T = exp(scale S^T - lse), dP^T = V dO^T,
 //   dS^T = P^T (dP^T - delta), dQ^T += K^T dS^T, dQ = scale * dQ.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256, 2) void mfma_dq(KernelArgs a) {
+__global__ __launch_bounds__(512) void mfma_dq(KernelArgs a) {
   const int32_t* item = a.plan + a.off_fwd + 4 * blockIdx.x;
   const int leaf = item[0];
   if (leaf < 0) return;
@@ -1011,7 +1011,7 @@ __global__ __launch_bounds__(256) void mfma_reduce(KernelArgs a) {
 }  // namespace
 
 int launch_mfma_fwd(const KernelArgs& a, hipStream_t s) {
-  if (a.n_items > 0) hipLaunchKernelGGL(mfma_fwd, dim3(a.n_items), dim3(256), 0, s, a);
+  if (a.n_items > 0) hipLaunchKernelGGL(mfma_fwd, dim3(a.n_items), dim3(64 * kFwdWaves), 0, s, a);
   return hipGetLastError() == hipSuccess ? 0 : 4;
 }
 
@@ -1035,7 +1035,7 @@ int launch_mfma_bwd(const KernelArgs& a, int n_fwd, int n_dkdv, int n_red, hipSt
     if (hipGetLastError() != hipSuccess) return 4;
   }
   if (n_fwd > 0) {
-    hipLaunchKernelGGL(mfma_dq, dim3(n_fwd), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(mfma_dq, dim3(n_fwd), dim3(64 * kFwdWaves), 0, s, a);
     if (hipGetLastError() != hipSuccess) return 4;
   }
   return 0;

@@ -1,6 +1,7 @@
 """CPU tests of the native planner (tpr_attn_plan): tree validation, work-list
 coverage, XCD-aware ordering and the segment-tree lowering. Host code only."""
 
+import math
 from collections import Counter
 
 import pytest
@@ -14,6 +15,8 @@ CPU = torch.device("cpu")
 PF = dict(MAGIC=0, NUM_LEAVES=2, NUM_NODES=3, MAX_DEPTH=4, TOTAL_Q=5, TOTAL_PREFIX=6, HQ=7, HKV=8, D=9,
           PATH=11, OFF_CU=12, OFF_NODE_OFF=13, OFF_ANC=14, OFF_NODE_LEAF=15, N_QBLK=16, OFF_QBLK=17,
           OFF_LEAF_QBLK=18, N_FWD=19, OFF_FWD=20, N_DKDV=21, OFF_DKDV=22, N_RED=23, TOTAL_WORDS=27)
+
+FWD_WAVES = 8  # waves per forward / dQ workgroup (kFwdWaves)
 
 
 def decode(plan):
@@ -33,8 +36,11 @@ def test_forward_items_cover_every_query_row_once(hq, hkv):
     assert plan.path == "mfma"
     _, fwd, _, _ = decode(plan)
     g = hq // hkv
-    hpw = max(x for x in (4, 2, 1) if g % x == 0)
-    tpw = 32 * (4 // hpw)
+    # a forward/dQ workgroup is FWD_WAVES waves of 32 tokens each: hpw query
+    # heads (the largest divisor of the group size that divides FWD_WAVES),
+    # FWD_WAVES / hpw waves per head
+    hpw = math.gcd(g, FWD_WAVES)
+    tpw = 32 * (FWD_WAVES // hpw)
     covered = Counter()
     for leaf, tok0, qh0, kvh in fwd:
         if leaf < 0:
@@ -54,14 +60,15 @@ def test_xcd_ordering_pins_kv_heads_and_is_lpt_per_xcd():
     plan = meta.plan(32, 8, 128, torch.bfloat16, CPU)
     _, fwd, dkdv, _ = decode(plan)
     # prefix tiles (4 siblings x 64 query blocks each) split into 4 chunks of 64 blocks
-    assert len(fwd) == 4 * 128 * 8 and len(dkdv) == (32 * 4 + 4 * 32) * 8
+    tpw = 32 * (FWD_WAVES // 4)  # tokens per forward workgroup (4 query heads of the group)
+    assert len(fwd) == 4 * (4096 // tpw) * 8 and len(dkdv) == (32 * 4 + 4 * 32) * 8
     for i, (leaf, tok0, qh0, kvh) in enumerate(fwd):
         assert leaf >= 0 and kvh == i % 8
     for i, item in enumerate(dkdv):
         assert item[3] == i % 8
     # decreasing causal work (prefix + tokens seen) within each XCD queue
     for x in range(8):
-        work = [4096 + min(tok0 + 32, 4096) for (_, tok0, _, _) in fwd[x::8]]
+        work = [4096 + min(tok0 + tpw, 4096) for (_, tok0, _, _) in fwd[x::8]]
         assert work == sorted(work, reverse=True)
 
 
