@@ -58,6 +58,20 @@ def workload(name: str):
     raise SystemExit(f"unknown workload {name!r}")
 
 
+def traffic_bytes(workload_name: str, kernel: str):
+    """HBM bytes (read + write) per launch of `kernel`, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary of this workload (scaled by the
+    copy-probe calibration), or None when there is none."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as f:
+            data = json.load(f)
+    except (OSError, ValueError):
+        return None
+    entry = data.get("per_launch", {}).get(kernel) if data.get("workload") == workload_name else None
+    return None if entry is None else int(entry["read_bytes"] + entry["write_bytes"])
+
+
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -149,24 +163,21 @@ def main() -> int:
                              if plan.workspace_bytes else None)}
     stream = torch.cuda.current_stream(device)
 
+    # one fwd+bwd step, enqueued phase by phase so that each kernel can be
+    # timed with events on the stream it runs on
+    phases = [None, _lib.TPR_BWD_DELTA, _lib.TPR_BWD_DKDV_TILES, _lib.TPR_BWD_DKDV_REDUCE, _lib.TPR_BWD_DQ]
+
     def step(events=None):
+        out = lse = None
+        for i, ph in enumerate(phases):
+            if events:
+                events[i].record(stream)
+            if ph is None:
+                out, lse = prefix_attention_forward(q, k, v, pk, pv, meta, scale)
+            else:
+                prefix_attention_backward(q, k, v, pk, pv, out, lse, dout, meta, scale, phases=ph, buffers=buffers)
         if events:
-            events[0].record(stream)
-        out, lse = prefix_attention_forward(q, k, v, pk, pv, meta, scale)
-        if events:
-            events[1].record(stream)
-        prefix_attention_backward(q, k, v, pk, pv, out, lse, dout, meta, scale,
-                                  phases=_lib.TPR_BWD_DELTA, buffers=buffers)
-        if events:
-            events[2].record(stream)
-        prefix_attention_backward(q, k, v, pk, pv, out, lse, dout, meta, scale,
-                                  phases=_lib.TPR_BWD_DKDV, buffers=buffers)
-        if events:
-            events[3].record(stream)
-        prefix_attention_backward(q, k, v, pk, pv, out, lse, dout, meta, scale,
-                                  phases=_lib.TPR_BWD_DQ, buffers=buffers)
-        if events:
-            events[4].record(stream)
+            events[len(phases)].record(stream)
 
     if args.copy_probe:
         src = torch.ones(args.copy_probe * (1 << 20) // 2, dtype=torch.bfloat16, device=device)
@@ -179,7 +190,7 @@ def main() -> int:
         step()
     torch.cuda.synchronize()
 
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(args.steps)]
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(len(phases) + 1)] for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
@@ -191,7 +202,7 @@ def main() -> int:
     def avg(a, b):
         return statistics.mean(e[a].elapsed_time(e[b]) for e in events)
 
-    fwd_ms, delta_ms, dkdv_ms, dq_ms = avg(0, 1), avg(1, 2), avg(2, 3), avg(3, 4)
+    fwd_ms, delta_ms, dkdv_ms, reduce_ms, dq_ms = avg(0, 1), avg(1, 2), avg(2, 3), avg(3, 4), avg(4, 5)
     pairs = meta.visible_pairs()
     unit = 2.0 * hq * d * pairs          # FLOP of one GEMM over the visible pairs
     total_flops = 7.0 * unit            # fwd (2 GEMMs) + bwd (5 GEMMs)
@@ -234,7 +245,7 @@ def main() -> int:
         "fwd_tflops": round(2.0 * unit / (fwd_ms * 1e-3) / 1e12, 2),
         "tokens_per_s": round(tq / (ms_per_step * 1e-3), 1),
         "kernel_ms": {"fwd": round(fwd_ms, 4), "delta": round(delta_ms, 4), "dkdv": round(dkdv_ms, 4),
-                      "dq": round(dq_ms, 4)},
+                      "dkdv_reduce": round(reduce_ms, 4), "dq": round(dq_ms, 4)},
         "roofline": {
             "kernel": dom_name,
             "bound": "mfma",
@@ -242,7 +253,7 @@ def main() -> int:
             "peak": peak,
             "unit": "TFLOP/s",
             "frac": round(achieved / peak, 4),
-            "traffic": None,
+            "traffic": traffic_bytes(args.workload, dom_name),
         },
         "cpu_baseline": None,
     }

@@ -36,6 +36,8 @@ EXPORTED_SYMBOLS = (
 TPR_BWD_DELTA = 1
 TPR_BWD_DKDV = 2
 TPR_BWD_DQ = 4
+TPR_BWD_DKDV_TILES = 8
+TPR_BWD_DKDV_REDUCE = 16
 
 _p = ctypes.c_void_p
 _i32p = ctypes.POINTER(ctypes.c_int32)

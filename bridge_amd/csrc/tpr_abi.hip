@@ -149,7 +149,8 @@ extern "C" int tpr_attn_bwd(const TprBwdParams* p, void* stream) {
 
 extern "C" int tpr_attn_bwd_phases(const TprBwdParams* p, int phases, void* stream) {
   clear_error();
-  if (phases <= 0 || (phases & ~(TPR_BWD_DELTA | TPR_BWD_DKDV | TPR_BWD_DQ)))
+  constexpr int kAllPhases = TPR_BWD_DELTA | TPR_BWD_DKDV | TPR_BWD_DQ | TPR_BWD_DKDV_TILES | TPR_BWD_DKDV_REDUCE;
+  if (phases <= 0 || (phases & ~kAllPhases))
     return fail(TPR_ERR_INVALID_ARGUMENT, "phases must be a non-empty mask of TPR_BWD_* bits, got %d", phases);
   if (!p) return fail(TPR_ERR_INVALID_ARGUMENT, "params must not be NULL");
   if (p->abi_version != TPR_ATTN_ABI_VERSION)
@@ -193,12 +194,12 @@ extern "C" int tpr_attn_bwd_phases(const TprBwdParams* p, int phases, void* stre
   a.ws = a.stat_ws + stat_floats(ph);
   const bool fp32 = ph[PF_DTYPE] == TPR_DTYPE_FP32;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int n_dkdv = (phases & TPR_BWD_DKDV) ? ph[PF_N_DKDV] : 0;
+  const int n_dkdv = (phases & (TPR_BWD_DKDV | TPR_BWD_DKDV_TILES)) ? ph[PF_N_DKDV] : 0;
+  const int n_red = (phases & (TPR_BWD_DKDV | TPR_BWD_DKDV_REDUCE)) ? ph[PF_N_RED] : 0;  // 0 on the SIMT path
   const int n_dq = (phases & TPR_BWD_DQ) ? ph[PF_N_FWD] : 0;
   rc = (phases & TPR_BWD_DELTA) ? (mfma ? launch_mfma_delta(a, s) : launch_delta(a, fp32, s)) : 0;
-  if (!rc && (n_dkdv || n_dq))
-    rc = mfma ? launch_mfma_bwd(a, n_dq, n_dkdv, (phases & TPR_BWD_DKDV) ? ph[PF_N_RED] : 0, s)
-              : launch_simt_bwd(a, n_dq, n_dkdv, fp32, s);
+  if (!rc && (n_dkdv || n_red || n_dq))
+    rc = mfma ? launch_mfma_bwd(a, n_dq, n_dkdv, n_red, s) : launch_simt_bwd(a, n_dq, n_dkdv, fp32, s);
   if (rc) return fail(TPR_ERR_LAUNCH, "backward launch failed: %s", hipGetErrorString(hipGetLastError()));
   return TPR_OK;
 }

@@ -183,9 +183,11 @@ def prefix_attention_backward(q, k, v, prefix_k, prefix_v, out, lse, dout, meta:
                               softmax_scale=None, *, phases=None, buffers=None):
     """Backward only: (dq, dk, dv, dprefix_k, dprefix_v) from saved out/lse.
 
-    ``phases`` selects backward phases (mask of TPR_BWD_DELTA / _DKDV / _DQ;
-    the delta phase must have run before the other two); ``buffers`` may hold
-    preallocated outputs and the fp32 ``delta`` scratch, keyed by name."""
+    ``phases`` selects backward phases (mask of TPR_BWD_DELTA / _DKDV / _DQ,
+    or _DKDV_TILES then _DKDV_REDUCE for the two steps of _DKDV; the delta
+    phase must have run before the others, with the same ``delta`` and
+    ``workspace``); ``buffers`` may hold preallocated outputs, the fp32
+    ``delta`` scratch and the ``workspace``, keyed by name."""
     scale = validate(q, k, v, prefix_k, prefix_v, meta, softmax_scale)
     tensors = [t.contiguous() for t in (q, k, v, prefix_k, prefix_v, out, lse, dout)]
     return _backward(*tensors[:7], tensors[7], meta, scale, phases=phases, buffers=buffers)

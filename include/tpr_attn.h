@@ -157,10 +157,14 @@ int tpr_attn_bwd(const TprBwdParams* params, void* stream);
 
 /* Backward phases, for callers that time them separately or run dK/dV and dQ
  * on two streams: TPR_BWD_DELTA must complete before the other two, which
- * are independent of each other. tpr_attn_bwd == all three in this order. */
-#define TPR_BWD_DELTA 1 /* delta = rowsum(dout * out), fp32 [Hq, Tq] */
-#define TPR_BWD_DKDV 2  /* dk, dv, dprefix_k, dprefix_v */
-#define TPR_BWD_DQ 4    /* dq */
+ * are independent of each other. tpr_attn_bwd == all three in this order.
+ * TPR_BWD_DKDV is the two steps TPR_BWD_DKDV_TILES then TPR_BWD_DKDV_REDUCE,
+ * which may also be enqueued separately (in that order, same workspace). */
+#define TPR_BWD_DELTA 1        /* delta = rowsum(dout * out), fp32 [Hq, Tq] */
+#define TPR_BWD_DKDV 2         /* dk, dv, dprefix_k, dprefix_v */
+#define TPR_BWD_DQ 4           /* dq */
+#define TPR_BWD_DKDV_TILES 8   /* dK/dV tiles; split prefix tiles leave fp32 partials in the workspace */
+#define TPR_BWD_DKDV_REDUCE 16 /* ordered sum of those partials into dprefix_k / dprefix_v */
 int tpr_attn_bwd_phases(const TprBwdParams* params, int phases, void* stream);
 
 #ifdef __cplusplus

@@ -71,7 +71,7 @@ def test_null_params_and_bad_version_fail_with_messages():
     b.abi_version = _lib.ABI_VERSION
     assert lib.tpr_attn_bwd(ctypes.byref(b), None) == _lib.TPR_ERR_INVALID_ARGUMENT
     assert b"plan" in lib.tpr_attn_last_error()
-    assert lib.tpr_attn_bwd_phases(ctypes.byref(b), 8, None) == _lib.TPR_ERR_INVALID_ARGUMENT
+    assert lib.tpr_attn_bwd_phases(ctypes.byref(b), 32, None) == _lib.TPR_ERR_INVALID_ARGUMENT
     assert b"phases" in lib.tpr_attn_last_error()
 
 
