@@ -39,6 +39,12 @@ def workload(name: str):
     if name == "qwen3-4b":
         return ("Qwen3-4B attention layer: prefix 4096 + 4 x 4096 sibling suffixes, GQA 32/8, d128, bf16",
                 TPRPrefixMeta.shared_prefix(4096, [4096] * 4), 32, 8, 128, torch.bfloat16)
+    if name == "qwen3-4b-1sibling":   # prefix-traffic probe: the headline shape with one sibling
+        return ("Qwen3-4B attention layer, one sibling: prefix 4096 + 1 x 4096, GQA 32/8, d128, bf16",
+                TPRPrefixMeta.shared_prefix(4096, [4096]), 32, 8, 128, torch.bfloat16)
+    if name == "qwen3-4b-noprefix":   # prefix-traffic probe: the headline siblings without the prefix
+        return ("Qwen3-4B attention layer, no prefix: 4 x 4096 causal suffixes, GQA 32/8, d128, bf16",
+                TPRPrefixMeta.shared_prefix(0, [4096] * 4), 32, 8, 128, torch.bfloat16)
     if name == "plumbing-fp32":
         return ("plumbing: prefix 512 + 2 x 512 suffixes, 4 heads MHA, d64, fp32",
                 TPRPrefixMeta.shared_prefix(512, [512] * 2), 4, 4, 64, torch.float32)
@@ -125,7 +131,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="qwen3-4b",
-                    choices=["qwen3-4b", "plumbing-fp32", "long-session", "ragged", "turn-tree"])
+                    choices=["qwen3-4b", "plumbing-fp32", "long-session", "ragged", "turn-tree",
+                             "qwen3-4b-1sibling", "qwen3-4b-noprefix"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="before the timed steps, run one plain device copy of MIB MiB (read MIB, write MIB): "

@@ -171,6 +171,17 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
     heads_per_wg = 1;
     tokens_per_wg = kSimtQ;
   }
+  // Leaf-major order (longest leaf first, largest token blocks first within a
+  // leaf): the workgroups that run together on an XCD then share one leaf's
+  // suffix K/V besides the prefix, which keeps both in its L2.
+  std::vector<int> leaf_rank(N);
+  {
+    std::vector<int> by_len(N);
+    for (int s = 0; s < N; s++) by_len[s] = s;
+    std::stable_sort(by_len.begin(), by_len.end(),
+                     [&](int x, int y) { return cu[x + 1] - cu[x] > cu[y + 1] - cu[y]; });
+    for (int r = 0; r < N; r++) leaf_rank[by_len[r]] = r;
+  }
   std::vector<Item> fwd;
   for (int s = 0; s < N; s++) {
     const int len = cu[s + 1] - cu[s];
@@ -179,7 +190,7 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
       for (int qh = 0; qh < Hq; qh += heads_per_wg) {
         Item it;
         it.words = {s, tok, qh, qh / G};
-        it.work = keys;
+        it.work = keys + static_cast<int64_t>(N - leaf_rank[s]) * (int64_t{1} << 40);
         it.kvh = qh / G;
         fwd.push_back(std::move(it));
       }

@@ -1,0 +1,82 @@
+"""GPU parity at the benchmark configurations' full sizes.
+
+The kernel runs on the whole workload (every head, every sibling); the fp32
+oracle runs on the GPU for one KV-head group -- KV head 5 and its query heads
+20..23 -- whose outputs and gradients depend on that group alone, so the
+comparison is exact for it: out, lse and dq of heads 20..23, dk/dv and the
+sibling-summed prefix dk/dv of KV head 5.
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from _helpers import (
+    BF16_FWD_COS,
+    BF16_FWD_MAX_ABS,
+    BF16_GRAD_COS,
+    BF16_PREFIX_GRAD_REL_L2,
+    cosine,
+    max_abs,
+    oracle,
+    rel_l2,
+)
+
+pytestmark = pytest.mark.gpu
+
+HQ, HKV, D = 32, 8, 128
+KVH = 5                                   # the checked KV-head group
+QH = slice(KVH * (HQ // HKV), (KVH + 1) * (HQ // HKV))
+
+
+def _configs():
+    from bridge_amd import TPRPrefixMeta as M
+    gen = torch.Generator(device="cpu").manual_seed(0)
+    ragged = torch.randint(256, 8193, (16,), generator=gen).tolist()
+    anc = tuple((0, 1 + i // 4) for i in range(16))
+    return {
+        "qwen3_4b": M.shared_prefix(4096, [4096] * 4),
+        "long_session": M.shared_prefix(32768, [2048] * 8),
+        "ragged_varlen": M.shared_prefix(8192, ragged),
+        "turn_tree_depth3": M(tuple(1024 * i for i in range(17)), (0, 2048, 3072, 4096, 5120, 6144), anc),
+    }
+
+
+@pytest.mark.parametrize("name", ["qwen3_4b", "long_session", "ragged_varlen", "turn_tree_depth3"])
+def test_full_size_config_matches_oracle_on_one_head_group(name, cuda_device):
+    from bridge_amd import TPRPrefixAttention
+    meta = _configs()[name]
+    scale = 1.0 / math.sqrt(D)
+    gen = torch.Generator(device="cpu").manual_seed(2024)
+    tq, tp = meta.total_q, meta.total_prefix
+    shapes = [(tq, HQ, D), (tq, HKV, D), (tq, HKV, D), (tp, HKV, D), (tp, HKV, D), (tq, HQ, D)]
+    q, k, v, pk, pv, dout = (torch.randn(s, generator=gen).to(torch.bfloat16).to(cuda_device) for s in shapes)
+    print(f"[{name}] tq={tq} tp={tp} leaves={meta.num_leaves}", flush=True)
+
+    tensors = [t.clone().requires_grad_(True) for t in (q, k, v, pk, pv)]
+    out, lse = TPRPrefixAttention.apply(*tensors, meta, scale)
+    out.backward(dout)
+    torch.cuda.synchronize()
+    grads = [t.grad for t in tensors]
+
+    # fp32 oracle of the head group, on the GPU
+    kv = slice(KVH, KVH + 1)
+    ro, rl, rg = oracle(meta, q[:, QH], k[:, kv], v[:, kv], pk[:, kv], pv[:, kv], dout[:, QH], scale,
+                        compute_dtype=torch.float32, device=cuda_device)
+    mine = [out[:, QH], lse[QH], grads[0][:, QH], grads[1][:, kv], grads[2][:, kv], grads[3][:, kv], grads[4][:, kv]]
+    ref = [ro, rl, *rg]
+    labels = ["out", "lse", "dq", "dk", "dv", "dprefix_k", "dprefix_v"]
+    for label, a, b in zip(labels, mine, ref):
+        print(f"  {label}: max_abs={max_abs(a, b):.3e} cos={cosine(a, b):.6f} rel_l2={rel_l2(a, b):.3e}", flush=True)
+    assert max_abs(mine[0], ref[0]) <= BF16_FWD_MAX_ABS and cosine(mine[0], ref[0]) >= BF16_FWD_COS
+    assert max_abs(mine[1], ref[1]) <= 1e-3
+    for a, b in zip(mine[2:], ref[2:]):
+        assert cosine(a, b) >= BF16_GRAD_COS
+    for a, b in zip(mine[5:], ref[5:]):
+        assert rel_l2(a, b) <= BF16_PREFIX_GRAD_REL_L2
+    # every other head was computed too: finite everywhere
+    for t in [out, lse, *grads]:
+        assert torch.isfinite(t.float()).all()

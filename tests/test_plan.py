@@ -66,10 +66,21 @@ def test_xcd_ordering_pins_kv_heads_and_is_lpt_per_xcd():
         assert leaf >= 0 and kvh == i % 8
     for i, item in enumerate(dkdv):
         assert item[3] == i % 8
-    # decreasing causal work (prefix + tokens seen) within each XCD queue
+    # forward: leaf-major (equal leaves keep their order), decreasing causal
+    # work (prefix + tokens seen) within a leaf, in each XCD queue
     for x in range(8):
-        work = [4096 + min(tok0 + tpw, 4096) for (_, tok0, _, _) in fwd[x::8]]
-        assert work == sorted(work, reverse=True)
+        key = [(leaf, -(4096 + min(tok0 + tpw, 4096))) for (leaf, tok0, _, _) in fwd[x::8]]
+        assert key == sorted(key)
+
+
+def test_forward_items_of_ragged_leaves_run_longest_leaf_first():
+    lens = [300, 900, 64, 900, 513]
+    meta = TPRPrefixMeta.shared_prefix(256, lens)
+    _, fwd, _, _ = decode(meta.plan(32, 8, 128, torch.bfloat16, CPU))
+    rank = {s: r for r, s in enumerate(sorted(range(len(lens)), key=lambda s: -lens[s]))}  # stable: 1 before 3
+    for x in range(8):
+        leaves = [leaf for (leaf, _, _, _) in fwd[x::8] if leaf >= 0]
+        assert [rank[s] for s in leaves] == sorted(rank[s] for s in leaves)
 
 
 def test_dkdv_items_cover_every_key_tile_and_query_block():
