@@ -827,11 +827,11 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
   //  * P = exp2(scale*S - lse) of sub-block j is computed under its dP and
   //    first dV MFMAs, dS = P (dP - delta) under its dV and first dK MFMAs,
   //    so the VALU work runs while the matrix core is busy.
-  // Key kp is visible from query index qi of sub-block j iff qi >= lim - 32j
-  // (lim <= -64 off the causal diagonal: all visible). Queries past the block
-  // end carry lse = +inf, so their P and dS are exactly 0.
+  // On a diagonal stage (diag), key kp is visible from query index qi of
+  // sub-block j iff qi >= lim - 32j; other stages skip the mask. Queries past
+  // the block end carry lse = +inf, so their P and dS are exactly 0.
   constexpr int kAhead = 4;
-  auto stage = [&](const char* qt, const char* gt, const float* st, int lim) __attribute__((always_inline)) {
+  auto stage = [&](auto diag, const char* qt, const char* gt, const float* st, int lim) __attribute__((always_inline)) {
     bf16x8 rq[2][8], rg[2][8], cg[2][2][4], cq[2][2][4];
     f32x4 l2v[2][4], dlv[2][4];
     f32x16 sc[2], dpv[2];
@@ -881,7 +881,7 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
     auto p_elem = [&](auto jc, auto rc) __attribute__((always_inline)) {
       constexpr int j = decltype(jc)::value, r = decltype(rc)::value, qi = 16 * (r >> 3) + (r & 7);
       float x = fmaf(sc[j][r], c2, -l2v[j][r >> 2][r & 3]);
-      x = qi >= lim - 32 * j ? x : -INFINITY;
+      if constexpr (decltype(diag)::value) x = qi >= lim - 32 * j ? x : -INFINITY;
       p[j][r] = fast_exp2(x);
       if constexpr ((r & 7) == 7) {
 #pragma unroll
@@ -916,28 +916,43 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
     });
   };
 
-  for (int sidx = 0; sidx < nstage; sidx++) {
-    const int buf = sidx & 1;
-    int row0, tok0, nq, qh;
-    stage_info(sidx, row0, tok0, nq, qh);
-    if (sidx + 1 < nstage) issue(sidx + 1, buf ^ 1);
-    if (wave_active) {
-      // (suffix) a stage that crosses the wave's causal diagonal is masked
-      const int lim = (!prefix && tok0 < kw0 + 31) ? kp - tok0 - 8 * h : -64;
+  // Stages [sidx, end) of the stage loop, with (diag) or without the causal
+  // mask in the body.
+  auto run_stages = [&](auto diag, int sidx, int end) __attribute__((always_inline)) {
+    for (; sidx < end; sidx++) {
+      const int buf = sidx & 1;
+      int row0, tok0, nq, qh;
+      stage_info(sidx, row0, tok0, nq, qh);
+      if (sidx + 1 < nstage) issue(sidx + 1, buf ^ 1);
+      if (wave_active) {
+        // key kp is visible from query index qi (of the stage) iff qi >= lim;
+        // off this wave's diagonal lim <= -64 (all visible)
+        const int lim = tok0 < kw0 + 31 ? kp - tok0 - 8 * h : -64;
 #pragma unroll
-      for (int hh = 0; hh < kHeads; hh++) {
-        const char* qt = smem + (buf * kHeads + hh) * 2 * kTileBytes;
-        stage(qt, qt + kTileBytes, &stats[buf][hh][0][0], lim);
+        for (int hh = 0; hh < kHeads; hh++) {
+          const char* qt = smem + (buf * kHeads + hh) * 2 * kTileBytes;
+          stage(diag, qt, qt + kTileBytes, &stats[buf][hh][0][0], lim);
+        }
       }
-    }
 #pragma unroll
-    for (int i = 0; i < 4; i++) {  // accumulators stay in AGPRs across the stage loop
-      settle_acc(dk[i]);
-      settle_acc(dv[i]);
+      for (int i = 0; i < 4; i++) {  // accumulators stay in AGPRs across the stage loop
+        settle_acc(dk[i]);
+        settle_acc(dv[i]);
+      }
+      wait_dma();  // stage sidx + 1 has landed
+      __syncthreads();
     }
-    wait_dma();  // stage sidx + 1 has landed
-    __syncthreads();
+  };
+  // (suffix) the leading stages whose query block crosses some wave's causal
+  // diagonal run with the mask, all later ones without it
+  int ndiag = 0;
+  if (!prefix) {
+    int nb = 0;
+    while (nb < qb_hi - qb_lo && qtab[nb].y < key0 + kDkdvKeys - 1) nb++;
+    ndiag = nb * spb;
   }
+  run_stages(std::true_type{}, 0, ndiag);
+  run_stages(std::false_type{}, ndiag, nstage);
 
   if (!wave_active) return;
   // accumulator register r of lane l: key 8*(r/4) + 4*h + r%4 of the wave, d = 32*db + n
