@@ -90,8 +90,9 @@ constexpr int kFwdKeys = 64;          // keys per LDS tile
 constexpr int kDkdvWaves = 4;         // waves per dK/dV workgroup
 constexpr int kDkdvKeys = 32 * kDkdvWaves;  // keys per dK/dV workgroup (32 per wave)
 constexpr int kDkdvQ = 64;            // queries per staged query block
-constexpr int kDkdvMaxBlocks = 128;   // query blocks one dK/dV item may stream (LDS table size)
-constexpr int kDkdvPrefixChunk = 64;  // query blocks per item when a prefix tile is split
+constexpr int kDkdvMaxBlocks = 256;   // query blocks one dK/dV item may stream (LDS table size)
+constexpr int kDkdvPrefixChunk = 64;  // smallest chunk a prefix tile is split into
+constexpr int kPlanCus = 256;         // compute units the dK/dV work is balanced over (MI355X)
 // MFMA backward workspace, ahead of the partial slots: two constants (+inf,
 // 0) that rows past a query block's end are copied from, then lse * log2e per
 // (query head, token) in the lse layout.

@@ -201,13 +201,26 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
 
   // ---- dK/dV items ---------------------------------------------------------
   // One item per (KV segment tile, KV head). On the MFMA path an item streams
-  // at most kDkdvMaxBlocks query blocks (its block table lives in LDS); a
-  // prefix tile whose query range is longer than kDkdvPrefixChunk blocks --
-  // the tile every sibling reads -- is split into chunks that each write an
-  // fp32 partial, summed afterwards in chunk (= leaf) order by a reduction
-  // item. The split also balances the dK/dV launch: an unsplit prefix tile
-  // carries N siblings' work.
+  // at most kDkdvMaxBlocks query blocks (its block table lives in LDS). A
+  // prefix tile -- the tile every sibling reads -- carries N siblings' work;
+  // when its query range exceeds about one CU's share of the whole launch
+  // (clamped to [kDkdvPrefixChunk, kDkdvMaxBlocks] blocks) it is split into
+  // chunks that each write an fp32 partial, summed afterwards in chunk (=
+  // leaf) order by a reduction item. Ranges that fit stay whole: no partials
+  // and no reduction.
   const int KT = path == PATH_MFMA ? kDkdvKeys : kSimtKeys;
+  int prefix_cap = kDkdvPrefixChunk;
+  if (path == PATH_MFMA) {
+    int64_t total = 0;  // query blocks streamed over all (tile, KV head) items
+    for (int n = 0; n < M; n++)
+      total += static_cast<int64_t>((no[n + 1] - no[n] + KT - 1) / KT) * Hkv *
+               (leaf_qblk[leaf_hi[n]] - leaf_qblk[leaf_lo[n]]);
+    for (int s = 0; s < N; s++)
+      for (int k0 = 0; k0 < cu[s + 1] - cu[s]; k0 += KT)
+        total += static_cast<int64_t>(Hkv) * (leaf_qblk[s + 1] - leaf_qblk[s] - k0 / BQ);
+    prefix_cap = static_cast<int>(std::min<int64_t>(kDkdvMaxBlocks,
+                                                    std::max<int64_t>(kDkdvPrefixChunk, total / kPlanCus)));
+  }
   std::vector<Item> dkdv;
   std::vector<int32_t> red;
   int32_t n_slots = 0, max_split = 1;
@@ -215,7 +228,7 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
     const int32_t range = hi - lo;
     int chunk = range;
     if (path == PATH_MFMA) {
-      const int cap = src == 0 ? kDkdvPrefixChunk : kDkdvMaxBlocks;
+      const int cap = src == 0 ? prefix_cap : kDkdvMaxBlocks;
       if (range > cap) {
         const int pieces = (range + cap - 1) / cap;
         chunk = (range + pieces - 1) / pieces;
