@@ -9,6 +9,8 @@ Public API:
   TPRPrefixAttention            autograd.Function (q, k, v, prefix_k, prefix_v, meta, scale) -> (out, lse)
   tpr_prefix_attention          functional form
   rectangular_causal_attention  drop-in for the reference's single-sequence operator
+  TPRKernelBackend              TPRAttentionBackend (parallel_size 1) for the model seam: one
+                                launch per layer for all sibling leaves of a parent
 """
 
 from .meta import LaunchPlan, TPRPrefixMeta
@@ -18,6 +20,7 @@ from .prefix_attention import (
     prefix_attention_forward,
     tpr_prefix_attention,
 )
+from .backend import TPRKernelBackend
 from .rectangular_attention import rectangular_causal_attention
 
 __all__ = [
@@ -28,4 +31,5 @@ __all__ = [
     "prefix_attention_forward",
     "prefix_attention_backward",
     "rectangular_causal_attention",
+    "TPRKernelBackend",
 ]
