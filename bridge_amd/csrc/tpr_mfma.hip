@@ -65,6 +65,41 @@ __device__ __forceinline__ bf16x8 lds_read_col8(const char* tile, int r0, int c0
   return r;
 }
 
+// Per-lane byte offsets, within a swizzled tile, of the forward's operand
+// reads. The swizzle of row r depends only on r mod 16, so rows 16m further
+// down are the same offsets plus 4096m: only the first 16 or 32 rows' offsets
+// are kept, and row blocks, buffers and tiles are immediate offsets.
+struct FwdLdsOffsets {
+  uint32_t k[8];     // K row sigma32(n), columns 16c + 8h .. +7 (c = 0..7)
+  uint32_t v[4][2];  // V rows 8h + (l%16)/4 (+4), column 32db + 16((l/16)&1) + 4(l%4)
+};
+
+__device__ __forceinline__ FwdLdsOffsets make_fwd_lds_offsets(int lane) {
+  FwdLdsOffsets o;
+  const int n = lane & 31, h = lane >> 5, g = lane >> 4, i = lane & 15;
+#pragma unroll
+  for (int c = 0; c < 8; c++) o.k[c] = static_cast<uint32_t>(swz_off(sigma32(n), 16 * c + 8 * h));
+#pragma unroll
+  for (int db = 0; db < 4; db++) {
+    const int row = 8 * h + (i >> 2), col = 32 * db + ((g & 1) << 4) + ((i & 3) << 2);
+    o.v[db][0] = static_cast<uint32_t>(swz_off(row, col));
+    o.v[db][1] = static_cast<uint32_t>(swz_off(row + 4, col));
+  }
+  return o;
+}
+
+// Transposed read of lds_read_col8 at precomputed offsets (lo: rows +0..3, hi: +4..7).
+__device__ __forceinline__ bf16x8 lds_col8_at(const char* base, uint32_t lo, uint32_t hi) {
+  const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + lo));
+  const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + hi));
+  bf16x8 r;
+  const bf16x4 l4 = __builtin_bit_cast(bf16x4, a);
+  const bf16x4 h4 = __builtin_bit_cast(bf16x4, b);
+  r[0] = l4[0]; r[1] = l4[1]; r[2] = l4[2]; r[3] = l4[3];
+  r[4] = h4[0]; r[5] = h4[1]; r[6] = h4[2]; r[7] = h4[3];
+  return r;
+}
+
 __device__ __forceinline__ bf16x8 to_bf16x8(const f32x16& x, int base) {
   bf16x8 r;
 #pragma unroll
@@ -255,6 +290,33 @@ __device__ __forceinline__ void dma_tile_s(const char* src, uint32_t row_bytes, 
   }
 }
 
+// Per-lane part of a 64-row tile copy by 4 waves, in two registers: lane l of
+// wave w moves, in block j = 0..3, row 16w + 4j + l/16 and the 16-byte source
+// chunk swz_chunk(row, l%16) = (l%16) ^ ((l/16) << 2) ^ j, i.e. chunk bytes
+// cb0 ^ 16j.
+struct TileLanes4 {
+  uint32_t row0;  // 16w + l/16
+  uint32_t cb0;   // 16 * ((l%16) ^ ((l/16) << 2))
+};
+
+__device__ __forceinline__ TileLanes4 make_tile_lanes4(int wave, int lane) {
+  return TileLanes4{static_cast<uint32_t>(16 * wave + (lane >> 4)),
+                    static_cast<uint32_t>(16 * ((lane & 15) ^ ((lane >> 4) << 2)))};
+}
+
+// Copy rows [0, 64) of the tile starting at `src` (uniform; rows at or beyond
+// `len` re-read row len - 1) into the swizzled LDS tile at `lds_tile`; this
+// wave moves its four 1 KiB blocks.
+__device__ __forceinline__ void dma_tile4(const char* src, uint32_t row_bytes, int len, uint32_t lds_tile,
+                                          TileLanes4 p, int wave) {
+  const uint32_t last = static_cast<uint32_t>(len - 1);
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const uint32_t row = min(p.row0 + 4u * j, last);
+    dma16s(src, row * row_bytes + (p.cb0 ^ (16u * j)), lds_tile + (wave * 4 + j) * 1024);
+  }
+}
+
 // Forward-only cursor over a workgroup's key stream (SegTable order). It
 // only changes segment at segment ends, so the common step is a compare.
 struct Cursor {
@@ -324,6 +386,13 @@ template <typename T>
 __device__ __forceinline__ void settle_acc(T& x) {
   asm volatile("" : "+a"(x));
 }
+// Make `x` final here: its computation stays before this point (it cannot be
+// sunk into a later block, e.g. past a workgroup barrier, towards its use).
+template <typename T>
+__device__ __forceinline__ void pin(T& x) {
+  asm volatile("" : "+v"(x));
+}
+
 
 // Calls f(std::integral_constant<int, i>) for i = 0 .. N-1, unrolled at
 // compile time (array indices derived from i are constants).
@@ -339,20 +408,24 @@ __device__ __forceinline__ void static_for(F&& f) {
 // ---------------------------------------------------------------------------
 // Forward
 //
-// Software-pipelined over 64-key tiles: iteration `it` computes the scores
-// of tile it+1 (S = K Q^T, MFMA) while it runs the softmax of tile it (VALU)
-// -- the two are independent, so the MFMA pipe and the VALU overlap -- and
-// then accumulates P V of tile it. K runs one tile ahead of V: the DMA of
-// iteration it fetches K of tile it+2 and V of tile it+1, so two K and two V
-// buffers (64 KiB) suffice and two workgroups fit on a CU.
+// The 8 waves form two groups of 4, one wave of each group per SIMD, that
+// alternate between two phases at every workgroup barrier:
+//   M(j): S[j+1] = K[j+1] Q^T and O += P[j] V[j]   (MFMA, LDS reads)
+//   V(j): P[j+1] = softmax(S[j+1]), rescaling O     (VALU only)
+// Group B runs one phase behind group A, so on every SIMD one wave's MFMAs
+// overlap the other wave's softmax. Group B also copies the K/V tiles: it
+// issues K[j+2] and V[j+1] at the start of its V(j-1) phase and waits for them
+// at the end of its M(j) phase, two barriers before group A reads them. K runs
+// one tile ahead of V; two K and two V buffers (64 KiB) suffice.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void qk_tile(const char* kt, const bf16x8 (&qv)[8], int n, int h, f32x16 (&s)[2]) {
+__device__ __forceinline__ void qk_tile(const char* kt, const bf16x8 (&qv)[8], const FwdLdsOffsets& lo,
+                                        f32x16 (&s)[2]) {
 #pragma unroll
   for (int kb = 0; kb < 2; kb++) {
     s[kb] = f32x16{};
-    const int krow = kb * 32 + sigma32(n);
 #pragma unroll
-    for (int c = 0; c < 8; c++) s[kb] = mfma(lds_read_b128(kt, krow, 16 * c + 8 * h), qv[c], s[kb]);
+    for (int c = 0; c < 8; c++)
+      s[kb] = mfma(*reinterpret_cast<const bf16x8*>(kt + kb * 32 * 256 + lo.k[c]), qv[c], s[kb]);
   }
 }
 
@@ -360,6 +433,11 @@ __device__ __forceinline__ void qk_tile(const char* kt, const bf16x8 (&qv)[8], i
 // when a row's max exceeds the max they are referenced to by more than this,
 // so unscaled probabilities stay <= 2^8 (exact arithmetic, fp32/bf16 safe).
 constexpr float kRescaleSlack = 8.f;
+
+#ifndef TPR_MPHASE_AHEAD
+#define TPR_MPHASE_AHEAD 4
+#endif
+constexpr int kMphaseAhead = TPR_MPHASE_AHEAD;  // LDS reads issued ahead in a forward M phase (even)
 
 __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
   const int32_t* item = a.plan + a.off_fwd + 4 * blockIdx.x;
@@ -370,6 +448,8 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
   const int row0 = cu[leaf], len = cu[leaf + 1] - cu[leaf];
 
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  static_assert(kFwdWaves == 8, "two groups of one wave per SIMD");
+  const int grp = wave >> 2;                         // 0: group A, 1: group B (copies the tiles)
   const int hpw = a.hpw;                             // query heads per workgroup
   const int head = qh0 + wave % hpw;
   const int tw0 = tok0 + kFwdTokens * (wave / hpw);  // first token of this wave
@@ -388,27 +468,26 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
   const char* vbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.v) + kvh * kMfmaD);
   const char* pkbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.pk) + kvh * kMfmaD);
   const char* pvbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.pv) + kvh * kMfmaD);
-  const DmaLanes<kFwdWaves> dl = make_dma_lanes<kFwdWaves>(row_bytes, wave, lane);
+  const TileLanes4 dl = make_tile_lanes4(wave & 3, lane);
+  const FwdLdsOffsets lo = make_fwd_lds_offsets(lane);
 
   const SegTable seg = load_segments(a, leaf, suffix_keys);
   const int ntiles = seg.ntiles;
-  Cursor cur = cursor_begin(seg);
-  TileLoc tl_cur = cursor_tile(cur), tl_v = tl_cur, tl_k = tl_cur;
   auto kv_src = [&](const TileLoc& x, bool is_k) {
     const char* b = x.suffix ? (is_k ? kbase : vbase) : (is_k ? pkbase : pvbase);
     return b + x.row * static_cast<int64_t>(row_bytes);
   };
-  dma_tile_s<kFwdWaves>(kv_src(tl_cur, true), row_bytes, tl_cur.len, lds0, dl, wave);
-  dma_tile_s<kFwdWaves>(kv_src(tl_cur, false), row_bytes, tl_cur.len, lds0 + 2 * kTileBytes, dl, wave);
+  // group B's copy cursor: the next K tile (tl_k) and the next V tile (tl_v)
+  Cursor dc = cursor_begin(seg);
+  TileLoc tl_k = cursor_tile(dc), tl_v = tl_k;
+  if (grp) dma_tile4(kv_src(tl_k, true), row_bytes, tl_k.len, lds0, dl, wave & 3);  // K[0]
   if (ntiles > 1) {
-    cursor_next(seg, cur);
-    tl_v = cursor_tile(cur);
-    dma_tile_s<kFwdWaves>(kv_src(tl_v, true), row_bytes, tl_v.len, lds0 + kTileBytes, dl, wave);
+    cursor_next(seg, dc);
+    tl_k = cursor_tile(dc);
   }
-  if (ntiles > 2) {
-    cursor_next(seg, cur);
-    tl_k = cursor_tile(cur);
-  }
+  // every wave's mask cursor: the tile whose scores the next V phase masks
+  Cursor mc = cursor_begin(seg);
+  TileLoc tl_m = cursor_tile(mc);
 
   // Q as the B operand of S^T = K Q^T: lane holds Q[t][16c + 8h .. +7]
   bf16x8 qv[8];
@@ -425,38 +504,65 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
   float m = -1e30f, l = 0.f;  // running max (raw score units) the O/l are referenced to
   const float c2 = a.scale * kLog2e;
   const float slack = kRescaleSlack / c2;
+  f32x16 s[2];
+  bf16x8 pb[2][2];
 
-#pragma unroll
-  for (int c = 0; c < 8; c++) settle(qv[c]);
-  wait_dma();
-  __syncthreads();
-  f32x16 sa[2], sb[2];
-  qk_tile(smem, qv, n, h, sa);
-  __syncthreads();  // every wave has read K0 before iteration 0 refills its buffer
-
-  // One pipeline step for tile `it` (parity P = it & 1): copies K[it+2] into
-  // K buffer P and V[it+1] into V buffer 1-P, computes S[it+1] from K buffer
-  // 1-P into `sn`, and runs softmax(S[it]) + P V[it] from V buffer P.
-  auto step = [&](auto par, int it, f32x16 (&s)[2], f32x16 (&sn)[2]) {
+  // group B, start of iteration j: copy K[j+2] into K buffer j&1 and V[j+1]
+  // into V buffer (j+1)&1
+  auto issue = [&](int j) {
+    if (j + 2 < ntiles)
+      dma_tile4(kv_src(tl_k, true), row_bytes, tl_k.len, lds0 + ((j + 2) & 1) * kTileBytes, dl, wave & 3);
+    if (j + 1 < ntiles)
+      dma_tile4(kv_src(tl_v, false), row_bytes, tl_v.len, lds0 + (2 + ((j + 1) & 1)) * kTileBytes, dl, wave & 3);
+    tl_v = tl_k;
+    if (j + 3 < ntiles) {
+      cursor_next(seg, dc);
+      tl_k = cursor_tile(dc);
+    }
+  };
+  // M(j): scores of tile j+1 (if with_s) and P[j] V[j] (if with_pv); par = j & 1
+  auto mphase = [&](auto with_s, auto with_pv, auto par) {
     constexpr int P = decltype(par)::value;
-    if (it + 2 < ntiles)
-      dma_tile_s<kFwdWaves>(kv_src(tl_k, true), row_bytes, tl_k.len, lds0 + P * kTileBytes, dl, wave);
-    if (it + 1 < ntiles)
-      dma_tile_s<kFwdWaves>(kv_src(tl_v, false), row_bytes, tl_v.len, lds0 + (3 - P) * kTileBytes, dl, wave);
-    // visibility of tile it: key kb*32 + 16*(r/8) + 8*h + r%8 <= lim. A tile
-    // entirely in this wave's future gets lim < 0 (nothing visible).
-    if (tl_cur.len < kTileRows || (tl_cur.suffix && tl_cur.pos0 + kTileRows - 1 > tw0)) {
-      int lim = tl_cur.len - 1 - 8 * h;
-      if (tl_cur.suffix) lim = min(lim, t - tl_cur.pos0 - 8 * h);
+    const char* kt = smem + (1 - P) * kTileBytes;
+    const char* vt = smem + (2 + P) * kTileBytes;
+    if constexpr (decltype(with_s)::value) qk_tile(kt, qv, lo, s);
+    if constexpr (decltype(with_pv)::value) {
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+        for (int cc = 0; cc < 2; cc++) {
+          const char* vr = vt + (kb * 32 + 16 * cc) * 256;
+#pragma unroll
+          for (int db = 0; db < 4; db++) o[db] = mfma(lds_col8_at(vr, lo.v[db][0], lo.v[db][1]), pb[kb][cc], o[db]);
+        }
+    }
+    if constexpr (decltype(with_s)::value && decltype(with_pv)::value) {
+      // 48 LDS reads (16 K rows, 32 transposed V halves) for 32 MFMAs: keep
+      // kMphaseAhead reads in flight ahead of the MFMA that consumes them
+      __builtin_amdgcn_sched_group_barrier(0x100, kMphaseAhead, 0);
+      static_for<(48 - kMphaseAhead) / 2>([&](auto) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      });
+      __builtin_amdgcn_sched_group_barrier(0x008, 32 - (48 - kMphaseAhead) / 2, 0);
+    }
+  };
+  // V(j): softmax of the scores of tile j+1 into pb, rescaling O and l
+  auto vphase = [&](int j) {
+    // visibility: key kb*32 + 16*(r/8) + 8*h + r%8 <= lim. A tile entirely in
+    // this wave's future gets lim < 0 (nothing visible).
+    if (tl_m.len < kTileRows || (tl_m.suffix && tl_m.pos0 + kTileRows - 1 > tw0)) {
+      int lim = tl_m.len - 1 - 8 * h;
+      if (tl_m.suffix) lim = min(lim, t - tl_m.pos0 - 8 * h);
 #pragma unroll
       for (int kb = 0; kb < 2; kb++)
 #pragma unroll
         for (int r = 0; r < 16; r++) s[kb][r] = (kb * 32 + 16 * (r >> 3) + (r & 7) <= lim) ? s[kb][r] : -INFINITY;
     }
-    // scores of tile it+1 (the last step recomputes a resident tile; unused)
-    qk_tile(smem + (1 - P) * kTileBytes, qv, n, h, sn);
-
-    // softmax of tile it (independent of the MFMAs above)
+    if (j + 2 < ntiles) {
+      cursor_next(seg, mc);
+      tl_m = cursor_tile(mc);
+    }
     float mt = s[0][0];
 #pragma unroll
     for (int kb = 0; kb < 2; kb++)
@@ -471,8 +577,7 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
 #pragma unroll
       for (int db = 0; db < 4; db++) o[db] *= alpha;
     }
-    const float mc = m * c2;
-    bf16x8 pb[2][2];
+    const float mc2 = m * c2;
     float ls = 0.f;
 #pragma unroll
     for (int kb = 0; kb < 2; kb++)
@@ -480,37 +585,83 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
       for (int cc = 0; cc < 2; cc++) {
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-          const float p = fast_exp2(fmaf(s[kb][8 * cc + i], c2, -mc));
+          const float p = fast_exp2(fmaf(s[kb][8 * cc + i], c2, -mc2));
           ls += p;  // fp32 row sum of the unrounded probabilities
           pb[kb][cc][i] = static_cast<bf16>(p);
         }
+        pin(pb[kb][cc]);
       }
     l += ls;
-    const char* vt = smem + (2 + P) * kTileBytes;
-#pragma unroll
-    for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-      for (int cc = 0; cc < 2; cc++) {
-        const int r0 = kb * 32 + 16 * cc + 8 * h;
-#pragma unroll
-        for (int db = 0; db < 4; db++) o[db] = mfma(lds_read_col8(vt, r0, 32 * db, lane), pb[kb][cc], o[db]);
-      }
-    wait_dma();
-    __syncthreads();
-    tl_cur = tl_v;
-    tl_v = tl_k;
-    if (it + 3 < ntiles) {
-      cursor_next(seg, cur);
-      tl_k = cursor_tile(cur);
-    }
   };
 
-  int it = 0;
-  for (; it + 1 < ntiles; it += 2) {
-    step(std::integral_constant<int, 0>{}, it, sa, sb);
-    step(std::integral_constant<int, 1>{}, it + 1, sb, sa);
+#pragma unroll
+  for (int c = 0; c < 8; c++) settle(qv[c]);
+  wait_dma();
+  __syncthreads();  // K[0] landed
+
+  // A workgroup barrier that also fences the instruction scheduler: the
+  // phases' register-only work (MFMAs, exps) must not migrate across it.
+  auto phase_barrier = [] {
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  constexpr std::true_type yes{};
+  constexpr std::false_type no{};
+  constexpr std::integral_constant<int, 0> even{};
+  constexpr std::integral_constant<int, 1> odd{};
+  // Both groups pass 2 * ntiles + 2 barriers; B's phase k runs between
+  // barriers k and k + 1, A's between barriers k - 1 and k. The tile loop is
+  // unrolled by two so that the buffer parity, and with it every LDS address
+  // offset, is a compile-time constant.
+  if (grp == 0) {
+    auto body = [&](auto par, int j) {
+      mphase(yes, yes, par);
+      phase_barrier();
+      vphase(j);
+      phase_barrier();
+    };
+    mphase(yes, no, odd);
+    phase_barrier();
+    vphase(-1);
+    phase_barrier();
+    int j = 0;
+    for (; j + 2 < ntiles; j += 2) {
+      body(even, j);
+      body(odd, j + 1);
+    }
+    if (j + 1 < ntiles) body(even, j++);
+    if (j & 1) mphase(no, yes, odd);
+    else mphase(no, yes, even);
+    phase_barrier();
+    phase_barrier();
+  } else {
+    auto body = [&](auto par, int j) {
+      issue(j);
+      vphase(j - 1);
+      phase_barrier();
+      mphase(yes, yes, par);
+      __builtin_amdgcn_sched_barrier(0);
+      wait_dma();
+      phase_barrier();
+    };
+    issue(-1);
+    phase_barrier();
+    mphase(yes, no, odd);
+    wait_dma();
+    phase_barrier();
+    int j = 0;
+    for (; j + 2 < ntiles; j += 2) {
+      body(even, j);
+      body(odd, j + 1);
+    }
+    if (j + 1 < ntiles) body(even, j++);
+    vphase(j - 1);
+    phase_barrier();
+    if (j & 1) mphase(no, yes, odd);
+    else mphase(no, yes, even);
+    phase_barrier();
   }
-  if (it < ntiles) step(std::integral_constant<int, 0>{}, it, sa, sb);
 
   const float lt = wave_sum32(l);  // all 64 lanes take part in the exchange
   if (tw0 >= len || t >= len) return;
