@@ -88,6 +88,28 @@ __device__ __forceinline__ FwdLdsOffsets make_fwd_lds_offsets(int lane) {
   return o;
 }
 
+// The same offsets from three base registers: the swizzle's XOR only changes
+// bits 5-7 of an offset within a 256-byte row, so row read c is at
+// k ^ 32c and transposed read db at v[x] ^ 64db (x = 0: rows +0..3, 1: +4..7).
+// The per-read XOR is one VALU op in place of a register per offset; `opaque`
+// keeps the compiler from hoisting the XORs back into registers.
+struct LdsBases {
+  uint32_t k;
+  uint32_t v[2];
+};
+
+__device__ __forceinline__ LdsBases make_lds_bases(int lane, uint32_t k_bias, uint32_t v_bias) {
+  const int n = lane & 31, h = lane >> 5, g = lane >> 4, i = lane & 15;
+  const int row = 8 * h + (i >> 2), col = ((g & 1) << 4) + ((i & 3) << 2);
+  return LdsBases{k_bias + static_cast<uint32_t>(swz_off(sigma32(n), 8 * h)),
+                  {v_bias + static_cast<uint32_t>(swz_off(row, col)),
+                   v_bias + static_cast<uint32_t>(swz_off(row + 4, col))}};
+}
+
+__device__ __forceinline__ void opaque(LdsBases& b) {
+  asm volatile("" : "+v"(b.k), "+v"(b.v[0]), "+v"(b.v[1]));
+}
+
 // Transposed read of lds_read_col8 at precomputed offsets (lo: rows +0..3, hi: +4..7).
 __device__ __forceinline__ bf16x8 lds_col8_at(const char* base, uint32_t lo, uint32_t hi) {
   const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + lo));
@@ -712,11 +734,33 @@ __global__ __launch_bounds__(256) void mfma_delta(KernelArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// dQ: same workgroup shape and key stream as the forward.
-//   S^T = K Q^T, P^T = exp(scale S^T - lse), dP^T = V dO^T,
-//   dS^T = P^T (dP^T - delta), dQ^T += K^T dS^T, dQ = scale * dQ.
+// dQ: same workgroup shape, key stream and two-group ping-pong as the forward.
+//   M(j): dQ^T += K[j]^T dS^T[j], S^T[j+1] = K[j+1] Q^T, dP^T[j+1] = V[j+1] dO^T
+//   V(j): dS^T[j+1] = P^T (dP^T - delta), P^T = exp(scale S^T - lse)
+// dQ = scale * dQ at the end. The A operand of dQ^T is K^T: instead of every
+// wave reading K column-wise (ds_read_tr16_b64, several times slower than row
+// reads), group A's V(j) phase transposes K[j+1] once into a K^T tile
+// (rows = head dims, 64 keys each) that all waves then read row-wise. Group B
+// copies K[j+2] and V[j+2] at the start of its V(j-1) phase and waits for them
+// at the end of its M(j). Two buffers each of K, V and K^T (96 KiB).
 // ---------------------------------------------------------------------------
+constexpr int kKtRowBytes = 128;  // K^T tile: 128 rows (head dims) x 64 keys
+
+// Byte offset of 16-byte chunk `chunk` (keys 8*chunk..+7) of row d of a K^T
+// tile. A 128-byte row covers half the 64 banks, so rows d and d + 1 sit in
+// opposite halves; XOR-ing the chunk with (d >> 1) & 7 puts the 16 rows that
+// a row-wise b128 access touches per pass on 16 distinct 16-byte bank groups.
+__device__ __forceinline__ uint32_t kt_off(int d, int chunk) {
+  return static_cast<uint32_t>(d * kKtRowBytes + ((chunk ^ ((d >> 1) & 7)) << 4));
+}
+
+#ifndef TPR_DQ_AHEAD
+#define TPR_DQ_AHEAD 4
+#endif
+constexpr int kDqAhead = TPR_DQ_AHEAD;  // LDS reads issued ahead in a dQ M phase
+
 __global__ __launch_bounds__(512) void mfma_dq(KernelArgs a) {
+  static_assert(kFwdWaves == 8, "two groups of one wave per SIMD");
   const int32_t* item = a.plan + a.off_fwd + 4 * blockIdx.x;
   const int leaf = item[0];
   if (leaf < 0) return;
@@ -725,6 +769,7 @@ __global__ __launch_bounds__(512) void mfma_dq(KernelArgs a) {
   const int row0 = cu[leaf], len = cu[leaf + 1] - cu[leaf];
 
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = wave >> 2;                         // 0: group A (transposes K), 1: group B (copies)
   const int hpw = a.hpw;
   const int head = qh0 + wave % hpw;
   const int tw0 = tok0 + kFwdTokens * (wave / hpw);
@@ -733,25 +778,46 @@ __global__ __launch_bounds__(512) void mfma_dq(KernelArgs a) {
   const int n = lane & 31, h = lane >> 5;
   const int t = tw0 + n;
   const int tc = min(t, len - 1);
-  const bool wave_active = tw0 < len;
 
   const int64_t qstride = static_cast<int64_t>(a.hq) * kMfmaD;
-  const int64_t kstride = static_cast<int64_t>(a.hkv) * kMfmaD;
+  const uint32_t row_bytes = static_cast<uint32_t>(a.hkv) * kMfmaD * 2;
 
-  __shared__ __attribute__((aligned(1024))) char smem[4 * kTileBytes];
+  // K0 K1 V0 V1 (row-major, swizzled) | T0 T1 (K^T)
+  __shared__ __attribute__((aligned(1024))) char smem[6 * kTileBytes];
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(smem));
+  constexpr int kT = 4 * kTileBytes;  // K^T buffers
 
-  const bf16* kbase = static_cast<const bf16*>(a.k) + kvh * kMfmaD;
-  const bf16* vbase = static_cast<const bf16*>(a.v) + kvh * kMfmaD;
-  const bf16* pkbase = static_cast<const bf16*>(a.pk) + kvh * kMfmaD;
-  const bf16* pvbase = static_cast<const bf16*>(a.pv) + kvh * kMfmaD;
+  const char* kbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.k) + kvh * kMfmaD);
+  const char* vbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.v) + kvh * kMfmaD);
+  const char* pkbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.pk) + kvh * kMfmaD);
+  const char* pvbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.pv) + kvh * kMfmaD);
+  const TileLanes4 dl = make_tile_lanes4(wave & 3, lane);
+  // K/V row reads (A operands of S, dP) and, for group A, the transposing reads
+  const FwdLdsOffsets lo = make_fwd_lds_offsets(lane);
+  // K^T reads (A operand of dQ^T): row 32db + n, keys 32kb + 16cc + 8h: the
+  // offset is ktb ^ (64kb + 32cc) + 4096db (+ buffer), as the swizzle of row
+  // 32db + n is that of row n
+  uint32_t ktb = static_cast<uint32_t>(kT) + kt_off(n, h);
 
   const SegTable seg = load_segments(a, leaf, suffix_keys);
   const int ntiles = seg.ntiles;
-  {
-    const TileLoc tl = locate_tile(seg, 0);
-    dma_tile<kFwdWaves>(tl.suffix ? kbase : pkbase, kstride, tl.row, tl.len, smem, wave, lane);
-    dma_tile<kFwdWaves>(tl.suffix ? vbase : pvbase, kstride, tl.row, tl.len, smem + kTileBytes, wave, lane);
+  auto kv_src = [&](const TileLoc& x, bool is_k) __attribute__((always_inline)) {
+    const char* b = x.suffix ? (is_k ? kbase : vbase) : (is_k ? pkbase : pvbase);
+    return b + x.row * static_cast<int64_t>(row_bytes);
+  };
+  // group B's copy cursor: the next tile whose K and V it copies
+  Cursor dc = cursor_begin(seg);
+  TileLoc tl_c = cursor_tile(dc);
+  if (grp) {
+    dma_tile4(kv_src(tl_c, true), row_bytes, tl_c.len, lds0, dl, wave & 3);
+    dma_tile4(kv_src(tl_c, false), row_bytes, tl_c.len, lds0 + 2 * kTileBytes, dl, wave & 3);
   }
+  if (ntiles > 1) {
+    cursor_next(seg, dc);
+    tl_c = cursor_tile(dc);
+  }
+  Cursor mc = cursor_begin(seg);
+  TileLoc tl_m = cursor_tile(mc);
 
   bf16x8 qv[8], gv[8];
   {
@@ -772,6 +838,123 @@ __global__ __launch_bounds__(512) void mfma_dq(KernelArgs a) {
   f32x16 dq[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) dq[i] = f32x16{};
+  f32x16 s[2], dp[2];
+  bf16x8 dsb[2][2];
+
+  // group B, start of iteration j: copy K[j+2] and V[j+2] into buffers j & 1
+  auto issue = [&](int j) __attribute__((always_inline)) {
+    if (j + 2 < ntiles) {
+      const int b = j & 1;
+      dma_tile4(kv_src(tl_c, true), row_bytes, tl_c.len, lds0 + b * kTileBytes, dl, wave & 3);
+      dma_tile4(kv_src(tl_c, false), row_bytes, tl_c.len, lds0 + (2 + b) * kTileBytes, dl, wave & 3);
+    }
+    if (j + 3 < ntiles) {
+      cursor_next(seg, dc);
+      tl_c = cursor_tile(dc);
+    }
+  };
+  // group A wave w: rows 32w..32w+31 of K^T[x] from K[x] (buffer parity P):
+  // four column reads of 16 keys x 32 dims, one 16-byte chunk per lane each
+  auto transpose_k = [&](auto par) __attribute__((always_inline)) {
+    constexpr int P = decltype(par)::value;
+    const char* src = smem + P * kTileBytes;
+    char* dst = smem + kT + P * kTileBytes;
+    const int d = 32 * (wave & 3) + n;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      const bf16x8 x = lds_col8_at(src + 16 * g * 256, lo.v[wave & 3][0], lo.v[wave & 3][1]);
+      *reinterpret_cast<bf16x8*>(dst + kt_off(d, 2 * g + h)) = x;
+    }
+  };
+  // M(j), P = j & 1: S, dP of tile j+1 (if with_sd) and dQ += dS[j] K[j] (if with_dq)
+  auto mphase = [&](auto with_sd, auto with_dq, auto par) __attribute__((always_inline)) {
+    constexpr int P = decltype(par)::value;
+    const char* kn = smem + (1 - P) * kTileBytes;        // K[j+1]
+    const char* vn = smem + (3 - P) * kTileBytes;        // V[j+1]
+    const char* kt = smem + P * kTileBytes;              // K^T[j] (+ kT in ktb)
+    if constexpr (decltype(with_dq)::value) {
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+        for (int cc = 0; cc < 2; cc++) {
+          const uint32_t o = ktb ^ static_cast<uint32_t>(64 * kb + 32 * cc);
+#pragma unroll
+          for (int db = 0; db < 4; db++)
+            dq[db] = mfma(*reinterpret_cast<const bf16x8*>(kt + 4096 * db + o), dsb[kb][cc], dq[db]);
+        }
+    }
+    if constexpr (decltype(with_sd)::value) {
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++) {
+        s[kb] = f32x16{};
+        dp[kb] = f32x16{};
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+          s[kb] = mfma(*reinterpret_cast<const bf16x8*>(kn + kb * 32 * 256 + lo.k[c]), qv[c], s[kb]);
+          dp[kb] = mfma(*reinterpret_cast<const bf16x8*>(vn + kb * 32 * 256 + lo.k[c]), gv[c], dp[kb]);
+        }
+      }
+    }
+    if constexpr (kDqAhead > 0 && decltype(with_sd)::value && decltype(with_dq)::value) {
+      // 48 row reads for 48 MFMAs: keep kDqAhead reads in flight
+      __builtin_amdgcn_sched_group_barrier(0x100, kDqAhead, 0);
+      static_for<48 - kDqAhead>([&](auto) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      });
+      __builtin_amdgcn_sched_group_barrier(0x008, kDqAhead, 0);
+    }
+  };
+  // V(j): dS of tile j+1 into dsb
+  auto vphase = [&](int j) __attribute__((always_inline)) {
+    if (tl_m.len < kTileRows || (tl_m.suffix && tl_m.pos0 + kTileRows - 1 > tw0)) {
+      int lim = tl_m.len - 1 - 8 * h;
+      if (tl_m.suffix) lim = min(lim, t - tl_m.pos0 - 8 * h);
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) s[kb][r] = (kb * 32 + 16 * (r >> 3) + (r & 7) <= lim) ? s[kb][r] : -INFINITY;
+    }
+    if (j + 2 < ntiles) {
+      cursor_next(seg, mc);
+      tl_m = cursor_tile(mc);
+    }
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+      for (int cc = 0; cc < 2; cc++) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          const float p = fast_exp2(fmaf(s[kb][8 * cc + i], c2, -lse2));
+          dsb[kb][cc][i] = static_cast<bf16>(p * (dp[kb][8 * cc + i] - delta));
+        }
+        pin(dsb[kb][cc]);
+      }
+  };
+  auto phase_barrier = [] {
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  constexpr std::true_type yes{};
+  constexpr std::false_type no{};
+  constexpr std::integral_constant<int, 0> even{};
+  constexpr std::integral_constant<int, 1> odd{};
+  // Every wave runs every phase: a tile it does not see is masked to P = 0
+  // (dS = 0). One M-phase body per buffer parity keeps the live registers
+  // within the two-waves-per-SIMD budget.
+  auto last_m = [&]() __attribute__((always_inline)) {
+    if ((ntiles - 1) & 1) mphase(no, yes, odd);
+    else mphase(no, yes, even);
+  };
+  auto run = [&](auto body) __attribute__((always_inline)) {
+    int j = 0;
+    for (; j + 2 < ntiles; j += 2) {
+      body(even, j);
+      body(odd, j + 1);
+    }
+    if (j + 1 < ntiles) body(even, j);
+  };
 
 #pragma unroll
   for (int c = 0; c < 8; c++) {
@@ -781,60 +964,50 @@ __global__ __launch_bounds__(512) void mfma_dq(KernelArgs a) {
   settle(lse2);
   settle(delta);
   wait_dma();
-  __syncthreads();
+  __syncthreads();  // K[0], V[0] landed
 
-  for (int it = 0; it < ntiles; it++) {
-    const char* kt = smem + (it & 1) * 2 * kTileBytes;
-    const char* vt = kt + kTileBytes;
-    const TileLoc tl = locate_tile(seg, it);
-    if (it + 1 < ntiles) {
-      const TileLoc nx = locate_tile(seg, it + 1);
-      char* nk = smem + ((it + 1) & 1) * 2 * kTileBytes;
-      dma_tile<kFwdWaves>(nx.suffix ? kbase : pkbase, kstride, nx.row, nx.len, nk, wave, lane);
-      dma_tile<kFwdWaves>(nx.suffix ? vbase : pvbase, kstride, nx.row, nx.len, nk + kTileBytes, wave, lane);
-    }
-    const bool skip = !wave_active || (tl.suffix && tl.pos0 > tw0 + kFwdTokens - 1);
-    if (!skip) {
-      f32x16 s[2], dp[2];
-#pragma unroll
-      for (int kb = 0; kb < 2; kb++) {
-        s[kb] = f32x16{};
-        dp[kb] = f32x16{};
-        const int krow = kb * 32 + sigma32(n);
-#pragma unroll
-        for (int c = 0; c < 8; c++) {
-          s[kb] = mfma(lds_read_b128(kt, krow, 16 * c + 8 * h), qv[c], s[kb]);
-          dp[kb] = mfma(lds_read_b128(vt, krow, 16 * c + 8 * h), gv[c], dp[kb]);
-        }
-      }
-      int lim = 1 << 30;
-      if (tl.len < kTileRows || (tl.suffix && tl.pos0 + kTileRows - 1 > tw0)) {
-        lim = tl.len - 1 - 8 * h;
-        if (tl.suffix) lim = min(lim, t - tl.pos0 - 8 * h);
-      }
-#pragma unroll
-      for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-          float p = fast_exp2(fmaf(s[kb][r], c2, -lse2));
-          p = (kb * 32 + 16 * (r >> 3) + (r & 7) <= lim) ? p : 0.f;
-          s[kb][r] = p * (dp[kb][r] - delta);  // dS^T
-        }
-#pragma unroll
-      for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-        for (int cc = 0; cc < 2; cc++) {
-          const bf16x8 dsb = to_bf16x8(s[kb], 8 * cc);
-          const int r0 = kb * 32 + 16 * cc + 8 * h;
-#pragma unroll
-          for (int db = 0; db < 4; db++) dq[db] = mfma(lds_read_col8(kt, r0, 32 * db, lane), dsb, dq[db]);
-        }
-    }
+  // Both groups pass 2 * ntiles + 2 barriers, B one phase behind A. A's V(j)
+  // also transposes K[j+1] (buffer parity of j + 1).
+  if (grp == 0) {
+    mphase(yes, no, odd);
+    phase_barrier();
+    transpose_k(even);
+    vphase(-1);
+    phase_barrier();
+    run([&](auto par, int j) __attribute__((always_inline)) {
+      constexpr int P = decltype(par)::value;
+      mphase(yes, yes, par);
+      phase_barrier();
+      if (j + 1 < ntiles) transpose_k(std::integral_constant<int, 1 - P>{});
+      vphase(j);
+      phase_barrier();
+    });
+    last_m();
+    phase_barrier();
+    phase_barrier();
+  } else {
+    issue(-1);
+    phase_barrier();
+    mphase(yes, no, odd);
+    __builtin_amdgcn_sched_barrier(0);
     wait_dma();
-    __syncthreads();
+    phase_barrier();
+    run([&](auto par, int j) __attribute__((always_inline)) {
+      issue(j);
+      vphase(j - 1);
+      phase_barrier();
+      mphase(yes, yes, par);
+      __builtin_amdgcn_sched_barrier(0);
+      wait_dma();
+      phase_barrier();
+    });
+    vphase(ntiles - 2);
+    phase_barrier();
+    last_m();
+    phase_barrier();
   }
 
-  if (!wave_active || t >= len) return;
+  if (tw0 >= len || t >= len) return;
   bf16* dst = static_cast<bf16*>(a.dq) + static_cast<int64_t>(row0 + t) * qstride + head * kMfmaD;
 #pragma unroll
   for (int db = 0; db < 4; db++)
