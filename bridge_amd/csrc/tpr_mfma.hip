@@ -65,8 +65,8 @@ __device__ __forceinline__ bf16x8 lds_read_col8(const char* tile, int r0, int c0
   return r;
 }
 
-// Per-lane byte offsets, within a swizzled tile, of the forward's operand
-// reads. The swizzle of row r depends only on r mod 16, so rows 16m further
+// Per-lane byte offsets, within a swizzled tile (plus `bias`), of the
+// operand reads. The swizzle of row r depends only on r mod 16, so rows 16m further
 // down are the same offsets plus 4096m: only the first 16 or 32 rows' offsets
 // are kept, and row blocks, buffers and tiles are immediate offsets.
 struct FwdLdsOffsets {
@@ -74,16 +74,16 @@ struct FwdLdsOffsets {
   uint32_t v[4][2];  // V rows 8h + (l%16)/4 (+4), column 32db + 16((l/16)&1) + 4(l%4)
 };
 
-__device__ __forceinline__ FwdLdsOffsets make_fwd_lds_offsets(int lane) {
+__device__ __forceinline__ FwdLdsOffsets make_fwd_lds_offsets(int lane, uint32_t bias = 0) {
   FwdLdsOffsets o;
   const int n = lane & 31, h = lane >> 5, g = lane >> 4, i = lane & 15;
 #pragma unroll
-  for (int c = 0; c < 8; c++) o.k[c] = static_cast<uint32_t>(swz_off(sigma32(n), 16 * c + 8 * h));
+  for (int c = 0; c < 8; c++) o.k[c] = bias + static_cast<uint32_t>(swz_off(sigma32(n), 16 * c + 8 * h));
 #pragma unroll
   for (int db = 0; db < 4; db++) {
     const int row = 8 * h + (i >> 2), col = 32 * db + ((g & 1) << 4) + ((i & 3) << 2);
-    o.v[db][0] = static_cast<uint32_t>(swz_off(row, col));
-    o.v[db][1] = static_cast<uint32_t>(swz_off(row + 4, col));
+    o.v[db][0] = bias + static_cast<uint32_t>(swz_off(row, col));
+    o.v[db][1] = bias + static_cast<uint32_t>(swz_off(row + 4, col));
   }
   return o;
 }
@@ -223,15 +223,8 @@ __device__ __forceinline__ void dma16(const void* src, uint32_t lds_dst) {
 
 // One dword per lane, lane l's landing at lds_dst + 4*l (global_load_lds_dword).
 __device__ __forceinline__ void dma4(const void* src, uint32_t lds_dst) {
-  uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %2\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dword %1, off\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "v"(src), "s"(lds_dst));
+  lds_dst = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(lds_dst)));
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(uintptr_t)lds_dst, 4, 0, 0);
 }
 
 template <int kWaves>
@@ -271,6 +264,17 @@ __device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, uint32_
       : "v"(voff), "s"(sbase), "s"(lds_dst));
 }
 
+// The same copy through the compiler's builtin, which manages M0 itself (no
+// save/restore around every copy); its placement is left to the scheduler.
+__device__ __forceinline__ void dma16sb(const void* sbase, uint32_t voff, uint32_t lds_dst) {
+  const uint64_t b = reinterpret_cast<uint64_t>(sbase);
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(b >> 32)));
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(b & 0xffffffffu)));
+  const char* bs = reinterpret_cast<const char*>((static_cast<uint64_t>(hi) << 32) | static_cast<uint64_t>(lo));
+  lds_dst = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(lds_dst)));
+  __builtin_amdgcn_global_load_lds(bs + voff, (__attribute__((address_space(3))) void*)(uintptr_t)lds_dst, 16, 0, 0);
+}
+
 // Per-lane part of a 64-row tile copy: which row / chunk this lane moves in
 // each of its 16 / kWaves DMA blocks, and the resulting byte offset for a
 // full tile (row stride `row_bytes`).
@@ -303,11 +307,11 @@ __device__ __forceinline__ void dma_tile_s(const char* src, uint32_t row_bytes, 
   constexpr int kBlocks = DmaLanes<kWaves>::kBlocks;
   if (len >= kTileRows) {
 #pragma unroll
-    for (int j = 0; j < kBlocks; j++) dma16s(src, p.voff[j], lds_tile + (wave * kBlocks + j) * 1024);
+    for (int j = 0; j < kBlocks; j++) dma16sb(src, p.voff[j], lds_tile + (wave * kBlocks + j) * 1024);
   } else {
 #pragma unroll
     for (int j = 0; j < kBlocks; j++)
-      dma16s(src, static_cast<uint32_t>(min(p.row[j], len - 1)) * row_bytes + p.cbytes[j],
+      dma16sb(src, static_cast<uint32_t>(min(p.row[j], len - 1)) * row_bytes + p.cbytes[j],
              lds_tile + (wave * kBlocks + j) * 1024);
   }
 }
@@ -1155,7 +1159,14 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
   // sub-block j iff qi >= lim - 32j; other stages skip the mask. Queries past
   // the block end carry lse = +inf, so their P and dS are exactly 0.
   constexpr int kAhead = 4;
-  auto stage = [&](auto diag, const char* qt, const char* gt, const float* st, int lim) __attribute__((always_inline)) {
+  // Lane offsets of the operand reads; the second set carries a 64 KiB bias so
+  // that the reads of stage buffer 1 (at 64 KiB when kHeads is 2) keep their
+  // constant part within the 16-bit LDS instruction offset.
+  constexpr uint32_t kBuf1Bias = kHeads * 2 * kTileBytes >= 65536 ? 65536u : 0u;
+  const FwdLdsOffsets lo0 = make_fwd_lds_offsets(lane);
+  const FwdLdsOffsets lo1 = make_fwd_lds_offsets(lane, kBuf1Bias);
+  auto stage = [&](auto diag, const char* qt, const char* gt, const float* st, int lim,
+                   const FwdLdsOffsets& lo) __attribute__((always_inline)) {
     bf16x8 rq[2][8], rg[2][8], cg[2][2][4], cq[2][2][4];
     f32x4 l2v[2][4], dlv[2][4];
     f32x16 sc[2], dpv[2];
@@ -1164,16 +1175,18 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
     // operands of MFMA m (sub-block m / 32, position m % 32)
     auto read_for = [&](auto mc) __attribute__((always_inline)) {
       constexpr int m = decltype(mc)::value, j = m >> 5, k = m & 31;
+      // rows 32j + sigma32(n) and the 16-row groups of the column reads are
+      // the lane offsets of lo plus 8192j / 4096(2j + cc) (immediates)
       if constexpr (k < 8) {
-        rq[j][k] = lds_read_b128(qt, 32 * j + sigma32(n), 16 * k + 8 * h);
+        rq[j][k] = *reinterpret_cast<const bf16x8*>(qt + 8192 * j + lo.k[k]);
       } else if constexpr (k < 16) {
-        rg[j][k - 8] = lds_read_b128(gt, 32 * j + sigma32(n), 16 * (k - 8) + 8 * h);
+        rg[j][k - 8] = *reinterpret_cast<const bf16x8*>(gt + 8192 * j + lo.k[k - 8]);
       } else if constexpr (k < 24) {
         constexpr int cc = (k - 16) >> 2, db = (k - 16) & 3;
-        cg[j][cc][db] = lds_read_col8(gt, 32 * j + 16 * cc + 8 * h, 32 * db, lane);
+        cg[j][cc][db] = lds_col8_at(gt + 4096 * (2 * j + cc), lo.v[db][0], lo.v[db][1]);
       } else {
         constexpr int cc = (k - 24) >> 2, db = (k - 24) & 3;
-        cq[j][cc][db] = lds_read_col8(qt, 32 * j + 16 * cc + 8 * h, 32 * db, lane);
+        cq[j][cc][db] = lds_col8_at(qt + 4096 * (2 * j + cc), lo.v[db][0], lo.v[db][1]);
       }
     };
     // lse*log2e (which 0) or delta (which 1) of the lane's 16 queries of sub-block j
@@ -1222,12 +1235,22 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
     };
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
-    static_for<kAhead>([&](auto mc) __attribute__((always_inline)) { read_for(mc); });
+    // Reads are issued in pairs, the later slot's first: LDS reads complete in
+    // order, so the wait before the earlier slot's MFMA covers both and the
+    // later slot's MFMA needs none.
+    static_for<kAhead / 2>([&](auto pc) __attribute__((always_inline)) {
+      constexpr int q = 2 * decltype(pc)::value;
+      read_for(std::integral_constant<int, q + 1>{});
+      read_for(std::integral_constant<int, q>{});
+    });
     read_stats(I0{}, I0{});
     static_for<64>([&](auto mc) __attribute__((always_inline)) {
       constexpr int m = decltype(mc)::value, j = m >> 5, k = m & 31;
       using J = std::integral_constant<int, j>;
-      if constexpr (m + kAhead < 64) read_for(std::integral_constant<int, m + kAhead>{});
+      if constexpr (m % 2 == 0 && m + kAhead + 1 < 64) {
+        read_for(std::integral_constant<int, m + kAhead + 1>{});
+        read_for(std::integral_constant<int, m + kAhead>{});
+      }
       if constexpr (j == 1 && k == 2) read_stats(I1{}, I0{});
       if constexpr (k == 10) read_stats(J{}, I1{});
       mfma_at(mc);
@@ -1242,30 +1265,47 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
 
   // Stages [sidx, end) of the stage loop, with (diag) or without the causal
   // mask in the body.
-  auto run_stages = [&](auto diag, int sidx, int end) __attribute__((always_inline)) {
-    for (; sidx < end; sidx++) {
-      const int buf = sidx & 1;
-      int row0, tok0, nq, qh;
-      stage_info(sidx, row0, tok0, nq, qh);
-      if (sidx + 1 < nstage) issue(sidx + 1, buf ^ 1);
-      if (wave_active) {
-        // key kp is visible from query index qi (of the stage) iff qi >= lim;
-        // off this wave's diagonal lim <= -64 (all visible)
-        const int lim = tok0 < kw0 + 31 ? kp - tok0 - 8 * h : -64;
+  // one stage; the buffer parity is a compile-time constant so that every
+  // LDS address in the stage is a precomputed lane offset plus an immediate
+  auto one_stage = [&](auto diag, auto bufc, int sidx) __attribute__((always_inline)) {
+    constexpr int buf = decltype(bufc)::value;
+    int row0, tok0, nq, qh;
+    stage_info(sidx, row0, tok0, nq, qh);
+    if (sidx + 1 < nstage) issue(sidx + 1, buf ^ 1);
+    if (wave_active) {
+      // key kp is visible from query index qi (of the stage) iff qi >= lim;
+      // off this wave's diagonal lim <= -64 (all visible)
+      const int lim = tok0 < kw0 + 31 ? kp - tok0 - 8 * h : -64;
 #pragma unroll
-        for (int hh = 0; hh < kHeads; hh++) {
-          const char* qt = smem + (buf * kHeads + hh) * 2 * kTileBytes;
-          stage(diag, qt, qt + kTileBytes, &stats[buf][hh][0][0], lim);
-        }
+      for (int hh = 0; hh < kHeads; hh++) {
+        // tile pointer minus the bias of the offset set used for this buffer
+        const char* qt = smem + (buf * kHeads + hh) * 2 * kTileBytes - (buf ? kBuf1Bias : 0u);
+        if constexpr (buf) stage(diag, qt, qt + kTileBytes, &stats[buf][hh][0][0], lim, lo1);
+        else stage(diag, qt, qt + kTileBytes, &stats[buf][hh][0][0], lim, lo0);
       }
-#pragma unroll
-      for (int i = 0; i < 4; i++) {  // accumulators stay in AGPRs across the stage loop
-        settle_acc(dk[i]);
-        settle_acc(dv[i]);
-      }
-      wait_dma();  // stage sidx + 1 has landed
-      __syncthreads();
     }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {  // accumulators stay in AGPRs across the stage loop
+      settle_acc(dk[i]);
+      settle_acc(dv[i]);
+    }
+#pragma unroll
+    for (int c = 0; c < 8; c++) {  // so do the K/V operands (MFMAs read them there)
+      settle_acc(kv[c]);
+      settle_acc(vv[c]);
+    }
+    wait_dma();  // stage sidx + 1 has landed
+    __syncthreads();
+  };
+  auto run_stages = [&](auto diag, int sidx, int end) __attribute__((always_inline)) {
+    constexpr std::integral_constant<int, 0> b0{};
+    constexpr std::integral_constant<int, 1> b1{};
+    if (sidx < end && (sidx & 1)) one_stage(diag, b1, sidx++);
+    for (; sidx + 1 < end; sidx += 2) {
+      one_stage(diag, b0, sidx);
+      one_stage(diag, b1, sidx + 1);
+    }
+    if (sidx < end) one_stage(diag, b0, sidx);
   };
   // (suffix) the leading stages whose query block crosses some wave's causal
   // diagonal run with the mask, all later ones without it
