@@ -751,11 +751,14 @@ __global__ __launch_bounds__(256) void mfma_delta(KernelArgs a) {
 constexpr int kKtRowBytes = 128;  // K^T tile: 128 rows (head dims) x 64 keys
 
 // Byte offset of 16-byte chunk `chunk` (keys 8*chunk..+7) of row d of a K^T
-// tile. A 128-byte row covers half the 64 banks, so rows d and d + 1 sit in
-// opposite halves; XOR-ing the chunk with (d >> 1) & 7 puts the 16 rows that
-// a row-wise b128 access touches per pass on 16 distinct 16-byte bank groups.
+// tile. The chunk is XOR-ed with ((d >> 1) & 7) ^ ((d & 1) << 2): measured
+// on gfx950 (LDS bank-conflict counter, one wave writing / reading this
+// pattern), this leaves both the transposing b128 writes (lane l: row l % 32,
+// chunk l / 32) and the row-wise b128 reads of the dQ MFMA free of bank
+// conflicts, where (d >> 1) & 7 alone costs 8 conflict cycles per write and
+// d & 7 alone 4 per read.
 __device__ __forceinline__ uint32_t kt_off(int d, int chunk) {
-  return static_cast<uint32_t>(d * kKtRowBytes + ((chunk ^ ((d >> 1) & 7)) << 4));
+  return static_cast<uint32_t>(d * kKtRowBytes + ((chunk ^ ((d >> 1) & 7) ^ ((d & 1) << 2)) << 4));
 }
 
 #ifndef TPR_DQ_AHEAD
@@ -802,6 +805,16 @@ __global__ __launch_bounds__(512) void mfma_dq(KernelArgs a) {
   // offset is ktb ^ (64kb + 32cc) + 4096db (+ buffer), as the swizzle of row
   // 32db + n is that of row n
   uint32_t ktb = static_cast<uint32_t>(kT) + kt_off(n, h);
+  // group A's transposing column reads: columns 32w.. (w = wave & 3), the
+  // offsets of lo.v[w] computed directly (a wave-indexed register array would
+  // be moved to memory by the compiler)
+  uint32_t tro[2];
+  {
+    const int g = lane >> 4, i = lane & 15;
+    const int row = 8 * h + (i >> 2), col = 32 * (wave & 3) + ((g & 1) << 4) + ((i & 3) << 2);
+    tro[0] = static_cast<uint32_t>(swz_off(row, col));
+    tro[1] = static_cast<uint32_t>(swz_off(row + 4, col));
+  }
 
   const SegTable seg = load_segments(a, leaf, suffix_keys);
   const int ntiles = seg.ntiles;
@@ -866,7 +879,7 @@ __global__ __launch_bounds__(512) void mfma_dq(KernelArgs a) {
     const int d = 32 * (wave & 3) + n;
 #pragma unroll
     for (int g = 0; g < 4; g++) {
-      const bf16x8 x = lds_col8_at(src + 16 * g * 256, lo.v[wave & 3][0], lo.v[wave & 3][1]);
+      const bf16x8 x = lds_col8_at(src + 16 * g * 256, tro[0], tro[1]);
       *reinterpret_cast<bf16x8*>(dst + kt_off(d, 2 * g + h)) = x;
     }
   };
