@@ -1047,6 +1047,18 @@ __global__ __launch_bounds__(512) void mfma_dq(KernelArgs a) {
 // block of kHeads query heads of the GQA group (2 when the group size is even:
 // half the stages, and with them half the per-stage barriers and copy waits).
 // ---------------------------------------------------------------------------
+#ifndef TPR_DKDV_INTERLEAVE
+#define TPR_DKDV_INTERLEAVE 1
+#endif
+// dK/dV stage slots: with kInterleave the two 32-query sub-blocks of a head
+// alternate slot by slot (slot m: sub-block m % 2, position m / 2), so each
+// sub-block's dependent steps (S -> P -> dV, dP -> dS -> dK) are two slots
+// apart and the other sub-block's work fills the gap; otherwise they run
+// one after the other (slot m: sub-block m / 32, position m % 32).
+constexpr bool kInterleave = TPR_DKDV_INTERLEAVE;
+constexpr int slot_sub(int m) { return kInterleave ? (m & 1) : (m >> 5); }
+constexpr int slot_pos(int m) { return kInterleave ? (m >> 1) : (m & 31); }
+
 template <int kHeads>
 __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
   const int32_t* item = a.plan + a.off_dkdv + DK_WORDS * blockIdx.x;
@@ -1163,15 +1175,16 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
   // 32-query sub-blocks j of 32 MFMAs each -- S (8), dP (8), dV (8), dK (8).
   // The stage is laid out as a fixed sequence of 64 slots, one MFMA per slot,
   // fenced so the compiler keeps the order:
-  //  * the LDS operands of the MFMA kAhead slots later are read in each slot,
-  //    so every read has about kAhead MFMAs (4 x 32 cycles) to land;
+  //  * the LDS operands of an MFMA are read kAhead MFMAs of the same
+  //    sub-block earlier, so every read has that many MFMAs to land;
   //  * P = exp2(scale*S - lse) of sub-block j is computed under its dP and
   //    first dV MFMAs, dS = P (dP - delta) under its dV and first dK MFMAs,
   //    so the VALU work runs while the matrix core is busy.
   // On a diagonal stage (diag), key kp is visible from query index qi of
   // sub-block j iff qi >= lim - 32j; other stages skip the mask. Queries past
   // the block end carry lse = +inf, so their P and dS are exactly 0.
-  constexpr int kAhead = 4;
+  constexpr int kAhead = 4;  // MFMAs of the same sub-block between a read and its use
+  constexpr int kSlotAhead = kInterleave ? 2 * kAhead : kAhead;
   // Lane offsets of the operand reads; the second set carries a 64 KiB bias so
   // that the reads of stage buffer 1 (at 64 KiB when kHeads is 2) keep their
   // constant part within the 16-bit LDS instruction offset.
@@ -1187,7 +1200,7 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
     bf16x8 pb[2][2], d8[2][2];
     // operands of MFMA m (sub-block m / 32, position m % 32)
     auto read_for = [&](auto mc) __attribute__((always_inline)) {
-      constexpr int m = decltype(mc)::value, j = m >> 5, k = m & 31;
+      constexpr int m = decltype(mc)::value, j = slot_sub(m), k = slot_pos(m);
       // rows 32j + sigma32(n) and the 16-row groups of the column reads are
       // the lane offsets of lo plus 8192j / 4096(2j + cc) (immediates)
       if constexpr (k < 8) {
@@ -1214,7 +1227,7 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
       }
     };
     auto mfma_at = [&](auto mc) __attribute__((always_inline)) {
-      constexpr int m = decltype(mc)::value, j = m >> 5, k = m & 31;
+      constexpr int m = decltype(mc)::value, j = slot_sub(m), k = slot_pos(m);
       if constexpr (k < 8) {
         sc[j] = mfma(rq[j][k], kv[k], k == 0 ? f32x16{} : sc[j]);
       } else if constexpr (k < 16) {
@@ -1251,18 +1264,18 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
     // Reads are issued in pairs, the later slot's first: LDS reads complete in
     // order, so the wait before the earlier slot's MFMA covers both and the
     // later slot's MFMA needs none.
-    static_for<kAhead / 2>([&](auto pc) __attribute__((always_inline)) {
+    static_for<kSlotAhead / 2>([&](auto pc) __attribute__((always_inline)) {
       constexpr int q = 2 * decltype(pc)::value;
       read_for(std::integral_constant<int, q + 1>{});
       read_for(std::integral_constant<int, q>{});
     });
     read_stats(I0{}, I0{});
     static_for<64>([&](auto mc) __attribute__((always_inline)) {
-      constexpr int m = decltype(mc)::value, j = m >> 5, k = m & 31;
+      constexpr int m = decltype(mc)::value, j = slot_sub(m), k = slot_pos(m);
       using J = std::integral_constant<int, j>;
-      if constexpr (m % 2 == 0 && m + kAhead + 1 < 64) {
-        read_for(std::integral_constant<int, m + kAhead + 1>{});
-        read_for(std::integral_constant<int, m + kAhead>{});
+      if constexpr (m % 2 == 0 && m + kSlotAhead + 1 < 64) {
+        read_for(std::integral_constant<int, m + kSlotAhead + 1>{});
+        read_for(std::integral_constant<int, m + kSlotAhead>{});
       }
       if constexpr (j == 1 && k == 2) read_stats(I1{}, I0{});
       if constexpr (k == 10) read_stats(J{}, I1{});
