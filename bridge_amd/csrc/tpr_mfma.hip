@@ -343,33 +343,36 @@ __device__ __forceinline__ void dma_tile4(const char* src, uint32_t row_bytes, i
   }
 }
 
-// Forward-only cursor over a workgroup's key stream (SegTable order). It
-// only changes segment at segment ends, so the common step is a compare.
+// Cursor over a forward / dQ workgroup's key stream: the leaf's own suffix
+// first, then its ancestor nodes (root first). Reading the shared prefix
+// last in every workgroup leaves it the most recently used data in the XCD's
+// L2 when the next workgroups (other query blocks and siblings of the same
+// KV head) start on their suffix, so their suffix tiles evict older suffix
+// lines rather than the prefix. The rows a workgroup reads or writes once
+// (Q, dO, O, dQ) go through non-temporal loads and stores for the same
+// reason. It only changes segment at segment ends, so the common step is a
+// compare.
 struct Cursor {
-  int d;     // segment: 0..kMfmaMaxDepth-1 = ancestor node, kMfmaMaxDepth = suffix
+  int d;     // position in the stream: 0 = suffix, 1 + e = ancestor node e
   int lt;    // tile within the segment
   int row;   // first row of the segment
-  int len;   // rows of the segment
+  int len;   // rows of the segment (0 past the stream's end)
 };
 
 __device__ __forceinline__ void cursor_load(const SegTable& t, Cursor& c) {
-  int row = t.suffix_row, len = t.suffix_keys;
+  int row = t.suffix_row, len = c.d == 0 ? t.suffix_keys : 0;
 #pragma unroll
   for (int e = 0; e < kMfmaMaxDepth; e++) {
-    row = c.d == e ? t.row[e] : row;
-    len = c.d == e ? t.len[e] : len;
+    row = c.d == e + 1 ? t.row[e] : row;
+    len = c.d == e + 1 ? t.len[e] : len;
   }
   c.row = row;
   c.len = len;
 }
 
 __device__ __forceinline__ Cursor cursor_begin(const SegTable& t) {
-  Cursor c{0, 0, 0, 0};
+  Cursor c{0, 0, 0, 0};  // the suffix holds at least one key
   cursor_load(t, c);
-  while (c.len == 0 && c.d < kMfmaMaxDepth) {
-    c.d++;
-    cursor_load(t, c);
-  }
   return c;
 }
 
@@ -386,7 +389,7 @@ __device__ __forceinline__ void cursor_next(const SegTable& t, Cursor& c) {
 
 __device__ __forceinline__ TileLoc cursor_tile(const Cursor& c) {
   return TileLoc{static_cast<int64_t>(c.row) + c.lt * kTileRows, min(kTileRows, c.len - c.lt * kTileRows),
-                 c.lt * kTileRows, c.d >= kMfmaMaxDepth};
+                 c.lt * kTileRows, c.d == 0};
 }
 
 // Wait until this wave's outstanding global->LDS copies have landed.
@@ -521,7 +524,7 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
     const bf16* qp = static_cast<const bf16*>(a.q) + static_cast<int64_t>(row0 + min(t, len - 1)) * qstride +
                      head * kMfmaD + 8 * h;
 #pragma unroll
-    for (int c = 0; c < 8; c++) qv[c] = *reinterpret_cast<const bf16x8*>(qp + 16 * c);
+    for (int c = 0; c < 8; c++) qv[c] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(qp + 16 * c));
   }
 
   f32x16 o[4];
@@ -700,7 +703,7 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
       bf16x4 v4;
 #pragma unroll
       for (int b = 0; b < 4; b++) v4[b] = static_cast<bf16>(o[db][4 * g + b] * inv);
-      *reinterpret_cast<bf16x4*>(op + 32 * db + 8 * g + 4 * h) = v4;
+      __builtin_nontemporal_store(v4, reinterpret_cast<bf16x4*>(op + 32 * db + 8 * g + 4 * h));
     }
   if (h == 0) a.lse[static_cast<int64_t>(head) * a.total_q + row0 + t] = m * a.scale + logf(lt);
 }
@@ -843,8 +846,8 @@ __global__ __launch_bounds__(512) void mfma_dq(KernelArgs a) {
     const bf16* gp = static_cast<const bf16*>(a.dout) + off;
 #pragma unroll
     for (int c = 0; c < 8; c++) {
-      qv[c] = *reinterpret_cast<const bf16x8*>(qp + 16 * c);
-      gv[c] = *reinterpret_cast<const bf16x8*>(gp + 16 * c);
+      qv[c] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(qp + 16 * c));
+      gv[c] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(gp + 16 * c));
     }
   }
   const int64_t stat = static_cast<int64_t>(head) * a.total_q + row0 + tc;
@@ -1033,7 +1036,7 @@ __global__ __launch_bounds__(512) void mfma_dq(KernelArgs a) {
       bf16x4 v4;
 #pragma unroll
       for (int b = 0; b < 4; b++) v4[b] = static_cast<bf16>(dq[db][4 * g + b] * a.scale);
-      *reinterpret_cast<bf16x4*>(dst + 32 * db + 8 * g + 4 * h) = v4;
+      __builtin_nontemporal_store(v4, reinterpret_cast<bf16x4*>(dst + 32 * db + 8 * g + 4 * h));
     }
 }
 
