@@ -11,6 +11,7 @@ Public API:
   rectangular_causal_attention  drop-in for the reference's single-sequence operator
   TPRKernelBackend              TPRAttentionBackend (parallel_size 1) for the model seam: one
                                 launch per layer for all sibling leaves of a parent
+  PrefixKVStack                 zero-copy K/V path stack with fp32 gradient relay (KVStack)
 """
 
 from .meta import LaunchPlan, TPRPrefixMeta
@@ -21,6 +22,7 @@ from .prefix_attention import (
     tpr_prefix_attention,
 )
 from .backend import TPRKernelBackend
+from .relay import PastKVAnchors, PastKVSlice, PrefixKVStack, StackSegment
 from .rectangular_attention import rectangular_causal_attention
 
 __all__ = [
@@ -32,4 +34,8 @@ __all__ = [
     "prefix_attention_backward",
     "rectangular_causal_attention",
     "TPRKernelBackend",
+    "PrefixKVStack",
+    "StackSegment",
+    "PastKVAnchors",
+    "PastKVSlice",
 ]

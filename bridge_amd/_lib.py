@@ -12,7 +12,7 @@ import threading
 
 LIB_NAME = "libtpr_attn.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 TPR_OK = 0
 TPR_ERR_INVALID_ARGUMENT = 1
@@ -38,6 +38,7 @@ TPR_BWD_DKDV = 2
 TPR_BWD_DQ = 4
 TPR_BWD_DKDV_TILES = 8
 TPR_BWD_DKDV_REDUCE = 16
+TPR_BWD_ACCUMULATE_PREFIX_F32 = 1  # TprBwdParams.flags: add prefix grads into fp32 buffers
 
 _p = ctypes.c_void_p
 _i32p = ctypes.POINTER(ctypes.c_int32)
@@ -80,7 +81,7 @@ class TprFwdParams(ctypes.Structure):
 class TprBwdParams(ctypes.Structure):
     _fields_ = [
         ("abi_version", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("flags", ctypes.c_int32),
         ("softmax_scale", ctypes.c_float),
         ("reserved_f", ctypes.c_float),
         ("plan_host", _p),

@@ -23,6 +23,12 @@ replaces the reference's sibling loop. The prefix K/V are autograd inputs:
 their gradient is the sum over the siblings, accumulated in fp32 inside the
 kernel in sibling order and cast once, in place of the per-sibling bf16
 ``add_`` of prefix_state.py:546-573.
+
+``TPRKernelBackend.from_stack`` takes the prefix from a ``PrefixKVStack``
+instead: the path K/V are views of the stack's buffers, and the kernel adds
+the prefix gradient straight into the stack's fp32 gradient rows, so the
+prefix K/V get no autograd gradient (the relay of kv_stack.py:156-203 without
+anchors).
 """
 
 from __future__ import annotations
@@ -75,7 +81,8 @@ class TPRKernelBackend:
     """
 
     def __init__(self, prefix_key_values: Mapping[int, KVPair], suffix_lengths: Sequence[int], *,
-                 prefix_length: Optional[int] = None):
+                 prefix_length: Optional[int] = None,
+                 prefix_grad_accumulators: Optional[Mapping[int, KVPair]] = None):
         lengths = tuple(suffix_lengths)
         if not lengths or any(not isinstance(s, int) or isinstance(s, bool) or s <= 0 for s in lengths):
             raise ValueError(f"suffix_lengths must be positive integers, got {suffix_lengths!r}")
@@ -91,10 +98,22 @@ class TPRKernelBackend:
             if not isinstance(pair, tuple) or len(pair) != 2:
                 raise TypeError(f"layer {layer_number} past KV must be a (key, value) tuple")
             _validate_kv_pair(layer_number, *pair, expected_sequence_length=prefix_length, kind="past")
+        accumulators = dict(prefix_grad_accumulators) if prefix_grad_accumulators is not None else None
+        if accumulators is not None and set(accumulators) != set(pairs):
+            raise ValueError(f"prefix_grad_accumulators layers {sorted(accumulators)} must match the past KV "
+                             f"layers {sorted(pairs)}")
         self._prefix = pairs
+        self._accumulators = accumulators
         self._prefix_length = prefix_length
         self._lengths = lengths
         self._meta = TPRPrefixMeta.shared_prefix(prefix_length, lengths)
+
+    @classmethod
+    def from_stack(cls, stack, suffix_lengths: Sequence[int]) -> "TPRKernelBackend":
+        """The siblings under the top of a ``PrefixKVStack``: prefix = the stack's
+        path (views), prefix gradient added into the stack's fp32 rows."""
+        return cls(stack.build_past_key_values(), suffix_lengths, prefix_length=stack.prefix_length,
+                   prefix_grad_accumulators=stack.past_gradient_accumulators() if stack.prefix_length else None)
 
     # -- the protocol ---------------------------------------------------------
     @property
@@ -134,8 +153,11 @@ class TPRKernelBackend:
         else:
             past_key = new_key.new_empty((0,) + tuple(new_key.shape[1:]))
             past_value = past_key
+        accumulators = None
+        if self._accumulators is not None and self._prefix_length:
+            accumulators = self._accumulators[layer_number]
         out, _ = TPRPrefixAttention.apply(query[:, 0], new_key[:, 0], new_value[:, 0], past_key[:, 0],
-                                          past_value[:, 0], self._meta, softmax_scale)
+                                          past_value[:, 0], self._meta, softmax_scale, accumulators)
         return out.reshape(query.shape[0], 1, query.shape[2] * query.shape[3])
 
     # -- packing helpers --------------------------------------------------------

@@ -159,6 +159,8 @@ extern "C" int tpr_attn_bwd_phases(const TprBwdParams* p, int phases, void* stre
   int rc = check_plan(p->plan_host, p->plan_device);
   if (rc) return rc;
   if ((rc = check_scale(p->softmax_scale))) return rc;
+  if (p->flags & ~TPR_BWD_ACCUMULATE_PREFIX_F32)
+    return fail(TPR_ERR_INVALID_ARGUMENT, "flags must be 0 or TPR_BWD_ACCUMULATE_PREFIX_F32, got %d", p->flags);
   const int32_t* ph = p->plan_host;
   const bool mfma = ph[PF_PATH] == PATH_MFMA;
   const bool any_q = ph[PF_TOTAL_Q] > 0, any_p = ph[PF_TOTAL_PREFIX] > 0;
@@ -190,6 +192,7 @@ extern "C" int tpr_attn_bwd_phases(const TprBwdParams* p, int phases, void* stre
   a.dv = p->dv;
   a.dpk = p->dprefix_k;
   a.dpv = p->dprefix_v;
+  a.acc_prefix = (p->flags & TPR_BWD_ACCUMULATE_PREFIX_F32) ? 1 : 0;
   a.stat_ws = static_cast<float*>(p->workspace);
   a.ws = a.stat_ws + stat_floats(ph);
   const bool fp32 = ph[PF_DTYPE] == TPR_DTYPE_FP32;

@@ -38,6 +38,7 @@ struct KernelArgs {
   void* dv;
   void* dpk;
   void* dpv;
+  int32_t acc_prefix;  // dpk/dpv are fp32 accumulators: add the prefix gradient instead of writing it
   float scale;
   int32_t hq, hkv, d, group;
   int32_t hpw;  // query heads per forward/dQ workgroup (MFMA path)

@@ -1365,6 +1365,25 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
     }
     return;
   }
+  if (prefix && a.acc_prefix) {
+    // fp32 relay accumulators: add this (unsplit) tile's gradient, the scaled
+    // product rounded as the ordinary path rounds it, then one add (no fma)
+#pragma clang fp contract(off)
+    float* dkf = static_cast<float*>(a.dpk);
+    float* dvf = static_cast<float*>(a.dpv);
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int key = kw0 + 8 * (r >> 2) + 4 * h + (r & 3);
+      if (key >= seg_len) continue;
+      const int64_t off = static_cast<int64_t>(seg_row0 + key) * kstride + kvh * kMfmaD + n;
+#pragma unroll
+      for (int db = 0; db < 4; db++) {
+        dkf[off + 32 * db] += dk[db][r] * a.scale;
+        dvf[off + 32 * db] += dv[db][r];
+      }
+    }
+    return;
+  }
   bf16* dkd = static_cast<bf16*>(prefix ? a.dpk : a.dk);
   bf16* dvd = static_cast<bf16*>(prefix ? a.dpv : a.dv);
 #pragma unroll
@@ -1408,11 +1427,16 @@ __global__ __launch_bounds__(256) void mfma_reduce(KernelArgs a) {
                        key * kMfmaD + 4 * d4;
     f32x4 acc = *reinterpret_cast<const f32x4*>(src);
     for (int j = 1; j < nslots; j++) acc += *reinterpret_cast<const f32x4*>(src + j * slot_floats);
+    const int64_t at = static_cast<int64_t>(seg_row0 + key0 + key) * kstride + kvh * kMfmaD + 4 * d4;
+    if (prefix && a.acc_prefix) {  // fp32 relay accumulators
+      f32x4* dst = reinterpret_cast<f32x4*>(static_cast<float*>(which ? a.dpv : a.dpk) + at);
+      *dst = *dst + acc;
+      continue;
+    }
     bf16x4 o;
 #pragma unroll
     for (int i = 0; i < 4; i++) o[i] = static_cast<bf16>(acc[i]);
-    bf16* dst = (which ? dvd : dkd) + static_cast<int64_t>(seg_row0 + key0 + key) * kstride + kvh * kMfmaD + 4 * d4;
-    *reinterpret_cast<bf16x4*>(dst) = o;
+    *reinterpret_cast<bf16x4*>((which ? dvd : dkd) + at) = o;
   }
 }
 

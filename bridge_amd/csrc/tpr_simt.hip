@@ -277,6 +277,16 @@ __global__ __launch_bounds__(kSimtKeys) void simt_dkdv(KernelArgs a) {
     }
   }
   if (!valid) return;
+  if (prefix && a.acc_prefix) {
+#pragma clang fp contract(off)  // rounded product, then one add
+    float* dkf = static_cast<float*>(a.dpk) + krow * ks + kvh * d;
+    float* dvf = static_cast<float*>(a.dpv) + krow * ks + kvh * d;
+    for (int i = 0; i < d; i++) {
+      dkf[i] += dk[i] * a.scale;
+      dvf[i] += dv[i];
+    }
+    return;
+  }
   T* dkd = static_cast<T*>(prefix ? a.dpk : a.dk) + krow * ks + kvh * d;
   T* dvd = static_cast<T*>(prefix ? a.dpv : a.dv) + krow * ks + kvh * d;
   for (int i = 0; i < d; i++) {

@@ -25,7 +25,7 @@ from __future__ import annotations
 
 import ctypes
 import math
-from typing import Optional
+from typing import Optional, Tuple
 
 import torch
 
@@ -114,18 +114,48 @@ def _forward(q, k, v, prefix_k, prefix_v, meta, scale):
     return out, lse
 
 
-def _backward(q, k, v, prefix_k, prefix_v, out, lse, dout, meta, scale, *, phases=None, buffers=None):
+def _check_accumulators(accumulators, prefix_k) -> Tuple[torch.Tensor, torch.Tensor]:
+    """fp32 [total_prefix, Hkv, D] pair on prefix_k's device, contiguous."""
+    if not isinstance(accumulators, (tuple, list)) or len(accumulators) != 2:
+        raise TypeError("prefix_grad_accumulators must be a (dprefix_k, dprefix_v) pair of fp32 tensors")
+    for name, t in zip(("dprefix_k", "dprefix_v"), accumulators):
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"prefix_grad_accumulators {name} must be a torch tensor")
+        if t.dtype != torch.float32:
+            raise ValueError(f"prefix_grad_accumulators {name} must be float32, got {t.dtype}")
+        if tuple(t.shape) != tuple(prefix_k.shape):
+            raise ValueError(f"prefix_grad_accumulators {name} must have shape {tuple(prefix_k.shape)}, "
+                             f"got {tuple(t.shape)}")
+        if t.device != prefix_k.device:
+            raise RuntimeError(f"prefix_grad_accumulators {name} must be on {prefix_k.device}, got {t.device}")
+        if not t.is_contiguous():
+            raise ValueError(f"prefix_grad_accumulators {name} must be contiguous")
+    return accumulators[0], accumulators[1]
+
+
+def _backward(q, k, v, prefix_k, prefix_v, out, lse, dout, meta, scale, *, phases=None, buffers=None,
+              prefix_grad_accumulators=None):
     """Enqueue the backward. ``buffers`` may supply preallocated dq, dk, dv,
     dprefix_k, dprefix_v and delta tensors; ``phases`` is a mask of
-    _lib.TPR_BWD_* bits (default: all)."""
+    _lib.TPR_BWD_* bits (default: all). With ``prefix_grad_accumulators`` (a
+    pair of fp32 tensors shaped like prefix_k) the prefix gradients are added
+    into that pair by the kernels (TPR_BWD_ACCUMULATE_PREFIX_F32), which is
+    also what is returned for them."""
     plan = meta.plan(q.shape[1], k.shape[1], q.shape[2], q.dtype, q.device)
     b = dict(buffers or {})
     dq = b.get("dq") if b.get("dq") is not None else torch.empty_like(q)
     dk = b.get("dk") if b.get("dk") is not None else torch.empty_like(k)
     dv = b.get("dv") if b.get("dv") is not None else torch.empty_like(v)
-    dpk = b.get("dprefix_k") if b.get("dprefix_k") is not None else torch.empty_like(prefix_k)
-    dpv = b.get("dprefix_v") if b.get("dprefix_v") is not None else torch.empty_like(prefix_v)
+    flags = 0
+    if prefix_grad_accumulators is not None:
+        dpk, dpv = _check_accumulators(prefix_grad_accumulators, prefix_k)
+        flags = _lib.TPR_BWD_ACCUMULATE_PREFIX_F32
+    else:
+        dpk = b.get("dprefix_k") if b.get("dprefix_k") is not None else torch.empty_like(prefix_k)
+        dpv = b.get("dprefix_v") if b.get("dprefix_v") is not None else torch.empty_like(prefix_v)
     if q.shape[0] == 0:
+        if flags:
+            return dq, dk, dv, dpk, dpv
         return dq, dk, dv, dpk.zero_(), dpv.zero_()
     delta = b.get("delta") if b.get("delta") is not None else torch.empty_like(lse)
     ws = b.get("workspace")
@@ -133,7 +163,7 @@ def _backward(q, k, v, prefix_k, prefix_v, out, lse, dout, meta, scale, *, phase
         ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=q.device)
     lib = _lib.load()
     params = _lib.TprBwdParams(
-        _lib.ABI_VERSION, 0, scale, 0.0,
+        _lib.ABI_VERSION, flags, scale, 0.0,
         plan.host.data_ptr(), plan.device.data_ptr(),
         _ptr(q), _ptr(k), _ptr(v), _ptr(prefix_k), _ptr(prefix_v), _ptr(out), _ptr(dout), _ptr(lse),
         _ptr(delta), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dpk), _ptr(dpv), _ptr(ws), plan.workspace_bytes)
@@ -144,16 +174,27 @@ def _backward(q, k, v, prefix_k, prefix_v, out, lse, dout, meta, scale, *, phase
 
 
 class TPRPrefixAttention(torch.autograd.Function):
-    """(q, k, v, prefix_k, prefix_v, meta, softmax_scale) -> (out, lse)."""
+    """(q, k, v, prefix_k, prefix_v, meta, softmax_scale, prefix_grad_accumulators) -> (out, lse).
+
+    With ``prefix_grad_accumulators`` = (dK, dV), fp32 tensors shaped like
+    prefix_k, the backward adds the prefix gradients into them (the relay of
+    prefix_state.py:546-573, in fp32 and inside the kernel) and gives
+    prefix_k / prefix_v no autograd gradient; they must then not require one.
+    """
 
     @staticmethod
-    def forward(ctx, q, k, v, prefix_k, prefix_v, meta, softmax_scale=None):
+    def forward(ctx, q, k, v, prefix_k, prefix_v, meta, softmax_scale=None, prefix_grad_accumulators=None):
         scale = validate(q, k, v, prefix_k, prefix_v, meta, softmax_scale)
+        if prefix_grad_accumulators is not None:
+            if prefix_k.requires_grad or prefix_v.requires_grad:
+                raise ValueError("prefix_k/prefix_v must not require grad when prefix_grad_accumulators is given")
+            _check_accumulators(prefix_grad_accumulators, prefix_k)
         q, k, v, prefix_k, prefix_v = (t.contiguous() for t in (q, k, v, prefix_k, prefix_v))
         out, lse = _forward(q, k, v, prefix_k, prefix_v, meta, scale)
         ctx.save_for_backward(q, k, v, prefix_k, prefix_v, out, lse)
         ctx.meta = meta
         ctx.scale = scale
+        ctx.accumulators = prefix_grad_accumulators
         ctx.mark_non_differentiable(lse)
         return out, lse
 
@@ -163,13 +204,17 @@ class TPRPrefixAttention(torch.autograd.Function):
         if dout is None:
             dout = torch.zeros_like(out)
         dout = dout.contiguous()
-        dq, dk, dv, dpk, dpv = _backward(q, k, v, prefix_k, prefix_v, out, lse, dout, ctx.meta, ctx.scale)
-        return dq, dk, dv, dpk, dpv, None, None
+        dq, dk, dv, dpk, dpv = _backward(q, k, v, prefix_k, prefix_v, out, lse, dout, ctx.meta, ctx.scale,
+                                         prefix_grad_accumulators=ctx.accumulators)
+        if ctx.accumulators is not None:
+            dpk = dpv = None
+        return dq, dk, dv, dpk, dpv, None, None, None
 
 
-def tpr_prefix_attention(q, k, v, prefix_k, prefix_v, meta: TPRPrefixMeta, softmax_scale=None):
+def tpr_prefix_attention(q, k, v, prefix_k, prefix_v, meta: TPRPrefixMeta, softmax_scale=None, *,
+                         prefix_grad_accumulators=None):
     """Functional form of TPRPrefixAttention; returns (out, lse)."""
-    return TPRPrefixAttention.apply(q, k, v, prefix_k, prefix_v, meta, softmax_scale)
+    return TPRPrefixAttention.apply(q, k, v, prefix_k, prefix_v, meta, softmax_scale, prefix_grad_accumulators)
 
 
 def prefix_attention_forward(q, k, v, prefix_k, prefix_v, meta: TPRPrefixMeta, softmax_scale=None):
@@ -180,14 +225,17 @@ def prefix_attention_forward(q, k, v, prefix_k, prefix_v, meta: TPRPrefixMeta, s
 
 
 def prefix_attention_backward(q, k, v, prefix_k, prefix_v, out, lse, dout, meta: TPRPrefixMeta,
-                              softmax_scale=None, *, phases=None, buffers=None):
+                              softmax_scale=None, *, phases=None, buffers=None, prefix_grad_accumulators=None):
     """Backward only: (dq, dk, dv, dprefix_k, dprefix_v) from saved out/lse.
 
     ``phases`` selects backward phases (mask of TPR_BWD_DELTA / _DKDV / _DQ,
     or _DKDV_TILES then _DKDV_REDUCE for the two steps of _DKDV; the delta
     phase must have run before the others, with the same ``delta`` and
     ``workspace``); ``buffers`` may hold preallocated outputs, the fp32
-    ``delta`` scratch and the ``workspace``, keyed by name."""
+    ``delta`` scratch and the ``workspace``, keyed by name.
+    ``prefix_grad_accumulators``: a (dK, dV) pair of fp32 tensors shaped like
+    prefix_k into which the prefix gradients are added (and returned)."""
     scale = validate(q, k, v, prefix_k, prefix_v, meta, softmax_scale)
     tensors = [t.contiguous() for t in (q, k, v, prefix_k, prefix_v, out, lse, dout)]
-    return _backward(*tensors[:7], tensors[7], meta, scale, phases=phases, buffers=buffers)
+    return _backward(*tensors[:7], tensors[7], meta, scale, phases=phases, buffers=buffers,
+                     prefix_grad_accumulators=prefix_grad_accumulators)

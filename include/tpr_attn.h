@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define TPR_ATTN_ABI_VERSION 1
+#define TPR_ATTN_ABI_VERSION 2
 
 typedef enum TprStatus {
   TPR_OK = 0,
@@ -108,10 +108,20 @@ typedef struct TprFwdParams {
  * over every descendant leaf of each node in leaf order (fixed-order
  * reduction, the deterministic counterpart of prefix_state.py:565-573).
  * delta is caller-provided scratch of lse's shape; workspace is caller-provided
- * scratch of tpr_attn_bwd_workspace_bytes() bytes (may be NULL when that is 0). */
+ * scratch of tpr_attn_bwd_workspace_bytes() bytes (may be NULL when that is 0).
+ *
+ * flags = TPR_BWD_ACCUMULATE_PREFIX_F32: dprefix_k/dprefix_v are fp32 buffers
+ * of [total_prefix, Hkv, D] whatever the dtype, and each node's gradient
+ * (still the fixed-order sum over its leaves) is ADDED to them instead of
+ * written. This is the gradient relay of KVPrefixState.accumulate_layer_gradients
+ * (prefix_state.py:546-573), where every backward that reads a prefix state
+ * adds its gradient to that state's buffer, with the buffer kept in fp32 and
+ * the add fused into the kernel's final write. One writer per element per
+ * call, so calls on one stream accumulate deterministically. */
+#define TPR_BWD_ACCUMULATE_PREFIX_F32 1
 typedef struct TprBwdParams {
   int32_t abi_version;
-  int32_t reserved;
+  int32_t flags; /* 0 or TPR_BWD_ACCUMULATE_PREFIX_F32 */
   float softmax_scale;
   float reserved_f;
   const int32_t* plan_host;
