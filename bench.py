@@ -125,6 +125,94 @@ def cpu_baseline(prefix_len: int, suffix_len: int, hq_sample: int, hkv: int, hq:
     }
 
 
+def relay_bench(args) -> int:
+    """One leaf-batch visit (fwd + bwd, one layer) under a two-segment path --
+    root 2048 + branch 2048 tokens, 4 sibling leaves of 4096, Qwen3-4B layer
+    dims -- two ways:
+      reference flow: torch.cat of the path K/V, detached anchors, the kernel
+        with autograd prefix gradients (bf16), then the per-ancestor split and
+        bf16 add_ (kv_stack.py:139-203, prefix_state.py:546-573);
+      relay flow: PrefixKVStack views and the kernel adding the prefix
+        gradient into the stack's fp32 rows (TPR_BWD_ACCUMULATE_PREFIX_F32).
+    Also times the reference flow's relay operations alone (cat + split/add)."""
+    from bridge_amd import PrefixKVStack, StackSegment, TPRPrefixAttention, TPRPrefixMeta
+    device = torch.device("cuda", 0)
+    hq, hkv, d, seg, lengths = 32, 8, 128, 2048, [4096] * 4
+    scale = 1.0 / math.sqrt(d)
+    meta = TPRPrefixMeta.shared_prefix(2 * seg, lengths)
+    gen = torch.Generator(device=device).manual_seed(99)
+    r = lambda *shape: torch.randn(*shape, device=device, generator=gen).bfloat16()  # noqa: E731
+    tq = sum(lengths)
+    q, k, v, dout = r(tq, hq, d), r(tq, hkv, d), r(tq, hkv, d), r(tq, hq, d)
+    seg_kv = [{1: (r(seg, 1, hkv, d), r(seg, 1, hkv, d))} for _ in range(2)]
+    seg_grad = [(torch.zeros(seg, 1, hkv, d, dtype=torch.bfloat16, device=device),
+                 torch.zeros(seg, 1, hkv, d, dtype=torch.bfloat16, device=device)) for _ in range(2)]
+    stack = PrefixKVStack(2 * seg)
+    stack.push(StackSegment(0, None, seg, 0, 0), seg_kv[0])
+    stack.push(StackSegment(1, 0, seg, seg, seg), seg_kv[1])
+    qa, ka, va = (t.clone().requires_grad_(True) for t in (q, k, v))
+
+    def reference_relay_ops_forward():
+        past_k = torch.cat([s[1][0] for s in seg_kv], 0)
+        past_v = torch.cat([s[1][1] for s in seg_kv], 0)
+        return past_k.detach().requires_grad_(True), past_v.detach().requires_grad_(True)
+
+    def reference_relay_ops_backward(gk, gv):
+        for i in range(2):
+            seg_grad[i][0].add_(gk[i * seg:(i + 1) * seg])
+            seg_grad[i][1].add_(gv[i * seg:(i + 1) * seg])
+
+    def reference_visit():
+        ak, av = reference_relay_ops_forward()
+        out, _ = TPRPrefixAttention.apply(qa, ka, va, ak[:, 0], av[:, 0], meta, scale)
+        out.backward(dout)
+        reference_relay_ops_backward(ak.grad, av.grad)
+
+    def relay_visit():
+        pk, pv = stack.build_past_key_values()[1]
+        acc = stack.past_gradient_accumulators()[1]
+        out, _ = TPRPrefixAttention.apply(qa, ka, va, pk[:, 0], pv[:, 0], meta, scale, acc)
+        out.backward(dout)
+
+    gk_fixed = r(2 * seg, 1, hkv, d)
+
+    def relay_ops_only():
+        ak, av = reference_relay_ops_forward()
+        reference_relay_ops_backward(gk_fixed, gk_fixed)
+
+    def timed(fn, n):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(n):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1))
+        return statistics.median(times)
+
+    ref_ms = timed(reference_visit, args.steps)
+    relay_ms = timed(relay_visit, args.steps)
+    ref_again_ms = timed(reference_visit, args.steps)
+    ops_ms = timed(relay_ops_only, args.steps)
+    row_bytes = hkv * d * 2
+    print(json.dumps({
+        "metric": "leaf-batch visit ms (fwd+bwd, one layer), reference relay flow vs PrefixKVStack relay",
+        "reference_flow_ms": round(statistics.mean([ref_ms, ref_again_ms]), 4),
+        "relay_flow_ms": round(relay_ms, 4),
+        "reference_relay_ops_ms": round(ops_ms, 4),
+        "reference_relay_ops_bytes": 2 * (2 * 2 * seg * row_bytes) + 2 * (3 * 2 * seg * row_bytes),
+        "relay_flow_copies_per_visit": 0,
+        "config": {"path_segments": [seg, seg], "siblings": len(lengths), "suffix_tokens": tq,
+                   "q_heads": hq, "kv_heads": hkv, "head_dim": d, "dtype": "bf16", "layers": 1},
+        "steps": args.steps, "warmup": args.warmup,
+    }), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -137,6 +225,9 @@ def main() -> int:
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="before the timed steps, run one plain device copy of MIB MiB (read MIB, write MIB): "
                          "the calibration dispatch for rocprofv3 FETCH_SIZE / WRITE_SIZE")
+    ap.add_argument("--relay", action="store_true",
+                    help="instead of the step benchmark, time one leaf-batch visit with the reference's "
+                         "concat/anchor/split relay and with PrefixKVStack's in-kernel fp32 relay")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -146,6 +237,9 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs an MI355X GPU", file=sys.stderr)
         return 2
+
+    if args.relay:
+        return relay_bench(args)
 
     from bridge_amd import _lib
     from bridge_amd.prefix_attention import prefix_attention_backward, prefix_attention_forward
