@@ -213,6 +213,92 @@ def relay_bench(args) -> int:
     return 0
 
 
+def tree_launch_bench(args) -> int:
+    """A depth-3 rollout tree -- 16 rollouts of 2048 shared + 1024 shared by 4
+    + 1024 own tokens, Qwen3-4B layer dims -- built with build_trajectory_trees
+    from synthetic token rows and run (fwd + bwd, one layer) two ways:
+      one launch: lower_tree's packing, every segment at once;
+      per segment: the reference executor's order, one visit per segment with
+        the concatenated path K/V as its prefix (kv_stack.py:139-154).
+    Both do the same visible pairs; reports ms and TFLOP/s of each, and the
+    host time of the trie build + lowering."""
+    from bridge_amd import TPRPrefixAttention, TPRPrefixMeta
+    from bridge_amd.topology import build_trajectory_trees, lower_tree
+    device = torch.device("cuda", 0)
+    hq, hkv, d = 32, 8, 128
+    scale = 1.0 / math.sqrt(d)
+    g = torch.Generator().manual_seed(5)
+    root = torch.randint(0, 150000, (2048,), generator=g)
+    branches = [torch.randint(0, 150000, (1024,), generator=g) for _ in range(4)]
+    rows = [torch.cat([root, branches[i // 4], torch.randint(0, 150000, (1024,), generator=g)]) for i in range(16)]
+    t0 = time.perf_counter()
+    (tree,) = build_trajectory_trees([f"u_s_{i}" for i in range(16)], {"input_ids": rows})
+    launch = lower_tree(tree)
+    host_ms = (time.perf_counter() - t0) * 1e3
+    meta = launch.meta
+    tq = meta.total_q
+    gd = torch.Generator(device=device).manual_seed(6)
+    r = lambda *shape: torch.randn(*shape, device=device, generator=gd).bfloat16()  # noqa: E731
+    q, k, v, dout = r(tq, hq, d), r(tq, hkv, d), r(tq, hkv, d), r(tq, hq, d)
+    qa, ka, va = (t.clone().requires_grad_(True) for t in (q, k, v))
+    index = launch.prefix_index.to(device)
+
+    def one_launch():
+        out, _ = TPRPrefixAttention.apply(qa, ka, va, ka.index_select(0, index), va.index_select(0, index), meta,
+                                          scale)
+        out.backward(dout)
+
+    spans = [(meta.cu_seqlens_q[i], meta.cu_seqlens_q[i + 1]) for i in range(meta.num_leaves)]
+    paths = []
+    for anc in meta.leaf_ancestors:
+        rows_idx = [torch.arange(meta.cu_seqlens_q[launch.segments.index(launch.prefix_segments[n])],
+                                 meta.cu_seqlens_q[launch.segments.index(launch.prefix_segments[n]) + 1])
+                    for n in anc]
+        paths.append(torch.cat(rows_idx).to(device) if rows_idx else None)
+    seg_meta = [TPRPrefixMeta.shared_prefix(0 if p is None else p.numel(), [b - a]) for (a, b), p in zip(spans, paths)]
+
+    def per_segment():
+        for (a, b), p, m in zip(spans, paths, seg_meta):
+            if p is None:
+                pk = pv = ka.new_empty((0, hkv, d))
+            else:
+                pk, pv = ka.index_select(0, p), va.index_select(0, p)
+            out, _ = TPRPrefixAttention.apply(qa[a:b], ka[a:b], va[a:b], pk, pv, m, scale)
+            out.backward(dout[a:b])
+
+    def timed(fn, n):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(n):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1))
+        return statistics.median(times)
+
+    one_ms = timed(one_launch, args.steps)
+    seg_ms = timed(per_segment, args.steps)
+    flops = 14.0 * hq * d * meta.visible_pairs()
+    print(json.dumps({
+        "metric": "rollout tree fwd+bwd (one layer): one launch for every segment vs one visit per segment",
+        "one_launch_ms": round(one_ms, 4),
+        "per_segment_ms": round(seg_ms, 4),
+        "one_launch_tflops": round(flops / (one_ms * 1e-3) / 1e12, 2),
+        "per_segment_tflops": round(flops / (seg_ms * 1e-3) / 1e12, 2),
+        "trie_build_and_lowering_host_ms": round(host_ms, 2),
+        "config": {"rollouts": 16, "tokens_per_rollout": 4096, "segments": meta.num_leaves,
+                   "prefix_nodes": meta.num_nodes, "packed_tokens": tq, "prefix_rows": meta.total_prefix,
+                   "visible_pairs_per_head": meta.visible_pairs(), "q_heads": hq, "kv_heads": hkv, "head_dim": d,
+                   "dtype": "bf16"},
+        "steps": args.steps, "warmup": args.warmup,
+    }), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -228,6 +314,9 @@ def main() -> int:
     ap.add_argument("--relay", action="store_true",
                     help="instead of the step benchmark, time one leaf-batch visit with the reference's "
                          "concat/anchor/split relay and with PrefixKVStack's in-kernel fp32 relay")
+    ap.add_argument("--tree-launch", action="store_true",
+                    help="instead of the step benchmark, time a depth-3 rollout tree run as one launch "
+                         "(lower_tree) and as one visit per segment")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -240,6 +329,8 @@ def main() -> int:
 
     if args.relay:
         return relay_bench(args)
+    if args.tree_launch:
+        return tree_launch_bench(args)
 
     from bridge_amd import _lib
     from bridge_amd.prefix_attention import prefix_attention_backward, prefix_attention_forward

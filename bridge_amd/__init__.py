@@ -12,6 +12,7 @@ Public API:
   TPRKernelBackend              TPRAttentionBackend (parallel_size 1) for the model seam: one
                                 launch per layer for all sibling leaves of a parent
   PrefixKVStack                 zero-copy K/V path stack with fp32 gradient relay (KVStack)
+  topology                      rollout tries (exact / Qwen3 turn units) and their one-launch lowering
 """
 
 from .meta import LaunchPlan, TPRPrefixMeta
@@ -23,6 +24,7 @@ from .prefix_attention import (
 )
 from .backend import TPRKernelBackend
 from .relay import PastKVAnchors, PastKVSlice, PrefixKVStack, StackSegment
+from . import topology
 from .rectangular_attention import rectangular_causal_attention
 
 __all__ = [
