@@ -11,6 +11,12 @@ token) is compressed by following single-child chains of equal membership
 with no terminal rows, numbering nodes in preorder. The result is plain
 tuples, so tests compare it field by field with ``bridge_amd.topology``.
 
+Pins: ``token_trie`` reproduces the known answers of the reference's own
+trie tests (unit/test_trajectory_tree.py:23-151, in tests/test_topology.py);
+``segment_visits`` is built on ``prefix_attention`` (pinned in
+tests/test_oracle.py) and is checked against the oracle's independent
+``tree_forward`` / ``tree_backward`` formulation on lowered layouts.
+
 ``segment_visits`` restates what the reference's executor computes for a
 tree, one segment at a time (segment_executor.py visit order, kv_stack.py:139-154
 path order): each segment's queries attend to the concatenated K/V of its

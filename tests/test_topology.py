@@ -156,6 +156,26 @@ def _random_batch(seed, n_uids=3, rows_per_uid=6, vocab=5):
     return [keys[i] for i in order], [rows[i] for i in order]
 
 
+def test_oracle_token_trie_reproduces_the_reference_known_answers():
+    # unit/test_trajectory_tree.py:23-50, :83-100 and :138-151 applied to the oracle itself
+    from oracle.trie_oracle import token_trie
+    rows = [[1, 2, 3, 4, 5], [1, 2, 3, 4, 6], [1, 2, 3, 7]]
+    ((uid, index, root_id, nodes),) = token_trie([("a", [0, 1, 2])], rows)
+    assert (uid, index, root_id) == ("a", 0, 0)
+    parent, (row, start, end), members, terminals, children = nodes[0]
+    assert (parent, (start, end), members, terminals) == (None, (0, 3), (0, 1, 2), ())
+    shared4, direct7 = nodes[children[0]], nodes[children[1]]
+    assert shared4[1][1:] == (3, 4) and shared4[2] == (0, 1) and shared4[3] == ()
+    assert [rows[nodes[c][1][0]][nodes[c][1][1]:nodes[c][1][2]] for c in shared4[4]] == [[5], [6]]
+    assert direct7[1][1:] == (3, 4) and direct7[2] == (2,) and direct7[3] == (2,) and direct7[4] == ()
+    ((_, _, _, nodes),) = token_trie([("u", [0, 1])], [[1, 2, 3], [1, 2, 3, 4, 5]])
+    assert nodes[0][1][1:] == (0, 3) and nodes[0][3] == (0,) and nodes[nodes[0][4][0]][1][1:] == (3, 5)
+    ((_, _, _, nodes),) = token_trie([("u", [0, 1])], [[1, 2, 3], [1, 2, 3]])
+    assert nodes[0][2] == (0, 1) and nodes[0][3] == (0, 1) and nodes[0][4] == ()
+    trees = token_trie([("u1", [0, 2])], [[1, 2, 3], [9, 8], [1, 2, 4]])
+    assert len(trees) == 1 and trees[0][3][0][2] == (0, 2)
+
+
 @pytest.mark.parametrize("seed", range(12))
 def test_radix_builder_equals_the_one_token_trie(seed):
     from oracle.trie_oracle import token_trie
