@@ -463,6 +463,10 @@ __device__ __forceinline__ void qk_tile(const char* kt, const bf16x8 (&qv)[8], c
 // so unscaled probabilities stay <= 2^8 (exact arithmetic, fp32/bf16 safe).
 constexpr float kRescaleSlack = 8.f;
 
+// dK/dV: S and dP MFMAs written as asm with their accumulators in VGPRs
+#ifndef TPR_DKDV_VGPR_SP
+#define TPR_DKDV_VGPR_SP 1
+#endif
 #ifndef TPR_MPHASE_AHEAD
 #define TPR_MPHASE_AHEAD 4
 #endif
@@ -1053,6 +1057,23 @@ __global__ __launch_bounds__(512) void mfma_dq(KernelArgs a) {
 #ifndef TPR_DKDV_INTERLEAVE
 #define TPR_DKDV_INTERLEAVE 1
 #endif
+// S / dP MFMAs of the dK/dV stage with the accumulator in VGPRs (the softmax
+// VALU reads it there) and the K / V operand in AGPRs. The compiler gives every
+// MFMA of a kernel one accumulator class; the dK/dV accumulators need AGPRs, so
+// these two chains are written as asm. Hazards the compiler no longer tracks
+// for them: a VALU read of the result needs ~19 wait states after the chain's
+// last MFMA (the stage schedule puts it at least 4 MFMA slots later), and a
+// chained MFMA reads its predecessor's result as srcC with the other
+// sub-block's MFMA between them, the spacing the builtin form also uses.
+__device__ __forceinline__ f32x16 mfma_vsp_first(bf16x8 a, bf16x8 b_agpr) {
+  f32x16 d;
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "a"(b_agpr));
+  return d;
+}
+__device__ __forceinline__ void mfma_vsp_acc(f32x16& d, bf16x8 a, bf16x8 b_agpr) {
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "a"(b_agpr));
+}
+
 // dK/dV stage slots: with kInterleave the two 32-query sub-blocks of a head
 // alternate slot by slot (slot m: sub-block m % 2, position m / 2), so each
 // sub-block's dependent steps (S -> P -> dV, dP -> dS -> dK) are two slots
@@ -1232,9 +1253,13 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
     auto mfma_at = [&](auto mc) __attribute__((always_inline)) {
       constexpr int m = decltype(mc)::value, j = slot_sub(m), k = slot_pos(m);
       if constexpr (k < 8) {
-        sc[j] = mfma(rq[j][k], kv[k], k == 0 ? f32x16{} : sc[j]);
+        if constexpr (!TPR_DKDV_VGPR_SP) sc[j] = mfma(rq[j][k], kv[k], k == 0 ? f32x16{} : sc[j]);
+        else if constexpr (k == 0) sc[j] = mfma_vsp_first(rq[j][k], kv[k]);
+        else mfma_vsp_acc(sc[j], rq[j][k], kv[k]);
       } else if constexpr (k < 16) {
-        dpv[j] = mfma(rg[j][k - 8], vv[k - 8], k == 8 ? f32x16{} : dpv[j]);
+        if constexpr (!TPR_DKDV_VGPR_SP) dpv[j] = mfma(rg[j][k - 8], vv[k - 8], k == 8 ? f32x16{} : dpv[j]);
+        else if constexpr (k == 8) dpv[j] = mfma_vsp_first(rg[j][k - 8], vv[k - 8]);
+        else mfma_vsp_acc(dpv[j], rg[j][k - 8], vv[k - 8]);
       } else if constexpr (k < 24) {
         constexpr int cc = (k - 16) >> 2, db = (k - 16) & 3;
         dv[db] = mfma(pb[j][cc], cg[j][cc][db], dv[db]);
