@@ -343,6 +343,38 @@ __device__ __forceinline__ void dma_tile4(const char* src, uint32_t row_bytes, i
   }
 }
 
+// Store a wave's 32-query x 128-d output tile (accumulator layout: lane n + 32h
+// holds query n, d = 32db + 8g + 4h + b in acc[db][4g + b]) scaled by `mul`
+// (per lane) as bf16, through the wave's private 8 KiB of LDS `stage`, so that
+// every global store is 16 lanes x 16 B = one whole 256-byte row. The stores
+// are non-temporal (the rows are written once and would otherwise evict the
+// shared prefix from L2) and cover full lines, which a non-temporal store of a
+// partial line would not: the direct 8-byte stores cost ~4.5x their bytes in
+// HBM writes. Rows r >= nrows are not stored. LDS layout: row r, 16-byte chunk
+// c at r * 256 + ((c ^ (r % 16)) << 4), so both the 8-byte writes and the
+// row-linear 16-byte reads spread over all banks.
+__device__ __forceinline__ void store_tile_rows(char* stage, const f32x16 (&acc)[4], float mul, bf16* dst,
+                                                int64_t row_stride, int nrows, int lane) {
+  const int n = lane & 31, h = lane >> 5;
+#pragma unroll
+  for (int db = 0; db < 4; db++)
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      bf16x4 v4;
+#pragma unroll
+      for (int b = 0; b < 4; b++) v4[b] = static_cast<bf16>(acc[db][4 * g + b] * mul);
+      *reinterpret_cast<bf16x4*>(stage + n * 256 + (((4 * db + g) ^ (n & 15)) << 4) + 8 * h) = v4;
+    }
+  // the wave's LDS writes are done before its reads (no other wave touches `stage`)
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const int row = 4 * i + (lane >> 4), c = lane & 15;
+    const bf16x8 v = *reinterpret_cast<const bf16x8*>(stage + row * 256 + ((c ^ (row & 15)) << 4));
+    if (row < nrows) __builtin_nontemporal_store(v, reinterpret_cast<bf16x8*>(dst + row * row_stride + 8 * c));
+  }
+}
+
 // Cursor over a forward / dQ workgroup's key stream: the leaf's own suffix
 // first, then its ancestor nodes (root first). Reading the shared prefix
 // last in every workgroup leaves it the most recently used data in the XCD's
@@ -699,6 +731,8 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
   const float lt = wave_sum32(l);  // all 64 lanes take part in the exchange
   if (tw0 >= len || t >= len) return;
   const float inv = 1.f / lt;
+  // ordinary (cacheable) stores: L2 merges the 8-byte pieces into whole lines,
+  // and the workgroup retires without waiting on write-through stores
   bf16* op = static_cast<bf16*>(a.out) + static_cast<int64_t>(row0 + t) * qstride + head * kMfmaD;
 #pragma unroll
   for (int db = 0; db < 4; db++)
@@ -707,7 +741,7 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
       bf16x4 v4;
 #pragma unroll
       for (int b = 0; b < 4; b++) v4[b] = static_cast<bf16>(o[db][4 * g + b] * inv);
-      __builtin_nontemporal_store(v4, reinterpret_cast<bf16x4*>(op + 32 * db + 8 * g + 4 * h));
+      *reinterpret_cast<bf16x4*>(op + 32 * db + 8 * g + 4 * h) = v4;
     }
   if (h == 0) a.lse[static_cast<int64_t>(head) * a.total_q + row0 + t] = m * a.scale + logf(lt);
 }
@@ -1031,17 +1065,11 @@ __global__ __launch_bounds__(512) void mfma_dq(KernelArgs a) {
     phase_barrier();
   }
 
-  if (tw0 >= len || t >= len) return;
-  bf16* dst = static_cast<bf16*>(a.dq) + static_cast<int64_t>(row0 + t) * qstride + head * kMfmaD;
-#pragma unroll
-  for (int db = 0; db < 4; db++)
-#pragma unroll
-    for (int g = 0; g < 4; g++) {
-      bf16x4 v4;
-#pragma unroll
-      for (int b = 0; b < 4; b++) v4[b] = static_cast<bf16>(dq[db][4 * g + b] * a.scale);
-      __builtin_nontemporal_store(v4, reinterpret_cast<bf16x4*>(dst + 32 * db + 8 * g + 4 * h));
-    }
+  if (tw0 >= len) return;
+  // every tile read finished before the last barrier: the tile buffers are free
+  store_tile_rows(smem + wave * 8192, dq, a.scale,
+                  static_cast<bf16*>(a.dq) + static_cast<int64_t>(row0 + tw0) * qstride + head * kMfmaD, qstride,
+                  len - tw0, lane);
 }
 
 // ---------------------------------------------------------------------------
