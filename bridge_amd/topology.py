@@ -265,15 +265,25 @@ def _insert_tokens(root: _Radix, row: int, tokens: np.ndarray, all_tokens: List[
         node, pos = child, child.end
 
 
-def _emit(start_node: _Radix, parent_id: Optional[int], nodes: Dict[int, TrajectoryNode]) -> int:
-    """Assign preorder node ids (trajectory_tree.py:197-245 numbering)."""
-    node_id = len(nodes)
-    seg = SegmentRef(row=start_node.members[0], start=start_node.start, end=start_node.end)
-    nodes[node_id] = None  # reserve the id before the children
-    child_ids = tuple(_emit(c, node_id, nodes) for c in start_node.children.values())
-    nodes[node_id] = TrajectoryNode(node_id, parent_id, seg, tuple(start_node.members),
-                                    tuple(start_node.terminals), child_ids)
-    return node_id
+def _emit(root: _Radix, nodes: Dict[int, TrajectoryNode]) -> int:
+    """Assign node ids in preorder, children in insertion order (the numbering
+    of trajectory_tree.py:197-245), without recursion."""
+    ids: Dict[int, int] = {}
+    order: List[Tuple[_Radix, Optional[int]]] = []
+    todo: List[Tuple[_Radix, Optional[int]]] = [(root, None)]
+    while todo:
+        node, parent = todo.pop()
+        ids[id(node)] = len(order)
+        order.append((node, parent))
+        todo.extend((c, ids[id(node)]) for c in reversed(list(node.children.values())))
+    base = len(nodes)
+    for node, parent in order:
+        nid = base + ids[id(node)]
+        nodes[nid] = TrajectoryNode(nid, None if parent is None else base + parent,
+                                    SegmentRef(row=node.members[0], start=node.start, end=node.end),
+                                    tuple(node.members), tuple(node.terminals),
+                                    tuple(base + ids[id(c)] for c in node.children.values()))
+    return base
 
 
 def build_trajectory_trees(keys: Sequence[str], batch: Any) -> Tuple[TrajectoryTree, ...]:
@@ -298,7 +308,7 @@ def build_trajectory_trees(keys: Sequence[str], batch: Any) -> Tuple[TrajectoryT
             _insert_tokens(dummy, row, tokens[row], tokens)
         for tree_index, real_root in enumerate(dummy.children.values()):
             nodes: Dict[int, TrajectoryNode] = {}
-            root_id = _emit(real_root, None, nodes)
+            root_id = _emit(real_root, nodes)
             trees.append(TrajectoryTree(uid, tree_index, root_id, nodes[root_id].member_rows, nodes))
     return tuple(trees)
 
