@@ -42,7 +42,7 @@ def _run_backward(meta, q, k, v, pk, pv, dout, scale, accumulators=None):
     return grads
 
 
-@pytest.mark.parametrize("case", ["mfma_unsplit", "mfma_split", "simt_fp32"])
+@pytest.mark.parametrize("case", ["mfma_unsplit", "mfma_split", "simt_fp32", "simt_bf16"])
 def test_accumulate_mode_adds_the_prefix_gradient(case, cuda_device):
     from bridge_amd import TPRPrefixMeta
     if case == "mfma_unsplit":
@@ -53,8 +53,10 @@ def test_accumulate_mode_adds_the_prefix_gradient(case, cuda_device):
         meta, hq, hkv, d, dtype = TPRPrefixMeta.shared_prefix(256, [300] * 16), 4, 1, 128, torch.bfloat16
         stat_bytes = (64 + (hq * meta.total_q + 63) // 64 * 64) * 4   # constants + lse rows
         assert meta.plan(hq, hkv, d, dtype, cuda_device).workspace_bytes == stat_bytes + 4 * 2 * 128 * 128 * 4
-    else:
+    elif case == "simt_fp32":
         meta, hq, hkv, d, dtype = TPRPrefixMeta.shared_prefix(96, [40, 17, 33]), 4, 2, 64, torch.float32
+    else:  # bf16 with head_dim 64 runs the SIMT kernels too
+        meta, hq, hkv, d, dtype = TPRPrefixMeta.shared_prefix(96, [40, 17, 33]), 4, 2, 64, torch.bfloat16
     scale = 1.0 / math.sqrt(d)
     q, k, v, pk, pv, dout = make_inputs(meta, hq, hkv, d, dtype, 31, cuda_device)
     print(f"[{case}] tq={meta.total_q} tp={meta.total_prefix} path={meta.plan(hq, hkv, d, dtype, cuda_device).path}",

@@ -78,3 +78,46 @@ def test_lowered_forest_matches_the_per_segment_visits(cuda_device):
     for label, a, b in (("dq", qa.grad, qr.grad), ("dk", ka.grad, kr.grad), ("dv", va.grad, vr.grad)):
         print(f"  {label}: cos={cosine(a, b):.6f}", flush=True)
         assert cosine(a, b) >= BF16_GRAD_COS
+
+
+def test_forest_deeper_than_the_mfma_path_runs_on_the_simt_kernels(cuda_device):
+    """A chain of 11 branchings (12 levels, beyond the MFMA path's 8 ancestors)
+    lowered to one launch: the planner picks the SIMT kernels, and the result
+    matches the per-segment visits."""
+    from bridge_amd import TPRPrefixAttention
+    from bridge_amd.topology import build_trajectory_trees, lower_forest
+    from oracle.trie_oracle import segment_visits
+    g = torch.Generator().manual_seed(4)
+    spine = torch.randint(0, 1000, (12 * 24,), generator=g)
+    # row i shares 24 (i + 1) tokens of the spine, then diverges for 16 tokens
+    rows = [torch.cat([spine[:24 * (i + 1)], torch.randint(1000, 2000, (16,), generator=g)]) for i in range(11)]
+    rows.append(spine.clone())
+    trees = build_trajectory_trees([f"u_s_{i}" for i in range(len(rows))], {"input_ids": rows})
+    launch = lower_forest(trees)
+    meta = launch.meta
+    depth = max(len(a) for a in meta.leaf_ancestors)
+    hq, hkv, d = 4, 2, 128
+    assert depth > 8
+    assert meta.plan(hq, hkv, d, torch.bfloat16, cuda_device).path == "simt"
+    print(f"[deep] segments={meta.num_leaves} depth={depth} tq={meta.total_q}", flush=True)
+    scale = 1.0 / math.sqrt(d)
+    q, k, v, dout = (torch.randn(meta.total_q, x, d, generator=g).bfloat16().to(cuda_device) for x in (hq, hkv, hkv, hq))
+    qa, ka, va = (x.clone().requires_grad_(True) for x in (q, k, v))
+    index = launch.prefix_index.to(cuda_device)
+    out, _ = TPRPrefixAttention.apply(qa, ka, va, ka.index_select(0, index), va.index_select(0, index), meta, scale)
+    out.backward(dout)
+    torch.cuda.synchronize()
+    spans = [(meta.cu_seqlens_q[i], meta.cu_seqlens_q[i + 1]) for i in range(meta.num_leaves)]
+    seg_index = {seg: i for i, seg in enumerate(launch.segments)}
+    parents = []
+    for t, node_id in launch.segments:
+        p = trees[t].get(node_id).parent_id
+        parents.append(None if p is None else seg_index[(t, p)])
+    qr, kr, vr = (x.float().clone().requires_grad_(True) for x in (q, k, v))
+    ref = segment_visits(qr, kr, vr, spans, parents, scale)
+    ref.backward(dout.float())
+    print(f"  out: max_abs={max_abs(out, ref):.3e} cos={cosine(out, ref):.6f}", flush=True)
+    assert max_abs(out, ref) <= BF16_FWD_MAX_ABS and cosine(out, ref) >= BF16_FWD_COS
+    for label, a_, b_ in (("dq", qa.grad, qr.grad), ("dk", ka.grad, kr.grad), ("dv", va.grad, vr.grad)):
+        print(f"  {label}: cos={cosine(a_, b_):.6f}", flush=True)
+        assert cosine(a_, b_) >= BF16_GRAD_COS
