@@ -372,5 +372,7 @@ class PrefixKVStack:
                                  f"got {name}={tuple(g.shape)}")
             if g.device != kbuf.device:
                 raise ValueError(f"{who} layer {layer} gradient device mismatch")
+            if g.dtype != kbuf.dtype:  # prefix_state.py:558-559 (the sum itself is kept in fp32)
+                raise ValueError(f"{who} layer {layer} gradient dtype mismatch")
         gk[start:end].add_(key_grad.detach().reshape(end - start, *gk.shape[1:]).float())
         gv[start:end].add_(value_grad.detach().reshape(end - start, *gv.shape[1:]).float())

@@ -181,6 +181,18 @@ def test_invalid_cached_kv_is_rejected(key_values, match):
         stack.push(segment, key_values)
 
 
+def test_gradient_checks_follow_the_reference():
+    # prefix_state.py:551-559: shape, device and dtype must match the segment's K/V
+    stack = PrefixKVStack(8)
+    entry = stack.push(_segment(0, None, 2, 0), _kv(2, layers=(1,)))
+    with pytest.raises(ValueError, match="shape mismatch"):
+        entry.accumulate(1, torch.ones(3, 1, 2, 4), torch.ones(3, 1, 2, 4))
+    with pytest.raises(ValueError, match="dtype mismatch"):
+        entry.accumulate(1, torch.ones(2, 1, 2, 4, dtype=torch.float64), torch.ones(2, 1, 2, 4, dtype=torch.float64))
+    with pytest.raises(KeyError, match="no KV for layer 2"):
+        entry.accumulate(2, torch.ones(2, 1, 2, 4), torch.ones(2, 1, 2, 4))
+
+
 def test_capacity_and_shape_checks():
     stack = PrefixKVStack(4)
     stack.push(_segment(0, None, 3, 0), _kv(3))
