@@ -321,7 +321,8 @@ def main() -> int:
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(sharding by KV-head group or by sibling is described in DESIGN.md)", file=sys.stderr)
+              "(the kernels would shard by KV-head group, with no exchange, or by sibling, with one "
+              "fixed-order reduction of the prefix gradient)", file=sys.stderr)
         return 2
     if not torch.cuda.is_available():
         print("bench.py needs an MI355X GPU", file=sys.stderr)

@@ -6,7 +6,7 @@ import torch
 
 from oracle.tpr_oracle import Tree, tree_backward, tree_forward
 
-# north-star tolerances
+# parity tolerances: bf16 kernels against the fp32 oracle
 BF16_FWD_MAX_ABS = 2e-2
 BF16_FWD_COS = 0.9999
 BF16_GRAD_COS = 0.999
