@@ -62,6 +62,8 @@ KernelArgs args_from_plan(const int32_t* ph, const int32_t* pd, float scale) {
   a.off_fwd = ph[PF_OFF_FWD];
   a.off_dkdv = ph[PF_OFF_DKDV];
   a.off_red = ph[PF_OFF_RED];
+  a.off_runs = ph[PF_OFF_RUNS];
+  a.max_runs = ph[PF_MAX_RUNS];
   return a;
 }
 

@@ -9,7 +9,7 @@
 namespace tpr {
 
 constexpr int32_t kPlanMagic = 0x31525054;  // "TPR1"
-constexpr int32_t kPlanVersion = 1;
+constexpr int32_t kPlanVersion = 2;
 
 // Header word indices.
 enum PlanField : int {
@@ -41,6 +41,10 @@ enum PlanField : int {
   PF_N_SLOTS,        // fp32 partial slots (each kDkdvKeys x D x 2 floats)
   PF_MAX_SPLIT,      // most partial slots reduced into one tile
   PF_TOTAL_WORDS,
+  PF_OFF_RUNS,       // key runs [N][max_runs][2] = {first row in prefix_k/v, rows}: the leaf's
+                     // ancestor nodes root first, nodes adjacent in prefix_k/v merged, empty
+                     // nodes dropped; {0, 0} pads a leaf with fewer runs
+  PF_MAX_RUNS,       // most key runs of any leaf
   PF_HEADER_WORDS = 32
 };
 
@@ -97,6 +101,7 @@ constexpr int kPlanCus = 256;         // compute units the dK/dV work is balance
 // 0) that rows past a query block's end are copied from, then lse * log2e per
 // (query head, token) in the lse layout.
 constexpr int kStatRowsOffset = 64;   // floats before the lse*log2e rows
-constexpr int kMfmaMaxDepth = 8;      // ancestor nodes per leaf handled by the MFMA path
+constexpr int kMfmaRegRuns = 8;       // key runs a forward / dQ workgroup holds in registers; a
+                                      // launch with longer run lists reads them from the plan
 
 }  // namespace tpr

@@ -45,6 +45,7 @@ struct KernelArgs {
   int32_t total_q, total_prefix, max_depth;
   int32_t off_cu, off_node_off, off_anc, off_node_leaf;
   int32_t off_qblk, off_leaf_qblk, off_fwd, off_dkdv, off_red;
+  int32_t off_runs, max_runs;  // key-run table [N][max_runs][2]
   int32_t n_items;
   float* ws;       // fp32 partial dK/dV slots of split tiles
   float* stat_ws;  // MFMA backward: [0] = +inf, [1] = 0, then lse*log2e rows from kStatRowsOffset

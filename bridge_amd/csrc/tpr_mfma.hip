@@ -129,16 +129,25 @@ __device__ __forceinline__ bf16x8 to_bf16x8(const f32x16& x, int base) {
   return r;
 }
 
-// Key stream of a forward/dQ workgroup: the leaf's ancestor nodes (fully
-// visible, root first) then its own suffix (right-down causal), cut into
-// 64-row tiles. The segment table is read from the plan once, before the
-// tile loop, and stays in (uniform) registers.
+// Key stream of a forward/dQ workgroup: the leaf's ancestor key runs (fully
+// visible; the plan's run table) and its own suffix (right-down causal), cut
+// into 64-row tiles. SegTable holds up to kMfmaRegRuns runs, read from the
+// plan once, before the tile loop, in (uniform) registers; RunList serves
+// launches whose longest run list is longer, and reads a run's (row, len)
+// from the plan when the cursor enters it.
 struct SegTable {
-  int row[kMfmaMaxDepth];   // first row of node d in prefix_k/v
-  int len[kMfmaMaxDepth];   // rows of node d (0 past the leaf's depth)
-  int end[kMfmaMaxDepth];   // tiles in nodes 0..d
+  int row[kMfmaRegRuns];    // first row of run e in prefix_k/v
+  int len[kMfmaRegRuns];    // rows of run e (0 past the leaf's runs)
   int suffix_row;           // first row of the leaf in k/v
   int suffix_keys;          // suffix keys the workgroup needs
+  int ntiles;
+};
+
+struct RunList {
+  const int32_t* runs;      // the leaf's [max_runs][2] = {row, len}; len 0 past its runs
+  int nruns;
+  int suffix_row;
+  int suffix_keys;
   int ntiles;
 };
 
@@ -150,19 +159,17 @@ struct TileLoc {
 };
 
 __device__ __forceinline__ SegTable load_segments(const KernelArgs& a, int leaf, int suffix_keys) {
-  const int32_t* no = a.plan + a.off_node_off;
-  const int32_t* anc = a.plan + a.off_anc + leaf * a.max_depth;
+  const int32_t* runs = a.plan + a.off_runs + 2 * leaf * a.max_runs;
   SegTable t;
   int tiles = 0;
 #pragma unroll
-  for (int d = 0; d < kMfmaMaxDepth; d++) {
-    const int n = d < a.max_depth ? anc[d] : -1;
-    const int r = n >= 0 ? no[n] : 0;
-    const int l = n >= 0 ? no[n + 1] - r : 0;
-    t.row[d] = r;
-    t.len[d] = l;
+  for (int e = 0; e < kMfmaRegRuns; e++) {
+    const bool have = e < a.max_runs;
+    const int r = have ? runs[2 * e] : 0;
+    const int l = have ? runs[2 * e + 1] : 0;
+    t.row[e] = r;
+    t.len[e] = l;
     tiles += (l + kTileRows - 1) / kTileRows;
-    t.end[d] = tiles;
   }
   t.suffix_row = a.plan[a.off_cu + leaf];
   t.suffix_keys = suffix_keys;
@@ -170,23 +177,26 @@ __device__ __forceinline__ SegTable load_segments(const KernelArgs& a, int leaf,
   return t;
 }
 
-// Branch-free: at most one segment contains tile `idx`; the suffix is the default.
-__device__ __forceinline__ TileLoc locate_tile(const SegTable& t, int idx) {
-  int seg_row = t.suffix_row, seg_len = t.suffix_keys, first = t.end[kMfmaMaxDepth - 1];
-  bool suffix = true;
-  int start = 0;
-#pragma unroll
-  for (int d = 0; d < kMfmaMaxDepth; d++) {
-    const bool in = (idx >= start) & (idx < t.end[d]);
-    seg_row = in ? t.row[d] : seg_row;
-    seg_len = in ? t.len[d] : seg_len;
-    first = in ? start : first;
-    suffix = in ? false : suffix;
-    start = t.end[d];
+__device__ __forceinline__ RunList load_runs(const KernelArgs& a, int leaf, int suffix_keys) {
+  RunList t;
+  t.runs = a.plan + a.off_runs + 2 * leaf * a.max_runs;
+  int n = 0, tiles = 0;
+  for (; n < a.max_runs; n++) {
+    const int l = t.runs[2 * n + 1];
+    if (l == 0) break;  // runs are non-empty; {0, 0} pads the list
+    tiles += (l + kTileRows - 1) / kTileRows;
   }
-  const int lt = idx - first;
-  return TileLoc{static_cast<int64_t>(seg_row) + lt * kTileRows, min(kTileRows, seg_len - lt * kTileRows),
-                 lt * kTileRows, suffix};
+  t.nruns = n;
+  t.suffix_row = a.plan[a.off_cu + leaf];
+  t.suffix_keys = suffix_keys;
+  t.ntiles = tiles + (suffix_keys + kTileRows - 1) / kTileRows;
+  return t;
+}
+
+template <bool kRunList>
+__device__ __forceinline__ auto load_keys(const KernelArgs& a, int leaf, int suffix_keys) {
+  if constexpr (kRunList) return load_runs(a, leaf, suffix_keys);
+  else return load_segments(a, leaf, suffix_keys);
 }
 
 // Direct global -> LDS copy (gfx950 global_load_lds_dwordx4) of the 64 rows
@@ -394,7 +404,7 @@ struct Cursor {
 __device__ __forceinline__ void cursor_load(const SegTable& t, Cursor& c) {
   int row = t.suffix_row, len = c.d == 0 ? t.suffix_keys : 0;
 #pragma unroll
-  for (int e = 0; e < kMfmaMaxDepth; e++) {
+  for (int e = 0; e < kMfmaRegRuns; e++) {
     row = c.d == e + 1 ? t.row[e] : row;
     len = c.d == e + 1 ? t.len[e] : len;
   }
@@ -402,20 +412,34 @@ __device__ __forceinline__ void cursor_load(const SegTable& t, Cursor& c) {
   c.len = len;
 }
 
-__device__ __forceinline__ Cursor cursor_begin(const SegTable& t) {
+// Reads run c.d - 1 of the plan only when it is one of the leaf's runs.
+__device__ __forceinline__ void cursor_load(const RunList& t, Cursor& c) {
+  int row = t.suffix_row, len = c.d == 0 ? t.suffix_keys : 0;
+  if (c.d > 0 && c.d <= t.nruns) {
+    row = t.runs[2 * (c.d - 1)];
+    len = t.runs[2 * (c.d - 1) + 1];
+  }
+  c.row = row;
+  c.len = len;
+}
+
+template <typename Keys>
+__device__ __forceinline__ Cursor cursor_begin(const Keys& t) {
   Cursor c{0, 0, 0, 0};  // the suffix holds at least one key
   cursor_load(t, c);
   return c;
 }
 
-__device__ __forceinline__ void cursor_next(const SegTable& t, Cursor& c) {
+// Past the last run the cursor stays at an empty segment (len 0).
+template <typename Keys>
+__device__ __forceinline__ void cursor_next(const Keys& t, Cursor& c) {
   c.lt++;
   if (c.lt * kTileRows >= c.len) {
     c.lt = 0;
     do {
       c.d++;
       cursor_load(t, c);
-    } while (c.len == 0 && c.d < kMfmaMaxDepth);
+    } while (c.len == 0 && c.d < kMfmaRegRuns);
   }
 }
 
@@ -504,6 +528,7 @@ constexpr float kRescaleSlack = 8.f;
 #endif
 constexpr int kMphaseAhead = TPR_MPHASE_AHEAD;  // LDS reads issued ahead in a forward M phase (even)
 
+template <bool kRunList>  // key runs read from the plan (more than kMfmaRegRuns)
 __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
   const int32_t* item = a.plan + a.off_fwd + 4 * blockIdx.x;
   const int leaf = item[0];
@@ -536,7 +561,7 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
   const TileLanes4 dl = make_tile_lanes4(wave & 3, lane);
   const FwdLdsOffsets lo = make_fwd_lds_offsets(lane);
 
-  const SegTable seg = load_segments(a, leaf, suffix_keys);
+  const auto seg = load_keys<kRunList>(a, leaf, suffix_keys);
   const int ntiles = seg.ntiles;
   auto kv_src = [&](const TileLoc& x, bool is_k) {
     const char* b = x.suffix ? (is_k ? kbase : vbase) : (is_k ? pkbase : pvbase);
@@ -807,6 +832,7 @@ __device__ __forceinline__ uint32_t kt_off(int d, int chunk) {
 #endif
 constexpr int kDqAhead = TPR_DQ_AHEAD;  // LDS reads issued ahead in a dQ M phase
 
+template <bool kRunList>  // key runs read from the plan (more than kMfmaRegRuns)
 __global__ __launch_bounds__(512) void mfma_dq(KernelArgs a) {
   static_assert(kFwdWaves == 8, "two groups of one wave per SIMD");
   const int32_t* item = a.plan + a.off_fwd + 4 * blockIdx.x;
@@ -857,7 +883,7 @@ __global__ __launch_bounds__(512) void mfma_dq(KernelArgs a) {
     tro[1] = static_cast<uint32_t>(swz_off(row + 4, col));
   }
 
-  const SegTable seg = load_segments(a, leaf, suffix_keys);
+  const auto seg = load_keys<kRunList>(a, leaf, suffix_keys);
   const int ntiles = seg.ntiles;
   auto kv_src = [&](const TileLoc& x, bool is_k) __attribute__((always_inline)) {
     const char* b = x.suffix ? (is_k ? kbase : vbase) : (is_k ? pkbase : pvbase);
@@ -1496,7 +1522,12 @@ __global__ __launch_bounds__(256) void mfma_reduce(KernelArgs a) {
 }  // namespace
 
 int launch_mfma_fwd(const KernelArgs& a, hipStream_t s) {
-  if (a.n_items > 0) hipLaunchKernelGGL(mfma_fwd, dim3(a.n_items), dim3(64 * kFwdWaves), 0, s, a);
+  if (a.n_items > 0) {
+    if (a.max_runs > kMfmaRegRuns)
+      hipLaunchKernelGGL(mfma_fwd<true>, dim3(a.n_items), dim3(64 * kFwdWaves), 0, s, a);
+    else
+      hipLaunchKernelGGL(mfma_fwd<false>, dim3(a.n_items), dim3(64 * kFwdWaves), 0, s, a);
+  }
   return hipGetLastError() == hipSuccess ? 0 : 4;
 }
 
@@ -1520,7 +1551,10 @@ int launch_mfma_bwd(const KernelArgs& a, int n_fwd, int n_dkdv, int n_red, hipSt
     if (hipGetLastError() != hipSuccess) return 4;
   }
   if (n_fwd > 0) {
-    hipLaunchKernelGGL(mfma_dq, dim3(n_fwd), dim3(64 * kFwdWaves), 0, s, a);
+    if (a.max_runs > kMfmaRegRuns)
+      hipLaunchKernelGGL(mfma_dq<true>, dim3(n_fwd), dim3(64 * kFwdWaves), 0, s, a);
+    else
+      hipLaunchKernelGGL(mfma_dq<false>, dim3(n_fwd), dim3(64 * kFwdWaves), 0, s, a);
     if (hipGetLastError() != hipSuccess) return 4;
   }
   return 0;

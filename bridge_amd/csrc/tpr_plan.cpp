@@ -140,7 +140,7 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
                   "descendant leaves of node %d are not contiguous; number leaves in DFS order", n);
   }
 
-  const int path = (t->dtype == TPR_DTYPE_BF16 && D == kMfmaD && depth <= kMfmaMaxDepth) ? PATH_MFMA : PATH_SIMT;
+  const int path = (t->dtype == TPR_DTYPE_BF16 && D == kMfmaD) ? PATH_MFMA : PATH_SIMT;
   const int G = Hq / Hkv;
   std::vector<int64_t> prefix_len(N, 0);
   for (int s = 0; s < N; s++)
@@ -148,6 +148,34 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
       int n = anc[s * depth + d];
       if (n >= 0) prefix_len[s] += no[n + 1] - no[n];
     }
+
+  // ---- key runs (the MFMA forward / dQ key streams) --------------------------
+  // A leaf's ancestors, root first, as runs of rows of prefix_k/v: an ancestor
+  // that starts where the previous one ends extends its run (in DFS layout a
+  // chain of first children is one run), and empty nodes add nothing. Every
+  // ancestor key is visible to every query of the leaf, so only the rows
+  // matter, not the node boundaries.
+  std::vector<int32_t> runs_flat;
+  int max_runs = 0;
+  std::vector<std::vector<int32_t>> leaf_runs(N);
+  for (int s = 0; s < N; s++) {
+    std::vector<int32_t>& r = leaf_runs[s];
+    for (int d = 0; d < depth; d++) {
+      const int n = anc[s * depth + d];
+      if (n < 0) break;
+      const int32_t row = no[n], len = no[n + 1] - no[n];
+      if (len == 0) continue;
+      if (!r.empty() && r[r.size() - 2] + r.back() == row)
+        r.back() += len;
+      else
+        r.insert(r.end(), {row, len});
+    }
+    max_runs = std::max(max_runs, static_cast<int>(r.size() / 2));
+  }
+  const int run_words = 2 * std::max(max_runs, 1);
+  runs_flat.assign(static_cast<size_t>(N) * run_words, 0);
+  for (int s = 0; s < N; s++)
+    std::copy(leaf_runs[s].begin(), leaf_runs[s].end(), runs_flat.begin() + static_cast<size_t>(s) * run_words);
 
   // ---- query-block list (dK/dV granularity) --------------------------------
   const int BQ = path == PATH_MFMA ? kDkdvQ : kSimtTile;
@@ -305,6 +333,8 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
   plan[PF_OFF_RED] = append(red.data(), red.size());
   plan[PF_N_SLOTS] = n_slots;
   plan[PF_MAX_SPLIT] = max_split;
+  plan[PF_OFF_RUNS] = append(runs_flat.data(), runs_flat.size());
+  plan[PF_MAX_RUNS] = std::max(max_runs, 1);
   plan[PF_TOTAL_WORDS] = static_cast<int32_t>(plan.size());
   return TPR_OK;
 }

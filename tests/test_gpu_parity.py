@@ -37,11 +37,31 @@ def _meta_cases():
                           leaf_ancestors=((0, 1), (0, 1), (0, 2), (0, 2))), 8, 2),
         "unused_node": (M(cu_seqlens_q=(0, 40), node_offsets=(0, 10, 30), leaf_ancestors=((0,),)), 4, 1),
         "empty_leaf": (M.shared_prefix(50, [0, 60, 0]), 4, 1),
+        # 12 nested nodes of ragged lengths laid out root first: every leaf's
+        # ancestors form one key run
+        "deep_chain_one_run": (M(cu_seqlens_q=(0, 50, 179, 243), node_offsets=_offsets(_DEEP_LENS),
+                                 leaf_ancestors=(tuple(range(12)), tuple(range(9)), tuple(range(3)))), 8, 2),
+        # the same chain laid out deepest node first: 12, 9 and 3 separate key
+        # runs, more than the forward / dQ kernels hold in registers
+        "deep_run_list": (M(cu_seqlens_q=(0, 50, 179, 243), node_offsets=_offsets(_DEEP_LENS[::-1]),
+                            leaf_ancestors=(tuple(range(11, -1, -1)), tuple(range(11, 2, -1)),
+                                            tuple(range(11, 8, -1)))), 8, 2),
     }
 
 
+_DEEP_LENS = (29, 66, 2, 40, 17, 90, 5, 33, 64, 1, 70, 13)
+
+
+def _offsets(lens):
+    out = [0]
+    for n in lens:
+        out.append(out[-1] + n)
+    return tuple(out)
+
+
 CASES = ["shared_prefix_gqa4", "no_prefix", "tile_aligned", "mha", "gqa2", "gqa3", "depth3_tree",
-         "unused_node", "empty_leaf"]
+         "unused_node", "empty_leaf", "deep_chain_one_run", "deep_run_list"]
+KEY_RUNS = {"deep_chain_one_run": 1, "deep_run_list": 12}   # plan header word 29: most runs of a leaf
 
 
 def _run(meta, q, k, v, pk, pv, dout, scale):
@@ -68,7 +88,10 @@ def test_mfma_bf16_matches_oracle(name, cuda_device):
     d = 128
     scale = 1.0 / math.sqrt(d)
     q, k, v, pk, pv, dout = make_inputs(meta, hq, hkv, d, torch.bfloat16, seed=1234, device=cuda_device)
-    assert meta.plan(hq, hkv, d, torch.bfloat16, cuda_device).path == "mfma"
+    plan = meta.plan(hq, hkv, d, torch.bfloat16, cuda_device)
+    assert plan.path == "mfma"
+    if name in KEY_RUNS:
+        assert int(plan.host[29]) == KEY_RUNS[name]
     out, lse, grads = _run(meta, q, k, v, pk, pv, dout, scale)
     ref = oracle(meta, q, k, v, pk, pv, dout, scale)
     _report(name, out, lse, grads, ref)

@@ -14,7 +14,8 @@ CPU = torch.device("cpu")
 # header word indices (bridge_amd/csrc/tpr_common.h)
 PF = dict(MAGIC=0, NUM_LEAVES=2, NUM_NODES=3, MAX_DEPTH=4, TOTAL_Q=5, TOTAL_PREFIX=6, HQ=7, HKV=8, D=9,
           PATH=11, OFF_CU=12, OFF_NODE_OFF=13, OFF_ANC=14, OFF_NODE_LEAF=15, N_QBLK=16, OFF_QBLK=17,
-          OFF_LEAF_QBLK=18, N_FWD=19, OFF_FWD=20, N_DKDV=21, OFF_DKDV=22, N_RED=23, TOTAL_WORDS=27)
+          OFF_LEAF_QBLK=18, N_FWD=19, OFF_FWD=20, N_DKDV=21, OFF_DKDV=22, N_RED=23, TOTAL_WORDS=27,
+          OFF_RUNS=28, MAX_RUNS=29)
 
 FWD_WAVES = 8  # waves per forward / dQ workgroup (kFwdWaves)
 
@@ -145,12 +146,50 @@ def test_split_prefix_tiles_have_ordered_partials_and_reductions():
     assert not direct & reduced
 
 
-def test_deep_trees_use_the_simt_path():
+def key_runs(plan):
+    """(max_runs, per-leaf [(row, len)]) from the plan's key-run table."""
+    w = plan.host.tolist()
+    off, width = w[PF["OFF_RUNS"]], w[PF["MAX_RUNS"]]
+    runs = []
+    for s in range(w[PF["NUM_LEAVES"]]):
+        e = w[off + 2 * width * s: off + 2 * width * (s + 1)]
+        pairs = [(e[2 * i], e[2 * i + 1]) for i in range(width)]
+        n = sum(1 for _, ln in pairs if ln > 0)
+        assert all(ln > 0 for _, ln in pairs[:n]) and pairs[n:] == [(0, 0)] * (width - n)
+        runs.append(pairs[:n])
+    return width, runs
+
+
+def test_deep_chain_laid_out_root_first_is_one_key_run():
     depth = 9
     meta = TPRPrefixMeta(cu_seqlens_q=(0, 5), node_offsets=tuple(range(0, 4 * depth + 1, 4)),
                          leaf_ancestors=(tuple(range(depth)),))
-    assert meta.plan(4, 2, 128, torch.bfloat16, CPU).path == "simt"
-    assert meta.plan(4, 2, 128, torch.bfloat16, CPU).workspace_bytes == 0
+    plan = meta.plan(4, 2, 128, torch.bfloat16, CPU)
+    assert plan.path == "mfma"
+    assert key_runs(plan) == (1, [[(0, 36)]])
+
+
+def test_deep_chain_laid_out_leaf_first_keeps_one_run_per_node():
+    # root = node 8 at rows [32, 36), its child node 7 at [28, 32), ...: no
+    # ancestor starts where the previous one (root first) ends
+    depth = 12
+    meta = TPRPrefixMeta(cu_seqlens_q=(0, 5), node_offsets=tuple(range(0, 4 * depth + 1, 4)),
+                         leaf_ancestors=(tuple(reversed(range(depth))),))
+    plan = meta.plan(4, 2, 128, torch.bfloat16, CPU)
+    assert plan.path == "mfma"
+    assert key_runs(plan) == (12, [[(4 * n, 4) for n in reversed(range(depth))]])
+
+
+def test_key_runs_merge_adjacent_ancestors_and_drop_empty_nodes():
+    # node 0 [0, 10), node 1 empty, node 2 [10, 30) under 1, node 3 [30, 45) under 0
+    meta = TPRPrefixMeta(cu_seqlens_q=(0, 5, 9, 12), node_offsets=(0, 10, 10, 30, 45),
+                         leaf_ancestors=((0, 1, 2), (0, 3), ()))
+    width, runs = key_runs(meta.plan(8, 2, 128, torch.bfloat16, CPU))
+    assert width == 2
+    assert runs == [[(0, 30)], [(0, 10), (30, 15)], []]
+    # the visible keys of each leaf are unchanged by the merging
+    for leaf, leaf_runs in enumerate(runs):
+        assert sum(ln for _, ln in leaf_runs) == meta.prefix_length(leaf)
 
 
 def test_simt_path_for_fp32_and_small_head_dim():
