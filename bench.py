@@ -29,7 +29,7 @@ import time
 import torch
 
 BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
-FP32_PEAK_TFLOPS = 157.3    # MI355X dense fp32 MFMA
+FP32_PEAK_TFLOPS = 157.3    # MI355X fp32 (matrix and vector)
 HBM_PEAK_GBS = 8000.0
 
 
@@ -56,6 +56,9 @@ def workload(name: str):
         lens = torch.randint(256, 8193, (16,), generator=g).tolist()
         return (f"ragged varlen: prefix 8192 + 16 suffixes U[256,8192] (seed 0), GQA 32/8, d128, bf16",
                 TPRPrefixMeta.shared_prefix(8192, lens), 32, 8, 128, torch.bfloat16)
+    if name == "qwen35-attn":   # head_dim 256: the SIMT kernels
+        return ("Qwen3.5 hybrid full-attention layer: prefix 4096 + 4 x 4096 sibling suffixes, GQA 8/2, d256, bf16",
+                TPRPrefixMeta.shared_prefix(4096, [4096] * 4), 8, 2, 256, torch.bfloat16)
     if name == "turn-tree":
         anc = tuple((0, 1 + i // 4) for i in range(16))
         meta = TPRPrefixMeta(tuple(1024 * i for i in range(17)), (0, 2048, 3072, 4096, 5120, 6144), anc)
@@ -305,7 +308,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="qwen3-4b",
-                    choices=["qwen3-4b", "plumbing-fp32", "long-session", "ragged", "turn-tree",
+                    choices=["qwen3-4b", "plumbing-fp32", "long-session", "ragged", "turn-tree", "qwen35-attn",
                              "qwen3-4b-1sibling", "qwen3-4b-noprefix"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -400,7 +403,8 @@ def main() -> int:
     unit = 2.0 * hq * d * pairs          # FLOP of one GEMM over the visible pairs
     total_flops = 7.0 * unit            # fwd (2 GEMMs) + bwd (5 GEMMs)
     value = total_flops / (ms_per_step * 1e-3) / 1e12
-    peak = BF16_PEAK_TFLOPS if dtype == torch.bfloat16 else FP32_PEAK_TFLOPS
+    # the SIMT kernels compute in fp32 on the vector ALUs, whatever the I/O dtype
+    peak = BF16_PEAK_TFLOPS if plan.path == "mfma" else FP32_PEAK_TFLOPS
     kernels = {
         "fwd": (fwd_ms, 2.0 * unit, "tpr::mfma_fwd" if plan.path == "mfma" else "tpr::simt_fwd"),
         "dkdv": (dkdv_ms, 4.0 * unit, "tpr::mfma_dkdv" if plan.path == "mfma" else "tpr::simt_dkdv"),

@@ -49,7 +49,7 @@ enum PlanField : int {
 };
 
 enum KernelPath : int32_t {
-  PATH_SIMT = 0,  // portable fp32-accumulate SIMT kernels (fp32, or any head_dim)
+  PATH_SIMT = 0,  // fp32-accumulate SIMT kernels (fp32, or bf16 with head_dim != 128)
   PATH_MFMA = 1   // bf16 MFMA kernels, head_dim 128
 };
 
@@ -81,7 +81,7 @@ enum RedField : int {
 };
 
 // ---- tile shapes -----------------------------------------------------------
-// SIMT family (any dtype / head_dim <= 128)
+// SIMT family (fp32, or bf16 with head_dim != 128; head_dim a multiple of 8, at most 256)
 constexpr int kSimtQ = 64;      // queries per forward / dQ block (one head)
 constexpr int kSimtKeys = 64;   // keys per dK/dV block
 constexpr int kSimtTile = 32;   // keys (fwd/dQ) or queries (dK/dV) staged per LDS tile

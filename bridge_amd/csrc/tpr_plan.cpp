@@ -93,8 +93,8 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
     return fail(TPR_ERR_INVALID_ARGUMENT, "head counts and head_dim must be positive, got Hq=%d Hkv=%d D=%d", Hq, Hkv, D);
   if (Hq % Hkv != 0)
     return fail(TPR_ERR_INVALID_ARGUMENT, "query head count must be divisible by KV head count, got Q=%d, KV=%d", Hq, Hkv);
-  if (D > 128 || D % 8 != 0)
-    return fail(TPR_ERR_UNSUPPORTED, "head_dim must be a multiple of 8 and at most 128, got %d", D);
+  if (D > 256 || D % 8 != 0)
+    return fail(TPR_ERR_UNSUPPORTED, "head_dim must be a multiple of 8 and at most 256, got %d", D);
   if (t->dtype != TPR_DTYPE_BF16 && t->dtype != TPR_DTYPE_FP32)
     return fail(TPR_ERR_INVALID_ARGUMENT, "unknown dtype %d", t->dtype);
   if (!t->cu_seqlens_q || !t->node_offsets || (N * depth > 0 && !t->leaf_ancestors))

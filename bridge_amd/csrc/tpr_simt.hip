@@ -1,9 +1,16 @@
 // tpr_simt.hip -- SIMT (non-MFMA) prefix-reuse attention kernels.
 //
 // The path for fp32 inputs (fp32 accumulate, tolerance 1e-4 against the fp64
-// oracle) and for any head_dim <= 128 the MFMA family does not cover. One
-// thread owns one query row (forward, dQ) or one key row (dK/dV); K/V (or
-// Q/dO) tiles are staged through LDS and shared by the 64 threads of a block.
+// oracle) and for the head dims the MFMA family does not cover (any multiple
+// of 8 up to 256). A row -- a query row in the forward and dQ, a key row in
+// dK/dV -- is spread over kL = DMAX / 32 adjacent lanes, each holding 32 of
+// its elements in registers: lane c of a group holds the 8 chunks of 4
+// elements starting at 4*kL*j + 4*c (j < 8), so the kL lanes reading chunk j
+// of an LDS row read 16*kL contiguous bytes. Dot products are summed over the
+// group with DPP lane swaps, in an order that gives every lane of the group
+// the same bits, so the softmax state stays identical across the group.
+// K/V (or Q/dO) tiles are staged in LDS as fp32 and read by every row group
+// at once (broadcast reads).
 //
 // Math (per leaf, per query head; reference: _fa_fp32_reference.py:12-28):
 //   s_j = scale * q . k_j over keys j = cat(ancestor nodes, suffix keys <= i)
@@ -12,108 +19,217 @@
 //   p_j = exp(s_j - lse), dv_j += p_j dout, dp_j = dout . v_j,
 //   ds_j = p_j (dp_j - delta), delta = dout . out,
 //   dq = scale sum_j ds_j k_j, dk_j += scale ds_j q.
+// Key streams: the leaf's own suffix, then its ancestors' key runs (the
+// plan's run table: ancestors root first, rows adjacent in prefix_k/v merged).
 
 #include "tpr_device.h"
 
 namespace tpr {
 namespace {
 
-template <typename T>
-__device__ __forceinline__ void load_row(const T* src, int d, float* dst) {
-  for (int i = 0; i < d; i++) dst[i] = to_f32(src[i]);
+// Rows staged per LDS tile: 16 KiB of fp32 per tile at most.
+template <int DMAX>
+constexpr int simt_tile() { return DMAX >= 256 ? 16 : 32; }
+
+__device__ __forceinline__ f32x4 load4(const float* p) { return f32x4{p[0], p[1], p[2], p[3]}; }
+__device__ __forceinline__ f32x4 load4(const bf16* p) {
+  return f32x4{static_cast<float>(p[0]), static_cast<float>(p[1]), static_cast<float>(p[2]),
+               static_cast<float>(p[3])};
+}
+__device__ __forceinline__ void store4(float* p, f32x4 v) {
+  p[0] = v.x;
+  p[1] = v.y;
+  p[2] = v.z;
+  p[3] = v.w;
+}
+__device__ __forceinline__ void store4(bf16* p, f32x4 v) {
+  p[0] = static_cast<bf16>(v.x);
+  p[1] = static_cast<bf16>(v.y);
+  p[2] = static_cast<bf16>(v.z);
+  p[3] = static_cast<bf16>(v.w);
 }
 
-// Stage `rows` rows of a [*, heads, d] tensor into an fp32 LDS tile; rows at
-// or beyond `valid` and columns at or beyond `d` are zero-filled.
-template <typename T, int DMAX>
-__device__ __forceinline__ void stage_rows(float (*tile)[DMAX + 1], const T* base, int64_t row_stride,
-                                           int row0, int rows, int valid, int d) {
-  for (int idx = threadIdx.x; idx < rows * DMAX; idx += blockDim.x) {
-    const int r = idx / DMAX, c = idx % DMAX;
-    tile[r][c] = (r < valid && c < d) ? to_f32(base[static_cast<int64_t>(row0 + r) * row_stride + c]) : 0.f;
+// The lane's 32 elements of one row of a global [*, heads, d] tensor, times
+// `mul`; elements at or beyond d are 0.
+template <int kL, typename T>
+__device__ __forceinline__ void load_slice(const T* row, int d, int c, float mul, f32x4 (&x)[8]) {
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const int e = 4 * kL * j + 4 * c;
+    x[j] = e < d ? load4(row + e) * mul : f32x4{0.f, 0.f, 0.f, 0.f};
   }
 }
 
+template <int kL, typename T>
+__device__ __forceinline__ void store_slice(T* row, int d, int c, float mul, const f32x4 (&x)[8]) {
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const int e = 4 * kL * j + 4 * c;
+    if (e < d) store4(row + e, x[j] * mul);
+  }
+}
+
+// The lane's 32 elements of one row of an fp32 LDS tile with DMAX columns.
+template <int kL>
+__device__ __forceinline__ void read_slice(const float* lds_row, int c, f32x4 (&x)[8]) {
+#pragma unroll
+  for (int j = 0; j < 8; j++) x[j] = *reinterpret_cast<const f32x4*>(lds_row + 4 * kL * j + 4 * c);
+}
+
+template <int kL>
+__device__ __forceinline__ float dot_lds(const f32x4 (&x)[8], const float* lds_row, int c) {
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const f32x4 y = *reinterpret_cast<const f32x4*>(lds_row + 4 * kL * j + 4 * c);
+    s += x[j].x * y.x;
+    s += x[j].y * y.y;
+    s += x[j].z * y.z;
+    s += x[j].w * y.w;
+  }
+  return s;
+}
+
+__device__ __forceinline__ float dot_regs(const f32x4 (&x)[8], const f32x4 (&y)[8]) {
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    s += x[j].x * y[j].x;
+    s += x[j].y * y[j].y;
+    s += x[j].z * y[j].z;
+    s += x[j].w * y[j].w;
+  }
+  return s;
+}
+
+// acc += p * lds row (the lane's 32 elements)
+template <int kL>
+__device__ __forceinline__ void axpy_lds(f32x4 (&acc)[8], float p, const float* lds_row, int c) {
+#pragma unroll
+  for (int j = 0; j < 8; j++) acc[j] += p * *reinterpret_cast<const f32x4*>(lds_row + 4 * kL * j + 4 * c);
+}
+
+// x from the lane the DPP control selects (quad_perm / row_half_mirror stay
+// within the lane's aligned group of 8, so every source lane is active).
+template <int kCtrl>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kCtrl, 0xF, 0xF, false));
+}
+
+// Sum over the kL (2, 4 or 8) adjacent lanes of an aligned group. Each step
+// adds the partner's partial sum of the same size, and addition commutes, so
+// all lanes of the group end with the same bits.
+template <int kL>
+__device__ __forceinline__ float group_sum(float x) {
+  static_assert(kL == 2 || kL == 4 || kL == 8, "2, 4 or 8 lanes per row");
+  x += dpp<0xB1>(x);                          // quad_perm(1, 0, 3, 2): lane ^ 1
+  if constexpr (kL >= 4) x += dpp<0x4E>(x);   // quad_perm(2, 3, 0, 1): lane ^ 2
+  if constexpr (kL >= 8) x += dpp<0x141>(x);  // row_half_mirror: lane i <-> 7 - i of 8
+  return x;
+}
+
+// Stage rows [row0, row0 + rows) of a [*, heads, d] tensor (row stride
+// `stride` elements, head offset applied to `base`) into an fp32 LDS tile of
+// DMAX columns; rows at or beyond `valid` and columns at or beyond d are 0.
+template <int DMAX, typename T>
+__device__ __forceinline__ void stage_tile(float* tile, const T* base, int64_t stride, int64_t row0, int rows,
+                                           int valid, int d) {
+  for (int idx = threadIdx.x; idx < rows * (DMAX / 4); idx += blockDim.x) {
+    const int r = idx / (DMAX / 4), e = 4 * (idx % (DMAX / 4));
+    f32x4 x = {0.f, 0.f, 0.f, 0.f};
+    if (r < valid && e < d) x = load4(base + (row0 + r) * stride + e);
+    *reinterpret_cast<f32x4*>(tile + r * DMAX + e) = x;
+  }
+}
+
+// Segment sg of a forward / dQ workgroup's key stream: 0 = the leaf's suffix
+// (the first `suffix_keys` keys, causal), 1 + r = key run r of the leaf.
+// Returns false past the last run.
+template <typename T>
+__device__ __forceinline__ bool key_segment(const KernelArgs& a, int leaf, int sg, int suffix_keys, int kvh,
+                                            const T*& kb, const T*& vb, int& seg_len) {
+  const int64_t ks = static_cast<int64_t>(a.hkv) * a.d;
+  if (sg == 0) {
+    const int row0 = a.plan[a.off_cu + leaf];
+    kb = static_cast<const T*>(a.k) + static_cast<int64_t>(row0) * ks + kvh * a.d;
+    vb = static_cast<const T*>(a.v) + static_cast<int64_t>(row0) * ks + kvh * a.d;
+    seg_len = suffix_keys;
+    return true;
+  }
+  if (sg > a.max_runs) return false;
+  const int32_t* run = a.plan + a.off_runs + 2 * (leaf * a.max_runs + sg - 1);
+  seg_len = run[1];
+  if (seg_len == 0) return false;  // {0, 0} pads the run list
+  kb = static_cast<const T*>(a.pk) + static_cast<int64_t>(run[0]) * ks + kvh * a.d;
+  vb = static_cast<const T*>(a.pv) + static_cast<int64_t>(run[0]) * ks + kvh * a.d;
+  return true;
+}
+
 // ---------------------------------------------------------------------------
-// Forward: block = 64 queries of one head of one leaf.
+// Forward: block = kSimtQ queries of one head of one leaf, kL lanes per query.
 template <typename T, int DMAX>
-__global__ __launch_bounds__(kSimtQ) void simt_fwd(KernelArgs a) {
+__global__ __launch_bounds__(kSimtQ * DMAX / 32) void simt_fwd(KernelArgs a) {
+  constexpr int kL = DMAX / 32, kTile = simt_tile<DMAX>();
   const int32_t* item = a.plan + a.off_fwd + 4 * blockIdx.x;
   const int leaf = item[0];
   if (leaf < 0) return;
   const int tok0 = item[1], qh = item[2], kvh = item[3];
   const int32_t* cu = a.plan + a.off_cu;
-  const int32_t* no = a.plan + a.off_node_off;
-  const int32_t* anc = a.plan + a.off_anc;
   const int row0 = cu[leaf], len = cu[leaf + 1] - cu[leaf];
   const int d = a.d;
-  const int t = tok0 + threadIdx.x;
+  const int c = threadIdx.x % kL;
+  const int t = tok0 + static_cast<int>(threadIdx.x) / kL;
   const bool valid = t < len;
   const int64_t qs = static_cast<int64_t>(a.hq) * d, ks = static_cast<int64_t>(a.hkv) * d;
 
-  __shared__ float Ks[kSimtTile][DMAX + 1];
-  __shared__ float Vs[kSimtTile][DMAX + 1];
+  __shared__ __attribute__((aligned(16))) float Ks[kTile * DMAX];
+  __shared__ __attribute__((aligned(16))) float Vs[kTile * DMAX];
 
-  float q[DMAX], acc[DMAX];
-  const float c = a.scale * kLog2e;
-  {
-    const T* src = static_cast<const T*>(a.q) + static_cast<int64_t>(row0 + (valid ? t : 0)) * qs + qh * d;
-    for (int i = 0; i < DMAX; i++) q[i] = i < d ? to_f32(src[i]) * c : 0.f;
-  }
-  for (int i = 0; i < DMAX; i++) acc[i] = 0.f;
+  f32x4 q[8], o[8];
+  load_slice<kL>(static_cast<const T*>(a.q) + static_cast<int64_t>(row0 + (valid ? t : 0)) * qs + qh * d, d, c,
+                 a.scale * kLog2e, q);
+#pragma unroll
+  for (int j = 0; j < 8; j++) o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, l = 0.f;
 
-  const int tok_last = min(len, tok0 + kSimtQ);  // suffix keys needed by the block
-  const int nseg = a.max_depth + 1;
-  for (int sg = 0; sg < nseg; sg++) {
-    const T *kb, *vb;
-    int seg_len;
-    bool causal;
-    if (sg < a.max_depth) {
-      const int n = anc[leaf * a.max_depth + sg];
-      if (n < 0) continue;
-      kb = static_cast<const T*>(a.pk) + static_cast<int64_t>(no[n]) * ks + kvh * d;
-      vb = static_cast<const T*>(a.pv) + static_cast<int64_t>(no[n]) * ks + kvh * d;
-      seg_len = no[n + 1] - no[n];
-      causal = false;
-    } else {
-      kb = static_cast<const T*>(a.k) + static_cast<int64_t>(row0) * ks + kvh * d;
-      vb = static_cast<const T*>(a.v) + static_cast<int64_t>(row0) * ks + kvh * d;
-      seg_len = tok_last;
-      causal = true;
-    }
-    for (int j0 = 0; j0 < seg_len; j0 += kSimtTile) {
-      const int nk = min(kSimtTile, seg_len - j0);
+  const int suffix_keys = min(len, tok0 + kSimtQ);
+  const T *kb, *vb;
+  int seg_len;
+  for (int sg = 0; key_segment<T>(a, leaf, sg, suffix_keys, kvh, kb, vb, seg_len); sg++) {
+    const bool causal = sg == 0;
+    for (int j0 = 0; j0 < seg_len; j0 += kTile) {
+      const int nk = min(kTile, seg_len - j0);
       __syncthreads();
-      stage_rows<T, DMAX>(Ks, kb, ks, j0, kSimtTile, nk, d);
-      stage_rows<T, DMAX>(Vs, vb, ks, j0, kSimtTile, nk, d);
+      stage_tile<DMAX>(Ks, kb, ks, j0, kTile, nk, d);
+      stage_tile<DMAX>(Vs, vb, ks, j0, kTile, nk, d);
       __syncthreads();
-      float s[kSimtTile];
+      float s[kTile];
       float mt = m;
-      for (int j = 0; j < kSimtTile; j++) {
-        float x = 0.f;
-        for (int i = 0; i < DMAX; i++) x += q[i] * Ks[j][i];
+#pragma unroll
+      for (int j = 0; j < kTile; j++) {
+        const float x = group_sum<kL>(dot_lds<kL>(q, Ks + j * DMAX, c));
         const bool vis = j < nk && (!causal || j0 + j <= t);
         s[j] = vis ? x : -INFINITY;
         mt = fmaxf(mt, s[j]);
       }
-      if (mt == -INFINITY) continue;  // nothing visible yet for this row
-      const float alpha = exp2f(m - mt);
+      // nothing visible yet for this row: keep the (empty) state as it is
+      const float mref = mt == -INFINITY ? 0.f : mt;
+      const float alpha = exp2f(m - mref);
       l *= alpha;
-      for (int i = 0; i < DMAX; i++) acc[i] *= alpha;
-      for (int j = 0; j < kSimtTile; j++) {
-        const float p = exp2f(s[j] - mt);
+#pragma unroll
+      for (int j = 0; j < 8; j++) o[j] *= alpha;
+#pragma unroll
+      for (int j = 0; j < kTile; j++) {
+        const float p = exp2f(s[j] - mref);
         l += p;
-        for (int i = 0; i < DMAX; i++) acc[i] += p * Vs[j][i];
+        axpy_lds<kL>(o, p, Vs + j * DMAX, c);
       }
       m = mt;
     }
   }
   if (!valid) return;
-  const float inv = 1.f / l;
-  T* dst = static_cast<T*>(a.out) + static_cast<int64_t>(row0 + t) * qs + qh * d;
-  for (int i = 0; i < d; i++) dst[i] = from_f32<T>(acc[i] * inv);
-  a.lse[static_cast<int64_t>(qh) * a.total_q + row0 + t] = (m + log2f(l)) * kLn2;
+  store_slice<kL>(static_cast<T*>(a.out) + static_cast<int64_t>(row0 + t) * qs + qh * d, d, c, 1.f / l, o);
+  if (c == 0) a.lse[static_cast<int64_t>(qh) * a.total_q + row0 + t] = (m + log2f(l)) * kLn2;
 }
 
 // ---------------------------------------------------------------------------
@@ -132,89 +248,69 @@ __global__ __launch_bounds__(256) void simt_delta(KernelArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// dQ: block = 64 queries of one head of one leaf (same items as the forward).
+// dQ: block = kSimtQ queries of one head of one leaf (the forward's items).
 template <typename T, int DMAX>
-__global__ __launch_bounds__(kSimtQ) void simt_dq(KernelArgs a) {
+__global__ __launch_bounds__(kSimtQ * DMAX / 32) void simt_dq(KernelArgs a) {
+  constexpr int kL = DMAX / 32, kTile = simt_tile<DMAX>();
   const int32_t* item = a.plan + a.off_fwd + 4 * blockIdx.x;
   const int leaf = item[0];
   if (leaf < 0) return;
   const int tok0 = item[1], qh = item[2], kvh = item[3];
   const int32_t* cu = a.plan + a.off_cu;
-  const int32_t* no = a.plan + a.off_node_off;
-  const int32_t* anc = a.plan + a.off_anc;
   const int row0 = cu[leaf], len = cu[leaf + 1] - cu[leaf];
   const int d = a.d;
-  const int t = tok0 + threadIdx.x;
+  const int c = threadIdx.x % kL;
+  const int t = tok0 + static_cast<int>(threadIdx.x) / kL;
   const bool valid = t < len;
   const int tr = valid ? t : 0;
   const int64_t qs = static_cast<int64_t>(a.hq) * d, ks = static_cast<int64_t>(a.hkv) * d;
 
-  __shared__ float Ks[kSimtTile][DMAX + 1];
-  __shared__ float Vs[kSimtTile][DMAX + 1];
+  __shared__ __attribute__((aligned(16))) float Ks[kTile * DMAX];
+  __shared__ __attribute__((aligned(16))) float Vs[kTile * DMAX];
 
-  float q[DMAX], g[DMAX], dq[DMAX];
-  {
-    const T* qsrc = static_cast<const T*>(a.q) + static_cast<int64_t>(row0 + tr) * qs + qh * d;
-    const T* gsrc = static_cast<const T*>(a.dout) + static_cast<int64_t>(row0 + tr) * qs + qh * d;
-    for (int i = 0; i < DMAX; i++) {
-      q[i] = i < d ? to_f32(qsrc[i]) : 0.f;
-      g[i] = i < d ? to_f32(gsrc[i]) : 0.f;
-      dq[i] = 0.f;
-    }
-  }
-  const float lse = a.lse_in[static_cast<int64_t>(qh) * a.total_q + row0 + tr];
-  const float delta = a.delta[static_cast<int64_t>(qh) * a.total_q + row0 + tr];
+  f32x4 q[8], g[8], dq[8];
+  load_slice<kL>(static_cast<const T*>(a.q) + static_cast<int64_t>(row0 + tr) * qs + qh * d, d, c,
+                 a.scale * kLog2e, q);
+  load_slice<kL>(static_cast<const T*>(a.dout) + static_cast<int64_t>(row0 + tr) * qs + qh * d, d, c, 1.f, g);
+#pragma unroll
+  for (int j = 0; j < 8; j++) dq[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int64_t stat = static_cast<int64_t>(qh) * a.total_q + row0 + tr;
+  const float lse2 = a.lse_in[stat] * kLog2e;
+  const float delta = a.delta[stat];
 
-  const int tok_last = min(len, tok0 + kSimtQ);
-  const int nseg = a.max_depth + 1;
-  for (int sg = 0; sg < nseg; sg++) {
-    const T *kb, *vb;
-    int seg_len;
-    bool causal;
-    if (sg < a.max_depth) {
-      const int n = anc[leaf * a.max_depth + sg];
-      if (n < 0) continue;
-      kb = static_cast<const T*>(a.pk) + static_cast<int64_t>(no[n]) * ks + kvh * d;
-      vb = static_cast<const T*>(a.pv) + static_cast<int64_t>(no[n]) * ks + kvh * d;
-      seg_len = no[n + 1] - no[n];
-      causal = false;
-    } else {
-      kb = static_cast<const T*>(a.k) + static_cast<int64_t>(row0) * ks + kvh * d;
-      vb = static_cast<const T*>(a.v) + static_cast<int64_t>(row0) * ks + kvh * d;
-      seg_len = tok_last;
-      causal = true;
-    }
-    for (int j0 = 0; j0 < seg_len; j0 += kSimtTile) {
-      const int nk = min(kSimtTile, seg_len - j0);
+  const int suffix_keys = min(len, tok0 + kSimtQ);
+  const T *kb, *vb;
+  int seg_len;
+  for (int sg = 0; key_segment<T>(a, leaf, sg, suffix_keys, kvh, kb, vb, seg_len); sg++) {
+    const bool causal = sg == 0;
+    for (int j0 = 0; j0 < seg_len; j0 += kTile) {
+      const int nk = min(kTile, seg_len - j0);
       __syncthreads();
-      stage_rows<T, DMAX>(Ks, kb, ks, j0, kSimtTile, nk, d);
-      stage_rows<T, DMAX>(Vs, vb, ks, j0, kSimtTile, nk, d);
+      stage_tile<DMAX>(Ks, kb, ks, j0, kTile, nk, d);
+      stage_tile<DMAX>(Vs, vb, ks, j0, kTile, nk, d);
       __syncthreads();
       for (int j = 0; j < nk; j++) {
-        if (causal && j0 + j > t) break;
-        float s = 0.f, dp = 0.f;
-        for (int i = 0; i < DMAX; i++) {
-          s += q[i] * Ks[j][i];
-          dp += g[i] * Vs[j][i];
-        }
-        const float p = expf(s * a.scale - lse);
-        const float ds = p * (dp - delta);
-        for (int i = 0; i < DMAX; i++) dq[i] += ds * Ks[j][i];
+        const float s = group_sum<kL>(dot_lds<kL>(q, Ks + j * DMAX, c));
+        const float dp = group_sum<kL>(dot_lds<kL>(g, Vs + j * DMAX, c));
+        const bool vis = !causal || j0 + j <= t;
+        const float ds = vis ? exp2f(s - lse2) * (dp - delta) : 0.f;
+        axpy_lds<kL>(dq, ds, Ks + j * DMAX, c);
       }
     }
   }
   if (!valid) return;
-  T* dst = static_cast<T*>(a.dq) + static_cast<int64_t>(row0 + t) * qs + qh * d;
-  for (int i = 0; i < d; i++) dst[i] = from_f32<T>(dq[i] * a.scale);
+  store_slice<kL>(static_cast<T*>(a.dq) + static_cast<int64_t>(row0 + t) * qs + qh * d, d, c, a.scale, dq);
 }
 
 // ---------------------------------------------------------------------------
-// dK/dV: block = 64 keys of one KV head of one segment (prefix node or leaf
-// suffix); loops over every query block (and every query head of the group)
-// that sees the keys, in the plan's fixed order, so a prefix node's gradient
-// is summed over its descendant leaves in leaf order without atomics.
+// dK/dV: block = kSimtKeys keys of one KV head of one segment (prefix node or
+// leaf suffix), kL lanes per key; loops over every query block (and every
+// query head of the group) that sees the keys, in the plan's fixed order, so
+// a prefix node's gradient is summed over its descendant leaves in leaf order
+// without atomics.
 template <typename T, int DMAX>
-__global__ __launch_bounds__(kSimtKeys) void simt_dkdv(KernelArgs a) {
+__global__ __launch_bounds__(kSimtKeys * DMAX / 32) void simt_dkdv(KernelArgs a) {
+  constexpr int kL = DMAX / 32, kTile = simt_tile<DMAX>();
   const int32_t* item = a.plan + a.off_dkdv + DK_WORDS * blockIdx.x;
   if (item[DK_SRC] < 0) return;
   const bool prefix = item[DK_SRC] == 0;
@@ -227,85 +323,112 @@ __global__ __launch_bounds__(kSimtKeys) void simt_dkdv(KernelArgs a) {
   const int64_t qs = static_cast<int64_t>(a.hq) * d, ks = static_cast<int64_t>(a.hkv) * d;
   const int seg_row0 = prefix ? no[seg] : cu[seg];
   const int seg_len = prefix ? no[seg + 1] - no[seg] : cu[seg + 1] - cu[seg];
-  const int kp = key0 + threadIdx.x;  // key position within its segment
+  const int c = threadIdx.x % kL;
+  const int kp = key0 + static_cast<int>(threadIdx.x) / kL;  // key position within its segment
   const bool valid = kp < seg_len;
   const int64_t krow = static_cast<int64_t>(seg_row0 + (valid ? kp : 0));
   const T* kbase = static_cast<const T*>(prefix ? a.pk : a.k);
   const T* vbase = static_cast<const T*>(prefix ? a.pv : a.v);
 
-  __shared__ float Qs[kSimtTile][DMAX + 1];
-  __shared__ float Gs[kSimtTile][DMAX + 1];
-  __shared__ float Ls[kSimtTile], Ds[kSimtTile];
+  __shared__ __attribute__((aligned(16))) float Qs[kTile * DMAX];
+  __shared__ __attribute__((aligned(16))) float Gs[kTile * DMAX];
+  __shared__ float Ls[kTile], Ds[kTile];  // lse * log2e, delta
 
-  float kr[DMAX], vr[DMAX], dk[DMAX], dv[DMAX];
-  for (int i = 0; i < DMAX; i++) {
-    kr[i] = i < d ? to_f32(kbase[krow * ks + kvh * d + i]) : 0.f;
-    vr[i] = i < d ? to_f32(vbase[krow * ks + kvh * d + i]) : 0.f;
-    dk[i] = 0.f;
-    dv[i] = 0.f;
+  f32x4 kr[8], vr[8], dk[8], dv[8];
+  load_slice<kL>(kbase + krow * ks + kvh * d, d, c, a.scale * kLog2e, kr);
+  load_slice<kL>(vbase + krow * ks + kvh * d, d, c, 1.f, vr);
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    dk[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    dv[j] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   for (int qb = qb_lo; qb < qb_hi; qb++) {
     const int leaf = qblk[2 * qb], tok0 = qblk[2 * qb + 1];
     const int row0 = cu[leaf], len = cu[leaf + 1] - cu[leaf];
-    const int nq = min(kSimtTile, len - tok0);
-    for (int g = 0; g < a.group; g++) {
-      const int qh = kvh * a.group + g;
-      __syncthreads();
-      stage_rows<T, DMAX>(Qs, static_cast<const T*>(a.q) + qh * d, qs, row0 + tok0, kSimtTile, nq, d);
-      stage_rows<T, DMAX>(Gs, static_cast<const T*>(a.dout) + qh * d, qs, row0 + tok0, kSimtTile, nq, d);
-      for (int i = threadIdx.x; i < kSimtTile; i += blockDim.x) {
-        const int64_t at = static_cast<int64_t>(qh) * a.total_q + row0 + tok0 + (i < nq ? i : 0);
-        Ls[i] = a.lse_in[at];
-        Ds[i] = a.delta[at];
-      }
-      __syncthreads();
-      if (!valid) continue;
-      for (int i = 0; i < nq; i++) {
-        if (!prefix && kp > tok0 + i) continue;  // causal: key kp visible to query tok0+i iff kp <= tok0+i
-        float s = 0.f, dp = 0.f;
-        for (int x = 0; x < DMAX; x++) {
-          s += kr[x] * Qs[i][x];
-          dp += vr[x] * Gs[i][x];
+    const int nblk = min(kSimtTile, len - tok0);
+    for (int gh = 0; gh < a.group; gh++) {
+      const int qh = kvh * a.group + gh;
+      for (int sub = 0; sub < nblk; sub += kTile) {
+        const int nq = min(kTile, nblk - sub);
+        const int64_t r0 = static_cast<int64_t>(row0) + tok0 + sub;
+        __syncthreads();
+        stage_tile<DMAX>(Qs, static_cast<const T*>(a.q) + qh * d, qs, r0, kTile, nq, d);
+        stage_tile<DMAX>(Gs, static_cast<const T*>(a.dout) + qh * d, qs, r0, kTile, nq, d);
+        for (int i = threadIdx.x; i < kTile; i += blockDim.x) {
+          const int64_t at = static_cast<int64_t>(qh) * a.total_q + r0 + (i < nq ? i : 0);
+          Ls[i] = a.lse_in[at] * kLog2e;
+          Ds[i] = a.delta[at];
         }
-        const float p = expf(s * a.scale - Ls[i]);
-        const float ds = p * (dp - Ds[i]);
-        for (int x = 0; x < DMAX; x++) {
-          dv[x] += p * Gs[i][x];
-          dk[x] += ds * Qs[i][x];
+        __syncthreads();
+        for (int i = 0; i < nq; i++) {
+          f32x4 qi[8], gi[8];
+          read_slice<kL>(Qs + i * DMAX, c, qi);
+          read_slice<kL>(Gs + i * DMAX, c, gi);
+          const float s = group_sum<kL>(dot_regs(kr, qi));
+          const float dp = group_sum<kL>(dot_regs(vr, gi));
+          // causal: key kp is visible to query tok0 + sub + i iff kp <= tok0 + sub + i
+          const bool vis = prefix || kp <= tok0 + sub + i;
+          const float p = vis ? exp2f(s - Ls[i]) : 0.f;
+          const float ds = p * (dp - Ds[i]);
+#pragma unroll
+          for (int j = 0; j < 8; j++) {
+            dv[j] += p * gi[j];
+            dk[j] += ds * qi[j];
+          }
         }
       }
     }
   }
   if (!valid) return;
+  const int64_t at = krow * ks + kvh * d;
   if (prefix && a.acc_prefix) {
 #pragma clang fp contract(off)  // rounded product, then one add
-    float* dkf = static_cast<float*>(a.dpk) + krow * ks + kvh * d;
-    float* dvf = static_cast<float*>(a.dpv) + krow * ks + kvh * d;
-    for (int i = 0; i < d; i++) {
-      dkf[i] += dk[i] * a.scale;
-      dvf[i] += dv[i];
+    float* dkf = static_cast<float*>(a.dpk) + at;
+    float* dvf = static_cast<float*>(a.dpv) + at;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const int e = 4 * kL * j + 4 * c;
+      if (e < d) {
+        store4(dkf + e, load4(dkf + e) + dk[j] * a.scale);
+        store4(dvf + e, load4(dvf + e) + dv[j]);
+      }
     }
     return;
   }
-  T* dkd = static_cast<T*>(prefix ? a.dpk : a.dk) + krow * ks + kvh * d;
-  T* dvd = static_cast<T*>(prefix ? a.dpv : a.dv) + krow * ks + kvh * d;
-  for (int i = 0; i < d; i++) {
-    dkd[i] = from_f32<T>(dk[i] * a.scale);
-    dvd[i] = from_f32<T>(dv[i]);
-  }
+  store_slice<kL>(static_cast<T*>(prefix ? a.dpk : a.dk) + at, d, c, a.scale, dk);
+  store_slice<kL>(static_cast<T*>(prefix ? a.dpv : a.dv) + at, d, c, 1.f, dv);
 }
 
-template <typename T, int DMAX>
-int launch_simt_fwd_t(const KernelArgs& a, hipStream_t s) {
-  if (a.n_items > 0) hipLaunchKernelGGL((simt_fwd<T, DMAX>), dim3(a.n_items), dim3(kSimtQ), 0, s, a);
+template <typename T>
+int launch_fwd_t(const KernelArgs& a, hipStream_t s) {
+  if (a.n_items <= 0) return 0;
+  if (a.d <= 64) hipLaunchKernelGGL((simt_fwd<T, 64>), dim3(a.n_items), dim3(kSimtQ * 2), 0, s, a);
+  else if (a.d <= 128) hipLaunchKernelGGL((simt_fwd<T, 128>), dim3(a.n_items), dim3(kSimtQ * 4), 0, s, a);
+  else hipLaunchKernelGGL((simt_fwd<T, 256>), dim3(a.n_items), dim3(kSimtQ * 8), 0, s, a);
   return hipGetLastError() == hipSuccess ? 0 : 4;
+}
+
+template <typename T>
+int launch_bwd_t(const KernelArgs& a, int n_fwd, int n_dkdv, hipStream_t s) {
+  if (n_dkdv > 0) {
+    if (a.d <= 64) hipLaunchKernelGGL((simt_dkdv<T, 64>), dim3(n_dkdv), dim3(kSimtKeys * 2), 0, s, a);
+    else if (a.d <= 128) hipLaunchKernelGGL((simt_dkdv<T, 128>), dim3(n_dkdv), dim3(kSimtKeys * 4), 0, s, a);
+    else hipLaunchKernelGGL((simt_dkdv<T, 256>), dim3(n_dkdv), dim3(kSimtKeys * 8), 0, s, a);
+    if (hipGetLastError() != hipSuccess) return 4;
+  }
+  if (n_fwd > 0) {
+    if (a.d <= 64) hipLaunchKernelGGL((simt_dq<T, 64>), dim3(n_fwd), dim3(kSimtQ * 2), 0, s, a);
+    else if (a.d <= 128) hipLaunchKernelGGL((simt_dq<T, 128>), dim3(n_fwd), dim3(kSimtQ * 4), 0, s, a);
+    else hipLaunchKernelGGL((simt_dq<T, 256>), dim3(n_fwd), dim3(kSimtQ * 8), 0, s, a);
+    if (hipGetLastError() != hipSuccess) return 4;
+  }
+  return 0;
 }
 
 }  // namespace
 
 int launch_simt_fwd(const KernelArgs& a, bool fp32, hipStream_t s) {
-  if (fp32) return a.d <= 64 ? launch_simt_fwd_t<float, 64>(a, s) : launch_simt_fwd_t<float, 128>(a, s);
-  return a.d <= 64 ? launch_simt_fwd_t<bf16, 64>(a, s) : launch_simt_fwd_t<bf16, 128>(a, s);
+  return fp32 ? launch_fwd_t<float>(a, s) : launch_fwd_t<bf16>(a, s);
 }
 
 int launch_delta(const KernelArgs& a, bool fp32, hipStream_t s) {
@@ -320,28 +443,7 @@ int launch_delta(const KernelArgs& a, bool fp32, hipStream_t s) {
 }
 
 int launch_simt_bwd(const KernelArgs& a, int n_fwd, int n_dkdv, bool fp32, hipStream_t s) {
-  KernelArgs b = a;
-  if (n_dkdv > 0) {
-    if (fp32) {
-      if (a.d <= 64) hipLaunchKernelGGL((simt_dkdv<float, 64>), dim3(n_dkdv), dim3(kSimtKeys), 0, s, b);
-      else hipLaunchKernelGGL((simt_dkdv<float, 128>), dim3(n_dkdv), dim3(kSimtKeys), 0, s, b);
-    } else {
-      if (a.d <= 64) hipLaunchKernelGGL((simt_dkdv<bf16, 64>), dim3(n_dkdv), dim3(kSimtKeys), 0, s, b);
-      else hipLaunchKernelGGL((simt_dkdv<bf16, 128>), dim3(n_dkdv), dim3(kSimtKeys), 0, s, b);
-    }
-    if (hipGetLastError() != hipSuccess) return 4;
-  }
-  if (n_fwd > 0) {
-    if (fp32) {
-      if (a.d <= 64) hipLaunchKernelGGL((simt_dq<float, 64>), dim3(n_fwd), dim3(kSimtQ), 0, s, b);
-      else hipLaunchKernelGGL((simt_dq<float, 128>), dim3(n_fwd), dim3(kSimtQ), 0, s, b);
-    } else {
-      if (a.d <= 64) hipLaunchKernelGGL((simt_dq<bf16, 64>), dim3(n_fwd), dim3(kSimtQ), 0, s, b);
-      else hipLaunchKernelGGL((simt_dq<bf16, 128>), dim3(n_fwd), dim3(kSimtQ), 0, s, b);
-    }
-    if (hipGetLastError() != hipSuccess) return 4;
-  }
-  return 0;
+  return fp32 ? launch_bwd_t<float>(a, n_fwd, n_dkdv, s) : launch_bwd_t<bf16>(a, n_fwd, n_dkdv, s);
 }
 
 }  // namespace tpr

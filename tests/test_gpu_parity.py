@@ -126,20 +126,44 @@ def test_fp32_plumbing_config_matches_oracle(cuda_device):
         assert max_abs(g, r) <= FP32_TOL
 
 
-def test_simt_bf16_head_dim_64_matches_oracle(cuda_device):
-    from bridge_amd import TPRPrefixMeta
-    meta = TPRPrefixMeta.shared_prefix(100, [70, 40])
-    hq, hkv, d = 8, 2, 64
+def _simt_cases():
+    from bridge_amd import TPRPrefixMeta as M
+    tree = _meta_cases()["depth3_tree"][0]
+    return {
+        # name: (meta, hq, hkv, head_dim, dtype)
+        "bf16_d64": (M.shared_prefix(100, [70, 40]), 8, 2, 64, torch.bfloat16),
+        "bf16_d96": (M.shared_prefix(77, [50, 33]), 6, 2, 96, torch.bfloat16),
+        # the full-attention layers of the reference's Qwen3.5 hybrid test model:
+        # 8 query heads, 2 KV heads, head_dim 256
+        "bf16_d256_qwen35": (M.shared_prefix(150, [90, 61]), 8, 2, 256, torch.bfloat16),
+        "bf16_d200_tree": (tree, 4, 1, 200, torch.bfloat16),
+        "fp32_d128_tree": (tree, 8, 2, 128, torch.float32),
+        "fp32_d256": (M.shared_prefix(64, [50, 17]), 4, 2, 256, torch.float32),
+    }
+
+
+@pytest.mark.parametrize("name", ["bf16_d64", "bf16_d96", "bf16_d256_qwen35", "bf16_d200_tree",
+                                  "fp32_d128_tree", "fp32_d256"])
+def test_simt_matches_oracle(name, cuda_device):
+    meta, hq, hkv, d, dtype = _simt_cases()[name]
     scale = 1.0 / math.sqrt(d)
-    q, k, v, pk, pv, dout = make_inputs(meta, hq, hkv, d, torch.bfloat16, seed=3, device=cuda_device)
-    assert meta.plan(hq, hkv, d, torch.bfloat16, cuda_device).path == "simt"
+    q, k, v, pk, pv, dout = make_inputs(meta, hq, hkv, d, dtype, seed=3, device=cuda_device)
+    assert meta.plan(hq, hkv, d, dtype, cuda_device).path == "simt"
     out, lse, grads = _run(meta, q, k, v, pk, pv, dout, scale)
     ref = oracle(meta, q, k, v, pk, pv, dout, scale)
-    _report("simt_bf16_d64", out, lse, grads, ref)
-    ro, _, rg = ref
+    _report("simt_" + name, out, lse, grads, ref)
+    ro, rl, rg = ref
+    if dtype == torch.float32:
+        assert max_abs(out, ro) <= FP32_TOL and max_abs(lse, rl) <= FP32_TOL
+        for g, r in zip(grads, rg):
+            assert max_abs(g, r) <= FP32_TOL
+        return
     assert max_abs(out, ro) <= BF16_FWD_MAX_ABS and cosine(out, ro) >= BF16_FWD_COS
+    assert max_abs(lse, rl) <= 1e-3
     for g, r in zip(grads, rg):
         assert cosine(g, r) >= BF16_GRAD_COS
+    for g, r in zip(grads[3:], rg[3:]):
+        assert rel_l2(g, r) <= BF16_PREFIX_GRAD_REL_L2
 
 
 def test_mfma_is_deterministic(cuda_device):

@@ -198,6 +198,8 @@ def test_simt_path_for_fp32_and_small_head_dim():
     assert meta.plan(4, 4, 64, torch.bfloat16, CPU).path == "simt"
     assert meta.plan(4, 4, 128, torch.float32, CPU).path == "simt"
     assert meta.plan(4, 4, 128, torch.bfloat16, CPU).path == "mfma"
+    assert meta.plan(8, 2, 256, torch.bfloat16, CPU).path == "simt"
+    assert meta.plan(8, 2, 256, torch.float32, CPU).path == "simt"
 
 
 def test_plan_is_cached_per_configuration():
@@ -230,7 +232,7 @@ def test_planner_rejects_invalid_trees(kwargs, exc, match):
 
 
 @pytest.mark.parametrize(("hq", "hkv", "d", "exc", "match"),
-                         [(6, 4, 128, ValueError, "divisible"), (4, 2, 256, NotImplementedError, "head_dim"),
+                         [(6, 4, 128, ValueError, "divisible"), (4, 2, 264, NotImplementedError, "at most 256"),
                           (4, 2, 60, NotImplementedError, "multiple of 8")])
 def test_planner_rejects_unsupported_heads(hq, hkv, d, exc, match):
     with pytest.raises(exc, match=match):
