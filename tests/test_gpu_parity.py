@@ -176,11 +176,12 @@ def test_mfma_is_deterministic(cuda_device):
         assert torch.equal(a, b)
 
 
-def test_rectangular_shim_matches_reference_oracle(cuda_device):
+@pytest.mark.parametrize("d", [128, 256])  # 256: the reference's Qwen3.5 full-attention head size
+def test_rectangular_shim_matches_reference_oracle(d, cuda_device):
     from bridge_amd import rectangular_causal_attention
     from oracle.tpr_oracle import prefix_attention
     gen = torch.Generator().manual_seed(44)
-    sq, skv, hq, hkv, d = 40, 100, 8, 2, 128
+    sq, skv, hq, hkv = 40, 100, 8, 2
     q = torch.randn(sq, 1, hq, d, generator=gen).bfloat16()
     k = torch.randn(skv, 1, hkv, d, generator=gen).bfloat16()
     v = torch.randn(skv, 1, hkv, d, generator=gen).bfloat16()
