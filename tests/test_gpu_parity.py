@@ -139,11 +139,13 @@ def _simt_cases():
         "bf16_d200_tree": (tree, 4, 1, 200, torch.bfloat16),
         "fp32_d128_tree": (tree, 8, 2, 128, torch.float32),
         "fp32_d256": (M.shared_prefix(64, [50, 17]), 4, 2, 256, torch.float32),
+        "fp32_deep_run_list": (_meta_cases()["deep_run_list"][0], 8, 2, 64, torch.float32),
+        "bf16_d256_empty_leaf": (M.shared_prefix(50, [0, 60, 0]), 4, 1, 256, torch.bfloat16),
     }
 
 
 @pytest.mark.parametrize("name", ["bf16_d64", "bf16_d96", "bf16_d256_qwen35", "bf16_d200_tree",
-                                  "fp32_d128_tree", "fp32_d256"])
+                                  "fp32_d128_tree", "fp32_d256", "fp32_deep_run_list", "bf16_d256_empty_leaf"])
 def test_simt_matches_oracle(name, cuda_device):
     meta, hq, hkv, d, dtype = _simt_cases()[name]
     scale = 1.0 / math.sqrt(d)
