@@ -56,8 +56,11 @@ typedef enum TprStatus {
   TPR_ERR_LAUNCH = 4            /* the HIP runtime rejected a launch */
 } TprStatus;
 
+/* head_dim: a multiple of 8, at most 256. bf16 with head_dim 128 runs on the
+ * MFMA kernels (any tree depth); fp32 and the other head sizes on the SIMT
+ * kernels. Both accumulate in fp32. */
 typedef enum TprDtype {
-  TPR_DTYPE_BF16 = 0, /* bf16 in/out, fp32 accumulation (MFMA path) */
+  TPR_DTYPE_BF16 = 0, /* bf16 in/out, fp32 accumulation */
   TPR_DTYPE_FP32 = 1  /* fp32 in/out, fp32 accumulation */
 } TprDtype;
 
