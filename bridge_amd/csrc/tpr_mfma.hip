@@ -41,30 +41,6 @@ __device__ __forceinline__ f32x16 mfma(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ bf16x8 lds_read_b128(const char* tile, int row, int col) {
-  return *reinterpret_cast<const bf16x8*>(tile + swz_off(row, col));
-}
-
-// Transposed operand read: lane l gets rows r0 + 0..7 (two ds_read_tr16_b64)
-// of column c0 + (l % 32) -- i.e. 8 consecutive rows of one column of a
-// row-major swizzled tile. r0 must be a multiple of 8 plus 8*(l/32) handled by
-// the caller; c0 a multiple of 32.
-__device__ __forceinline__ bf16x8 lds_read_col8(const char* tile, int r0, int c0, int lane) {
-  const int g = lane >> 4, i = lane & 15;
-  const int row = r0 + (i >> 2);
-  const int col = c0 + ((g & 1) << 4) + ((i & 3) << 2);
-  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (lds_s16x4*)(tile + swz_off(row, col)));
-  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (lds_s16x4*)(tile + swz_off(row + 4, col)));
-  bf16x8 r;
-  const bf16x4 l4 = __builtin_bit_cast(bf16x4, lo);
-  const bf16x4 h4 = __builtin_bit_cast(bf16x4, hi);
-  r[0] = l4[0]; r[1] = l4[1]; r[2] = l4[2]; r[3] = l4[3];
-  r[4] = h4[0]; r[5] = h4[1]; r[6] = h4[2]; r[7] = h4[3];
-  return r;
-}
-
 // Per-lane byte offsets, within a swizzled tile (plus `bias`), of the
 // operand reads. The swizzle of row r depends only on r mod 16, so rows 16m further
 // down are the same offsets plus 4096m: only the first 16 or 32 rows' offsets
@@ -88,29 +64,10 @@ __device__ __forceinline__ FwdLdsOffsets make_fwd_lds_offsets(int lane, uint32_t
   return o;
 }
 
-// The same offsets from three base registers: the swizzle's XOR only changes
-// bits 5-7 of an offset within a 256-byte row, so row read c is at
-// k ^ 32c and transposed read db at v[x] ^ 64db (x = 0: rows +0..3, 1: +4..7).
-// The per-read XOR is one VALU op in place of a register per offset; `opaque`
-// keeps the compiler from hoisting the XORs back into registers.
-struct LdsBases {
-  uint32_t k;
-  uint32_t v[2];
-};
-
-__device__ __forceinline__ LdsBases make_lds_bases(int lane, uint32_t k_bias, uint32_t v_bias) {
-  const int n = lane & 31, h = lane >> 5, g = lane >> 4, i = lane & 15;
-  const int row = 8 * h + (i >> 2), col = ((g & 1) << 4) + ((i & 3) << 2);
-  return LdsBases{k_bias + static_cast<uint32_t>(swz_off(sigma32(n), 8 * h)),
-                  {v_bias + static_cast<uint32_t>(swz_off(row, col)),
-                   v_bias + static_cast<uint32_t>(swz_off(row + 4, col))}};
-}
-
-__device__ __forceinline__ void opaque(LdsBases& b) {
-  asm volatile("" : "+v"(b.k), "+v"(b.v[0]), "+v"(b.v[1]));
-}
-
-// Transposed read of lds_read_col8 at precomputed offsets (lo: rows +0..3, hi: +4..7).
+// Transposed operand read at precomputed offsets (two ds_read_tr16_b64; lo:
+// rows +0..3, hi: rows +4..7): lane l gets 8 consecutive rows of column
+// c0 + (l % 32) of a row-major swizzled tile -- the B operand layout of a
+// 32x32x16 MFMA whose k index runs down the tile.
 __device__ __forceinline__ bf16x8 lds_col8_at(const char* base, uint32_t lo, uint32_t hi) {
   const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + lo));
   const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + hi));
@@ -119,13 +76,6 @@ __device__ __forceinline__ bf16x8 lds_col8_at(const char* base, uint32_t lo, uin
   const bf16x4 h4 = __builtin_bit_cast(bf16x4, b);
   r[0] = l4[0]; r[1] = l4[1]; r[2] = l4[2]; r[3] = l4[3];
   r[4] = h4[0]; r[5] = h4[1]; r[6] = h4[2]; r[7] = h4[3];
-  return r;
-}
-
-__device__ __forceinline__ bf16x8 to_bf16x8(const f32x16& x, int base) {
-  bf16x8 r;
-#pragma unroll
-  for (int i = 0; i < 8; i++) r[i] = static_cast<bf16>(x[base + i]);
   return r;
 }
 
@@ -199,36 +149,8 @@ __device__ __forceinline__ auto load_keys(const KernelArgs& a, int leaf, int suf
   else return load_segments(a, leaf, suffix_keys);
 }
 
-// Direct global -> LDS copy (gfx950 global_load_lds_dwordx4) of the 64 rows
-// [row0, row0 + 64) of a bf16 tensor (128 columns at `base`, row stride
-// `stride` elements) into a swizzled 64 x 256 B tile; rows at or beyond `len`
-// re-read row len - 1. Each wave issues 16 / kWaves DMA blocks of 1 KiB: lane
-// l of a block lands at block + 16*l, i.e. at (row 4*blk + l/16, physical
-// chunk l%16), so the lane fetches the logical chunk that swizzles there. No
-// registers hold the data, and the wave's vmcnt covers the copy.
-// The copy is issued from inline asm (M0 = wave-uniform LDS destination,
-// restored afterwards):
-// the compiler does not track it, so it does not serialise the next tile's
-// copy against the current tile's LDS reads; wait_dma() before the barrier
-// that publishes the tile is the only wait it needs. vmcnt retires in
-// order, so the compiler's own waits on its loads stay correct (they can
-// only become stricter). The asm needs no memory clobber: the kernel never
-// writes the global data it reads, and the LDS it writes is read only after
-// wait_dma() and a barrier.
 __device__ __forceinline__ uint32_t lds_address(const void* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)(p)));
-}
-
-__device__ __forceinline__ void dma16(const void* src, uint32_t lds_dst) {
-  uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %2\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %1, off\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "v"(src), "s"(lds_dst));
 }
 
 // One dword per lane, lane l's landing at lds_dst + 4*l (global_load_lds_dword).
@@ -237,23 +159,21 @@ __device__ __forceinline__ void dma4(const void* src, uint32_t lds_dst) {
   __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(uintptr_t)lds_dst, 4, 0, 0);
 }
 
-template <int kWaves>
-__device__ __forceinline__ void dma_tile(const bf16* base, int64_t stride, int64_t row0, int len, char* tile,
-                                         int wave, int lane) {
-  constexpr int kBlocks = 16 / kWaves;
-  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(tile));
-#pragma unroll
-  for (int j = 0; j < kBlocks; j++) {
-    const int blk = wave * kBlocks + j;
-    const int row = 4 * blk + (lane >> 4);
-    const int chunk = swz_chunk(row, lane & 15);
-    const bf16* src = base + (row0 + min(row, len - 1)) * stride + chunk * 8;
-    dma16(src, __builtin_amdgcn_readfirstlane(lds0 + blk * 1024));
-  }
-}
-
-// Same copy with a uniform 64-bit source base (SGPRs) and a per-lane 32-bit
-// byte offset: no per-copy 64-bit address arithmetic in the tile loop.
+// Direct global -> LDS copy (gfx950 global_load_lds_dwordx4) of one 1 KiB
+// block of a swizzled 64 x 256 B tile: lane l of the block lands at
+// lds_dst + 16 l, i.e. at (row 4 blk + l/16, physical chunk l%16), so the
+// lane fetches the logical chunk that swizzles there. No registers hold the
+// data, and the wave's vmcnt covers the copy. The source is a uniform 64-bit
+// base (SGPRs) plus a per-lane 32-bit byte offset, so the tile loop does no
+// 64-bit address arithmetic.
+// The copy is issued from inline asm (M0 = wave-uniform LDS destination,
+// restored afterwards): the compiler does not track it, so it does not
+// serialise the next tile's copy against the current tile's LDS reads;
+// wait_dma() before the barrier that publishes the tile is the only wait it
+// needs. vmcnt retires in order, so the compiler's own waits on its loads
+// stay correct (they can only become stricter). The asm needs no memory
+// clobber: the kernel never writes the global data it reads, and the LDS it
+// writes is read only after wait_dma() and a barrier.
 __device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, uint32_t lds_dst) {
   // readfirstlane returns a signed int: go through uint32_t, or the low word
   // would be sign-extended into the high word of the address.
