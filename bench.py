@@ -415,7 +415,9 @@ def main() -> int:
     achieved = dom_flops / (dom_ms * 1e-3) / 1e12
 
     result = {
-        "metric": "prefix-attn fwd+bwd TFLOP/s & % bf16 MFMA peak, Qwen3-4B shape, 1 GPU",
+        "metric": ("prefix-attn fwd+bwd TFLOP/s & % bf16 MFMA peak, Qwen3-4B shape, 1 GPU"
+                   if args.workload == "qwen3-4b" else
+                   f"prefix-attn fwd+bwd TFLOP/s & % of peak, {args.workload} workload, 1 GPU"),
         "value": round(value, 2),
         "unit": "TFLOP/s",
         "n_gpus": 1,
