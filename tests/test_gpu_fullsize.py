@@ -45,16 +45,16 @@ def _configs():
     }
 
 
-@pytest.mark.parametrize("name", ["qwen3_4b", "long_session", "ragged_varlen", "turn_tree_depth3"])
-def test_full_size_config_matches_oracle_on_one_head_group(name, cuda_device):
+def _check_head_group(name, meta, hq, hkv, d, kvh, device):
     from bridge_amd import TPRPrefixAttention
-    meta = _configs()[name]
-    scale = 1.0 / math.sqrt(D)
+    qh = slice(kvh * (hq // hkv), (kvh + 1) * (hq // hkv))
+    scale = 1.0 / math.sqrt(d)
     gen = torch.Generator(device="cpu").manual_seed(2024)
     tq, tp = meta.total_q, meta.total_prefix
-    shapes = [(tq, HQ, D), (tq, HKV, D), (tq, HKV, D), (tp, HKV, D), (tp, HKV, D), (tq, HQ, D)]
-    q, k, v, pk, pv, dout = (torch.randn(s, generator=gen).to(torch.bfloat16).to(cuda_device) for s in shapes)
-    print(f"[{name}] tq={tq} tp={tp} leaves={meta.num_leaves}", flush=True)
+    shapes = [(tq, hq, d), (tq, hkv, d), (tq, hkv, d), (tp, hkv, d), (tp, hkv, d), (tq, hq, d)]
+    q, k, v, pk, pv, dout = (torch.randn(s, generator=gen).to(torch.bfloat16).to(device) for s in shapes)
+    print(f"[{name}] tq={tq} tp={tp} leaves={meta.num_leaves} hq={hq} hkv={hkv} d={d} "
+          f"path={meta.plan(hq, hkv, d, torch.bfloat16, device).path}", flush=True)
 
     tensors = [t.clone().requires_grad_(True) for t in (q, k, v, pk, pv)]
     out, lse = TPRPrefixAttention.apply(*tensors, meta, scale)
@@ -63,10 +63,10 @@ def test_full_size_config_matches_oracle_on_one_head_group(name, cuda_device):
     grads = [t.grad for t in tensors]
 
     # fp32 oracle of the head group, on the GPU
-    kv = slice(KVH, KVH + 1)
-    ro, rl, rg = oracle(meta, q[:, QH], k[:, kv], v[:, kv], pk[:, kv], pv[:, kv], dout[:, QH], scale,
-                        compute_dtype=torch.float32, device=cuda_device)
-    mine = [out[:, QH], lse[QH], grads[0][:, QH], grads[1][:, kv], grads[2][:, kv], grads[3][:, kv], grads[4][:, kv]]
+    kv = slice(kvh, kvh + 1)
+    ro, rl, rg = oracle(meta, q[:, qh], k[:, kv], v[:, kv], pk[:, kv], pv[:, kv], dout[:, qh], scale,
+                        compute_dtype=torch.float32, device=device)
+    mine = [out[:, qh], lse[qh], grads[0][:, qh], grads[1][:, kv], grads[2][:, kv], grads[3][:, kv], grads[4][:, kv]]
     ref = [ro, rl, *rg]
     labels = ["out", "lse", "dq", "dk", "dv", "dprefix_k", "dprefix_v"]
     for label, a, b in zip(labels, mine, ref):
@@ -80,3 +80,16 @@ def test_full_size_config_matches_oracle_on_one_head_group(name, cuda_device):
     # every other head was computed too: finite everywhere
     for t in [out, lse, *grads]:
         assert torch.isfinite(t.float()).all()
+
+
+@pytest.mark.parametrize("name", ["qwen3_4b", "long_session", "ragged_varlen", "turn_tree_depth3"])
+def test_full_size_config_matches_oracle_on_one_head_group(name, cuda_device):
+    _check_head_group(name, _configs()[name], HQ, HKV, D, KVH, cuda_device)
+
+
+def test_qwen35_full_attention_shape_matches_oracle_on_one_head_group(cuda_device):
+    """head_dim 256 (the SIMT kernels) at the headline sequence shape: prefix
+    4096 + 4 x 4096, GQA 8/2 -- the full-attention layers of the reference's
+    Qwen3.5 hybrid test model (kv_channels=256). KV head 1, query heads 4..7."""
+    from bridge_amd import TPRPrefixMeta
+    _check_head_group("qwen35_d256", TPRPrefixMeta.shared_prefix(4096, [4096] * 4), 8, 2, 256, 1, cuda_device)
