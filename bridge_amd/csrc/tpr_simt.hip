@@ -128,6 +128,71 @@ __device__ __forceinline__ float group_sum(float x) {
   return x;
 }
 
+// bf16 dot-product operands. With bf16 inputs the dot products (q . k,
+// dout . v) take their operands as bf16 -- the inputs' own values, so the
+// products are exact -- two per v_dot2c_f32_bf16 into an fp32 sum: half the
+// instructions of the fp32 FMA chain. Lane c of a row group holds the 4
+// chunks of 8 elements at 8*kL*j + 8*c (16-byte LDS reads); the fp32 axpy
+// operands keep the 4-element chunks above, a different partition of the
+// same row, which the group sum does not care about.
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+struct Bf16Pairs {
+  bf16x2 p[4];
+};
+
+template <int kL>
+__device__ __forceinline__ void load_slice_bf(const bf16* row, int d, int c, bf16x8 (&x)[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int e = 8 * kL * j + 8 * c;
+    bf16x8 v;
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = e < d ? row[e + i] : static_cast<bf16>(0.f);
+    x[j] = v;
+  }
+}
+
+__device__ __forceinline__ float dot_bf(const bf16x8 (&x)[4], const bf16x8 (&y)[4]) {
+  float s0 = 0.f, s1 = 0.f;  // two chains: half the dependent latency
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const Bf16Pairs a = __builtin_bit_cast(Bf16Pairs, x[j]);
+    const Bf16Pairs b = __builtin_bit_cast(Bf16Pairs, y[j]);
+    s0 = __builtin_amdgcn_fdot2_f32_bf16(a.p[0], b.p[0], s0, false);
+    s1 = __builtin_amdgcn_fdot2_f32_bf16(a.p[1], b.p[1], s1, false);
+    s0 = __builtin_amdgcn_fdot2_f32_bf16(a.p[2], b.p[2], s0, false);
+    s1 = __builtin_amdgcn_fdot2_f32_bf16(a.p[3], b.p[3], s1, false);
+  }
+  return s0 + s1;
+}
+
+template <int kL>
+__device__ __forceinline__ float dot_lds_bf(const bf16x8 (&x)[4], const bf16* lds_row, int c) {
+  bf16x8 y[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) y[j] = *reinterpret_cast<const bf16x8*>(lds_row + 8 * kL * j + 8 * c);
+  return dot_bf(x, y);
+}
+
+// Stage rows of a bf16 tensor into a bf16 LDS tile of DMAX columns (as
+// stage_tile, without the conversion).
+template <int DMAX>
+__device__ __forceinline__ void stage_tile_bf(bf16* tile, const bf16* base, int64_t stride, int64_t row0, int rows,
+                                              int valid, int d) {
+  for (int idx = threadIdx.x; idx < rows * (DMAX / 8); idx += blockDim.x) {
+    const int r = idx / (DMAX / 8), e = 8 * (idx % (DMAX / 8));
+    bf16x8 x;
+#pragma unroll
+    for (int i = 0; i < 8; i++) x[i] = static_cast<bf16>(0.f);
+    if (r < valid && e < d) {
+      const bf16* src = base + (row0 + r) * stride + e;
+#pragma unroll
+      for (int i = 0; i < 8; i++) x[i] = src[i];
+    }
+    *reinterpret_cast<bf16x8*>(tile + r * DMAX + e) = x;
+  }
+}
+
 // Stage rows [row0, row0 + rows) of a [*, heads, d] tensor (row stride
 // `stride` elements, head offset applied to `base`) into an fp32 LDS tile of
 // DMAX columns; rows at or beyond `valid` and columns at or beyond d are 0.
@@ -182,12 +247,17 @@ __global__ __launch_bounds__(kSimtQ * DMAX / 32) void simt_fwd(KernelArgs a) {
   const bool valid = t < len;
   const int64_t qs = static_cast<int64_t>(a.hq) * d, ks = static_cast<int64_t>(a.hkv) * d;
 
-  __shared__ __attribute__((aligned(16))) float Ks[kTile * DMAX];
+  constexpr bool kBf = __is_same(T, bf16);  // bf16 dot operands (K tile in bf16)
+  __shared__ __attribute__((aligned(16))) float Ks[kBf ? 4 : kTile * DMAX];
+  __shared__ __attribute__((aligned(16))) bf16 Kb[kBf ? kTile * DMAX : 8];
   __shared__ __attribute__((aligned(16))) float Vs[kTile * DMAX];
 
+  const float cs = a.scale * kLog2e;
   f32x4 q[8], o[8];
-  load_slice<kL>(static_cast<const T*>(a.q) + static_cast<int64_t>(row0 + (valid ? t : 0)) * qs + qh * d, d, c,
-                 a.scale * kLog2e, q);
+  bf16x8 qb[4];
+  const T* qrow = static_cast<const T*>(a.q) + static_cast<int64_t>(row0 + (valid ? t : 0)) * qs + qh * d;
+  if constexpr (kBf) load_slice_bf<kL>(qrow, d, c, qb);
+  else load_slice<kL>(qrow, d, c, cs, q);
 #pragma unroll
   for (int j = 0; j < 8; j++) o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, l = 0.f;
@@ -200,14 +270,17 @@ __global__ __launch_bounds__(kSimtQ * DMAX / 32) void simt_fwd(KernelArgs a) {
     for (int j0 = 0; j0 < seg_len; j0 += kTile) {
       const int nk = min(kTile, seg_len - j0);
       __syncthreads();
-      stage_tile<DMAX>(Ks, kb, ks, j0, kTile, nk, d);
+      if constexpr (kBf) stage_tile_bf<DMAX>(Kb, kb, ks, j0, kTile, nk, d);
+      else stage_tile<DMAX>(Ks, kb, ks, j0, kTile, nk, d);
       stage_tile<DMAX>(Vs, vb, ks, j0, kTile, nk, d);
       __syncthreads();
       float s[kTile];
       float mt = m;
 #pragma unroll
       for (int j = 0; j < kTile; j++) {
-        const float x = group_sum<kL>(dot_lds<kL>(q, Ks + j * DMAX, c));
+        float x;
+        if constexpr (kBf) x = group_sum<kL>(dot_lds_bf<kL>(qb, Kb + j * DMAX, c)) * cs;
+        else x = group_sum<kL>(dot_lds<kL>(q, Ks + j * DMAX, c));
         const bool vis = j < nk && (!causal || j0 + j <= t);
         s[j] = vis ? x : -INFINITY;
         mt = fmaxf(mt, s[j]);
@@ -265,13 +338,24 @@ __global__ __launch_bounds__(kSimtQ * DMAX / 32) void simt_dq(KernelArgs a) {
   const int tr = valid ? t : 0;
   const int64_t qs = static_cast<int64_t>(a.hq) * d, ks = static_cast<int64_t>(a.hkv) * d;
 
+  constexpr bool kBf = __is_same(T, bf16);  // bf16 dot operands (K, V tiles also in bf16)
   __shared__ __attribute__((aligned(16))) float Ks[kTile * DMAX];
-  __shared__ __attribute__((aligned(16))) float Vs[kTile * DMAX];
+  __shared__ __attribute__((aligned(16))) float Vs[kBf ? 4 : kTile * DMAX];
+  __shared__ __attribute__((aligned(16))) bf16 Kb[kBf ? kTile * DMAX : 8];
+  __shared__ __attribute__((aligned(16))) bf16 Vb[kBf ? kTile * DMAX : 8];
 
+  const float cs = a.scale * kLog2e;
   f32x4 q[8], g[8], dq[8];
-  load_slice<kL>(static_cast<const T*>(a.q) + static_cast<int64_t>(row0 + tr) * qs + qh * d, d, c,
-                 a.scale * kLog2e, q);
-  load_slice<kL>(static_cast<const T*>(a.dout) + static_cast<int64_t>(row0 + tr) * qs + qh * d, d, c, 1.f, g);
+  bf16x8 qb[4], gb[4];
+  const T* qrow = static_cast<const T*>(a.q) + static_cast<int64_t>(row0 + tr) * qs + qh * d;
+  const T* grow = static_cast<const T*>(a.dout) + static_cast<int64_t>(row0 + tr) * qs + qh * d;
+  if constexpr (kBf) {
+    load_slice_bf<kL>(qrow, d, c, qb);
+    load_slice_bf<kL>(grow, d, c, gb);
+  } else {
+    load_slice<kL>(qrow, d, c, cs, q);
+    load_slice<kL>(grow, d, c, 1.f, g);
+  }
 #pragma unroll
   for (int j = 0; j < 8; j++) dq[j] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int64_t stat = static_cast<int64_t>(qh) * a.total_q + row0 + tr;
@@ -287,11 +371,22 @@ __global__ __launch_bounds__(kSimtQ * DMAX / 32) void simt_dq(KernelArgs a) {
       const int nk = min(kTile, seg_len - j0);
       __syncthreads();
       stage_tile<DMAX>(Ks, kb, ks, j0, kTile, nk, d);
-      stage_tile<DMAX>(Vs, vb, ks, j0, kTile, nk, d);
+      if constexpr (kBf) {
+        stage_tile_bf<DMAX>(Kb, kb, ks, j0, kTile, nk, d);
+        stage_tile_bf<DMAX>(Vb, vb, ks, j0, kTile, nk, d);
+      } else {
+        stage_tile<DMAX>(Vs, vb, ks, j0, kTile, nk, d);
+      }
       __syncthreads();
       for (int j = 0; j < nk; j++) {
-        const float s = group_sum<kL>(dot_lds<kL>(q, Ks + j * DMAX, c));
-        const float dp = group_sum<kL>(dot_lds<kL>(g, Vs + j * DMAX, c));
+        float s, dp;
+        if constexpr (kBf) {
+          s = group_sum<kL>(dot_lds_bf<kL>(qb, Kb + j * DMAX, c)) * cs;
+          dp = group_sum<kL>(dot_lds_bf<kL>(gb, Vb + j * DMAX, c));
+        } else {
+          s = group_sum<kL>(dot_lds<kL>(q, Ks + j * DMAX, c));
+          dp = group_sum<kL>(dot_lds<kL>(g, Vs + j * DMAX, c));
+        }
         const bool vis = !causal || j0 + j <= t;
         const float ds = vis ? exp2f(s - lse2) * (dp - delta) : 0.f;
         axpy_lds<kL>(dq, ds, Ks + j * DMAX, c);
@@ -330,6 +425,9 @@ __global__ __launch_bounds__(kSimtKeys * DMAX / 32) void simt_dkdv(KernelArgs a)
   const T* kbase = static_cast<const T*>(prefix ? a.pk : a.k);
   const T* vbase = static_cast<const T*>(prefix ? a.pv : a.v);
 
+  // The dot operands stay fp32 here: q_i and dout_i are needed in fp32 for
+  // the dK/dV updates anyway, and bf16 copies of the Q/dO tiles as well cost
+  // more in LDS traffic than the bf16 dot products save (measured).
   __shared__ __attribute__((aligned(16))) float Qs[kTile * DMAX];
   __shared__ __attribute__((aligned(16))) float Gs[kTile * DMAX];
   __shared__ float Ls[kTile], Ds[kTile];  // lse * log2e, delta
