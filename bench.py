@@ -92,38 +92,70 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def cpu_baseline(prefix_len: int, suffix_len: int, hq_sample: int, hkv: int, hq: int, d: int, reps: int = 3):
-    """The reference's CPU fp32 path (dense prefix attention + autograd), timed
-    on a bounded sample: one sibling and one KV-head group."""
+def cpu_threads() -> int:
+    """Host threads the CPU baseline may use: the CPUs this process may run on,
+    capped by OMP_NUM_THREADS when the environment sets it (the GPU box gives a
+    job a share of the host's cores)."""
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count() or 1
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    if cap.isdigit() and int(cap) > 0:
+        usable = min(usable, int(cap))
+    return max(1, usable)
+
+
+def cpu_baseline(meta, hq: int, hkv: int, d: int, reps: int = 3, max_siblings: int = 4):
+    """The reference's CPU fp32 path, timed on a bounded sample: the first
+    ``max_siblings`` siblings of the workload, one KV-head group (its Hq/Hkv
+    query heads), run one sibling after another as the reference's executor
+    visits leaves (dense fp32 prefix attention + autograd per sibling, prefix
+    gradients summed in sibling order)."""
     from oracle.tpr_oracle import prefix_attention
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
     g = torch.Generator(device="cpu").manual_seed(0)
-    group = hq // hkv
-    heads = max(1, min(hq_sample, group))
-    q = torch.randn(suffix_len, 1, heads, d, generator=g)
-    k = torch.randn(suffix_len, 1, 1, d, generator=g)
-    v = torch.randn(suffix_len, 1, 1, d, generator=g)
-    pk = torch.randn(prefix_len, 1, 1, d, generator=g)
-    pv = torch.randn(prefix_len, 1, 1, d, generator=g)
-    dout = torch.randn(suffix_len, 1, heads * d, generator=g)
+    heads = hq // hkv
+    nsib = min(max_siblings, meta.num_leaves)
+    sibs = []
+    for i in range(nsib):
+        s, p = meta.suffix_lengths()[i], meta.prefix_length(i)
+        sibs.append((p, [torch.randn(s, 1, heads, d, generator=g), torch.randn(s, 1, 1, d, generator=g),
+                         torch.randn(s, 1, 1, d, generator=g), torch.randn(s, 1, heads * d, generator=g)]))
+    plen = max(p for p, _ in sibs)
+    pk = torch.randn(plen, 1, 1, d, generator=g)
+    pv = torch.randn(plen, 1, 1, d, generator=g)
+    scale = 1.0 / math.sqrt(d)
     times = []
     for i in range(reps + 1):
-        tensors = [t.clone().requires_grad_(True) for t in (q, k, v, pk, pv)]
         t0 = time.perf_counter()
-        out = prefix_attention(*tensors, 1.0 / math.sqrt(d))
-        torch.autograd.grad(out, tensors, grad_outputs=dout)
+        dpk = dpv = None
+        for p, (q, k, v, dout) in sibs:
+            tensors = [q.clone().requires_grad_(True), k.clone().requires_grad_(True),
+                       v.clone().requires_grad_(True), pk[:p].clone().requires_grad_(True),
+                       pv[:p].clone().requires_grad_(True)]
+            out = prefix_attention(*tensors, scale)
+            grads = torch.autograd.grad(out, tensors, grad_outputs=dout)
+            dpk = grads[3] if dpk is None else dpk + grads[3]
+            dpv = grads[4] if dpv is None else dpv + grads[4]
         dt = time.perf_counter() - t0
         if i > 0:
             times.append(dt)
-    pairs = suffix_len * prefix_len + suffix_len * (suffix_len + 1) // 2
+    pairs = sum(s * p + s * (s + 1) // 2 for p, s in
+                ((p, t[0].shape[0]) for p, t in sibs))
     flops = 14.0 * heads * d * pairs
     med = statistics.median(times)
     return {
         "value": round(flops / med / 1e12, 4),
         "unit": "TFLOP/s",
-        "cores": torch.get_num_threads(),
+        "cores": threads,
+        "cpu_count": os.cpu_count(),
+        "threads": torch.get_num_threads(),
+        "cpu_model": cpu_model(),
         "kind": "port",
-        "sample": (f"1 sibling (prefix {prefix_len} + suffix {suffix_len}) x {heads} query heads of one KV group, "
-                   f"fp32 dense prefix attention + autograd on the host CPU ({cpu_model()}), "
+        "sample": (f"{nsib} of {meta.num_leaves} siblings x 1 KV-head group ({heads} query heads of {hq}), "
+                   f"fp32 dense prefix attention + autograd per sibling, prefix grads summed in sibling order; "
                    f"median of {reps} after 1 warmup, {med:.2f} s per rep"),
     }
 
@@ -457,9 +489,7 @@ def main() -> int:
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:
-        p0 = meta.prefix_length(0)
-        s0 = meta.suffix_lengths()[0]
-        result["cpu_baseline"] = cpu_baseline(p0, s0, hq // hkv, hkv, hq, d)
+        result["cpu_baseline"] = cpu_baseline(meta, hq, hkv, d)
     print(json.dumps(result), flush=True)
     return 0
 

@@ -179,6 +179,10 @@ extern "C" int tpr_attn_bwd_phases(const TprBwdParams* p, int phases, void* stre
   const size_t need = tpr_attn_bwd_workspace_bytes(ph);
   if (need > 0 && (!p->workspace || p->workspace_bytes < need))
     return fail(TPR_ERR_BUFFER_TOO_SMALL, "backward workspace needs %zu bytes, got %zu", need, p->workspace_bytes);
+  // the MFMA backward reads the partial slots as 16-byte vectors and DMA-copies
+  // the stat rows; the layout keeps every slot 256-byte aligned from the base
+  if (need > 0 && (reinterpret_cast<uintptr_t>(p->workspace) & 255u) != 0)
+    return fail(TPR_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
   KernelArgs a = args_from_plan(ph, p->plan_device, p->softmax_scale);
   a.q = p->q;
   a.k = p->k;

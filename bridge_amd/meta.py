@@ -122,18 +122,22 @@ class TPRPrefixMeta:
                 children[p].append(s)
         nodes, leaves, paths = [], [], []
         node_index: Dict[int, int] = {}
-
-        def visit(seg, path):
+        # DFS preorder on an explicit stack (a chain of thousands of segments
+        # must not hit Python's recursion limit); children are pushed in
+        # reverse so they are visited in insertion order.
+        stack = [(roots[0], ())]
+        while stack:
+            seg, path = stack.pop()
             if children[seg]:
                 node_index[seg] = len(nodes)
                 nodes.append(seg)
-                for c in children[seg]:
-                    visit(c, path + [node_index[seg]])
+                below = path + (node_index[seg],)
+                for c in reversed(children[seg]):
+                    stack.append((c, below))
             else:
                 leaves.append(seg)
-                paths.append(tuple(path))
+                paths.append(path)
 
-        visit(roots[0], [])
         if len(nodes) + len(leaves) != len(parents):
             raise ValueError("segment tree is not connected")
         node_offsets = [0]

@@ -106,3 +106,29 @@ def test_plan_capacity_and_workspace_queries():
     lib = _lib.load()
     assert lib.tpr_attn_bwd_workspace_bytes(ctypes.c_void_p(plan.host.data_ptr())) == plan.workspace_bytes > 0
     assert lib.tpr_attn_bwd_workspace_bytes(None) == 0
+
+
+def test_misaligned_workspace_is_rejected_before_any_launch():
+    """The MFMA backward needs a 256-byte aligned workspace; the check runs on
+    the host before anything is enqueued (the pointers below are never
+    dereferenced)."""
+    import torch
+
+    from bridge_amd import TPRPrefixMeta
+    lib = _lib.load()
+    plan = TPRPrefixMeta.shared_prefix(64, [64]).plan(4, 2, 128, torch.bfloat16, torch.device("cpu"))
+    need = plan.workspace_bytes
+    assert need > 0
+    b = _lib.TprBwdParams()
+    b.abi_version = _lib.ABI_VERSION
+    b.softmax_scale = 0.1
+    b.plan_host = b.plan_device = plan.host.data_ptr()
+    fake = 1 << 20
+    for name in ("q", "k", "v", "prefix_k", "prefix_v", "out", "dout", "lse", "delta", "dq", "dk", "dv",
+                 "dprefix_k", "dprefix_v"):
+        setattr(b, name, fake)
+        fake += 1 << 20
+    b.workspace = fake + 16
+    b.workspace_bytes = need + 256
+    assert lib.tpr_attn_bwd(ctypes.byref(b), None) == _lib.TPR_ERR_INVALID_ARGUMENT
+    assert b"256-byte aligned" in lib.tpr_attn_last_error()

@@ -262,6 +262,21 @@ def test_segment_tree_lowering_turn_tree():
     meta.plan(32, 8, 128, torch.bfloat16, CPU)  # valid for the planner
 
 
+def test_segment_tree_lowering_of_a_long_chain_is_iterative():
+    """A chain of 2500 segments (deeper than Python's recursion limit) lowers to
+    2499 nested nodes and one leaf; a side branch keeps insertion order."""
+    n = 2500
+    parents = {0: None, **{s: s - 1 for s in range(1, n)}}
+    lengths = {s: 1 + s % 3 for s in range(n)}
+    parents[n] = 0                      # second child of the root, inserted last
+    lengths[n] = 7
+    meta, nodes, leaves = TPRPrefixMeta.from_segment_tree(parents, lengths)
+    assert nodes == tuple(range(n - 1)) and leaves == (n - 1, n)
+    assert meta.leaf_ancestors[0] == tuple(range(n - 1)) and meta.leaf_ancestors[1] == (0,)
+    assert meta.cu_seqlens_q == (0, lengths[n - 1], lengths[n - 1] + 7)
+    assert meta.node_offsets[-1] == sum(lengths[s] for s in range(n - 1))
+
+
 def test_segment_tree_lowering_rejects_two_roots():
     with pytest.raises(ValueError, match="exactly one root"):
         TPRPrefixMeta.from_segment_tree({0: None, 1: None}, {0: 1, 1: 1})
