@@ -31,6 +31,8 @@ EXPORTED_SYMBOLS = (
     "tpr_attn_fwd",
     "tpr_attn_bwd",
     "tpr_attn_bwd_phases",
+    "tpr_attn_bwd_noalloc",
+    "tpr_attn_bwd_noalloc_max_workspace_bytes",
 )
 
 TPR_BWD_DELTA = 1
@@ -140,6 +142,10 @@ def load():
         lib.tpr_attn_bwd.argtypes = [ctypes.POINTER(TprBwdParams), _p]
         lib.tpr_attn_bwd_phases.restype = ctypes.c_int
         lib.tpr_attn_bwd_phases.argtypes = [ctypes.POINTER(TprBwdParams), ctypes.c_int, _p]
+        lib.tpr_attn_bwd_noalloc.restype = ctypes.c_int
+        lib.tpr_attn_bwd_noalloc.argtypes = [ctypes.POINTER(TprBwdParams), _p]
+        lib.tpr_attn_bwd_noalloc_max_workspace_bytes.restype = ctypes.c_size_t
+        lib.tpr_attn_bwd_noalloc_max_workspace_bytes.argtypes = []
         version = lib.tpr_attn_abi_version()
         if version != ABI_VERSION:
             raise RuntimeError(f"{path} has ABI version {version}, expected {ABI_VERSION}; rebuild it")

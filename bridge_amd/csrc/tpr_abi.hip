@@ -5,6 +5,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 
 #include "../../include/tpr_attn.h"
 #include "tpr_device.h"
@@ -149,8 +150,11 @@ extern "C" int tpr_attn_bwd(const TprBwdParams* p, void* stream) {
   return tpr_attn_bwd_phases(p, TPR_BWD_DELTA | TPR_BWD_DKDV | TPR_BWD_DQ, stream);
 }
 
-extern "C" int tpr_attn_bwd_phases(const TprBwdParams* p, int phases, void* stream) {
-  clear_error();
+namespace tpr {
+namespace {
+// tpr_attn_bwd_phases with the workspace given separately (the caller's, or
+// the library's static scratch for tpr_attn_bwd_noalloc).
+int bwd_phases(const TprBwdParams* p, int phases, void* stream, void* workspace, size_t workspace_bytes) {
   constexpr int kAllPhases = TPR_BWD_DELTA | TPR_BWD_DKDV | TPR_BWD_DQ | TPR_BWD_DKDV_TILES | TPR_BWD_DKDV_REDUCE;
   if (phases <= 0 || (phases & ~kAllPhases))
     return fail(TPR_ERR_INVALID_ARGUMENT, "phases must be a non-empty mask of TPR_BWD_* bits, got %d", phases);
@@ -177,11 +181,11 @@ extern "C" int tpr_attn_bwd_phases(const TprBwdParams* p, int phases, void* stre
       (rc = check_tensor(p->dprefix_v, "dprefix_v", any_p, mfma)))
     return rc;
   const size_t need = tpr_attn_bwd_workspace_bytes(ph);
-  if (need > 0 && (!p->workspace || p->workspace_bytes < need))
-    return fail(TPR_ERR_BUFFER_TOO_SMALL, "backward workspace needs %zu bytes, got %zu", need, p->workspace_bytes);
+  if (need > 0 && (!workspace || workspace_bytes < need))
+    return fail(TPR_ERR_BUFFER_TOO_SMALL, "backward workspace needs %zu bytes, got %zu", need, workspace_bytes);
   // the MFMA backward reads the partial slots as 16-byte vectors and DMA-copies
   // the stat rows; the layout keeps every slot 256-byte aligned from the base
-  if (need > 0 && (reinterpret_cast<uintptr_t>(p->workspace) & 255u) != 0)
+  if (need > 0 && (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
     return fail(TPR_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
   KernelArgs a = args_from_plan(ph, p->plan_device, p->softmax_scale);
   a.q = p->q;
@@ -199,7 +203,7 @@ extern "C" int tpr_attn_bwd_phases(const TprBwdParams* p, int phases, void* stre
   a.dpk = p->dprefix_k;
   a.dpv = p->dprefix_v;
   a.acc_prefix = (p->flags & TPR_BWD_ACCUMULATE_PREFIX_F32) ? 1 : 0;
-  a.stat_ws = static_cast<float*>(p->workspace);
+  a.stat_ws = static_cast<float*>(workspace);
   a.ws = a.stat_ws + stat_floats(ph);
   const bool fp32 = ph[PF_DTYPE] == TPR_DTYPE_FP32;
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -211,4 +215,66 @@ extern "C" int tpr_attn_bwd_phases(const TprBwdParams* p, int phases, void* stre
     rc = mfma ? launch_mfma_bwd(a, n_dq, n_dkdv, n_red, s) : launch_simt_bwd(a, n_dq, n_dkdv, fp32, s);
   if (rc) return fail(TPR_ERR_LAUNCH, "backward launch failed: %s", hipGetErrorString(hipGetLastError()));
   return TPR_OK;
+}
+}  // namespace
+}  // namespace tpr
+
+extern "C" int tpr_attn_bwd_phases(const TprBwdParams* p, int phases, void* stream) {
+  clear_error();
+  if (!p) return fail(TPR_ERR_INVALID_ARGUMENT, "params must not be NULL");
+  return bwd_phases(p, phases, stream, p->workspace, p->workspace_bytes);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free backward. The workspace is a file-scope device array, one
+// copy per GPU, sized for kScratchBytes; its device address is looked up once
+// per device (hipGetSymbolAddress, with that device current) and kept. Host
+// code never passes the array's own name to a kernel: on the host it is only
+// a stand-in for the symbol.
+// ---------------------------------------------------------------------------
+namespace tpr {
+namespace {
+constexpr size_t kScratchBytes = size_t{64} << 20;  // 64 MiB per GPU
+constexpr int kMaxDevices = 64;
+
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_for_current_device(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0)
+    return fail(TPR_ERR_LAUNCH, "hipGetDevice failed: %s", hipGetErrorString(hipGetLastError()));
+  if (dev >= kMaxDevices) return fail(TPR_ERR_UNSUPPORTED, "device %d is beyond the %d this library tracks", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(TPR_ERR_LAUNCH, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return TPR_OK;
+}
+}  // namespace
+}  // namespace tpr
+
+extern "C" size_t tpr_attn_bwd_noalloc_max_workspace_bytes(void) { return kScratchBytes; }
+
+extern "C" int tpr_attn_bwd_noalloc(const TprBwdParams* p, void* stream) {
+  clear_error();
+  if (!p) return fail(TPR_ERR_INVALID_ARGUMENT, "params must not be NULL");
+  if (p->abi_version == TPR_ATTN_ABI_VERSION && p->plan_host && p->plan_host[PF_MAGIC] == kPlanMagic) {
+    const size_t need = tpr_attn_bwd_workspace_bytes(p->plan_host);
+    if (need > kScratchBytes)
+      return fail(TPR_ERR_UNSUPPORTED,
+                  "backward workspace needs %zu bytes, more than the %zu bytes of the library's static scratch; "
+                  "use tpr_attn_bwd with a caller-allocated workspace", need, kScratchBytes);
+  }
+  void* ws = nullptr;
+  int rc = scratch_for_current_device(&ws);
+  if (rc) return rc;
+  return bwd_phases(p, TPR_BWD_DELTA | TPR_BWD_DKDV | TPR_BWD_DQ, stream, ws, kScratchBytes);
 }

@@ -180,6 +180,25 @@ int tpr_attn_bwd(const TprBwdParams* params, void* stream);
 #define TPR_BWD_DKDV_REDUCE 16 /* ordered sum of those partials into dprefix_k / dprefix_v */
 int tpr_attn_bwd_phases(const TprBwdParams* params, int phases, void* stream);
 
+/* Allocation-free backward. No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). Same as tpr_attn_bwd, except
+ * that params->workspace / workspace_bytes are ignored: the workspace is the
+ * library's static device scratch array, one per GPU, of
+ * tpr_attn_bwd_noalloc_max_workspace_bytes() bytes (64 MiB), held from the
+ * library's first use on a GPU until the process ends. A plan whose
+ * tpr_attn_bwd_workspace_bytes() exceeds that is rejected with
+ * TPR_ERR_UNSUPPORTED. The call allocates and frees nothing; the scratch
+ * address is looked up once per device (with that device current) on the
+ * first call there. Every call on one GPU shares that GPU's scratch: calls
+ * that overlap on one GPU (two streams, two threads) race and must be
+ * serialised by the caller. Nothing in the scratch needs to start at zero:
+ * each call writes every workspace element it later reads. */
+int tpr_attn_bwd_noalloc(const TprBwdParams* params, void* stream);
+
+/* Bytes of static scratch tpr_attn_bwd_noalloc has per GPU. */
+size_t tpr_attn_bwd_noalloc_max_workspace_bytes(void);
+
 #ifdef __cplusplus
 }
 #endif
