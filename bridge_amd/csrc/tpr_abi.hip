@@ -96,12 +96,17 @@ extern "C" const char* tpr_attn_last_error(void) { return g_error; }
 
 namespace tpr {
 namespace {
-// floats of the MFMA backward's stat area (constants + lse*log2e rows), a
-// multiple of 64 so the partial slots after it stay 256-byte aligned
-size_t stat_floats(const int32_t* ph) {
+// floats of one stat row set of the MFMA backward ([Hq, Tq] padded to a
+// multiple of 64, so every area after it stays 256-byte aligned)
+size_t stat_row_floats(const int32_t* ph) {
   if (ph[PF_PATH] != PATH_MFMA || ph[PF_TOTAL_Q] <= 0) return 0;
   const size_t rows = static_cast<size_t>(ph[PF_HQ]) * static_cast<size_t>(ph[PF_TOTAL_Q]);
-  return kStatRowsOffset + (rows + 63) / 64 * 64;
+  return (rows + 63) / 64 * 64;
+}
+// floats of the stat area: the constants, the lse*log2e rows, the -delta rows
+size_t stat_floats(const int32_t* ph) {
+  const size_t rows = stat_row_floats(ph);
+  return rows ? kStatRowsOffset + 2 * rows : 0;
 }
 }  // namespace
 }  // namespace tpr
@@ -204,6 +209,7 @@ int bwd_phases(const TprBwdParams* p, int phases, void* stream, void* workspace,
   a.dpv = p->dprefix_v;
   a.acc_prefix = (p->flags & TPR_BWD_ACCUMULATE_PREFIX_F32) ? 1 : 0;
   a.stat_ws = static_cast<float*>(workspace);
+  a.ndelta_ws = a.stat_ws ? a.stat_ws + kStatRowsOffset + stat_row_floats(ph) : nullptr;
   a.ws = a.stat_ws + stat_floats(ph);
   const bool fp32 = ph[PF_DTYPE] == TPR_DTYPE_FP32;
   hipStream_t s = static_cast<hipStream_t>(stream);

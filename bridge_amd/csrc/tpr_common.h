@@ -99,7 +99,7 @@ constexpr int kDkdvPrefixChunk = 64;  // smallest chunk a prefix tile is split i
 constexpr int kPlanCus = 256;         // compute units the dK/dV work is balanced over (MI355X)
 // MFMA backward workspace, ahead of the partial slots: two constants (+inf,
 // 0) that rows past a query block's end are copied from, then lse * log2e per
-// (query head, token) in the lse layout.
+// (query head, token) in the lse layout, then -delta in the same layout.
 constexpr int kStatRowsOffset = 64;   // floats before the lse*log2e rows
 constexpr int kMfmaRegRuns = 8;       // key runs a forward / dQ workgroup holds in registers; a
                                       // launch with longer run lists reads them from the plan

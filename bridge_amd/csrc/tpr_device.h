@@ -49,6 +49,7 @@ struct KernelArgs {
   int32_t n_items;
   float* ws;       // fp32 partial dK/dV slots of split tiles
   float* stat_ws;  // MFMA backward: [0] = +inf, [1] = 0, then lse*log2e rows from kStatRowsOffset
+  float* ndelta_ws;  // MFMA backward: -delta rows [Hq, Tq] (the dK/dV kernel's dP accumulator start)
 };
 
 __device__ __forceinline__ float to_f32(float x) { return x; }

@@ -246,6 +246,49 @@ __device__ __forceinline__ void dma_tile_s(const char* src, uint32_t row_bytes, 
   }
 }
 
+// Four 1 KiB global -> LDS copies (global_load_lds_dwordx4) of one wave: block
+// j lands at lds_dst + 1024 j (M0, stepped in SALU) from the uniform base
+// `sbase` (SGPRs) plus the lane's 32-bit offset voff[j]. One asm block per
+// tile: M0 is saved and restored once, and the copies need no per-lane
+// 64-bit address arithmetic. Like dma16s, the compiler does not track these
+// loads; the stage's wait_dma() before the barrier that publishes the tile
+// is their only wait.
+__device__ __forceinline__ void dma_blocks4(const char* sbase, uint32_t v0, uint32_t v1, uint32_t v2, uint32_t v3,
+                                            uint32_t lds_dst) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %5\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %6\n\t"
+      "s_add_u32 m0, m0, 0x400\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %2, %6\n\t"
+      "s_add_u32 m0, m0, 0x400\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %3, %6\n\t"
+      "s_add_u32 m0, m0, 0x400\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %4, %6\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(v0), "v"(v1), "v"(v2), "v"(v3), "s"(lds_dst), "s"(sbase));
+}
+
+// One dword per lane from a per-lane address, landing at lds_dst + 4 l
+// (global_load_lds_dword), untracked by the compiler like dma_blocks4.
+__device__ __forceinline__ void dma4_lane(const float* src, uint32_t lds_dst) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dword %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(src), "s"(lds_dst));
+}
+
 // Per-lane part of a 64-row tile copy by 4 waves, in two registers: lane l of
 // wave w moves, in block j = 0..3, row 16w + 4j + l/16 and the 16-byte source
 // chunk swz_chunk(row, l%16) = (l%16) ^ ((l/16) << 2) ^ j, i.e. chunk bytes
@@ -716,10 +759,11 @@ __global__ __launch_bounds__(256) void mfma_delta(KernelArgs a) {
     const int64_t at = (row % a.hq) * a.total_q + row / a.hq;
     a.delta[at] = s;
     a.stat_ws[kStatRowsOffset + at] = a.lse_in[at] * kLog2e;  // the dK/dV kernel copies these rows
+    a.ndelta_ws[at] = -s;
   }
   if (blockIdx.x == 0 && threadIdx.x == 0) {
     a.stat_ws[0] = INFINITY;  // lse*log2e of a query past a block's end: P = 0
-    a.stat_ws[1] = 0.f;       // its delta
+    a.stat_ws[1] = 0.f;       // its -delta
   }
 }
 
@@ -1044,6 +1088,11 @@ __device__ __forceinline__ f32x16 mfma_vsp_first(bf16x8 a, bf16x8 b_agpr) {
   asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "a"(b_agpr));
   return d;
 }
+__device__ __forceinline__ f32x16 mfma_vsp_init(bf16x8 a, bf16x8 b_agpr, f32x16 c) {
+  f32x16 d;
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %3" : "=&v"(d) : "v"(a), "a"(b_agpr), "v"(c));
+  return d;
+}
 __device__ __forceinline__ void mfma_vsp_acc(f32x16& d, bf16x8 a, bf16x8 b_agpr) {
   asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "a"(b_agpr));
 }
@@ -1101,46 +1150,61 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
   }
   __syncthreads();
 
-  auto stage_info = [&](int sidx, int& row0, int& tok0, int& nq, int& qh) {  // qh: first head of the stage
-    const int4 e = qtab[sidx / spb];
-    qh = kvh * a.group + (sidx % spb) * kHeads;
-    row0 = e.x - e.y;
-    tok0 = e.y;
-    nq = e.z;
+  // Stage s is (query block s / spb, head pair s % spb), tracked by counters
+  // (no division in the loop): `cur` is the stage being computed, `nxt` the
+  // one being copied.
+  struct StageCursor {
+    int blk, sub;
+  };
+  auto advance = [&](StageCursor c) __attribute__((always_inline)) {
+    return c.sub + 1 == spb ? StageCursor{c.blk + 1, 0} : StageCursor{c.blk, c.sub + 1};
   };
   const uint32_t qrow_bytes = static_cast<uint32_t>(a.hq) * kMfmaD * 2;
   const DmaLanes<kDkdvWaves> dl = make_dma_lanes<kDkdvWaves>(qrow_bytes, wave, lane);
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(smem));
-  // copy the Q and dO rows [row, row + 64) of query head qh into the stage buffer at `tile`
-  auto issue_stage = [&](int row, int nq, int qh, const char* tile) {
+  // copy the Q and dO rows [row, row + 64) of query head qh into the stage buffer at byte `tile`
+  auto issue_stage = [&](int row, int nq, int qh, uint32_t tile) __attribute__((always_inline)) {
     const int64_t off = static_cast<int64_t>(qh) * kMfmaD * 2 + static_cast<int64_t>(row) * qrow_bytes;
-    const uint32_t dst = lds0 + static_cast<uint32_t>(tile - smem);
-    dma_tile_s<kDkdvWaves>(reinterpret_cast<const char*>(qbase) + off, qrow_bytes, nq, dst, dl, wave);
-    dma_tile_s<kDkdvWaves>(reinterpret_cast<const char*>(gbase) + off, qrow_bytes, nq, dst + kTileBytes, dl, wave);
+    const uint32_t dst = lds0 + tile + wave * 4096;
+    const char* qs = reinterpret_cast<const char*>(qbase) + off;
+    const char* gs = reinterpret_cast<const char*>(gbase) + off;
+    if (nq >= kTileRows) {
+      dma_blocks4(qs, dl.voff[0], dl.voff[1], dl.voff[2], dl.voff[3], dst);
+      dma_blocks4(gs, dl.voff[0], dl.voff[1], dl.voff[2], dl.voff[3], dst + kTileBytes);
+    } else {  // rows at or beyond nq re-read row nq - 1
+      uint32_t v[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) v[j] = static_cast<uint32_t>(min(dl.row[j], nq - 1)) * qrow_bytes + dl.cbytes[j];
+      dma_blocks4(qs, v[0], v[1], v[2], v[3], dst);
+      dma_blocks4(gs, v[0], v[1], v[2], v[3], dst + kTileBytes);
+    }
   };
 
-  // lse*log2e (which 0) and delta (which 1) of the stage's 64 query rows of
+  // lse*log2e (which 0) and -delta (which 1) of the stage's 64 query rows of
   // each of its heads, copied into its stat buffer like the tiles -- wave w
   // copies (head w / 2, which w % 2); rows past the block end copy the
   // constants +inf / 0 of the workspace, so their P and dS are exactly 0.
   const uint32_t stats0 = __builtin_amdgcn_readfirstlane(lds_address(stats));
-  auto issue_stats = [&](int row, int nq, int qh, int buf) {
+  auto issue_stats = [&](int row, int nq, int qh, int buf) __attribute__((always_inline)) {
     const int hh = wave >> 1, which = wave & 1;
     if (hh < kHeads) {
       const int64_t at = static_cast<int64_t>(qh + hh) * a.total_q + row + lane;
-      const float* rows = which == 0 ? a.stat_ws + kStatRowsOffset : a.delta;
-      dma4(lane < nq ? rows + at : a.stat_ws + which, stats0 + ((buf * kHeads + hh) * 2 + which) * kTileRows * 4);
+      const float* rows = which == 0 ? a.stat_ws + kStatRowsOffset : a.ndelta_ws;
+      dma4_lane(lane < nq ? rows + at : a.stat_ws + which,
+                stats0 + ((buf * kHeads + hh) * 2 + which) * kTileRows * 4);
     }
   };
-  auto issue = [&](int sidx, int buf) {
-    int row0, tok0, nq, qh;
-    stage_info(sidx, row0, tok0, nq, qh);
-    issue_stats(row0 + tok0, nq, qh, buf);
+  auto issue = [&](StageCursor c, int buf) __attribute__((always_inline)) {
+    const int4 e = qtab[c.blk];
+    const int row = __builtin_amdgcn_readfirstlane(e.x), nq = __builtin_amdgcn_readfirstlane(e.z);
+    const int qh = kvh * a.group + c.sub * kHeads;
+    issue_stats(row, nq, qh, buf);
 #pragma unroll
     for (int hh = 0; hh < kHeads; hh++)
-      issue_stage(row0 + tok0, nq, qh + hh, smem + (buf * kHeads + hh) * 2 * kTileBytes);
+      issue_stage(row, nq, qh + hh, static_cast<uint32_t>((buf * kHeads + hh) * 2 * kTileBytes));
   };
-  if (nstage > 0) issue(0, 0);
+  StageCursor cur{0, 0};
+  if (nstage > 0) issue(cur, 0);
 
   bf16x8 kv[8], vv[8];
   {
@@ -1224,6 +1288,17 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
         else l2v[j][i] = v;
       }
     };
+    // -delta of the sub-block's queries in the accumulator layout: register
+    // 4i + e holds query 16 (i / 2) + 4 (i % 2) + e of the lane's 8-row group,
+    // the order the stats were read in
+    auto ndelta_acc = [&](int j) __attribute__((always_inline)) {
+      f32x16 c;
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) c[4 * i + e] = dlv[j][i][e];
+      return c;
+    };
     auto mfma_at = [&](auto mc) __attribute__((always_inline)) {
       constexpr int m = decltype(mc)::value, j = slot_sub(m), k = slot_pos(m);
       if constexpr (k < 8) {
@@ -1231,8 +1306,8 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
         else if constexpr (k == 0) sc[j] = mfma_vsp_first(rq[j][k], kv[k]);
         else mfma_vsp_acc(sc[j], rq[j][k], kv[k]);
       } else if constexpr (k < 16) {
-        if constexpr (!TPR_DKDV_VGPR_SP) dpv[j] = mfma(rg[j][k - 8], vv[k - 8], k == 8 ? f32x16{} : dpv[j]);
-        else if constexpr (k == 8) dpv[j] = mfma_vsp_first(rg[j][k - 8], vv[k - 8]);
+        if constexpr (!TPR_DKDV_VGPR_SP) dpv[j] = mfma(rg[j][k - 8], vv[k - 8], k == 8 ? ndelta_acc(j) : dpv[j]);
+        else if constexpr (k == 8) dpv[j] = mfma_vsp_init(rg[j][k - 8], vv[k - 8], ndelta_acc(j));
         else mfma_vsp_acc(dpv[j], rg[j][k - 8], vv[k - 8]);
       } else if constexpr (k < 24) {
         constexpr int cc = (k - 16) >> 2, db = (k - 16) & 3;
@@ -1255,7 +1330,7 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
     };
     auto ds_elem = [&](auto jc, auto rc) __attribute__((always_inline)) {
       constexpr int j = decltype(jc)::value, r = decltype(rc)::value;
-      dsv[j][r] = p[j][r] * (dpv[j][r] - dlv[j][r >> 2][r & 3]);
+      dsv[j][r] = p[j][r] * dpv[j][r];  // the dP chain started from -delta
       if constexpr ((r & 7) == 7) {
 #pragma unroll
         for (int i = 0; i < 8; i++) d8[j][r >> 3][i] = static_cast<bf16>(dsv[j][(r & 8) + i]);
@@ -1280,7 +1355,7 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
         read_for(std::integral_constant<int, m + kSlotAhead>{});
       }
       if constexpr (j == 1 && k == 2) read_stats(I1{}, I0{});
-      if constexpr (k == 10) read_stats(J{}, I1{});
+      if constexpr (k == 4) read_stats(J{}, I1{});  // -delta: the dP chain starts from it at k = 8
       mfma_at(mc);
       static_for<16>([&](auto rc) __attribute__((always_inline)) {
         constexpr int r = decltype(rc)::value;
@@ -1297,9 +1372,9 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
   // LDS address in the stage is a precomputed lane offset plus an immediate
   auto one_stage = [&](auto diag, auto bufc, int sidx) __attribute__((always_inline)) {
     constexpr int buf = decltype(bufc)::value;
-    int row0, tok0, nq, qh;
-    stage_info(sidx, row0, tok0, nq, qh);
-    if (sidx + 1 < nstage) issue(sidx + 1, buf ^ 1);
+    const int tok0 = __builtin_amdgcn_readfirstlane(qtab[cur.blk].y);
+    const StageCursor nxt = advance(cur);
+    if (sidx + 1 < nstage) issue(nxt, buf ^ 1);
     if (wave_active) {
       // key kp is visible from query index qi (of the stage) iff qi >= lim;
       // off this wave's diagonal lim <= -64 (all visible)
@@ -1322,6 +1397,7 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
       settle_acc(kv[c]);
       settle_acc(vv[c]);
     }
+    cur = nxt;
     wait_dma();  // stage sidx + 1 has landed
     __syncthreads();
   };

@@ -51,7 +51,7 @@ def test_accumulate_mode_adds_the_prefix_gradient(case, cuda_device):
         # 80 query blocks on every prefix tile: the planner splits each into 2 chunks
         # whose fp32 partials a reduction item sums (4 partial slots)
         meta, hq, hkv, d, dtype = TPRPrefixMeta.shared_prefix(256, [300] * 16), 4, 1, 128, torch.bfloat16
-        stat_bytes = (64 + (hq * meta.total_q + 63) // 64 * 64) * 4   # constants + lse rows
+        stat_bytes = (64 + 2 * ((hq * meta.total_q + 63) // 64 * 64)) * 4   # constants + lse and -delta rows
         assert meta.plan(hq, hkv, d, dtype, cuda_device).workspace_bytes == stat_bytes + 4 * 2 * 128 * 128 * 4
     elif case == "simt_fp32":
         meta, hq, hkv, d, dtype = TPRPrefixMeta.shared_prefix(96, [40, 17, 33]), 4, 2, 64, torch.float32
