@@ -124,10 +124,11 @@ def test_split_prefix_tiles_have_ordered_partials_and_reductions():
     w, _, dkdv, qblk = decode(plan)
     reds = [tuple(w[w[24] + 8 * i: w[24] + 8 * i + 8]) for i in range(w[PF["N_RED"]])]
     n_slots = w[25]
-    # workspace: stat area (2 constants padded to 64 floats, then lse*log2e per
-    # (query head, token) rounded up to 64 floats), then the fp32 partial slots
+    # workspace: stat area (2 constants padded to 64 floats, then lse*log2e and
+    # -delta per (query head, token), each rounded up to 64 floats), then the
+    # fp32 partial slots
     total_q = 4096 * 3 + 100
-    stat_floats = 64 + (8 * total_q + 63) // 64 * 64
+    stat_floats = 64 + 2 * ((8 * total_q + 63) // 64 * 64)
     assert n_slots > 0 and plan.workspace_bytes == (stat_floats + n_slots * 2 * 128 * 128) * 4
     by_slot = {item[6]: item for item in dkdv if item[0] >= 0 and item[6] >= 0}
     assert sorted(by_slot) == list(range(n_slots))
