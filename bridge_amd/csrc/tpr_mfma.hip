@@ -246,15 +246,37 @@ __device__ __forceinline__ void dma_tile_s(const char* src, uint32_t row_bytes, 
   }
 }
 
-// Four 1 KiB global -> LDS copies (global_load_lds_dwordx4) of one wave: block
-// j lands at lds_dst + 1024 j (M0, stepped in SALU) from the uniform base
-// `sbase` (SGPRs) plus the lane's 32-bit offset voff[j]. One asm block per
-// tile: M0 is saved and restored once, and the copies need no per-lane
-// 64-bit address arithmetic. Like dma16s, the compiler does not track these
-// loads; the stage's wait_dma() before the barrier that publishes the tile
-// is their only wait.
+// Four 1 KiB global -> LDS copies (global_load_lds_dwordx4) of one wave, block
+// j landing at lds_dst + 1024 j from the uniform base `sbase` (SGPRs) plus the
+// lane's 32-bit offset vj, with M0 saved and restored once around the group.
+// Like dma16s, the compiler does not track these loads; the wait_dma()
+// before the barrier that publishes the tile is their only wait.
+//
+// dma_blocks4 writes M0 once: blocks 1-3 use the instruction offset (1024 j),
+// which applies to both the LDS and the global address, so their lane offsets
+// are passed as vj - 1024 j. That needs vj >= 1024 j in every lane (the
+// offset is an unsigned 32-bit VGPR): true for a full tile, whose block j
+// starts at row 4 j of rows of at least 256 bytes; NOT for a tile whose rows
+// are clamped to a short tile's last row -- those use dma_blocks4_m0, which
+// steps M0 between the blocks instead.
 __device__ __forceinline__ void dma_blocks4(const char* sbase, uint32_t v0, uint32_t v1, uint32_t v2, uint32_t v3,
                                             uint32_t lds_dst) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %5\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %6\n\t"
+      "global_load_lds_dwordx4 %2, %6 offset:1024\n\t"
+      "global_load_lds_dwordx4 %3, %6 offset:2048\n\t"
+      "global_load_lds_dwordx4 %4, %6 offset:3072\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(v0), "v"(v1 - 1024u), "v"(v2 - 2048u), "v"(v3 - 3072u), "s"(lds_dst), "s"(sbase));
+}
+
+__device__ __forceinline__ void dma_blocks4_m0(const char* sbase, uint32_t v0, uint32_t v1, uint32_t v2, uint32_t v3,
+                                               uint32_t lds_dst) {
   uint32_t saved;
   asm volatile(
       "s_mov_b32 %0, m0\n\t"
@@ -289,25 +311,63 @@ __device__ __forceinline__ void dma4_lane(const float* src, uint32_t lds_dst) {
       : "v"(src), "s"(lds_dst));
 }
 
-// Per-lane part of a 64-row tile copy by 4 waves, in two registers: lane l of
+// Per-lane part of a 64-row tile copy by 4 waves: lane l of wave w moves, in
+// block j = 0..3, row 16w + 4j + l/16 and the 16-byte source chunk
+// swz_chunk(row, l%16) = (l%16) ^ ((l/16) << 2) ^ j, i.e. chunk bytes
+// cb0 ^ 16j; full[j] is that block's byte offset in a full tile.
+struct TileLanes4 {
+  uint32_t row0;     // 16w + l/16
+  uint32_t cb0;      // 16 * ((l%16) ^ ((l/16) << 2))
+  uint32_t full[4];  // (row0 + 4j) * row_bytes + (cb0 ^ 16j)
+};
+
+__device__ __forceinline__ TileLanes4 make_tile_lanes4(int wave, int lane, uint32_t row_bytes) {
+  TileLanes4 p;
+  p.row0 = static_cast<uint32_t>(16 * wave + (lane >> 4));
+  p.cb0 = static_cast<uint32_t>(16 * ((lane & 15) ^ ((lane >> 4) << 2)));
+#pragma unroll
+  for (int j = 0; j < 4; j++) p.full[j] = (p.row0 + 4u * j) * row_bytes + (p.cb0 ^ (16u * j));
+  return p;
+}
+
+// Copy rows [0, 64) of the tile starting at `src` (uniform; rows at or beyond
+// `len` re-read row len - 1) into the swizzled LDS tile at `lds_tile`; this
+// wave moves its four 1 KiB blocks (one asm group).
+__device__ __forceinline__ void dma_tile4(const char* src, uint32_t row_bytes, int len, uint32_t lds_tile,
+                                          const TileLanes4& p, int wave) {
+  const uint32_t dst = lds_tile + wave * 4096;
+  if (len >= kTileRows) {
+    dma_blocks4(src, p.full[0], p.full[1], p.full[2], p.full[3], dst);
+  } else {
+    const uint32_t last = static_cast<uint32_t>(len - 1);
+    uint32_t v[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) v[j] = min(p.row0 + 4u * j, last) * row_bytes + (p.cb0 ^ (16u * j));
+    dma_blocks4_m0(src, v[0], v[1], v[2], v[3], dst);
+  }
+}
+
+// The forward's tile copy: the same lanes as TileLanes4, the offsets computed
+// per copy (the forward runs slower holding four more offset registers
+// through its tile loop). Per-lane part of a 64-row tile copy by 4 waves, in two registers: lane l of
 // wave w moves, in block j = 0..3, row 16w + 4j + l/16 and the 16-byte source
 // chunk swz_chunk(row, l%16) = (l%16) ^ ((l/16) << 2) ^ j, i.e. chunk bytes
 // cb0 ^ 16j.
-struct TileLanes4 {
+struct FwdTileLanes {
   uint32_t row0;  // 16w + l/16
   uint32_t cb0;   // 16 * ((l%16) ^ ((l/16) << 2))
 };
 
-__device__ __forceinline__ TileLanes4 make_tile_lanes4(int wave, int lane) {
-  return TileLanes4{static_cast<uint32_t>(16 * wave + (lane >> 4)),
+__device__ __forceinline__ FwdTileLanes make_fwd_tile_lanes(int wave, int lane) {
+  return FwdTileLanes{static_cast<uint32_t>(16 * wave + (lane >> 4)),
                     static_cast<uint32_t>(16 * ((lane & 15) ^ ((lane >> 4) << 2)))};
 }
 
 // Copy rows [0, 64) of the tile starting at `src` (uniform; rows at or beyond
 // `len` re-read row len - 1) into the swizzled LDS tile at `lds_tile`; this
 // wave moves its four 1 KiB blocks.
-__device__ __forceinline__ void dma_tile4(const char* src, uint32_t row_bytes, int len, uint32_t lds_tile,
-                                          TileLanes4 p, int wave) {
+__device__ __forceinline__ void dma_tile4_fwd(const char* src, uint32_t row_bytes, int len, uint32_t lds_tile,
+                                              FwdTileLanes p, int wave) {
   const uint32_t last = static_cast<uint32_t>(len - 1);
 #pragma unroll
   for (int j = 0; j < 4; j++) {
@@ -521,7 +581,7 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
   const char* vbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.v) + kvh * kMfmaD);
   const char* pkbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.pk) + kvh * kMfmaD);
   const char* pvbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.pv) + kvh * kMfmaD);
-  const TileLanes4 dl = make_tile_lanes4(wave & 3, lane);
+  const FwdTileLanes dl = make_fwd_tile_lanes(wave & 3, lane);
   const FwdLdsOffsets lo = make_fwd_lds_offsets(lane);
 
   const auto seg = load_keys<kRunList>(a, leaf, suffix_keys);
@@ -533,7 +593,7 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
   // group B's copy cursor: the next K tile (tl_k) and the next V tile (tl_v)
   Cursor dc = cursor_begin(seg);
   TileLoc tl_k = cursor_tile(dc), tl_v = tl_k;
-  if (grp) dma_tile4(kv_src(tl_k, true), row_bytes, tl_k.len, lds0, dl, wave & 3);  // K[0]
+  if (grp) dma_tile4_fwd(kv_src(tl_k, true), row_bytes, tl_k.len, lds0, dl, wave & 3);  // K[0]
   if (ntiles > 1) {
     cursor_next(seg, dc);
     tl_k = cursor_tile(dc);
@@ -564,9 +624,9 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
   // into V buffer (j+1)&1
   auto issue = [&](int j) {
     if (j + 2 < ntiles)
-      dma_tile4(kv_src(tl_k, true), row_bytes, tl_k.len, lds0 + ((j + 2) & 1) * kTileBytes, dl, wave & 3);
+      dma_tile4_fwd(kv_src(tl_k, true), row_bytes, tl_k.len, lds0 + ((j + 2) & 1) * kTileBytes, dl, wave & 3);
     if (j + 1 < ntiles)
-      dma_tile4(kv_src(tl_v, false), row_bytes, tl_v.len, lds0 + (2 + ((j + 1) & 1)) * kTileBytes, dl, wave & 3);
+      dma_tile4_fwd(kv_src(tl_v, false), row_bytes, tl_v.len, lds0 + (2 + ((j + 1) & 1)) * kTileBytes, dl, wave & 3);
     tl_v = tl_k;
     if (j + 3 < ntiles) {
       cursor_next(seg, dc);
@@ -829,7 +889,7 @@ __global__ __launch_bounds__(512) void mfma_dq(KernelArgs a) {
   const char* vbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.v) + kvh * kMfmaD);
   const char* pkbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.pk) + kvh * kMfmaD);
   const char* pvbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.pv) + kvh * kMfmaD);
-  const TileLanes4 dl = make_tile_lanes4(wave & 3, lane);
+  const TileLanes4 dl = make_tile_lanes4(wave & 3, lane, row_bytes);
   // K/V row reads (A operands of S, dP) and, for group A, the transposing reads
   const FwdLdsOffsets lo = make_fwd_lds_offsets(lane);
   // K^T reads (A operand of dQ^T): row 32db + n, keys 32kb + 16cc + 8h: the
@@ -1175,8 +1235,8 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
       uint32_t v[4];
 #pragma unroll
       for (int j = 0; j < 4; j++) v[j] = static_cast<uint32_t>(min(dl.row[j], nq - 1)) * qrow_bytes + dl.cbytes[j];
-      dma_blocks4(qs, v[0], v[1], v[2], v[3], dst);
-      dma_blocks4(gs, v[0], v[1], v[2], v[3], dst + kTileBytes);
+      dma_blocks4_m0(qs, v[0], v[1], v[2], v[3], dst);
+      dma_blocks4_m0(gs, v[0], v[1], v[2], v[3], dst + kTileBytes);
     }
   };
 

@@ -135,7 +135,6 @@ __device__ __forceinline__ float group_sum(float x) {
 // chunks of 8 elements at 8*kL*j + 8*c (16-byte LDS reads); the fp32 axpy
 // operands keep the 4-element chunks above, a different partition of the
 // same row, which the group sum does not care about.
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 struct Bf16Pairs {
   bf16x2 p[4];
 };
