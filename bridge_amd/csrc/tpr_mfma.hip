@@ -818,11 +818,11 @@ __global__ __launch_bounds__(256) void mfma_delta(KernelArgs a) {
   if (c == 0 && row < rows) {
     const int64_t at = (row % a.hq) * a.total_q + row / a.hq;
     a.delta[at] = s;
-    a.stat_ws[kStatRowsOffset + at] = a.lse_in[at] * kLog2e;  // the dK/dV kernel copies these rows
+    a.stat_ws[kStatRowsOffset + at] = -(a.lse_in[at] * kLog2e);  // the dK/dV kernel copies these rows
     a.ndelta_ws[at] = -s;
   }
   if (blockIdx.x == 0 && threadIdx.x == 0) {
-    a.stat_ws[0] = INFINITY;  // lse*log2e of a query past a block's end: P = 0
+    a.stat_ws[0] = -INFINITY;  // -lse*log2e of a query past a block's end: P = 0
     a.stat_ws[1] = 0.f;       // its -delta
   }
 }
@@ -1191,7 +1191,7 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
   // two stage buffers of kHeads (Q, dO) tile pairs: the copies of stage s + 1
   // run during stage s
   __shared__ __attribute__((aligned(1024))) char smem[2 * kHeads * 2 * kTileBytes];
-  __shared__ __attribute__((aligned(256))) float stats[2][kHeads][2][kTileRows];  // [buf][head][lse*log2e | delta][row]
+  __shared__ __attribute__((aligned(256))) float stats[2][kHeads][2][kTileRows];  // [buf][head][-lse*log2e | -delta][row]
 
   const int spb = a.group / kHeads;  // stages per query block
   const int nstage = (qb_hi - qb_lo) * spb;
@@ -1240,10 +1240,10 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
     }
   };
 
-  // lse*log2e (which 0) and -delta (which 1) of the stage's 64 query rows of
+  // -lse*log2e (which 0) and -delta (which 1) of the stage's 64 query rows of
   // each of its heads, copied into its stat buffer like the tiles -- wave w
   // copies (head w / 2, which w % 2); rows past the block end copy the
-  // constants +inf / 0 of the workspace, so their P and dS are exactly 0.
+  // constants -inf / 0 of the workspace, so their P and dS are exactly 0.
   const uint32_t stats0 = __builtin_amdgcn_readfirstlane(lds_address(stats));
   auto issue_stats = [&](int row, int nq, int qh, int buf) __attribute__((always_inline)) {
     const int hh = wave >> 1, which = wave & 1;
@@ -1283,117 +1283,142 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
     dk[i] = f32x16{};
     dv[i] = f32x16{};
   }
-  const float c2 = a.scale * kLog2e;
+  // K as the S operand, pre-scaled by scale*log2e (rounded to bf16): the S
+  // chain then produces the exponent of P directly
+  {
+    const float c2 = a.scale * kLog2e;
+#pragma unroll
+    for (int c = 0; c < 8; c++)
+#pragma unroll
+      for (int i = 0; i < 8; i++) kv[c][i] = static_cast<bf16>(static_cast<float>(kv[c][i]) * c2);
+  }
 
+  // K/V live in AGPRs from here on: the S / dP MFMAs that read them are
+  // inline asm, before which the compiler inserts no wait states, so the
+  // accvgpr writes must not land next to their first use inside the loop.
 #pragma unroll
   for (int c = 0; c < 8; c++) {
-    settle(kv[c]);
-    settle(vv[c]);
+    settle_acc(kv[c]);
+    settle_acc(vv[c]);
   }
   wait_dma();
   __syncthreads();
 
-  // One stage: 64 queries of one head against the wave's 32 keys, as two
-  // 32-query sub-blocks j of 32 MFMAs each -- S (8), dP (8), dV (8), dK (8).
-  // The stage is laid out as a fixed sequence of 64 slots, one MFMA per slot,
-  // fenced so the compiler keeps the order:
+  // One stage: 64 queries of each of its kHeads heads against the wave's 32
+  // keys, each head as two 32-query sub-blocks j of 32 MFMAs -- S (8), dP (8),
+  // dV (8), dK (8). The stage is laid out as one fixed sequence of 64 kHeads
+  // slots, one MFMA per slot (head m / 64), fenced so the compiler keeps the
+  // order:
   //  * the LDS operands of an MFMA are read kAhead MFMAs of the same
-  //    sub-block earlier, so every read has that many MFMAs to land;
-  //  * P = exp2(scale*S - lse) of sub-block j is computed under its dP and
-  //    first dV MFMAs, dS = P (dP - delta) under its dV and first dK MFMAs,
-  //    so the VALU work runs while the matrix core is busy.
+  //    sub-block earlier -- across the boundary between heads too, so the
+  //    second head's first MFMAs do not wait for a fresh pipeline;
+  //  * the S chain starts from -lse*log2e and the K operand is pre-scaled by
+  //    scale*log2e, so the chain ends at the exponent: P = exp2(acc). P of
+  //    sub-block j is computed under its dP and first dV MFMAs, dS = P * acc
+  //    (the dP chain started from -delta) under its dV and first dK MFMAs, so
+  //    the VALU work runs while the matrix core is busy.
   // On a diagonal stage (diag), key kp is visible from query index qi of
   // sub-block j iff qi >= lim - 32j; other stages skip the mask. Queries past
-  // the block end carry lse = +inf, so their P and dS are exactly 0.
+  // the block end carry -lse*log2e = -inf, so their P and dS are exactly 0.
   constexpr int kAhead = 4;  // MFMAs of the same sub-block between a read and its use
   constexpr int kSlotAhead = kInterleave ? 2 * kAhead : kAhead;
+  constexpr int kSlots = 64 * kHeads;
   // Lane offsets of the operand reads; the second set carries a 64 KiB bias so
   // that the reads of stage buffer 1 (at 64 KiB when kHeads is 2) keep their
   // constant part within the 16-bit LDS instruction offset.
   constexpr uint32_t kBuf1Bias = kHeads * 2 * kTileBytes >= 65536 ? 65536u : 0u;
   const FwdLdsOffsets lo0 = make_fwd_lds_offsets(lane);
   const FwdLdsOffsets lo1 = make_fwd_lds_offsets(lane, kBuf1Bias);
-  auto stage = [&](auto diag, const char* qt, const char* gt, const float* st, int lim,
-                   const FwdLdsOffsets& lo) __attribute__((always_inline)) {
-    bf16x8 rq[2][8], rg[2][8], cg[2][2][4], cq[2][2][4];
-    f32x4 l2v[2][4], dlv[2][4];
-    f32x16 sc[2], dpv[2];
-    float p[2][16], dsv[2][16];
-    bf16x8 pb[2][2], d8[2][2];
-    // operands of MFMA m (sub-block m / 32, position m % 32)
+  auto stage = [&](auto diag, auto bufc, int lim) __attribute__((always_inline)) {
+    constexpr int buf = decltype(bufc)::value;
+    const FwdLdsOffsets& lo = buf ? lo1 : lo0;
+    bf16x8 rq[kHeads][2][8], rg[kHeads][2][8], cg[kHeads][2][2][4], cq[kHeads][2][2][4];
+    f32x4 l2v[kHeads][2][4], dlv[kHeads][2][4];
+    f32x16 sc[kHeads][2], dpv[kHeads][2];
+    float p[kHeads][2][16], dsv[kHeads][2][16];
+    bf16x8 pb[kHeads][2][2], d8[kHeads][2][2];
+    // Q tile of head hh (minus the bias of the offset set used for this
+    // buffer); its dO tile follows it
+    auto qtile = [&](int hh) __attribute__((always_inline)) {
+      return smem + (buf * kHeads + hh) * 2 * kTileBytes - (buf ? kBuf1Bias : 0u);
+    };
+    // operands of slot M (head M / 64; sub-block and position of M % 64)
     auto read_for = [&](auto mc) __attribute__((always_inline)) {
-      constexpr int m = decltype(mc)::value, j = slot_sub(m), k = slot_pos(m);
+      constexpr int M = decltype(mc)::value, hh = M / 64, m = M % 64, j = slot_sub(m), k = slot_pos(m);
+      const char* qt = qtile(hh);
+      const char* gt = qt + kTileBytes;
       // rows 32j + sigma32(n) and the 16-row groups of the column reads are
       // the lane offsets of lo plus 8192j / 4096(2j + cc) (immediates)
       if constexpr (k < 8) {
-        rq[j][k] = *reinterpret_cast<const bf16x8*>(qt + 8192 * j + lo.k[k]);
+        rq[hh][j][k] = *reinterpret_cast<const bf16x8*>(qt + 8192 * j + lo.k[k]);
       } else if constexpr (k < 16) {
-        rg[j][k - 8] = *reinterpret_cast<const bf16x8*>(gt + 8192 * j + lo.k[k - 8]);
+        rg[hh][j][k - 8] = *reinterpret_cast<const bf16x8*>(gt + 8192 * j + lo.k[k - 8]);
       } else if constexpr (k < 24) {
         constexpr int cc = (k - 16) >> 2, db = (k - 16) & 3;
-        cg[j][cc][db] = lds_col8_at(gt + 4096 * (2 * j + cc), lo.v[db][0], lo.v[db][1]);
+        cg[hh][j][cc][db] = lds_col8_at(gt + 4096 * (2 * j + cc), lo.v[db][0], lo.v[db][1]);
       } else {
         constexpr int cc = (k - 24) >> 2, db = (k - 24) & 3;
-        cq[j][cc][db] = lds_col8_at(qt + 4096 * (2 * j + cc), lo.v[db][0], lo.v[db][1]);
+        cq[hh][j][cc][db] = lds_col8_at(qt + 4096 * (2 * j + cc), lo.v[db][0], lo.v[db][1]);
       }
     };
-    // lse*log2e (which 0) or delta (which 1) of the lane's 16 queries of sub-block j
-    auto read_stats = [&](auto jc, auto wc) __attribute__((always_inline)) {
-      constexpr int j = decltype(jc)::value, which = decltype(wc)::value;
-      const float* src = st + which * kTileRows + 32 * j + 8 * h;
+    // -lse*log2e (which 0) or -delta (which 1) of the lane's 16 queries of
+    // sub-block j of head hh, in the accumulator layout: register 4i + e holds
+    // query 16 (i / 2) + 4 (i % 2) + e of the lane's 8-row group
+    auto read_stats = [&](auto hc, auto jc, auto wc) __attribute__((always_inline)) {
+      constexpr int hh = decltype(hc)::value, j = decltype(jc)::value, which = decltype(wc)::value;
+      const float* src = &stats[buf][hh][which][0] + 32 * j + 8 * h;
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const f32x4 v = *reinterpret_cast<const f32x4*>(src + 16 * (i >> 1) + 4 * (i & 1));
-        if constexpr (which) dlv[j][i] = v;
-        else l2v[j][i] = v;
+        if constexpr (which) dlv[hh][j][i] = v;
+        else l2v[hh][j][i] = v;
       }
     };
-    // -delta of the sub-block's queries in the accumulator layout: register
-    // 4i + e holds query 16 (i / 2) + 4 (i % 2) + e of the lane's 8-row group,
-    // the order the stats were read in
-    auto ndelta_acc = [&](int j) __attribute__((always_inline)) {
+    auto acc_of = [&](const f32x4 (&x)[4]) __attribute__((always_inline)) {
       f32x16 c;
 #pragma unroll
       for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int e = 0; e < 4; e++) c[4 * i + e] = dlv[j][i][e];
+        for (int e = 0; e < 4; e++) c[4 * i + e] = x[i][e];
       return c;
     };
     auto mfma_at = [&](auto mc) __attribute__((always_inline)) {
-      constexpr int m = decltype(mc)::value, j = slot_sub(m), k = slot_pos(m);
+      constexpr int M = decltype(mc)::value, hh = M / 64, m = M % 64, j = slot_sub(m), k = slot_pos(m);
       if constexpr (k < 8) {
-        if constexpr (!TPR_DKDV_VGPR_SP) sc[j] = mfma(rq[j][k], kv[k], k == 0 ? f32x16{} : sc[j]);
-        else if constexpr (k == 0) sc[j] = mfma_vsp_first(rq[j][k], kv[k]);
-        else mfma_vsp_acc(sc[j], rq[j][k], kv[k]);
+        if constexpr (!TPR_DKDV_VGPR_SP) sc[hh][j] = mfma(rq[hh][j][k], kv[k], k == 0 ? acc_of(l2v[hh][j]) : sc[hh][j]);
+        else if constexpr (k == 0) sc[hh][j] = mfma_vsp_init(rq[hh][j][k], kv[k], acc_of(l2v[hh][j]));
+        else mfma_vsp_acc(sc[hh][j], rq[hh][j][k], kv[k]);
       } else if constexpr (k < 16) {
-        if constexpr (!TPR_DKDV_VGPR_SP) dpv[j] = mfma(rg[j][k - 8], vv[k - 8], k == 8 ? ndelta_acc(j) : dpv[j]);
-        else if constexpr (k == 8) dpv[j] = mfma_vsp_init(rg[j][k - 8], vv[k - 8], ndelta_acc(j));
-        else mfma_vsp_acc(dpv[j], rg[j][k - 8], vv[k - 8]);
+        if constexpr (!TPR_DKDV_VGPR_SP)
+          dpv[hh][j] = mfma(rg[hh][j][k - 8], vv[k - 8], k == 8 ? acc_of(dlv[hh][j]) : dpv[hh][j]);
+        else if constexpr (k == 8) dpv[hh][j] = mfma_vsp_init(rg[hh][j][k - 8], vv[k - 8], acc_of(dlv[hh][j]));
+        else mfma_vsp_acc(dpv[hh][j], rg[hh][j][k - 8], vv[k - 8]);
       } else if constexpr (k < 24) {
         constexpr int cc = (k - 16) >> 2, db = (k - 16) & 3;
-        dv[db] = mfma(pb[j][cc], cg[j][cc][db], dv[db]);
+        dv[db] = mfma(pb[hh][j][cc], cg[hh][j][cc][db], dv[db]);
       } else {
         constexpr int cc = (k - 24) >> 2, db = (k - 24) & 3;
-        dk[db] = mfma(d8[j][cc], cq[j][cc][db], dk[db]);
+        dk[db] = mfma(d8[hh][j][cc], cq[hh][j][cc][db], dk[db]);
       }
     };
     // register r of a sub-block holds query 16*(r/8) + r%8 of the lane's 8-row group
-    auto p_elem = [&](auto jc, auto rc) __attribute__((always_inline)) {
-      constexpr int j = decltype(jc)::value, r = decltype(rc)::value, qi = 16 * (r >> 3) + (r & 7);
-      float x = fmaf(sc[j][r], c2, -l2v[j][r >> 2][r & 3]);
+    auto p_elem = [&](auto hc, auto jc, auto rc) __attribute__((always_inline)) {
+      constexpr int hh = decltype(hc)::value, j = decltype(jc)::value, r = decltype(rc)::value;
+      constexpr int qi = 16 * (r >> 3) + (r & 7);
+      float x = sc[hh][j][r];  // scale*log2e*S - lse*log2e
       if constexpr (decltype(diag)::value) x = qi >= lim - 32 * j ? x : -INFINITY;
-      p[j][r] = fast_exp2(x);
+      p[hh][j][r] = fast_exp2(x);
       if constexpr ((r & 7) == 7) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) pb[j][r >> 3][i] = static_cast<bf16>(p[j][(r & 8) + i]);
+        for (int i = 0; i < 8; i++) pb[hh][j][r >> 3][i] = static_cast<bf16>(p[hh][j][(r & 8) + i]);
       }
     };
-    auto ds_elem = [&](auto jc, auto rc) __attribute__((always_inline)) {
-      constexpr int j = decltype(jc)::value, r = decltype(rc)::value;
-      dsv[j][r] = p[j][r] * dpv[j][r];  // the dP chain started from -delta
+    auto ds_elem = [&](auto hc, auto jc, auto rc) __attribute__((always_inline)) {
+      constexpr int hh = decltype(hc)::value, j = decltype(jc)::value, r = decltype(rc)::value;
+      dsv[hh][j][r] = p[hh][j][r] * dpv[hh][j][r];  // the dP chain started from -delta
       if constexpr ((r & 7) == 7) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) d8[j][r >> 3][i] = static_cast<bf16>(dsv[j][(r & 8) + i]);
+        for (int i = 0; i < 8; i++) d8[hh][j][r >> 3][i] = static_cast<bf16>(dsv[hh][j][(r & 8) + i]);
       }
     };
     using I0 = std::integral_constant<int, 0>;
@@ -1406,21 +1431,26 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
       read_for(std::integral_constant<int, q + 1>{});
       read_for(std::integral_constant<int, q>{});
     });
-    read_stats(I0{}, I0{});
-    static_for<64>([&](auto mc) __attribute__((always_inline)) {
-      constexpr int m = decltype(mc)::value, j = slot_sub(m), k = slot_pos(m);
+    read_stats(I0{}, I0{}, I0{});
+    read_stats(I0{}, I1{}, I0{});
+    static_for<kSlots>([&](auto mc) __attribute__((always_inline)) {
+      constexpr int M = decltype(mc)::value, hh = M / 64, m = M % 64, j = slot_sub(m), k = slot_pos(m);
+      using H = std::integral_constant<int, hh>;
       using J = std::integral_constant<int, j>;
-      if constexpr (m % 2 == 0 && m + kSlotAhead + 1 < 64) {
-        read_for(std::integral_constant<int, m + kSlotAhead + 1>{});
-        read_for(std::integral_constant<int, m + kSlotAhead>{});
+      if constexpr (m % 2 == 0 && M + kSlotAhead + 1 < kSlots) {
+        read_for(std::integral_constant<int, M + kSlotAhead + 1>{});
+        read_for(std::integral_constant<int, M + kSlotAhead>{});
       }
-      if constexpr (j == 1 && k == 2) read_stats(I1{}, I0{});
-      if constexpr (k == 4) read_stats(J{}, I1{});  // -delta: the dP chain starts from it at k = 8
+      if constexpr (m == 56 && hh + 1 < kHeads) {  // the next head's -lse rows, ahead of its S chains
+        read_stats(std::integral_constant<int, hh + 1>{}, I0{}, I0{});
+        read_stats(std::integral_constant<int, hh + 1>{}, I1{}, I0{});
+      }
+      if constexpr (k == 4) read_stats(H{}, J{}, I1{});  // -delta: the dP chain starts from it at k = 8
       mfma_at(mc);
       static_for<16>([&](auto rc) __attribute__((always_inline)) {
         constexpr int r = decltype(rc)::value;
-        if constexpr (k == 9 + (r * 10) / 16) p_elem(J{}, rc);   // P: slots 9..18 (pb[0] by 13, pb[1] by 18)
-        if constexpr (k == 19 + (r * 9) / 16) ds_elem(J{}, rc);  // dS: slots 19..27 (d8[0] by 22, d8[1] by 27)
+        if constexpr (k == 9 + (r * 10) / 16) p_elem(H{}, J{}, rc);   // P: slots 9..18 (pb[0] by 13, pb[1] by 18)
+        if constexpr (k == 19 + (r * 9) / 16) ds_elem(H{}, J{}, rc);  // dS: slots 19..27 (d8[0] by 22, d8[1] by 27)
       });
       __builtin_amdgcn_sched_barrier(0);
     });
@@ -1439,13 +1469,7 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
       // key kp is visible from query index qi (of the stage) iff qi >= lim;
       // off this wave's diagonal lim <= -64 (all visible)
       const int lim = tok0 < kw0 + 31 ? kp - tok0 - 8 * h : -64;
-#pragma unroll
-      for (int hh = 0; hh < kHeads; hh++) {
-        // tile pointer minus the bias of the offset set used for this buffer
-        const char* qt = smem + (buf * kHeads + hh) * 2 * kTileBytes - (buf ? kBuf1Bias : 0u);
-        if constexpr (buf) stage(diag, qt, qt + kTileBytes, &stats[buf][hh][0][0], lim, lo1);
-        else stage(diag, qt, qt + kTileBytes, &stats[buf][hh][0][0], lim, lo0);
-      }
+      stage(diag, bufc, lim);
     }
 #pragma unroll
     for (int i = 0; i < 4; i++) {  // accumulators stay in AGPRs across the stage loop
