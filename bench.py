@@ -56,9 +56,12 @@ def workload(name: str):
         lens = torch.randint(256, 8193, (16,), generator=g).tolist()
         return (f"ragged varlen: prefix 8192 + 16 suffixes U[256,8192] (seed 0), GQA 32/8, d128, bf16",
                 TPRPrefixMeta.shared_prefix(8192, lens), 32, 8, 128, torch.bfloat16)
-    if name == "qwen35-attn":   # head_dim 256: the SIMT kernels
+    if name == "qwen35-attn":   # head_dim 256: the 16-wide MFMA kernels
         return ("Qwen3.5 hybrid full-attention layer: prefix 4096 + 4 x 4096 sibling suffixes, GQA 8/2, d256, bf16",
                 TPRPrefixMeta.shared_prefix(4096, [4096] * 4), 8, 2, 256, torch.bfloat16)
+    if name == "head64":   # head_dim 64 (the reference's operator-test head size) at the headline sequence shape
+        return ("head_dim 64: prefix 4096 + 4 x 4096 sibling suffixes, GQA 32/8, d64, bf16",
+                TPRPrefixMeta.shared_prefix(4096, [4096] * 4), 32, 8, 64, torch.bfloat16)
     if name == "turn-tree":
         anc = tuple((0, 1 + i // 4) for i in range(16))
         meta = TPRPrefixMeta(tuple(1024 * i for i in range(17)), (0, 2048, 3072, 4096, 5120, 6144), anc)
@@ -340,7 +343,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="qwen3-4b",
-                    choices=["qwen3-4b", "plumbing-fp32", "long-session", "ragged", "turn-tree", "qwen35-attn",
+                    choices=["qwen3-4b", "plumbing-fp32", "long-session", "ragged", "turn-tree", "qwen35-attn", "head64",
                              "qwen3-4b-1sibling", "qwen3-4b-noprefix"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -436,11 +439,12 @@ def main() -> int:
     total_flops = 7.0 * unit            # fwd (2 GEMMs) + bwd (5 GEMMs)
     value = total_flops / (ms_per_step * 1e-3) / 1e12
     # the SIMT kernels compute in fp32 on the vector ALUs, whatever the I/O dtype
-    peak = BF16_PEAK_TFLOPS if plan.path == "mfma" else FP32_PEAK_TFLOPS
+    peak = BF16_PEAK_TFLOPS if plan.path in ("mfma", "mfma16") else FP32_PEAK_TFLOPS
+    prefix = {"mfma": "tpr::mfma_", "mfma16": "tpr::m16_", "simt": "tpr::simt_"}[plan.path]
     kernels = {
-        "fwd": (fwd_ms, 2.0 * unit, "tpr::mfma_fwd" if plan.path == "mfma" else "tpr::simt_fwd"),
-        "dkdv": (dkdv_ms, 4.0 * unit, "tpr::mfma_dkdv" if plan.path == "mfma" else "tpr::simt_dkdv"),
-        "dq": (dq_ms, 3.0 * unit, "tpr::mfma_dq" if plan.path == "mfma" else "tpr::simt_dq"),
+        "fwd": (fwd_ms, 2.0 * unit, prefix + "fwd"),
+        "dkdv": (dkdv_ms, 4.0 * unit, prefix + "dkdv"),
+        "dq": (dq_ms, 3.0 * unit, prefix + "dq"),
     }
     dom = max(kernels, key=lambda n: kernels[n][0])
     dom_ms, dom_flops, dom_name = kernels[dom]

@@ -18,7 +18,7 @@ BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_PATH = os.path.join(PKG_DIR, "libtpr_attn.so")
 ARCH = os.environ.get("TPR_OFFLOAD_ARCH", "gfx950")
 
-HIP_SOURCES = ["tpr_abi.hip", "tpr_simt.hip", "tpr_mfma.hip"]
+HIP_SOURCES = ["tpr_abi.hip", "tpr_simt.hip", "tpr_mfma.hip", "tpr_mfma16.hip"]
 CXX_SOURCES = ["tpr_plan.cpp"]
 
 

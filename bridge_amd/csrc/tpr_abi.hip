@@ -19,6 +19,9 @@ int launch_simt_bwd(const KernelArgs& a, int n_fwd, int n_dkdv, bool fp32, hipSt
 int launch_mfma_fwd(const KernelArgs& a, hipStream_t s);
 int launch_mfma_bwd(const KernelArgs& a, int n_fwd, int n_dkdv, int n_red, hipStream_t s);
 int launch_mfma_delta(const KernelArgs& a, hipStream_t s);
+int launch_m16_fwd(const KernelArgs& a, hipStream_t s);
+int launch_m16_delta(const KernelArgs& a, hipStream_t s);
+int launch_m16_bwd(const KernelArgs& a, int n_fwd, int n_dkdv, int n_red, hipStream_t s);
 
 namespace {
 thread_local char g_error[512] = "";
@@ -48,9 +51,11 @@ KernelArgs args_from_plan(const int32_t* ph, const int32_t* pd, float scale) {
   a.hkv = ph[PF_HKV];
   a.d = ph[PF_D];
   a.group = a.hq / a.hkv;
+  // query heads per forward / dQ workgroup: gcd(group, waves per workgroup)
+  const int waves = ph[PF_PATH] == PATH_MFMA16 ? kM16Waves : kFwdWaves;
   a.hpw = 1;
-  for (int g = kFwdWaves; g >= 1; g--)
-    if (a.group % g == 0 && kFwdWaves % g == 0) { a.hpw = g; break; }
+  for (int g = waves; g >= 1; g--)
+    if (a.group % g == 0 && waves % g == 0) { a.hpw = g; break; }
   a.total_q = ph[PF_TOTAL_Q];
   a.total_prefix = ph[PF_TOTAL_PREFIX];
   a.max_depth = ph[PF_MAX_DEPTH];
@@ -99,7 +104,7 @@ namespace {
 // floats of one stat row set of the MFMA backward ([Hq, Tq] padded to a
 // multiple of 64, so every area after it stays 256-byte aligned)
 size_t stat_row_floats(const int32_t* ph) {
-  if (ph[PF_PATH] != PATH_MFMA || ph[PF_TOTAL_Q] <= 0) return 0;
+  if (ph[PF_PATH] == PATH_SIMT || ph[PF_TOTAL_Q] <= 0) return 0;
   const size_t rows = static_cast<size_t>(ph[PF_HQ]) * static_cast<size_t>(ph[PF_TOTAL_Q]);
   return (rows + 63) / 64 * 64;
 }
@@ -114,8 +119,8 @@ size_t stat_floats(const int32_t* ph) {
 extern "C" size_t tpr_attn_bwd_workspace_bytes(const int32_t* plan_host) {
   if (!plan_host || plan_host[PF_MAGIC] != kPlanMagic) return 0;
   const size_t slots = static_cast<size_t>(plan_host[PF_N_SLOTS]);
-  return (stat_floats(plan_host) +
-          slots * static_cast<size_t>(kDkdvKeys) * static_cast<size_t>(plan_host[PF_D]) * 2) * sizeof(float);
+  const size_t keys = plan_host[PF_PATH] == PATH_MFMA16 ? kM16Keys : kDkdvKeys;  // keys per partial slot
+  return (stat_floats(plan_host) + slots * keys * static_cast<size_t>(plan_host[PF_D]) * 2) * sizeof(float);
 }
 
 extern "C" int tpr_attn_fwd(const TprFwdParams* p, void* stream) {
@@ -128,7 +133,7 @@ extern "C" int tpr_attn_fwd(const TprFwdParams* p, void* stream) {
   if (rc) return rc;
   if ((rc = check_scale(p->softmax_scale))) return rc;
   const int32_t* ph = p->plan_host;
-  const bool mfma = ph[PF_PATH] == PATH_MFMA;
+  const bool mfma = ph[PF_PATH] != PATH_SIMT;  // either MFMA family: 16-byte aligned rows
   const bool any_q = ph[PF_TOTAL_Q] > 0, any_p = ph[PF_TOTAL_PREFIX] > 0;
   if ((rc = check_tensor(p->q, "q", any_q, mfma)) || (rc = check_tensor(p->k, "k", any_q, mfma)) ||
       (rc = check_tensor(p->v, "v", any_q, mfma)) || (rc = check_tensor(p->out, "out", any_q, mfma)) ||
@@ -146,7 +151,9 @@ extern "C" int tpr_attn_fwd(const TprFwdParams* p, void* stream) {
   a.lse = p->lse;
   a.n_items = ph[PF_N_FWD];
   hipStream_t s = static_cast<hipStream_t>(stream);
-  rc = mfma ? launch_mfma_fwd(a, s) : launch_simt_fwd(a, ph[PF_DTYPE] == TPR_DTYPE_FP32, s);
+  rc = ph[PF_PATH] == PATH_MFMA     ? launch_mfma_fwd(a, s)
+       : ph[PF_PATH] == PATH_MFMA16 ? launch_m16_fwd(a, s)
+                                    : launch_simt_fwd(a, ph[PF_DTYPE] == TPR_DTYPE_FP32, s);
   if (rc) return fail(TPR_ERR_LAUNCH, "forward launch failed: %s", hipGetErrorString(hipGetLastError()));
   return TPR_OK;
 }
@@ -173,7 +180,8 @@ int bwd_phases(const TprBwdParams* p, int phases, void* stream, void* workspace,
   if (p->flags & ~TPR_BWD_ACCUMULATE_PREFIX_F32)
     return fail(TPR_ERR_INVALID_ARGUMENT, "flags must be 0 or TPR_BWD_ACCUMULATE_PREFIX_F32, got %d", p->flags);
   const int32_t* ph = p->plan_host;
-  const bool mfma = ph[PF_PATH] == PATH_MFMA;
+  const int path = ph[PF_PATH];
+  const bool mfma = path != PATH_SIMT;  // either MFMA family: 16-byte aligned rows
   const bool any_q = ph[PF_TOTAL_Q] > 0, any_p = ph[PF_TOTAL_PREFIX] > 0;
   if ((rc = check_tensor(p->q, "q", any_q, mfma)) || (rc = check_tensor(p->k, "k", any_q, mfma)) ||
       (rc = check_tensor(p->v, "v", any_q, mfma)) || (rc = check_tensor(p->out, "out", any_q, mfma)) ||
@@ -216,9 +224,13 @@ int bwd_phases(const TprBwdParams* p, int phases, void* stream, void* workspace,
   const int n_dkdv = (phases & (TPR_BWD_DKDV | TPR_BWD_DKDV_TILES)) ? ph[PF_N_DKDV] : 0;
   const int n_red = (phases & (TPR_BWD_DKDV | TPR_BWD_DKDV_REDUCE)) ? ph[PF_N_RED] : 0;  // 0 on the SIMT path
   const int n_dq = (phases & TPR_BWD_DQ) ? ph[PF_N_FWD] : 0;
-  rc = (phases & TPR_BWD_DELTA) ? (mfma ? launch_mfma_delta(a, s) : launch_delta(a, fp32, s)) : 0;
+  if (phases & TPR_BWD_DELTA)
+    rc = path == PATH_MFMA ? launch_mfma_delta(a, s) : path == PATH_MFMA16 ? launch_m16_delta(a, s)
+                                                                          : launch_delta(a, fp32, s);
   if (!rc && (n_dkdv || n_red || n_dq))
-    rc = mfma ? launch_mfma_bwd(a, n_dq, n_dkdv, n_red, s) : launch_simt_bwd(a, n_dq, n_dkdv, fp32, s);
+    rc = path == PATH_MFMA     ? launch_mfma_bwd(a, n_dq, n_dkdv, n_red, s)
+         : path == PATH_MFMA16 ? launch_m16_bwd(a, n_dq, n_dkdv, n_red, s)
+                               : launch_simt_bwd(a, n_dq, n_dkdv, fp32, s);
   if (rc) return fail(TPR_ERR_LAUNCH, "backward launch failed: %s", hipGetErrorString(hipGetLastError()));
   return TPR_OK;
 }

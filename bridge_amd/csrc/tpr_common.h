@@ -49,8 +49,9 @@ enum PlanField : int {
 };
 
 enum KernelPath : int32_t {
-  PATH_SIMT = 0,  // fp32-accumulate SIMT kernels (fp32, or bf16 with head_dim != 128)
-  PATH_MFMA = 1   // bf16 MFMA kernels, head_dim 128
+  PATH_SIMT = 0,    // fp32-accumulate SIMT kernels (fp32, or bf16 with another head_dim)
+  PATH_MFMA = 1,    // bf16 MFMA kernels, head_dim 128 (32x32x16 MFMA)
+  PATH_MFMA16 = 2   // bf16 MFMA kernels, head_dim 64 or 256 (16x16x32 MFMA)
 };
 
 // dK/dV work item: one (KV segment tile, KV head) and the query blocks that see it.
@@ -101,6 +102,10 @@ constexpr int kPlanCus = 256;         // compute units the dK/dV work is balance
 // 0) that rows past a query block's end are copied from, then lse * log2e per
 // (query head, token) in the lse layout, then -delta in the same layout.
 constexpr int kStatRowsOffset = 64;   // floats before the lse*log2e rows
+// MFMA16 family (bf16, head_dim 64 and 256)
+constexpr int kM16Waves = 4;          // waves per workgroup (all kernels)
+constexpr int kM16Tokens = 32;        // forward / dQ tokens per wave (two 16-query sub-blocks)
+constexpr int kM16Keys = 16 * kM16Waves;  // keys per dK/dV workgroup (16 per wave)
 constexpr int kMfmaRegRuns = 8;       // key runs a forward / dQ workgroup holds in registers; a
                                       // launch with longer run lists reads them from the plan
 

@@ -1,0 +1,810 @@
+// tpr_mfma16.hip -- gfx950 bf16 MFMA prefix-reuse attention kernels for head_dim
+// 64 and 256 (v_mfma_f32_16x16x32_bf16).
+//
+// Same math, key streams, work lists and fixed-order sibling sum as the
+// head_dim-128 family (tpr_mfma.hip); the tiling is built on the 16-wide MFMA
+// so that head_dim 256 fits the register file: a forward / dQ wave owns 32
+// query tokens of one head as two 16-query sub-blocks, a dK/dV wave owns 16
+// keys. One wave per SIMD, 4 waves per workgroup; K/V (forward, dQ) and Q/dO
+// (dK/dV) tiles of 64 rows are staged in LDS by the gfx950 DMA, double
+// buffered, one workgroup barrier per tile.
+//
+// MFMA layout (measured on gfx950): A lane l holds row l%16, k-slots
+// 8*(l/16)+i; B lane l holds column l%16, the same k-slots; result register r
+// of lane l holds (row 4*(l/16) + r, column l%16).
+//
+// Score tiles are computed with the 64 rows of a tile (keys in the forward
+// and dQ, queries in dK/dV) permuted inside each 32-row half: accumulator block
+// b (16 rows) row m = 4g + r holds tile row 32(b/2) + 8g + 4(b%2) + r. Lane l
+// (g = l/16) then holds, over blocks 2t and 2t+1, the 8 consecutive tile rows
+// 32t + 8g + 0..7 of its column -- exactly the k-slots the next MFMA (P.V,
+// dS.K, P^T.dO, dS^T.Q) reads as an operand from registers.
+//
+// LDS tiles are row-major, 2*D bytes per row, with the 16-byte chunk index
+// XOR-swizzled by the row (row % 16 for D = 256, (row / 2) % 8 for D = 64) so
+// that the row reads of 16 consecutive (permuted) rows and the transposed
+// reads (ds_read_tr16_b64) spread over the banks.
+
+#include "tpr_kernel_util.h"
+
+namespace tpr {
+namespace {
+
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4_m16;
+
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+template <int kD>
+struct Geo {
+  static_assert(kD == 64 || kD == 256, "the 16-wide family serves head_dim 64 and 256");
+  static constexpr int RB = 2 * kD;              // bytes per tile row
+  static constexpr int NC = kD / 8;              // 16-byte chunks per row
+  static constexpr int TB = kTileRows * RB;      // bytes per 64-row tile
+  static constexpr int NS = kD / 32;             // 32-wide k-steps over head_dim
+  static constexpr int ND = kD / 16;             // 16-wide head_dim blocks
+  static constexpr int RPB = 1024 / RB;          // tile rows per 1 KiB DMA block
+  static constexpr int BPW = TB / 1024 / kM16Waves;  // DMA blocks per wave per tile
+  __device__ static __forceinline__ int swz(int row) { return kD == 256 ? (row & 15) : ((row >> 1) & 7); }
+  // byte offset of element (row, col) of a swizzled tile
+  __device__ static __forceinline__ uint32_t off(int row, int col) {
+    return static_cast<uint32_t>(row * RB + (((col >> 3) ^ swz(row)) << 4) + ((col & 7) << 1));
+  }
+};
+
+// tile row of accumulator block b, row m (see the file comment)
+__device__ __forceinline__ int perm_row(int b, int m) { return 32 * (b >> 1) + 8 * (m >> 2) + 4 * (b & 1) + (m & 3); }
+
+// Row read: the A operand rows 16..31 of a 32-wide k-step s of block b: lane
+// l reads tile row perm_row(b, l % 16), columns 32 s + 8 (l / 16) .. +7.
+template <int kD>
+__device__ __forceinline__ bf16x8 row_operand(const char* tile, int b, int s, int lane) {
+  const int row = perm_row(b, lane & 15);
+  return *reinterpret_cast<const bf16x8*>(tile + Geo<kD>::off(row, 32 * s + 8 * (lane >> 4)));
+}
+
+// Transposed read: the operand whose lane l holds column c0 + l % 16 and the 8
+// consecutive tile rows r0 + 8 (l / 16) .. +7 (two ds_read_tr16_b64: lane i of
+// each 16-lane group addresses row r0 + 8 g + i / 4 (+ 4), columns
+// c0 + 4 (i % 4) .. +3, and receives column c0 + i of the group's 4 rows).
+template <int kD>
+__device__ __forceinline__ bf16x8 col_operand(const char* tile, int r0, int c0, int lane) {
+  const int i = lane & 15, g = lane >> 4;
+  const int row = r0 + 8 * g + (i >> 2), col = c0 + 4 * (i & 3);
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_m16*)(tile + Geo<kD>::off(row, col)));
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_m16*)(tile + Geo<kD>::off(row + 4, col)));
+  const bf16x4 l4 = __builtin_bit_cast(bf16x4, lo), h4 = __builtin_bit_cast(bf16x4, hi);
+  bf16x8 r;
+  r[0] = l4[0]; r[1] = l4[1]; r[2] = l4[2]; r[3] = l4[3];
+  r[4] = h4[0]; r[5] = h4[1]; r[6] = h4[2]; r[7] = h4[3];
+  return r;
+}
+
+// Copy rows [0, 64) of the tile whose row 0 is at `src` (uniform; rows at or
+// beyond `len` re-read row len - 1; row stride `stride` bytes) into the
+// swizzled LDS tile at `lds_tile`: this wave's BPW 1 KiB blocks. Lane l of
+// block b lands at physical chunk l % NC of tile row b*RPB + l/NC, so it
+// fetches the logical chunk that swizzles there.
+template <int kD>
+__device__ __forceinline__ void copy_tile(const char* src, uint32_t stride, int len, uint32_t lds_tile, int wave,
+                                          int lane) {
+  using T = Geo<kD>;
+#pragma unroll
+  for (int j = 0; j < T::BPW; j++) {
+    const int b = wave * T::BPW + j;
+    const int row = b * T::RPB + lane / T::NC;
+    const int chunk = (lane % T::NC) ^ T::swz(row);
+    const uint32_t voff = static_cast<uint32_t>(min(row, len - 1)) * stride + 16u * chunk;
+    dma16s(src, voff, lds_tile + b * 1024);
+  }
+}
+
+// bf16x8 operand from two accumulator blocks: [x[0..3], y[0..3]]
+__device__ __forceinline__ bf16x8 pack8(const float (&x)[4], const float (&y)[4]) {
+  bf16x8 r;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    r[i] = static_cast<bf16>(x[i]);
+    r[4 + i] = static_cast<bf16>(y[i]);
+  }
+  return r;
+}
+
+__device__ __forceinline__ float xmax16(float x) {  // max over lanes l, l^16, l^32, l^48
+  x = fmaxf(x, __shfl_xor(x, 16));
+  return fmaxf(x, __shfl_xor(x, 32));
+}
+__device__ __forceinline__ float xsum16(float x) {
+  x += __shfl_xor(x, 16);
+  return x + __shfl_xor(x, 32);
+}
+
+constexpr float kSlack16 = 8.f;  // lazy-rescale slack in log2 units (as the head_dim-128 forward)
+
+// ---------------------------------------------------------------------------
+// Forward. Wave w: query head qh0 + w % hpw, tokens tw0 .. tw0 + 31 as two
+// 16-query sub-blocks qs. Per 64-key tile: S^T (4 blocks of 16 keys x 16
+// queries per sub-block) = K Q^T with K rows from LDS (A) and Q in registers
+// (B); online softmax in registers (lane l holds 16 keys of query l % 16; the
+// other 48 keys of the tile sit in lanes l ^ 16, l ^ 32, l ^ 48); then
+// O^T += V^T P^T with V^T read transposed from LDS (A) and P^T from registers.
+// ---------------------------------------------------------------------------
+template <int kD, bool kRunList>
+__global__ __launch_bounds__(256) void m16_fwd(KernelArgs a) {
+  using T = Geo<kD>;
+  const int32_t* item = a.plan + a.off_fwd + 4 * blockIdx.x;
+  const int leaf = item[0];
+  if (leaf < 0) return;
+  const int tok0 = item[1], qh0 = item[2], kvh = item[3];
+  const int32_t* cu = a.plan + a.off_cu;
+  const int row0 = cu[leaf], len = cu[leaf + 1] - cu[leaf];
+
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hpw = a.hpw;
+  const int head = qh0 + wave % hpw;
+  const int tw0 = tok0 + kM16Tokens * (wave / hpw);
+  const int tpw = kM16Tokens * (kM16Waves / hpw);
+  const int suffix_keys = min(len, tok0 + tpw);
+  const int i16 = lane & 15, g = lane >> 4;
+
+  const int64_t qstride = static_cast<int64_t>(a.hq) * kD;
+  const uint32_t row_bytes = static_cast<uint32_t>(a.hkv) * kD * 2;
+  __shared__ __attribute__((aligned(1024))) char smem[4 * T::TB];  // K0 K1 V0 V1
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(smem));
+  const char* kbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.k) + kvh * kD);
+  const char* vbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.v) + kvh * kD);
+  const char* pkbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.pk) + kvh * kD);
+  const char* pvbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.pv) + kvh * kD);
+  auto kv_src = [&](const TileLoc& x, bool is_k) {
+    const char* b = x.suffix ? (is_k ? kbase : vbase) : (is_k ? pkbase : pvbase);
+    return b + x.row * static_cast<int64_t>(row_bytes);
+  };
+
+  const auto seg = load_keys<kRunList>(a, leaf, suffix_keys);
+  const int ntiles = seg.ntiles;
+  Cursor cc = cursor_begin(seg);  // the tile being copied
+  TileLoc tl_c = cursor_tile(cc);
+  Cursor mc = cursor_begin(seg);  // the tile being computed
+  TileLoc tl = cursor_tile(mc);
+  copy_tile<kD>(kv_src(tl_c, true), row_bytes, tl_c.len, lds0, wave, lane);
+  copy_tile<kD>(kv_src(tl_c, false), row_bytes, tl_c.len, lds0 + 2 * T::TB, wave, lane);
+
+  // Q of the lane's query l % 16 of each sub-block: the B operand of S^T
+  bf16x8 qv[2][T::NS];
+#pragma unroll
+  for (int qs = 0; qs < 2; qs++) {
+    const int t = min(tw0 + 16 * qs + i16, len - 1);
+    const bf16* qp = static_cast<const bf16*>(a.q) + static_cast<int64_t>(row0 + t) * qstride + head * kD + 8 * g;
+#pragma unroll
+    for (int s = 0; s < T::NS; s++) qv[qs][s] = *reinterpret_cast<const bf16x8*>(qp + 32 * s);
+  }
+  f32x4 o[2][T::ND];
+#pragma unroll
+  for (int qs = 0; qs < 2; qs++)
+#pragma unroll
+    for (int db = 0; db < T::ND; db++) o[qs][db] = f32x4{};
+  float m[2] = {-1e30f, -1e30f}, l[2] = {0.f, 0.f};  // running max (raw score units), lane-partial sum
+  const float c2 = a.scale * kLog2e;
+  const float slack = kSlack16 / c2;
+
+#pragma unroll
+  for (int qs = 0; qs < 2; qs++)
+#pragma unroll
+    for (int s = 0; s < T::NS; s++) settle(qv[qs][s]);
+  wait_dma();
+  __syncthreads();
+
+  for (int j = 0; j < ntiles; j++) {
+    const int buf = j & 1;
+    if (j + 1 < ntiles) {  // copy tile j+1 into the other buffer (read by tile j-1, released by the last barrier)
+      cursor_next(seg, cc);
+      tl_c = cursor_tile(cc);
+      copy_tile<kD>(kv_src(tl_c, true), row_bytes, tl_c.len, lds0 + (1 - buf) * T::TB, wave, lane);
+      copy_tile<kD>(kv_src(tl_c, false), row_bytes, tl_c.len, lds0 + (3 - buf) * T::TB, wave, lane);
+    }
+    const char* kt = smem + buf * T::TB;
+    const char* vt = smem + (2 + buf) * T::TB;
+
+    float sv[2][4][4];  // [sub-block][key block][register]
+    {
+      f32x4 sa[2][4];
+#pragma unroll
+      for (int qs = 0; qs < 2; qs++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) sa[qs][b] = f32x4{};
+#pragma unroll
+      for (int s = 0; s < T::NS; s++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+          const bf16x8 kop = row_operand<kD>(kt, b, s, lane);
+#pragma unroll
+          for (int qs = 0; qs < 2; qs++) sa[qs][b] = mfma16(kop, qv[qs][s], sa[qs][b]);
+        }
+#pragma unroll
+      for (int qs = 0; qs < 2; qs++)
+#pragma unroll
+        for (int b = 0; b < 4; b++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) sv[qs][b][r] = sa[qs][b][r];
+    }
+    // mask: register r of key block b holds key 32 (b/2) + 8 g + 4 (b%2) + r of the tile
+    const bool partial = tl.len < kTileRows || (tl.suffix && tl.pos0 + kTileRows - 1 > tw0);
+    if (partial) {
+#pragma unroll
+      for (int qs = 0; qs < 2; qs++) {
+        const int t = tw0 + 16 * qs + i16;
+        int lim = tl.len - 1;
+        if (tl.suffix) lim = min(lim, t - tl.pos0);
+#pragma unroll
+        for (int b = 0; b < 4; b++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            const int key = 32 * (b >> 1) + 8 * g + 4 * (b & 1) + r;
+            sv[qs][b][r] = key <= lim ? sv[qs][b][r] : -INFINITY;
+          }
+      }
+    }
+    bf16x8 pb[2][2];
+#pragma unroll
+    for (int qs = 0; qs < 2; qs++) {
+      float mt = sv[qs][0][0];
+#pragma unroll
+      for (int b = 0; b < 4; b++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) mt = fmaxf(mt, sv[qs][b][r]);
+      mt = xmax16(mt);
+      if (__any(mt > m[qs] + slack)) {  // some query outgrew its reference max: rescale
+        const float m_new = fmaxf(m[qs], mt);
+        const float alpha = fast_exp2((m[qs] - m_new) * c2);
+        m[qs] = m_new;
+        l[qs] *= alpha;
+#pragma unroll
+        for (int db = 0; db < T::ND; db++) o[qs][db] *= alpha;
+      }
+      const float mc2 = m[qs] * c2;
+      float pf[4][4];
+      float ls = 0.f;
+#pragma unroll
+      for (int b = 0; b < 4; b++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          pf[b][r] = fast_exp2(fmaf(sv[qs][b][r], c2, -mc2));
+          ls += pf[b][r];
+        }
+      l[qs] += ls;
+      pb[qs][0] = pack8(pf[0], pf[1]);
+      pb[qs][1] = pack8(pf[2], pf[3]);
+    }
+    // O^T += V^T P^T: A = V^T (16 head dims x 32 keys of step t), B = P^T
+#pragma unroll
+    for (int db = 0; db < T::ND; db++)
+#pragma unroll
+      for (int t = 0; t < 2; t++) {
+        const bf16x8 vop = col_operand<kD>(vt, 32 * t, 16 * db, lane);
+#pragma unroll
+        for (int qs = 0; qs < 2; qs++) o[qs][db] = mfma16(vop, pb[qs][t], o[qs][db]);
+      }
+    if (j + 1 < ntiles) {
+      cursor_next(seg, mc);
+      tl = cursor_tile(mc);
+    }
+    wait_dma();
+    __syncthreads();
+  }
+
+  // O^T register r of block db: head dim 16 db + 4 g + r of query l % 16
+#pragma unroll
+  for (int qs = 0; qs < 2; qs++) {
+    const float lt = xsum16(l[qs]);
+    const int t = tw0 + 16 * qs + i16;
+    if (tw0 + 16 * qs >= len || t >= len) continue;
+    const float inv = 1.f / lt;
+    bf16* op = static_cast<bf16*>(a.out) + static_cast<int64_t>(row0 + t) * qstride + head * kD + 4 * g;
+#pragma unroll
+    for (int db = 0; db < T::ND; db++) {
+      bf16x4 v4;
+#pragma unroll
+      for (int r = 0; r < 4; r++) v4[r] = static_cast<bf16>(o[qs][db][r] * inv);
+      *reinterpret_cast<bf16x4*>(op + 16 * db) = v4;
+    }
+    if (g == 0) a.lse[static_cast<int64_t>(head) * a.total_q + row0 + t] = m[qs] * a.scale + logf(lt);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// delta = rowsum(dO * O) per (token, head); also the stat rows the dK/dV kernel
+// copies: -lse*log2e, -delta, and the constants (-inf, 0) of rows past a
+// query block's end. 16 lanes per row.
+// ---------------------------------------------------------------------------
+template <int kD>
+__global__ __launch_bounds__(256) void m16_delta(KernelArgs a) {
+  const int64_t rows = static_cast<int64_t>(a.total_q) * a.hq;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 16 + (threadIdx.x >> 4);
+  const int c = threadIdx.x & 15;
+  float s = 0.f;
+  if (row < rows) {
+#pragma unroll
+    for (int k = 0; k < kD / 128 + (kD < 128 ? 1 : 0); k++) {
+      const int col = kD >= 128 ? 128 * k + 8 * c : 4 * c;
+      if (kD >= 128) {
+        const bf16x8 o = *reinterpret_cast<const bf16x8*>(static_cast<const bf16*>(a.out_in) + row * kD + col);
+        const bf16x8 d = *reinterpret_cast<const bf16x8*>(static_cast<const bf16*>(a.dout) + row * kD + col);
+#pragma unroll
+        for (int i = 0; i < 8; i++) s = fmaf(static_cast<float>(o[i]), static_cast<float>(d[i]), s);
+      } else {
+        const bf16x4 o = *reinterpret_cast<const bf16x4*>(static_cast<const bf16*>(a.out_in) + row * kD + col);
+        const bf16x4 d = *reinterpret_cast<const bf16x4*>(static_cast<const bf16*>(a.dout) + row * kD + col);
+#pragma unroll
+        for (int i = 0; i < 4; i++) s = fmaf(static_cast<float>(o[i]), static_cast<float>(d[i]), s);
+      }
+    }
+  }
+  s += __shfl_xor(s, 8);
+  s += __shfl_xor(s, 4);
+  s += __shfl_xor(s, 2);
+  s += __shfl_xor(s, 1);
+  if (c == 0 && row < rows) {
+    const int64_t at = (row % a.hq) * a.total_q + row / a.hq;
+    a.delta[at] = s;
+    a.stat_ws[kStatRowsOffset + at] = -(a.lse_in[at] * kLog2e);
+    a.ndelta_ws[at] = -s;
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    a.stat_ws[0] = -INFINITY;
+    a.stat_ws[1] = 0.f;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dQ. Same workgroup shape and key stream as the forward. Per 64-key tile:
+// S^T = K Q^T and dP^T = V dO^T (K, V rows from LDS; Q, dO in registers),
+// P = exp2(scale*log2e S - lse*log2e), dS = P (dP - delta), then
+// dQ^T += K^T dS^T with K^T read transposed from the K tile.
+// ---------------------------------------------------------------------------
+template <int kD, bool kRunList>
+__global__ __launch_bounds__(256) void m16_dq(KernelArgs a) {
+  using T = Geo<kD>;
+  const int32_t* item = a.plan + a.off_fwd + 4 * blockIdx.x;
+  const int leaf = item[0];
+  if (leaf < 0) return;
+  const int tok0 = item[1], qh0 = item[2], kvh = item[3];
+  const int32_t* cu = a.plan + a.off_cu;
+  const int row0 = cu[leaf], len = cu[leaf + 1] - cu[leaf];
+
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hpw = a.hpw;
+  const int head = qh0 + wave % hpw;
+  const int tw0 = tok0 + kM16Tokens * (wave / hpw);
+  const int tpw = kM16Tokens * (kM16Waves / hpw);
+  const int suffix_keys = min(len, tok0 + tpw);
+  const int i16 = lane & 15, g = lane >> 4;
+
+  const int64_t qstride = static_cast<int64_t>(a.hq) * kD;
+  const uint32_t row_bytes = static_cast<uint32_t>(a.hkv) * kD * 2;
+  __shared__ __attribute__((aligned(1024))) char smem[4 * T::TB];  // K0 K1 V0 V1
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(smem));
+  const char* kbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.k) + kvh * kD);
+  const char* vbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.v) + kvh * kD);
+  const char* pkbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.pk) + kvh * kD);
+  const char* pvbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.pv) + kvh * kD);
+  auto kv_src = [&](const TileLoc& x, bool is_k) {
+    const char* b = x.suffix ? (is_k ? kbase : vbase) : (is_k ? pkbase : pvbase);
+    return b + x.row * static_cast<int64_t>(row_bytes);
+  };
+
+  const auto seg = load_keys<kRunList>(a, leaf, suffix_keys);
+  const int ntiles = seg.ntiles;
+  Cursor cc = cursor_begin(seg);
+  TileLoc tl_c = cursor_tile(cc);
+  Cursor mc = cursor_begin(seg);
+  TileLoc tl = cursor_tile(mc);
+  copy_tile<kD>(kv_src(tl_c, true), row_bytes, tl_c.len, lds0, wave, lane);
+  copy_tile<kD>(kv_src(tl_c, false), row_bytes, tl_c.len, lds0 + 2 * T::TB, wave, lane);
+
+  bf16x8 qv[2][T::NS], gv[2][T::NS];
+  float lse2[2], delta[2];
+#pragma unroll
+  for (int qs = 0; qs < 2; qs++) {
+    const int t = min(tw0 + 16 * qs + i16, len - 1);
+    const int64_t off = static_cast<int64_t>(row0 + t) * qstride + head * kD + 8 * g;
+#pragma unroll
+    for (int s = 0; s < T::NS; s++) {
+      qv[qs][s] = *reinterpret_cast<const bf16x8*>(static_cast<const bf16*>(a.q) + off + 32 * s);
+      gv[qs][s] = *reinterpret_cast<const bf16x8*>(static_cast<const bf16*>(a.dout) + off + 32 * s);
+    }
+    const int64_t at = static_cast<int64_t>(head) * a.total_q + row0 + t;
+    lse2[qs] = a.lse_in[at] * kLog2e;
+    delta[qs] = a.delta[at];
+  }
+  f32x4 dq[2][T::ND];
+#pragma unroll
+  for (int qs = 0; qs < 2; qs++)
+#pragma unroll
+    for (int db = 0; db < T::ND; db++) dq[qs][db] = f32x4{};
+  const float c2 = a.scale * kLog2e;
+
+#pragma unroll
+  for (int qs = 0; qs < 2; qs++) {
+#pragma unroll
+    for (int s = 0; s < T::NS; s++) {
+      settle(qv[qs][s]);
+      settle(gv[qs][s]);
+    }
+    settle(lse2[qs]);
+    settle(delta[qs]);
+  }
+  wait_dma();
+  __syncthreads();
+
+  for (int j = 0; j < ntiles; j++) {
+    const int buf = j & 1;
+    if (j + 1 < ntiles) {
+      cursor_next(seg, cc);
+      tl_c = cursor_tile(cc);
+      copy_tile<kD>(kv_src(tl_c, true), row_bytes, tl_c.len, lds0 + (1 - buf) * T::TB, wave, lane);
+      copy_tile<kD>(kv_src(tl_c, false), row_bytes, tl_c.len, lds0 + (3 - buf) * T::TB, wave, lane);
+    }
+    const char* kt = smem + buf * T::TB;
+    const char* vt = smem + (2 + buf) * T::TB;
+
+    float sv[2][4][4], pv[2][4][4];
+    {
+      f32x4 sa[2][4], pa[2][4];
+#pragma unroll
+      for (int qs = 0; qs < 2; qs++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+          sa[qs][b] = f32x4{};
+          pa[qs][b] = f32x4{};
+        }
+#pragma unroll
+      for (int s = 0; s < T::NS; s++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+          const bf16x8 kop = row_operand<kD>(kt, b, s, lane);
+          const bf16x8 vop = row_operand<kD>(vt, b, s, lane);
+#pragma unroll
+          for (int qs = 0; qs < 2; qs++) {
+            sa[qs][b] = mfma16(kop, qv[qs][s], sa[qs][b]);
+            pa[qs][b] = mfma16(vop, gv[qs][s], pa[qs][b]);
+          }
+        }
+#pragma unroll
+      for (int qs = 0; qs < 2; qs++)
+#pragma unroll
+        for (int b = 0; b < 4; b++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            sv[qs][b][r] = sa[qs][b][r];
+            pv[qs][b][r] = pa[qs][b][r];
+          }
+    }
+    const bool partial = tl.len < kTileRows || (tl.suffix && tl.pos0 + kTileRows - 1 > tw0);
+    bf16x8 dsb[2][2];
+#pragma unroll
+    for (int qs = 0; qs < 2; qs++) {
+      const int t = tw0 + 16 * qs + i16;
+      int lim = tl.len - 1;
+      if (tl.suffix) lim = min(lim, t - tl.pos0);
+      float df[4][4];
+#pragma unroll
+      for (int b = 0; b < 4; b++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const int key = 32 * (b >> 1) + 8 * g + 4 * (b & 1) + r;
+          float x = fmaf(sv[qs][b][r], c2, -lse2[qs]);
+          if (partial) x = key <= lim ? x : -INFINITY;
+          df[b][r] = fast_exp2(x) * (pv[qs][b][r] - delta[qs]);
+        }
+      dsb[qs][0] = pack8(df[0], df[1]);
+      dsb[qs][1] = pack8(df[2], df[3]);
+    }
+    // dQ^T += K^T dS^T: A = K^T (16 head dims x 32 keys of step t), B = dS^T
+#pragma unroll
+    for (int db = 0; db < T::ND; db++)
+#pragma unroll
+      for (int t = 0; t < 2; t++) {
+        const bf16x8 kop = col_operand<kD>(kt, 32 * t, 16 * db, lane);
+#pragma unroll
+        for (int qs = 0; qs < 2; qs++) dq[qs][db] = mfma16(kop, dsb[qs][t], dq[qs][db]);
+      }
+    if (j + 1 < ntiles) {
+      cursor_next(seg, mc);
+      tl = cursor_tile(mc);
+    }
+    wait_dma();
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int qs = 0; qs < 2; qs++) {
+    const int t = tw0 + 16 * qs + i16;
+    if (tw0 + 16 * qs >= len || t >= len) continue;
+    bf16* dp = static_cast<bf16*>(a.dq) + static_cast<int64_t>(row0 + t) * qstride + head * kD + 4 * g;
+#pragma unroll
+    for (int db = 0; db < T::ND; db++) {
+      bf16x4 v4;
+#pragma unroll
+      for (int r = 0; r < 4; r++) v4[r] = static_cast<bf16>(dq[qs][db][r] * a.scale);
+      *reinterpret_cast<bf16x4*>(dp + 16 * db) = v4;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dK/dV. One workgroup = 4 waves x 16 keys of one KV segment tile (64 keys)
+// and KV head; it streams every 64-query block that sees the tile -- for a
+// prefix node every descendant leaf and every query head of the group -- in
+// the plan's fixed order, so a prefix node's gradient is the sum over its
+// leaves in registers, without atomics. Per stage (one block, one head):
+//   S = Q K^T, dP = dO V^T (Q, dO rows from LDS, permuted; K, V in registers),
+//   P = exp2(scale*log2e S - lse*log2e), dS = P (dP - delta),
+//   dV += P^T dO, dK += dS^T Q (dO, Q read transposed from LDS).
+// ---------------------------------------------------------------------------
+template <int kD>
+__global__ __launch_bounds__(256) void m16_dkdv(KernelArgs a) {
+  using T = Geo<kD>;
+  const int32_t* item = a.plan + a.off_dkdv + DK_WORDS * blockIdx.x;
+  if (item[DK_SRC] < 0) return;
+  const bool prefix = item[DK_SRC] == 0;
+  const int seg = item[DK_SEG], key0 = item[DK_KEY0], kvh = item[DK_KVH];
+  const int qb_lo = item[DK_QB_LO], qb_hi = item[DK_QB_HI];
+  const int32_t* cu = a.plan + a.off_cu;
+  const int32_t* no = a.plan + a.off_node_off;
+  const int32_t* qblk = a.plan + a.off_qblk;
+  const int seg_row0 = prefix ? no[seg] : cu[seg];
+  const int seg_len = prefix ? no[seg + 1] - no[seg] : cu[seg + 1] - cu[seg];
+
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int i16 = lane & 15, g = lane >> 4;
+  const int kw0 = key0 + 16 * wave;  // first key position of this wave
+  const int kp = kw0 + i16;          // this lane's key (B-operand column)
+  const bool wave_active = kw0 < seg_len;
+
+  const int64_t qstride = static_cast<int64_t>(a.hq) * kD;
+  const int64_t kstride = static_cast<int64_t>(a.hkv) * kD;
+  const uint32_t qrow_bytes = static_cast<uint32_t>(a.hq) * kD * 2;
+
+  __shared__ __attribute__((aligned(1024))) char smem[2 * 2 * T::TB];           // [buf][Q | dO]
+  __shared__ __attribute__((aligned(256))) float stats[2][2][kTileRows];       // [buf][-lse*log2e | -delta][row]
+  __shared__ int4 qtab[kDkdvMaxBlocks];
+  for (int i = threadIdx.x; i < qb_hi - qb_lo; i += blockDim.x) {
+    const int qb = qb_lo + i;
+    const int lf = qblk[2 * qb], tok = qblk[2 * qb + 1];
+    const int r0 = cu[lf];
+    qtab[i] = int4{r0 + tok, tok, min(kTileRows, cu[lf + 1] - r0 - tok), 0};
+  }
+  __syncthreads();
+
+  const int group = a.group;
+  const int nstage = (qb_hi - qb_lo) * group;  // stage s: query block s / group, head s % group
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(smem));
+  const uint32_t stats0 = __builtin_amdgcn_readfirstlane(lds_address(stats));
+  auto issue = [&](int blk, int hh, int buf) {
+    const int4 e = qtab[blk];
+    const int row = __builtin_amdgcn_readfirstlane(e.x), nq = __builtin_amdgcn_readfirstlane(e.z);
+    const int qh = kvh * group + hh;
+    const int64_t off = static_cast<int64_t>(qh) * kD * 2 + static_cast<int64_t>(row) * qrow_bytes;
+    const uint32_t tile = lds0 + buf * 2 * T::TB;
+    copy_tile<kD>(reinterpret_cast<const char*>(a.q) + off, qrow_bytes, nq, tile, wave, lane);
+    copy_tile<kD>(reinterpret_cast<const char*>(a.dout) + off, qrow_bytes, nq, tile + T::TB, wave, lane);
+    if (wave < 2) {  // wave 0: -lse*log2e, wave 1: -delta; rows past the block end copy -inf / 0
+      const int64_t at = static_cast<int64_t>(qh) * a.total_q + row + lane;
+      const float* rows = wave == 0 ? a.stat_ws + kStatRowsOffset : a.ndelta_ws;
+      dma4_lane(lane < nq ? rows + at : a.stat_ws + wave, stats0 + (buf * 2 + wave) * kTileRows * 4);
+    }
+  };
+  if (nstage > 0) issue(0, 0, 0);
+
+  // K / V of the lane's key kp: the B operands of S = Q K^T and dP = dO V^T
+  bf16x8 kv[T::NS], vv[T::NS];
+  {
+    const bf16* kb = static_cast<const bf16*>(prefix ? a.pk : a.k);
+    const bf16* vb = static_cast<const bf16*>(prefix ? a.pv : a.v);
+    const int64_t off = static_cast<int64_t>(seg_row0 + min(kp, seg_len - 1)) * kstride + kvh * kD + 8 * g;
+#pragma unroll
+    for (int s = 0; s < T::NS; s++) {
+      kv[s] = *reinterpret_cast<const bf16x8*>(kb + off + 32 * s);
+      vv[s] = *reinterpret_cast<const bf16x8*>(vb + off + 32 * s);
+    }
+  }
+  f32x4 dk[T::ND], dv[T::ND];  // register r of block db: key 4 g + r of the wave, head dim 16 db + l % 16
+#pragma unroll
+  for (int db = 0; db < T::ND; db++) {
+    dk[db] = f32x4{};
+    dv[db] = f32x4{};
+  }
+  const float c2 = a.scale * kLog2e;
+#pragma unroll
+  for (int s = 0; s < T::NS; s++) {
+    settle(kv[s]);
+    settle(vv[s]);
+  }
+  wait_dma();
+  __syncthreads();
+
+  for (int sidx = 0; sidx < nstage; sidx++) {
+    const int buf = sidx & 1;
+    const int blk = sidx / group;
+    if (sidx + 1 < nstage) issue((sidx + 1) / group, (sidx + 1) % group, buf ^ 1);
+    if (wave_active) {
+      const int tok0 = __builtin_amdgcn_readfirstlane(qtab[blk].y);
+      const char* qt = smem + buf * 2 * T::TB;
+      const char* gt = qt + T::TB;
+      const float* nlse = &stats[buf][0][0];
+      const float* ndel = &stats[buf][1][0];
+      // query q of the block visible from key kp iff kp <= tok0 + q (suffix tiles)
+      const bool diag = !prefix && tok0 < kw0 + 15;
+      float pf[4][4], df[4][4];  // [query block][register]: query 32 (b/2) + 8 g + 4 (b%2) + r
+#pragma unroll
+      for (int b = 0; b < 4; b++) {
+        f32x4 sa = f32x4{}, pa = f32x4{};
+#pragma unroll
+        for (int s = 0; s < T::NS; s++) {
+          sa = mfma16(row_operand<kD>(qt, b, s, lane), kv[s], sa);
+          pa = mfma16(row_operand<kD>(gt, b, s, lane), vv[s], pa);
+        }
+        const int q0 = 32 * (b >> 1) + 8 * g + 4 * (b & 1);
+        const f32x4 ls = *reinterpret_cast<const f32x4*>(nlse + q0);
+        const f32x4 dl = *reinterpret_cast<const f32x4*>(ndel + q0);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          float x = fmaf(sa[r], c2, ls[r]);
+          if (diag) x = kp <= tok0 + q0 + r ? x : -INFINITY;
+          pf[b][r] = fast_exp2(x);
+          df[b][r] = pf[b][r] * (pa[r] + dl[r]);
+        }
+      }
+      const bf16x8 pT[2] = {pack8(pf[0], pf[1]), pack8(pf[2], pf[3])};
+      const bf16x8 dT[2] = {pack8(df[0], df[1]), pack8(df[2], df[3])};
+#pragma unroll
+      for (int db = 0; db < T::ND; db++)
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+          dv[db] = mfma16(pT[t], col_operand<kD>(gt, 32 * t, 16 * db, lane), dv[db]);
+          dk[db] = mfma16(dT[t], col_operand<kD>(qt, 32 * t, 16 * db, lane), dk[db]);
+        }
+    }
+    wait_dma();  // stage sidx + 1 has landed
+    __syncthreads();
+  }
+
+  if (!wave_active) return;
+  const int slot = item[DK_SLOT];
+  if (slot >= 0) {  // split tile: fp32 partial [kM16Keys][kD] for dK (already scaled) then dV
+    float* pk = a.ws + static_cast<int64_t>(slot) * 2 * kM16Keys * kD;
+    float* pv = pk + kM16Keys * kD;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int key = 16 * wave + 4 * g + r;
+#pragma unroll
+      for (int db = 0; db < T::ND; db++) {
+        pk[key * kD + 16 * db + i16] = dk[db][r] * a.scale;
+        pv[key * kD + 16 * db + i16] = dv[db][r];
+      }
+    }
+    return;
+  }
+  if (prefix && a.acc_prefix) {
+#pragma clang fp contract(off)
+    float* dkf = static_cast<float*>(a.dpk);
+    float* dvf = static_cast<float*>(a.dpv);
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int key = kw0 + 4 * g + r;
+      if (key >= seg_len) continue;
+      const int64_t off = static_cast<int64_t>(seg_row0 + key) * kstride + kvh * kD + i16;
+#pragma unroll
+      for (int db = 0; db < T::ND; db++) {
+        dkf[off + 16 * db] += dk[db][r] * a.scale;
+        dvf[off + 16 * db] += dv[db][r];
+      }
+    }
+    return;
+  }
+  bf16* dkd = static_cast<bf16*>(prefix ? a.dpk : a.dk);
+  bf16* dvd = static_cast<bf16*>(prefix ? a.dpv : a.dv);
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int key = kw0 + 4 * g + r;
+    if (key >= seg_len) continue;
+    const int64_t off = static_cast<int64_t>(seg_row0 + key) * kstride + kvh * kD + i16;
+#pragma unroll
+    for (int db = 0; db < T::ND; db++) {
+      dkd[off + 16 * db] = static_cast<bf16>(dk[db][r] * a.scale);
+      dvd[off + 16 * db] = static_cast<bf16>(dv[db][r]);
+    }
+  }
+}
+
+// Second pass of split dK/dV tiles: the fp32 partial slots of one (segment
+// tile, KV head) summed in slot (= leaf) order, written once.
+template <int kD>
+__global__ __launch_bounds__(256) void m16_reduce(KernelArgs a) {
+  const int32_t* item = a.plan + a.off_red + RD_WORDS * blockIdx.x;
+  const bool prefix = item[RD_SRC] == 0;
+  const int seg = item[RD_SEG], key0 = item[RD_KEY0], kvh = item[RD_KVH];
+  const int slot0 = item[RD_SLOT0], nslots = item[RD_NSLOTS];
+  const int32_t* cu = a.plan + a.off_cu;
+  const int32_t* no = a.plan + a.off_node_off;
+  const int seg_row0 = prefix ? no[seg] : cu[seg];
+  const int keys = min(kM16Keys, (prefix ? no[seg + 1] - no[seg] : cu[seg + 1] - cu[seg]) - key0);
+  const int64_t kstride = static_cast<int64_t>(a.hkv) * kD;
+  bf16* dkd = static_cast<bf16*>(prefix ? a.dpk : a.dk);
+  bf16* dvd = static_cast<bf16*>(prefix ? a.dpv : a.dv);
+  const int64_t slot_floats = 2 * kM16Keys * kD;
+  for (int e = threadIdx.x; e < 2 * keys * (kD / 4); e += blockDim.x) {
+    const int which = e / (keys * (kD / 4));  // 0 = dK, 1 = dV
+    const int rem = e % (keys * (kD / 4));
+    const int key = rem / (kD / 4), d4 = rem % (kD / 4);
+    const float* src = a.ws + static_cast<int64_t>(slot0) * slot_floats + which * kM16Keys * kD + key * kD + 4 * d4;
+    f32x4 acc = *reinterpret_cast<const f32x4*>(src);
+    for (int j = 1; j < nslots; j++) acc += *reinterpret_cast<const f32x4*>(src + j * slot_floats);
+    const int64_t at = static_cast<int64_t>(seg_row0 + key0 + key) * kstride + kvh * kD + 4 * d4;
+    if (prefix && a.acc_prefix) {
+      f32x4* dst = reinterpret_cast<f32x4*>(static_cast<float*>(which ? a.dpv : a.dpk) + at);
+      *dst = *dst + acc;
+      continue;
+    }
+    bf16x4 o;
+#pragma unroll
+    for (int i = 0; i < 4; i++) o[i] = static_cast<bf16>(acc[i]);
+    *reinterpret_cast<bf16x4*>((which ? dvd : dkd) + at) = o;
+  }
+}
+
+template <int kD>
+int launch_fwd_d(const KernelArgs& a, hipStream_t s) {
+  if (a.n_items > 0) {
+    if (a.max_runs > kMfmaRegRuns)
+      hipLaunchKernelGGL((m16_fwd<kD, true>), dim3(a.n_items), dim3(64 * kM16Waves), 0, s, a);
+    else
+      hipLaunchKernelGGL((m16_fwd<kD, false>), dim3(a.n_items), dim3(64 * kM16Waves), 0, s, a);
+  }
+  return hipGetLastError() == hipSuccess ? 0 : 4;
+}
+
+template <int kD>
+int launch_bwd_d(const KernelArgs& a, int n_fwd, int n_dkdv, int n_red, hipStream_t s) {
+  if (n_dkdv > 0) {
+    hipLaunchKernelGGL((m16_dkdv<kD>), dim3(n_dkdv), dim3(64 * kM16Waves), 0, s, a);
+    if (hipGetLastError() != hipSuccess) return 4;
+  }
+  if (n_red > 0) {
+    hipLaunchKernelGGL((m16_reduce<kD>), dim3(n_red), dim3(256), 0, s, a);
+    if (hipGetLastError() != hipSuccess) return 4;
+  }
+  if (n_fwd > 0) {
+    if (a.max_runs > kMfmaRegRuns)
+      hipLaunchKernelGGL((m16_dq<kD, true>), dim3(n_fwd), dim3(64 * kM16Waves), 0, s, a);
+    else
+      hipLaunchKernelGGL((m16_dq<kD, false>), dim3(n_fwd), dim3(64 * kM16Waves), 0, s, a);
+    if (hipGetLastError() != hipSuccess) return 4;
+  }
+  return 0;
+}
+
+}  // namespace
+
+int launch_m16_fwd(const KernelArgs& a, hipStream_t s) {
+  return a.d == 64 ? launch_fwd_d<64>(a, s) : launch_fwd_d<256>(a, s);
+}
+
+int launch_m16_delta(const KernelArgs& a, hipStream_t s) {
+  const int64_t rows = static_cast<int64_t>(a.total_q) * a.hq;
+  const int blocks = static_cast<int>((rows + 15) / 16);
+  if (blocks > 0) {
+    if (a.d == 64)
+      hipLaunchKernelGGL(m16_delta<64>, dim3(blocks), dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL(m16_delta<256>, dim3(blocks), dim3(256), 0, s, a);
+  }
+  return hipGetLastError() == hipSuccess ? 0 : 4;
+}
+
+int launch_m16_bwd(const KernelArgs& a, int n_fwd, int n_dkdv, int n_red, hipStream_t s) {
+  return a.d == 64 ? launch_bwd_d<64>(a, n_fwd, n_dkdv, n_red, s) : launch_bwd_d<256>(a, n_fwd, n_dkdv, n_red, s);
+}
+
+}  // namespace tpr

@@ -140,7 +140,11 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
                   "descendant leaves of node %d are not contiguous; number leaves in DFS order", n);
   }
 
-  const int path = (t->dtype == TPR_DTYPE_BF16 && D == kMfmaD) ? PATH_MFMA : PATH_SIMT;
+  const int path = t->dtype != TPR_DTYPE_BF16 ? PATH_SIMT
+                   : D == kMfmaD             ? PATH_MFMA
+                   : (D == 64 || D == 256)   ? PATH_MFMA16
+                                             : PATH_SIMT;
+  const bool mfma_family = path != PATH_SIMT;
   const int G = Hq / Hkv;
   std::vector<int64_t> prefix_len(N, 0);
   for (int s = 0; s < N; s++)
@@ -178,7 +182,7 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
     std::copy(leaf_runs[s].begin(), leaf_runs[s].end(), runs_flat.begin() + static_cast<size_t>(s) * run_words);
 
   // ---- query-block list (dK/dV granularity) --------------------------------
-  const int BQ = path == PATH_MFMA ? kDkdvQ : kSimtTile;
+  const int BQ = mfma_family ? kDkdvQ : kSimtTile;
   std::vector<int32_t> qblk, leaf_qblk(N + 1, 0);
   for (int s = 0; s < N; s++) {
     leaf_qblk[s] = static_cast<int32_t>(qblk.size() / 2);
@@ -195,6 +199,9 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
   if (path == PATH_MFMA) {
     heads_per_wg = gcd_int(G, kFwdWaves);
     tokens_per_wg = kFwdTokens * (kFwdWaves / heads_per_wg);
+  } else if (path == PATH_MFMA16) {
+    heads_per_wg = gcd_int(G, kM16Waves);
+    tokens_per_wg = kM16Tokens * (kM16Waves / heads_per_wg);
   } else {
     heads_per_wg = 1;
     tokens_per_wg = kSimtQ;
@@ -236,9 +243,9 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
   // chunks that each write an fp32 partial, summed afterwards in chunk (=
   // leaf) order by a reduction item. Ranges that fit stay whole: no partials
   // and no reduction.
-  const int KT = path == PATH_MFMA ? kDkdvKeys : kSimtKeys;
+  const int KT = path == PATH_MFMA ? kDkdvKeys : path == PATH_MFMA16 ? kM16Keys : kSimtKeys;
   int prefix_cap = kDkdvPrefixChunk;
-  if (path == PATH_MFMA) {
+  if (mfma_family) {
     int64_t total = 0;  // query blocks streamed over all (tile, KV head) items
     for (int n = 0; n < M; n++)
       total += static_cast<int64_t>((no[n + 1] - no[n] + KT - 1) / KT) * Hkv *
@@ -255,7 +262,7 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
   auto add_tile = [&](int src, int seg, int k0, int h, int32_t lo, int32_t hi) {
     const int32_t range = hi - lo;
     int chunk = range;
-    if (path == PATH_MFMA) {
+    if (mfma_family) {
       const int cap = src == 0 ? prefix_cap : kDkdvMaxBlocks;
       if (range > cap) {
         const int pieces = (range + cap - 1) / cap;

@@ -45,7 +45,9 @@ class LaunchPlan:
 
     @property
     def path(self) -> str:
-        return "mfma" if int(self.host[_PF_PATH]) == 1 else "simt"
+        """Kernel family: "mfma" (bf16, head_dim 128), "mfma16" (bf16, head_dim
+        64 or 256) or "simt" (fp32, and bf16 with other head sizes)."""
+        return {1: "mfma", 2: "mfma16"}.get(int(self.host[_PF_PATH]), "simt")
 
     @property
     def num_forward_items(self) -> int:

@@ -96,7 +96,7 @@ def test_full_size_config_matches_oracle_on_head_groups(name, cuda_device):
 
 
 def test_qwen35_full_attention_shape_matches_oracle_on_one_head_group(cuda_device):
-    """head_dim 256 (the SIMT kernels) at the headline sequence shape: prefix
+    """head_dim 256 (the 16-wide MFMA kernels) at the headline sequence shape: prefix
     4096 + 4 x 4096, GQA 8/2 -- the full-attention layers of the reference's
     Qwen3.5 hybrid test model (kv_channels=256). KV head 1, query heads 4..7."""
     from bridge_amd import TPRPrefixMeta

@@ -4,8 +4,10 @@
   caller fp32 buffers. Into zeros it gives the same gradient twice (bitwise,
   deterministic); into a prefilled buffer exactly prefill + that gradient (one
   fp32 add per element); dq/dk/dv are those of the ordinary backward; and the
-  gradient matches the fp32 oracle -- on the MFMA path with unsplit and with
-  split (reduced) prefix tiles, and on the fp32 SIMT path.
+  gradient matches the fp32 oracle -- on the head_dim-128 MFMA path with
+  unsplit and with split (reduced) prefix tiles, on the 16-wide MFMA path
+  (head_dim 64, and 256 with split tiles), and on the SIMT paths (fp32, and
+  bf16 at head_dim 96).
 * A DFS through PrefixKVStack with TPRKernelBackend.from_stack relays every
   node's gradient (fp32, summed over two sibling batches for the root) to the
   values of the oracle's whole-tree backward -- the reference's relay
@@ -42,7 +44,8 @@ def _run_backward(meta, q, k, v, pk, pv, dout, scale, accumulators=None):
     return grads
 
 
-@pytest.mark.parametrize("case", ["mfma_unsplit", "mfma_split", "simt_fp32", "simt_bf16"])
+@pytest.mark.parametrize("case", ["mfma_unsplit", "mfma_split", "simt_fp32", "mfma16_bf16_d64", "mfma16_split_d256",
+                                  "simt_bf16_d96"])
 def test_accumulate_mode_adds_the_prefix_gradient(case, cuda_device):
     from bridge_amd import TPRPrefixMeta
     if case == "mfma_unsplit":
@@ -55,8 +58,13 @@ def test_accumulate_mode_adds_the_prefix_gradient(case, cuda_device):
         assert meta.plan(hq, hkv, d, dtype, cuda_device).workspace_bytes == stat_bytes + 4 * 2 * 128 * 128 * 4
     elif case == "simt_fp32":
         meta, hq, hkv, d, dtype = TPRPrefixMeta.shared_prefix(96, [40, 17, 33]), 4, 2, 64, torch.float32
-    else:  # bf16 with head_dim 64 runs the SIMT kernels too
+    elif case == "mfma16_bf16_d64":  # bf16 with head_dim 64: the 16-wide MFMA kernels
         meta, hq, hkv, d, dtype = TPRPrefixMeta.shared_prefix(96, [40, 17, 33]), 4, 2, 64, torch.bfloat16
+    elif case == "mfma16_split_d256":  # head_dim 256 with split prefix tiles (partials + reduction)
+        meta, hq, hkv, d, dtype = TPRPrefixMeta.shared_prefix(100, [1300, 1300, 70, 2400]), 4, 1, 256, torch.bfloat16
+        assert int(meta.plan(hq, hkv, d, dtype, cuda_device).host[25]) > 0
+    else:  # bf16 with head_dim 96 runs the SIMT kernels
+        meta, hq, hkv, d, dtype = TPRPrefixMeta.shared_prefix(96, [40, 17, 33]), 4, 2, 96, torch.bfloat16
     scale = 1.0 / math.sqrt(d)
     q, k, v, pk, pv, dout = make_inputs(meta, hq, hkv, d, dtype, 31, cuda_device)
     print(f"[{case}] tq={meta.total_q} tp={meta.total_prefix} path={meta.plan(hq, hkv, d, dtype, cuda_device).path}",

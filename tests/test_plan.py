@@ -193,14 +193,32 @@ def test_key_runs_merge_adjacent_ancestors_and_drop_empty_nodes():
         assert sum(ln for _, ln in leaf_runs) == meta.prefix_length(leaf)
 
 
-def test_simt_path_for_fp32_and_small_head_dim():
+def test_kernel_family_by_dtype_and_head_dim():
     meta = TPRPrefixMeta.shared_prefix(512, [512, 512])
     assert meta.plan(4, 4, 64, torch.float32, CPU).path == "simt"
-    assert meta.plan(4, 4, 64, torch.bfloat16, CPU).path == "simt"
+    assert meta.plan(4, 4, 64, torch.bfloat16, CPU).path == "mfma16"
     assert meta.plan(4, 4, 128, torch.float32, CPU).path == "simt"
     assert meta.plan(4, 4, 128, torch.bfloat16, CPU).path == "mfma"
-    assert meta.plan(8, 2, 256, torch.bfloat16, CPU).path == "simt"
+    assert meta.plan(8, 2, 256, torch.bfloat16, CPU).path == "mfma16"
     assert meta.plan(8, 2, 256, torch.float32, CPU).path == "simt"
+    assert meta.plan(6, 2, 96, torch.bfloat16, CPU).path == "simt"
+
+
+def test_mfma16_work_items():
+    """head_dim 64 / 256: forward items of 32 tokens x 4 waves / gcd(G, 4) heads,
+    dK/dV items of 64 keys, 64-query blocks."""
+    meta = TPRPrefixMeta.shared_prefix(100, [130, 64])
+    plan = meta.plan(8, 2, 256, torch.bfloat16, CPU)
+    w, fwd, dkdv, qblk = decode(plan)
+    items = [i for i in fwd if i[0] >= 0]
+    # G = 4: 4 heads x 32 tokens per item
+    assert sorted((i[0], i[1], i[2]) for i in items) == sorted(
+        (leaf, tok, qh) for leaf, n in ((0, 130), (1, 64)) for tok in range(0, n, 32) for qh in (0, 4))
+    tiles = [i for i in dkdv if i[0] >= 0]
+    prefix_tiles = sorted((i[2], i[3]) for i in tiles if i[0] == 0)
+    assert prefix_tiles == [(k0, h) for k0 in (0, 64) for h in (0, 1)]
+    assert all(i[2] % 64 == 0 for i in tiles)
+    assert qblk == [(0, 0), (0, 64), (0, 128), (1, 0)]
 
 
 def test_plan_is_cached_per_configuration():
