@@ -119,7 +119,7 @@ size_t stat_floats(const int32_t* ph) {
 extern "C" size_t tpr_attn_bwd_workspace_bytes(const int32_t* plan_host) {
   if (!plan_host || plan_host[PF_MAGIC] != kPlanMagic) return 0;
   const size_t slots = static_cast<size_t>(plan_host[PF_N_SLOTS]);
-  const size_t keys = plan_host[PF_PATH] == PATH_MFMA16 ? kM16Keys : kDkdvKeys;  // keys per partial slot
+  const size_t keys = plan_host[PF_PATH] == PATH_MFMA16 ? m16_keys(plan_host[PF_D]) : kDkdvKeys;  // per partial slot
   return (stat_floats(plan_host) + slots * keys * static_cast<size_t>(plan_host[PF_D]) * 2) * sizeof(float);
 }
 

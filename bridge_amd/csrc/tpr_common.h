@@ -105,7 +105,10 @@ constexpr int kStatRowsOffset = 64;   // floats before the lse*log2e rows
 // MFMA16 family (bf16, head_dim 64 and 256)
 constexpr int kM16Waves = 4;          // waves per workgroup (all kernels)
 constexpr int kM16Tokens = 32;        // forward / dQ tokens per wave (two 16-query sub-blocks)
-constexpr int kM16Keys = 16 * kM16Waves;  // keys per dK/dV workgroup (16 per wave)
+// dK/dV keys per wave: one 16-key block (at head_dim 256 the accumulators of
+// two would not fit the register file; at 64 two measured no faster)
+constexpr int m16_wave_keys(int /*head_dim*/) { return 16; }
+constexpr int m16_keys(int d) { return m16_wave_keys(d) * kM16Waves; }  // keys per dK/dV workgroup
 constexpr int kMfmaRegRuns = 8;       // key runs a forward / dQ workgroup holds in registers; a
                                       // launch with longer run lists reads them from the plan
 

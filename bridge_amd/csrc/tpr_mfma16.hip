@@ -4,8 +4,8 @@
 // Same math, key streams, work lists and fixed-order sibling sum as the
 // head_dim-128 family (tpr_mfma.hip); the tiling is built on the 16-wide MFMA
 // so that head_dim 256 fits the register file: a forward / dQ wave owns 32
-// query tokens of one head as two 16-query sub-blocks, a dK/dV wave owns 16
-// keys. One wave per SIMD, 4 waves per workgroup; K/V (forward, dQ) and Q/dO
+// query tokens of one head as two 16-query sub-blocks, a dK/dV wave owns 32
+// keys as two 16-key blocks (16 keys at head_dim 256). One wave per SIMD, 4 waves per workgroup; K/V (forward, dQ) and Q/dO
 // (dK/dV) tiles of 64 rows are staged in LDS by the gfx950 DMA, double
 // buffered, one workgroup barrier per tile.
 //
@@ -214,13 +214,16 @@ __global__ __launch_bounds__(256) void m16_fwd(KernelArgs a) {
 #pragma unroll
         for (int b = 0; b < 4; b++) sa[qs][b] = f32x4{};
 #pragma unroll
-      for (int s = 0; s < T::NS; s++)
+      for (int s = 0; s < T::NS; s++) {
 #pragma unroll
         for (int b = 0; b < 4; b++) {
           const bf16x8 kop = row_operand<kD>(kt, b, s, lane);
 #pragma unroll
           for (int qs = 0; qs < 2; qs++) sa[qs][b] = mfma16(kop, qv[qs][s], sa[qs][b]);
         }
+        // keep each step's reads next to its MFMAs (measured faster at head_dim 64, slower at 256)
+        if constexpr (kD == 64) __builtin_amdgcn_sched_barrier(0);
+      }
 #pragma unroll
       for (int qs = 0; qs < 2; qs++)
 #pragma unroll
@@ -278,13 +281,15 @@ __global__ __launch_bounds__(256) void m16_fwd(KernelArgs a) {
     }
     // O^T += V^T P^T: A = V^T (16 head dims x 32 keys of step t), B = P^T
 #pragma unroll
-    for (int db = 0; db < T::ND; db++)
+    for (int db = 0; db < T::ND; db++) {
 #pragma unroll
       for (int t = 0; t < 2; t++) {
         const bf16x8 vop = col_operand<kD>(vt, 32 * t, 16 * db, lane);
 #pragma unroll
         for (int qs = 0; qs < 2; qs++) o[qs][db] = mfma16(vop, pb[qs][t], o[qs][db]);
       }
+      if constexpr (kD == 64) __builtin_amdgcn_sched_barrier(0);
+    }
     if (j + 1 < ntiles) {
       cursor_next(seg, mc);
       tl = cursor_tile(mc);
@@ -459,7 +464,7 @@ __global__ __launch_bounds__(256) void m16_dq(KernelArgs a) {
           pa[qs][b] = f32x4{};
         }
 #pragma unroll
-      for (int s = 0; s < T::NS; s++)
+      for (int s = 0; s < T::NS; s++) {
 #pragma unroll
         for (int b = 0; b < 4; b++) {
           const bf16x8 kop = row_operand<kD>(kt, b, s, lane);
@@ -470,6 +475,8 @@ __global__ __launch_bounds__(256) void m16_dq(KernelArgs a) {
             pa[qs][b] = mfma16(vop, gv[qs][s], pa[qs][b]);
           }
         }
+        if constexpr (kD == 64) __builtin_amdgcn_sched_barrier(0);
+      }
 #pragma unroll
       for (int qs = 0; qs < 2; qs++)
 #pragma unroll
@@ -502,13 +509,15 @@ __global__ __launch_bounds__(256) void m16_dq(KernelArgs a) {
     }
     // dQ^T += K^T dS^T: A = K^T (16 head dims x 32 keys of step t), B = dS^T
 #pragma unroll
-    for (int db = 0; db < T::ND; db++)
+    for (int db = 0; db < T::ND; db++) {
 #pragma unroll
       for (int t = 0; t < 2; t++) {
         const bf16x8 kop = col_operand<kD>(kt, 32 * t, 16 * db, lane);
 #pragma unroll
         for (int qs = 0; qs < 2; qs++) dq[qs][db] = mfma16(kop, dsb[qs][t], dq[qs][db]);
       }
+      if constexpr (kD == 64) __builtin_amdgcn_sched_barrier(0);
+    }
     if (j + 1 < ntiles) {
       cursor_next(seg, mc);
       tl = cursor_tile(mc);
@@ -533,18 +542,24 @@ __global__ __launch_bounds__(256) void m16_dq(KernelArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// dK/dV. One workgroup = 4 waves x 16 keys of one KV segment tile (64 keys)
-// and KV head; it streams every 64-query block that sees the tile -- for a
-// prefix node every descendant leaf and every query head of the group -- in
-// the plan's fixed order, so a prefix node's gradient is the sum over its
-// leaves in registers, without atomics. Per stage (one block, one head):
-//   S = Q K^T, dP = dO V^T (Q, dO rows from LDS, permuted; K, V in registers),
+// dK/dV. One workgroup = 4 waves x 32 keys (two 16-key blocks kb; one block
+// of 16 at head_dim 256) of one KV segment tile and KV head; it streams every 64-query block that
+// sees the tile -- for a prefix node every descendant leaf and every query
+// head of the group -- in the plan's fixed order, so a prefix node's gradient
+// is the sum over its leaves in registers, without atomics. Per stage (one
+// block, one head), for each pair of 16-query blocks t:
+//   S = Q K^T, dP = dO V^T (Q, dO rows from LDS, permuted; K, V of both key
+//   blocks in registers, so every row read feeds two MFMAs),
 //   P = exp2(scale*log2e S - lse*log2e), dS = P (dP - delta),
-//   dV += P^T dO, dK += dS^T Q (dO, Q read transposed from LDS).
+//   dV += P^T dO, dK += dS^T Q (dO, Q read transposed from LDS, again shared
+//   by the two key blocks).
 // ---------------------------------------------------------------------------
 template <int kD>
 __global__ __launch_bounds__(256) void m16_dkdv(KernelArgs a) {
   using T = Geo<kD>;
+  constexpr int kWaveKeys = m16_wave_keys(kD);
+  constexpr int kKeys = m16_keys(kD);
+  constexpr int KB = kWaveKeys / 16;  // 16-key blocks per wave
   const int32_t* item = a.plan + a.off_dkdv + DK_WORDS * blockIdx.x;
   if (item[DK_SRC] < 0) return;
   const bool prefix = item[DK_SRC] == 0;
@@ -558,11 +573,9 @@ __global__ __launch_bounds__(256) void m16_dkdv(KernelArgs a) {
 
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int i16 = lane & 15, g = lane >> 4;
-  const int kw0 = key0 + 16 * wave;  // first key position of this wave
-  const int kp = kw0 + i16;          // this lane's key (B-operand column)
+  const int kw0 = key0 + kWaveKeys * wave;  // first key position of this wave
   const bool wave_active = kw0 < seg_len;
 
-  const int64_t qstride = static_cast<int64_t>(a.hq) * kD;
   const int64_t kstride = static_cast<int64_t>(a.hkv) * kD;
   const uint32_t qrow_bytes = static_cast<uint32_t>(a.hq) * kD * 2;
 
@@ -597,30 +610,38 @@ __global__ __launch_bounds__(256) void m16_dkdv(KernelArgs a) {
   };
   if (nstage > 0) issue(0, 0, 0);
 
-  // K / V of the lane's key kp: the B operands of S = Q K^T and dP = dO V^T
-  bf16x8 kv[T::NS], vv[T::NS];
-  {
-    const bf16* kb = static_cast<const bf16*>(prefix ? a.pk : a.k);
-    const bf16* vb = static_cast<const bf16*>(prefix ? a.pv : a.v);
-    const int64_t off = static_cast<int64_t>(seg_row0 + min(kp, seg_len - 1)) * kstride + kvh * kD + 8 * g;
+  // K / V of the lane's key kw0 + 16 kb + l % 16: the B operands of
+  // S = Q K^T and dP = dO V^T
+  bf16x8 kv[KB][T::NS], vv[KB][T::NS];
+#pragma unroll
+  for (int kb = 0; kb < KB; kb++) {
+    const bf16* kbase = static_cast<const bf16*>(prefix ? a.pk : a.k);
+    const bf16* vbase = static_cast<const bf16*>(prefix ? a.pv : a.v);
+    const int key = min(kw0 + 16 * kb + i16, seg_len - 1);
+    const int64_t off = static_cast<int64_t>(seg_row0 + key) * kstride + kvh * kD + 8 * g;
 #pragma unroll
     for (int s = 0; s < T::NS; s++) {
-      kv[s] = *reinterpret_cast<const bf16x8*>(kb + off + 32 * s);
-      vv[s] = *reinterpret_cast<const bf16x8*>(vb + off + 32 * s);
+      kv[kb][s] = *reinterpret_cast<const bf16x8*>(kbase + off + 32 * s);
+      vv[kb][s] = *reinterpret_cast<const bf16x8*>(vbase + off + 32 * s);
     }
   }
-  f32x4 dk[T::ND], dv[T::ND];  // register r of block db: key 4 g + r of the wave, head dim 16 db + l % 16
+  // register r of block [kb][db]: key 16 kb + 4 g + r of the wave, head dim 16 db + l % 16
+  f32x4 dk[KB][T::ND], dv[KB][T::ND];
 #pragma unroll
-  for (int db = 0; db < T::ND; db++) {
-    dk[db] = f32x4{};
-    dv[db] = f32x4{};
-  }
+  for (int kb = 0; kb < KB; kb++)
+#pragma unroll
+    for (int db = 0; db < T::ND; db++) {
+      dk[kb][db] = f32x4{};
+      dv[kb][db] = f32x4{};
+    }
   const float c2 = a.scale * kLog2e;
 #pragma unroll
-  for (int s = 0; s < T::NS; s++) {
-    settle(kv[s]);
-    settle(vv[s]);
-  }
+  for (int kb = 0; kb < KB; kb++)
+#pragma unroll
+    for (int s = 0; s < T::NS; s++) {
+      settle(kv[kb][s]);
+      settle(vv[kb][s]);
+    }
   wait_dma();
   __syncthreads();
 
@@ -635,36 +656,64 @@ __global__ __launch_bounds__(256) void m16_dkdv(KernelArgs a) {
       const float* nlse = &stats[buf][0][0];
       const float* ndel = &stats[buf][1][0];
       // query q of the block visible from key kp iff kp <= tok0 + q (suffix tiles)
-      const bool diag = !prefix && tok0 < kw0 + 15;
-      float pf[4][4], df[4][4];  // [query block][register]: query 32 (b/2) + 8 g + 4 (b%2) + r
+      const bool diag = !prefix && tok0 < kw0 + kWaveKeys - 1;
 #pragma unroll
-      for (int b = 0; b < 4; b++) {
-        f32x4 sa = f32x4{}, pa = f32x4{};
+      for (int t = 0; t < 2; t++) {
+        float pf[KB][2][4], df[KB][2][4];  // [key block][query block 2t + e][register]
 #pragma unroll
-        for (int s = 0; s < T::NS; s++) {
-          sa = mfma16(row_operand<kD>(qt, b, s, lane), kv[s], sa);
-          pa = mfma16(row_operand<kD>(gt, b, s, lane), vv[s], pa);
+        for (int e = 0; e < 2; e++) {
+          const int b = 2 * t + e;
+          f32x4 sa[KB], pa[KB];
+#pragma unroll
+          for (int kb = 0; kb < KB; kb++) {
+            sa[kb] = f32x4{};
+            pa[kb] = f32x4{};
+          }
+#pragma unroll
+          for (int s = 0; s < T::NS; s++) {
+            const bf16x8 qop = row_operand<kD>(qt, b, s, lane);
+            const bf16x8 gop = row_operand<kD>(gt, b, s, lane);
+#pragma unroll
+            for (int kb = 0; kb < KB; kb++) {
+              sa[kb] = mfma16(qop, kv[kb][s], sa[kb]);
+              pa[kb] = mfma16(gop, vv[kb][s], pa[kb]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+          }
+          // register r: query q0 + r of the block
+          const int q0 = 32 * t + 8 * g + 4 * e;
+          const f32x4 ls = *reinterpret_cast<const f32x4*>(nlse + q0);
+          const f32x4 dl = *reinterpret_cast<const f32x4*>(ndel + q0);
+#pragma unroll
+          for (int kb = 0; kb < KB; kb++) {
+            const int kp = kw0 + 16 * kb + i16;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+              float x = fmaf(sa[kb][r], c2, ls[r]);
+              if (diag) x = kp <= tok0 + q0 + r ? x : -INFINITY;
+              pf[kb][e][r] = fast_exp2(x);
+              df[kb][e][r] = pf[kb][e][r] * (pa[kb][r] + dl[r]);
+            }
+          }
         }
-        const int q0 = 32 * (b >> 1) + 8 * g + 4 * (b & 1);
-        const f32x4 ls = *reinterpret_cast<const f32x4*>(nlse + q0);
-        const f32x4 dl = *reinterpret_cast<const f32x4*>(ndel + q0);
+        bf16x8 pT[KB], dT[KB];  // queries 32 t + 8 g + 0..7 of key 16 kb + l % 16
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-          float x = fmaf(sa[r], c2, ls[r]);
-          if (diag) x = kp <= tok0 + q0 + r ? x : -INFINITY;
-          pf[b][r] = fast_exp2(x);
-          df[b][r] = pf[b][r] * (pa[r] + dl[r]);
+        for (int kb = 0; kb < KB; kb++) {
+          pT[kb] = pack8(pf[kb][0], pf[kb][1]);
+          dT[kb] = pack8(df[kb][0], df[kb][1]);
+        }
+#pragma unroll
+        for (int db = 0; db < T::ND; db++) {
+          const bf16x8 gcol = col_operand<kD>(gt, 32 * t, 16 * db, lane);
+          const bf16x8 qcol = col_operand<kD>(qt, 32 * t, 16 * db, lane);
+#pragma unroll
+          for (int kb = 0; kb < KB; kb++) {
+            dv[kb][db] = mfma16(pT[kb], gcol, dv[kb][db]);
+            dk[kb][db] = mfma16(dT[kb], qcol, dk[kb][db]);
+          }
+          __builtin_amdgcn_sched_barrier(0);
         }
       }
-      const bf16x8 pT[2] = {pack8(pf[0], pf[1]), pack8(pf[2], pf[3])};
-      const bf16x8 dT[2] = {pack8(df[0], df[1]), pack8(df[2], df[3])};
-#pragma unroll
-      for (int db = 0; db < T::ND; db++)
-#pragma unroll
-        for (int t = 0; t < 2; t++) {
-          dv[db] = mfma16(pT[t], col_operand<kD>(gt, 32 * t, 16 * db, lane), dv[db]);
-          dk[db] = mfma16(dT[t], col_operand<kD>(qt, 32 * t, 16 * db, lane), dk[db]);
-        }
     }
     wait_dma();  // stage sidx + 1 has landed
     __syncthreads();
@@ -672,18 +721,20 @@ __global__ __launch_bounds__(256) void m16_dkdv(KernelArgs a) {
 
   if (!wave_active) return;
   const int slot = item[DK_SLOT];
-  if (slot >= 0) {  // split tile: fp32 partial [kM16Keys][kD] for dK (already scaled) then dV
-    float* pk = a.ws + static_cast<int64_t>(slot) * 2 * kM16Keys * kD;
-    float* pv = pk + kM16Keys * kD;
+  if (slot >= 0) {  // split tile: fp32 partial [kKeys][kD] for dK (already scaled) then dV
+    float* pk = a.ws + static_cast<int64_t>(slot) * 2 * kKeys * kD;
+    float* pv = pk + kKeys * kD;
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int key = 16 * wave + 4 * g + r;
+    for (int kb = 0; kb < KB; kb++)
 #pragma unroll
-      for (int db = 0; db < T::ND; db++) {
-        pk[key * kD + 16 * db + i16] = dk[db][r] * a.scale;
-        pv[key * kD + 16 * db + i16] = dv[db][r];
+      for (int r = 0; r < 4; r++) {
+        const int key = kWaveKeys * wave + 16 * kb + 4 * g + r;
+#pragma unroll
+        for (int db = 0; db < T::ND; db++) {
+          pk[key * kD + 16 * db + i16] = dk[kb][db][r] * a.scale;
+          pv[key * kD + 16 * db + i16] = dv[kb][db][r];
+        }
       }
-    }
     return;
   }
   if (prefix && a.acc_prefix) {
@@ -691,37 +742,42 @@ __global__ __launch_bounds__(256) void m16_dkdv(KernelArgs a) {
     float* dkf = static_cast<float*>(a.dpk);
     float* dvf = static_cast<float*>(a.dpv);
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int key = kw0 + 4 * g + r;
-      if (key >= seg_len) continue;
-      const int64_t off = static_cast<int64_t>(seg_row0 + key) * kstride + kvh * kD + i16;
+    for (int kb = 0; kb < KB; kb++)
 #pragma unroll
-      for (int db = 0; db < T::ND; db++) {
-        dkf[off + 16 * db] += dk[db][r] * a.scale;
-        dvf[off + 16 * db] += dv[db][r];
+      for (int r = 0; r < 4; r++) {
+        const int key = kw0 + 16 * kb + 4 * g + r;
+        if (key >= seg_len) continue;
+        const int64_t off = static_cast<int64_t>(seg_row0 + key) * kstride + kvh * kD + i16;
+#pragma unroll
+        for (int db = 0; db < T::ND; db++) {
+          dkf[off + 16 * db] += dk[kb][db][r] * a.scale;
+          dvf[off + 16 * db] += dv[kb][db][r];
+        }
       }
-    }
     return;
   }
   bf16* dkd = static_cast<bf16*>(prefix ? a.dpk : a.dk);
   bf16* dvd = static_cast<bf16*>(prefix ? a.dpv : a.dv);
 #pragma unroll
-  for (int r = 0; r < 4; r++) {
-    const int key = kw0 + 4 * g + r;
-    if (key >= seg_len) continue;
-    const int64_t off = static_cast<int64_t>(seg_row0 + key) * kstride + kvh * kD + i16;
+  for (int kb = 0; kb < KB; kb++)
 #pragma unroll
-    for (int db = 0; db < T::ND; db++) {
-      dkd[off + 16 * db] = static_cast<bf16>(dk[db][r] * a.scale);
-      dvd[off + 16 * db] = static_cast<bf16>(dv[db][r]);
+    for (int r = 0; r < 4; r++) {
+      const int key = kw0 + 16 * kb + 4 * g + r;
+      if (key >= seg_len) continue;
+      const int64_t off = static_cast<int64_t>(seg_row0 + key) * kstride + kvh * kD + i16;
+#pragma unroll
+      for (int db = 0; db < T::ND; db++) {
+        dkd[off + 16 * db] = static_cast<bf16>(dk[kb][db][r] * a.scale);
+        dvd[off + 16 * db] = static_cast<bf16>(dv[kb][db][r]);
+      }
     }
-  }
 }
 
 // Second pass of split dK/dV tiles: the fp32 partial slots of one (segment
 // tile, KV head) summed in slot (= leaf) order, written once.
 template <int kD>
 __global__ __launch_bounds__(256) void m16_reduce(KernelArgs a) {
+  constexpr int kKeys = m16_keys(kD);
   const int32_t* item = a.plan + a.off_red + RD_WORDS * blockIdx.x;
   const bool prefix = item[RD_SRC] == 0;
   const int seg = item[RD_SEG], key0 = item[RD_KEY0], kvh = item[RD_KVH];
@@ -729,16 +785,16 @@ __global__ __launch_bounds__(256) void m16_reduce(KernelArgs a) {
   const int32_t* cu = a.plan + a.off_cu;
   const int32_t* no = a.plan + a.off_node_off;
   const int seg_row0 = prefix ? no[seg] : cu[seg];
-  const int keys = min(kM16Keys, (prefix ? no[seg + 1] - no[seg] : cu[seg + 1] - cu[seg]) - key0);
+  const int keys = min(kKeys, (prefix ? no[seg + 1] - no[seg] : cu[seg + 1] - cu[seg]) - key0);
   const int64_t kstride = static_cast<int64_t>(a.hkv) * kD;
   bf16* dkd = static_cast<bf16*>(prefix ? a.dpk : a.dk);
   bf16* dvd = static_cast<bf16*>(prefix ? a.dpv : a.dv);
-  const int64_t slot_floats = 2 * kM16Keys * kD;
+  const int64_t slot_floats = 2 * kKeys * kD;
   for (int e = threadIdx.x; e < 2 * keys * (kD / 4); e += blockDim.x) {
     const int which = e / (keys * (kD / 4));  // 0 = dK, 1 = dV
     const int rem = e % (keys * (kD / 4));
     const int key = rem / (kD / 4), d4 = rem % (kD / 4);
-    const float* src = a.ws + static_cast<int64_t>(slot0) * slot_floats + which * kM16Keys * kD + key * kD + 4 * d4;
+    const float* src = a.ws + static_cast<int64_t>(slot0) * slot_floats + which * kKeys * kD + key * kD + 4 * d4;
     f32x4 acc = *reinterpret_cast<const f32x4*>(src);
     for (int j = 1; j < nslots; j++) acc += *reinterpret_cast<const f32x4*>(src + j * slot_floats);
     const int64_t at = static_cast<int64_t>(seg_row0 + key0 + key) * kstride + kvh * kD + 4 * d4;

@@ -243,7 +243,7 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
   // chunks that each write an fp32 partial, summed afterwards in chunk (=
   // leaf) order by a reduction item. Ranges that fit stay whole: no partials
   // and no reduction.
-  const int KT = path == PATH_MFMA ? kDkdvKeys : path == PATH_MFMA16 ? kM16Keys : kSimtKeys;
+  const int KT = path == PATH_MFMA ? kDkdvKeys : path == PATH_MFMA16 ? m16_keys(D) : kSimtKeys;
   int prefix_cap = kDkdvPrefixChunk;
   if (mfma_family) {
     int64_t total = 0;  // query blocks streamed over all (tile, KV head) items
