@@ -63,7 +63,8 @@ enum DkdvField : int {
   DK_QB_LO,     // query-block range [lo, hi) in the global query-block list
   DK_QB_HI,
   DK_SLOT,      // -1: write dK/dV directly; else fp32 partial slot
-  DK_PAD,
+  DK_PAIR,      // 0, or 1 + first key of a second suffix tile of the same leaf
+                // and KV head, streamed after this one (pairs are never split)
   DK_WORDS = 8
 };
 

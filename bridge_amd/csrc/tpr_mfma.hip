@@ -874,8 +874,7 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
   const int32_t* item = a.plan + a.off_dkdv + DK_WORDS * blockIdx.x;
   if (item[DK_SRC] < 0) return;
   const bool prefix = item[DK_SRC] == 0;
-  const int seg = item[DK_SEG], key0 = item[DK_KEY0], kvh = item[DK_KVH];
-  const int qb_lo = item[DK_QB_LO], qb_hi = item[DK_QB_HI];
+  const int seg = item[DK_SEG], kvh = item[DK_KVH];
   const int32_t* cu = a.plan + a.off_cu;
   const int32_t* no = a.plan + a.off_node_off;
   const int32_t* qblk = a.plan + a.off_qblk;
@@ -884,9 +883,6 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
 
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 31, h = lane >> 5;
-  const int kw0 = key0 + 32 * wave;          // first key position of this wave
-  const int kp = kw0 + n;                     // this lane's key position (B-operand column)
-  const bool wave_active = kw0 < seg_len;
 
   const int64_t qstride = static_cast<int64_t>(a.hq) * kMfmaD;
   const int64_t kstride = static_cast<int64_t>(a.hkv) * kMfmaD;
@@ -895,370 +891,401 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
   // run during stage s
   __shared__ __attribute__((aligned(1024))) char smem[2 * kHeads * 2 * kTileBytes];
   __shared__ __attribute__((aligned(256))) float stats[2][kHeads][2][kTileRows];  // [buf][head][-lse*log2e | -delta][row]
+  // query-block table of the current tile: {first packed row, token start
+  // within the leaf, valid rows}
+  __shared__ int4 qtab[kDkdvMaxBlocks];
 
   const int spb = a.group / kHeads;  // stages per query block
-  const int nstage = (qb_hi - qb_lo) * spb;
   const bf16* qbase = static_cast<const bf16*>(a.q);
   const bf16* gbase = static_cast<const bf16*>(a.dout);
 
-  // Query-block table of this item (planner guarantees <= kDkdvMaxBlocks):
-  // {first packed row, token start within the leaf, valid rows}. Read from the
-  // plan once, so the stage loop touches no plan memory.
-  __shared__ int4 qtab[kDkdvMaxBlocks];
-  for (int i = threadIdx.x; i < qb_hi - qb_lo; i += blockDim.x) {
-    const int qb = qb_lo + i;
-    const int lf = qblk[2 * qb], tok = qblk[2 * qb + 1];
-    const int r0 = cu[lf];
-    qtab[i] = int4{r0 + tok, tok, min(kTileRows, cu[lf + 1] - r0 - tok), 0};
-  }
-  __syncthreads();
+  // An item is one key tile, or two suffix tiles of one leaf and KV head
+  // (DK_PAIR): a tile and its mirror, so that all pairs of a leaf stream about
+  // the same number of query blocks. A suffix tile alone, or the first of a
+  // pair, streams its blocks last-first; the second of a pair streams
+  // first-last. The pairs of a leaf that run together on one XCD then read
+  // the same query block at the same time -- the first tiles count down from
+  // the leaf's last block, the second ones up from their diagonal at the
+  // same pace -- and share its copies in L2. Prefix tiles stream first-last:
+  // they all start together and see the same blocks.
+  const int ntiles = item[DK_PAIR] > 0 ? 2 : 1;
+  for (int tile = 0; tile < ntiles; tile++) {
+    const int key0 = tile == 0 ? item[DK_KEY0] : item[DK_PAIR] - 1;
+    const int qb_hi = item[DK_QB_HI];
+    const int qb_lo = tile == 0 ? item[DK_QB_LO] : item[DK_QB_LO] - (item[DK_KEY0] - key0) / kTileRows;
+    const bool first_last = prefix || tile == 1;
+    const int kw0 = key0 + 32 * wave;          // first key position of this wave
+    const int kp = kw0 + n;                     // this lane's key position (B-operand column)
+    const bool wave_active = kw0 < seg_len;
+    const int nstage = (qb_hi - qb_lo) * spb;
 
-  // Stage s is (query block s / spb, head pair s % spb), tracked by counters
-  // (no division in the loop): `cur` is the stage being computed, `nxt` the
-  // one being copied.
-  struct StageCursor {
-    int blk, sub;
-  };
-  auto advance = [&](StageCursor c) __attribute__((always_inline)) {
-    return c.sub + 1 == spb ? StageCursor{c.blk + 1, 0} : StageCursor{c.blk, c.sub + 1};
-  };
-  const uint32_t qrow_bytes = static_cast<uint32_t>(a.hq) * kMfmaD * 2;
-  const DmaLanes<kDkdvWaves> dl = make_dma_lanes<kDkdvWaves>(qrow_bytes, wave, lane);
-  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(smem));
-  // copy the Q and dO rows [row, row + 64) of query head qh into the stage buffer at byte `tile`
-  auto issue_stage = [&](int row, int nq, int qh, uint32_t tile) __attribute__((always_inline)) {
-    const int64_t off = static_cast<int64_t>(qh) * kMfmaD * 2 + static_cast<int64_t>(row) * qrow_bytes;
-    const uint32_t dst = lds0 + tile + wave * 4096;
-    const char* qs = reinterpret_cast<const char*>(qbase) + off;
-    const char* gs = reinterpret_cast<const char*>(gbase) + off;
-    if (nq >= kTileRows) {
-      dma_blocks4(qs, dl.voff[0], dl.voff[1], dl.voff[2], dl.voff[3], dst);
-      dma_blocks4(gs, dl.voff[0], dl.voff[1], dl.voff[2], dl.voff[3], dst + kTileBytes);
-    } else {  // rows at or beyond nq re-read row nq - 1
-      uint32_t v[4];
-#pragma unroll
-      for (int j = 0; j < 4; j++) v[j] = static_cast<uint32_t>(min(dl.row[j], nq - 1)) * qrow_bytes + dl.cbytes[j];
-      dma_blocks4_m0(qs, v[0], v[1], v[2], v[3], dst);
-      dma_blocks4_m0(gs, v[0], v[1], v[2], v[3], dst + kTileBytes);
+    // block table of this tile (planner guarantees <= kDkdvMaxBlocks), read
+    // from the plan once, so the stage loop touches no plan memory
+    if (tile > 0) __syncthreads();  // every wave is done with the previous tile's table
+    const int nblk = qb_hi - qb_lo;
+    for (int i = threadIdx.x; i < nblk; i += blockDim.x) {
+      const int qb = first_last ? qb_lo + i : qb_hi - 1 - i;
+      const int lf = qblk[2 * qb], tok = qblk[2 * qb + 1];
+      const int r0 = cu[lf];
+      qtab[i] = int4{r0 + tok, tok, min(kTileRows, cu[lf + 1] - r0 - tok), 0};
     }
-  };
+    __syncthreads();
 
-  // -lse*log2e (which 0) and -delta (which 1) of the stage's 64 query rows of
-  // each of its heads, copied into its stat buffer like the tiles -- wave w
-  // copies (head w / 2, which w % 2); rows past the block end copy the
-  // constants -inf / 0 of the workspace, so their P and dS are exactly 0.
-  const uint32_t stats0 = __builtin_amdgcn_readfirstlane(lds_address(stats));
-  auto issue_stats = [&](int row, int nq, int qh, int buf) __attribute__((always_inline)) {
-    const int hh = wave >> 1, which = wave & 1;
-    if (hh < kHeads) {
-      const int64_t at = static_cast<int64_t>(qh + hh) * a.total_q + row + lane;
-      const float* rows = which == 0 ? a.stat_ws + kStatRowsOffset : a.ndelta_ws;
-      dma4_lane(lane < nq ? rows + at : a.stat_ws + which,
-                stats0 + ((buf * kHeads + hh) * 2 + which) * kTileRows * 4);
-    }
-  };
-  auto issue = [&](StageCursor c, int buf) __attribute__((always_inline)) {
-    const int4 e = qtab[c.blk];
-    const int row = __builtin_amdgcn_readfirstlane(e.x), nq = __builtin_amdgcn_readfirstlane(e.z);
-    const int qh = kvh * a.group + c.sub * kHeads;
-    issue_stats(row, nq, qh, buf);
+    // Stage s is (query block s / spb, head pair s % spb), tracked by counters
+    // (no division in the loop): `cur` is the stage being computed, `nxt` the
+    // one being copied.
+    struct StageCursor {
+      int blk, sub;
+    };
+    auto advance = [&](StageCursor c) __attribute__((always_inline)) {
+      return c.sub + 1 == spb ? StageCursor{c.blk + 1, 0} : StageCursor{c.blk, c.sub + 1};
+    };
+    const uint32_t qrow_bytes = static_cast<uint32_t>(a.hq) * kMfmaD * 2;
+    const DmaLanes<kDkdvWaves> dl = make_dma_lanes<kDkdvWaves>(qrow_bytes, wave, lane);
+    const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(smem));
+    // copy the Q and dO rows [row, row + 64) of query head qh into the stage buffer at byte `tile`
+    auto issue_stage = [&](int row, int nq, int qh, uint32_t tile) __attribute__((always_inline)) {
+      const int64_t off = static_cast<int64_t>(qh) * kMfmaD * 2 + static_cast<int64_t>(row) * qrow_bytes;
+      const uint32_t dst = lds0 + tile + wave * 4096;
+      const char* qs = reinterpret_cast<const char*>(qbase) + off;
+      const char* gs = reinterpret_cast<const char*>(gbase) + off;
+      if (nq >= kTileRows) {
+        dma_blocks4(qs, dl.voff[0], dl.voff[1], dl.voff[2], dl.voff[3], dst);
+        dma_blocks4(gs, dl.voff[0], dl.voff[1], dl.voff[2], dl.voff[3], dst + kTileBytes);
+      } else {  // rows at or beyond nq re-read row nq - 1
+        uint32_t v[4];
 #pragma unroll
-    for (int hh = 0; hh < kHeads; hh++)
-      issue_stage(row, nq, qh + hh, static_cast<uint32_t>((buf * kHeads + hh) * 2 * kTileBytes));
-  };
-  StageCursor cur{0, 0};
-  if (nstage > 0) issue(cur, 0);
+        for (int j = 0; j < 4; j++) v[j] = static_cast<uint32_t>(min(dl.row[j], nq - 1)) * qrow_bytes + dl.cbytes[j];
+        dma_blocks4_m0(qs, v[0], v[1], v[2], v[3], dst);
+        dma_blocks4_m0(gs, v[0], v[1], v[2], v[3], dst + kTileBytes);
+      }
+    };
 
-  bf16x8 kv[8], vv[8];
-  {
-    const bf16* kb = static_cast<const bf16*>(prefix ? a.pk : a.k);
-    const bf16* vb = static_cast<const bf16*>(prefix ? a.pv : a.v);
-    const int64_t off = static_cast<int64_t>(seg_row0 + min(kp, seg_len - 1)) * kstride + kvh * kMfmaD + 8 * h;
+    // -lse*log2e (which 0) and -delta (which 1) of the stage's 64 query rows of
+    // each of its heads, copied into its stat buffer like the tiles -- wave w
+    // copies (head w / 2, which w % 2); rows past the block end copy the
+    // constants -inf / 0 of the workspace, so their P and dS are exactly 0.
+    const uint32_t stats0 = __builtin_amdgcn_readfirstlane(lds_address(stats));
+    auto issue_stats = [&](int row, int nq, int qh, int buf) __attribute__((always_inline)) {
+      const int hh = wave >> 1, which = wave & 1;
+      if (hh < kHeads) {
+        const int64_t at = static_cast<int64_t>(qh + hh) * a.total_q + row + lane;
+        const float* rows = which == 0 ? a.stat_ws + kStatRowsOffset : a.ndelta_ws;
+        dma4_lane(lane < nq ? rows + at : a.stat_ws + which,
+                  stats0 + ((buf * kHeads + hh) * 2 + which) * kTileRows * 4);
+      }
+    };
+    auto issue = [&](StageCursor c, int buf) __attribute__((always_inline)) {
+      const int4 e = qtab[c.blk];
+      const int row = __builtin_amdgcn_readfirstlane(e.x), nq = __builtin_amdgcn_readfirstlane(e.z);
+      const int qh = kvh * a.group + c.sub * kHeads;
+      issue_stats(row, nq, qh, buf);
+#pragma unroll
+      for (int hh = 0; hh < kHeads; hh++)
+        issue_stage(row, nq, qh + hh, static_cast<uint32_t>((buf * kHeads + hh) * 2 * kTileBytes));
+    };
+    StageCursor cur{0, 0};
+    if (nstage > 0) issue(cur, 0);
+
+    bf16x8 kv[8], vv[8];
+    {
+      const bf16* kb = static_cast<const bf16*>(prefix ? a.pk : a.k);
+      const bf16* vb = static_cast<const bf16*>(prefix ? a.pv : a.v);
+      const int64_t off = static_cast<int64_t>(seg_row0 + min(kp, seg_len - 1)) * kstride + kvh * kMfmaD + 8 * h;
+#pragma unroll
+      for (int c = 0; c < 8; c++) {
+        kv[c] = *reinterpret_cast<const bf16x8*>(kb + off + 16 * c);
+        vv[c] = *reinterpret_cast<const bf16x8*>(vb + off + 16 * c);
+      }
+    }
+    f32x16 dk[4], dv[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      dk[i] = f32x16{};
+      dv[i] = f32x16{};
+    }
+    // K as the S operand, pre-scaled by scale*log2e (rounded to bf16): the S
+    // chain then produces the exponent of P directly
+    {
+      const float c2 = a.scale * kLog2e;
+#pragma unroll
+      for (int c = 0; c < 8; c++)
+#pragma unroll
+        for (int i = 0; i < 8; i++) kv[c][i] = static_cast<bf16>(static_cast<float>(kv[c][i]) * c2);
+    }
+
+    // K/V live in AGPRs from here on: the S / dP MFMAs that read them are
+    // inline asm, before which the compiler inserts no wait states, so the
+    // accvgpr writes must not land next to their first use inside the loop.
 #pragma unroll
     for (int c = 0; c < 8; c++) {
-      kv[c] = *reinterpret_cast<const bf16x8*>(kb + off + 16 * c);
-      vv[c] = *reinterpret_cast<const bf16x8*>(vb + off + 16 * c);
-    }
-  }
-  f32x16 dk[4], dv[4];
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    dk[i] = f32x16{};
-    dv[i] = f32x16{};
-  }
-  // K as the S operand, pre-scaled by scale*log2e (rounded to bf16): the S
-  // chain then produces the exponent of P directly
-  {
-    const float c2 = a.scale * kLog2e;
-#pragma unroll
-    for (int c = 0; c < 8; c++)
-#pragma unroll
-      for (int i = 0; i < 8; i++) kv[c][i] = static_cast<bf16>(static_cast<float>(kv[c][i]) * c2);
-  }
-
-  // K/V live in AGPRs from here on: the S / dP MFMAs that read them are
-  // inline asm, before which the compiler inserts no wait states, so the
-  // accvgpr writes must not land next to their first use inside the loop.
-#pragma unroll
-  for (int c = 0; c < 8; c++) {
-    settle_acc(kv[c]);
-    settle_acc(vv[c]);
-  }
-  wait_dma();
-  __syncthreads();
-
-  // One stage: 64 queries of each of its kHeads heads against the wave's 32
-  // keys, each head as two 32-query sub-blocks j of 32 MFMAs -- S (8), dP (8),
-  // dV (8), dK (8). The stage is laid out as one fixed sequence of 64 kHeads
-  // slots, one MFMA per slot (head m / 64), fenced so the compiler keeps the
-  // order:
-  //  * the LDS operands of an MFMA are read kAhead MFMAs of the same
-  //    sub-block earlier -- across the boundary between heads too, so the
-  //    second head's first MFMAs do not wait for a fresh pipeline;
-  //  * the S chain starts from -lse*log2e and the K operand is pre-scaled by
-  //    scale*log2e, so the chain ends at the exponent: P = exp2(acc). P of
-  //    sub-block j is computed under its dP and first dV MFMAs, dS = P * acc
-  //    (the dP chain started from -delta) under its dV and first dK MFMAs, so
-  //    the VALU work runs while the matrix core is busy.
-  // On a diagonal stage (diag), key kp is visible from query index qi of
-  // sub-block j iff qi >= lim - 32j; other stages skip the mask. Queries past
-  // the block end carry -lse*log2e = -inf, so their P and dS are exactly 0.
-  constexpr int kAhead = 4;  // MFMAs of the same sub-block between a read and its use
-  constexpr int kSlotAhead = kInterleave ? 2 * kAhead : kAhead;
-  constexpr int kSlots = 64 * kHeads;
-  // Lane offsets of the operand reads; the second set carries a 64 KiB bias so
-  // that the reads of stage buffer 1 (at 64 KiB when kHeads is 2) keep their
-  // constant part within the 16-bit LDS instruction offset.
-  constexpr uint32_t kBuf1Bias = kHeads * 2 * kTileBytes >= 65536 ? 65536u : 0u;
-  const FwdLdsOffsets lo0 = make_fwd_lds_offsets(lane);
-  const FwdLdsOffsets lo1 = make_fwd_lds_offsets(lane, kBuf1Bias);
-  auto stage = [&](auto diag, auto bufc, int lim) __attribute__((always_inline)) {
-    constexpr int buf = decltype(bufc)::value;
-    const FwdLdsOffsets& lo = buf ? lo1 : lo0;
-    bf16x8 rq[kHeads][2][8], rg[kHeads][2][8], cg[kHeads][2][2][4], cq[kHeads][2][2][4];
-    f32x4 l2v[kHeads][2][4], dlv[kHeads][2][4];
-    f32x16 sc[kHeads][2], dpv[kHeads][2];
-    float p[kHeads][2][16], dsv[kHeads][2][16];
-    bf16x8 pb[kHeads][2][2], d8[kHeads][2][2];
-    // Q tile of head hh (minus the bias of the offset set used for this
-    // buffer); its dO tile follows it
-    auto qtile = [&](int hh) __attribute__((always_inline)) {
-      return smem + (buf * kHeads + hh) * 2 * kTileBytes - (buf ? kBuf1Bias : 0u);
-    };
-    // operands of slot M (head M / 64; sub-block and position of M % 64)
-    auto read_for = [&](auto mc) __attribute__((always_inline)) {
-      constexpr int M = decltype(mc)::value, hh = M / 64, m = M % 64, j = slot_sub(m), k = slot_pos(m);
-      const char* qt = qtile(hh);
-      const char* gt = qt + kTileBytes;
-      // rows 32j + sigma32(n) and the 16-row groups of the column reads are
-      // the lane offsets of lo plus 8192j / 4096(2j + cc) (immediates)
-      if constexpr (k < 8) {
-        rq[hh][j][k] = *reinterpret_cast<const bf16x8*>(qt + 8192 * j + lo.k[k]);
-      } else if constexpr (k < 16) {
-        rg[hh][j][k - 8] = *reinterpret_cast<const bf16x8*>(gt + 8192 * j + lo.k[k - 8]);
-      } else if constexpr (k < 24) {
-        constexpr int cc = (k - 16) >> 2, db = (k - 16) & 3;
-        cg[hh][j][cc][db] = lds_col8_at(gt + 4096 * (2 * j + cc), lo.v[db][0], lo.v[db][1]);
-      } else {
-        constexpr int cc = (k - 24) >> 2, db = (k - 24) & 3;
-        cq[hh][j][cc][db] = lds_col8_at(qt + 4096 * (2 * j + cc), lo.v[db][0], lo.v[db][1]);
-      }
-    };
-    // -lse*log2e (which 0) or -delta (which 1) of the lane's 16 queries of
-    // sub-block j of head hh, in the accumulator layout: register 4i + e holds
-    // query 16 (i / 2) + 4 (i % 2) + e of the lane's 8-row group
-    auto read_stats = [&](auto hc, auto jc, auto wc) __attribute__((always_inline)) {
-      constexpr int hh = decltype(hc)::value, j = decltype(jc)::value, which = decltype(wc)::value;
-      const float* src = &stats[buf][hh][which][0] + 32 * j + 8 * h;
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(src + 16 * (i >> 1) + 4 * (i & 1));
-        if constexpr (which) dlv[hh][j][i] = v;
-        else l2v[hh][j][i] = v;
-      }
-    };
-    auto acc_of = [&](const f32x4 (&x)[4]) __attribute__((always_inline)) {
-      f32x16 c;
-#pragma unroll
-      for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) c[4 * i + e] = x[i][e];
-      return c;
-    };
-    auto mfma_at = [&](auto mc) __attribute__((always_inline)) {
-      constexpr int M = decltype(mc)::value, hh = M / 64, m = M % 64, j = slot_sub(m), k = slot_pos(m);
-      if constexpr (k < 8) {
-        if constexpr (!TPR_DKDV_VGPR_SP) sc[hh][j] = mfma(rq[hh][j][k], kv[k], k == 0 ? acc_of(l2v[hh][j]) : sc[hh][j]);
-        else if constexpr (k == 0) sc[hh][j] = mfma_vsp_init(rq[hh][j][k], kv[k], acc_of(l2v[hh][j]));
-        else mfma_vsp_acc(sc[hh][j], rq[hh][j][k], kv[k]);
-      } else if constexpr (k < 16) {
-        if constexpr (!TPR_DKDV_VGPR_SP)
-          dpv[hh][j] = mfma(rg[hh][j][k - 8], vv[k - 8], k == 8 ? acc_of(dlv[hh][j]) : dpv[hh][j]);
-        else if constexpr (k == 8) dpv[hh][j] = mfma_vsp_init(rg[hh][j][k - 8], vv[k - 8], acc_of(dlv[hh][j]));
-        else mfma_vsp_acc(dpv[hh][j], rg[hh][j][k - 8], vv[k - 8]);
-      } else if constexpr (k < 24) {
-        constexpr int cc = (k - 16) >> 2, db = (k - 16) & 3;
-        dv[db] = mfma(pb[hh][j][cc], cg[hh][j][cc][db], dv[db]);
-      } else {
-        constexpr int cc = (k - 24) >> 2, db = (k - 24) & 3;
-        dk[db] = mfma(d8[hh][j][cc], cq[hh][j][cc][db], dk[db]);
-      }
-    };
-    // register r of a sub-block holds query 16*(r/8) + r%8 of the lane's 8-row group
-    auto p_elem = [&](auto hc, auto jc, auto rc) __attribute__((always_inline)) {
-      constexpr int hh = decltype(hc)::value, j = decltype(jc)::value, r = decltype(rc)::value;
-      constexpr int qi = 16 * (r >> 3) + (r & 7);
-      float x = sc[hh][j][r];  // scale*log2e*S - lse*log2e
-      if constexpr (decltype(diag)::value) x = qi >= lim - 32 * j ? x : -INFINITY;
-      p[hh][j][r] = fast_exp2(x);
-      if constexpr ((r & 7) == 7) {
-#pragma unroll
-        for (int i = 0; i < 8; i++) pb[hh][j][r >> 3][i] = static_cast<bf16>(p[hh][j][(r & 8) + i]);
-      }
-    };
-    auto ds_elem = [&](auto hc, auto jc, auto rc) __attribute__((always_inline)) {
-      constexpr int hh = decltype(hc)::value, j = decltype(jc)::value, r = decltype(rc)::value;
-      dsv[hh][j][r] = p[hh][j][r] * dpv[hh][j][r];  // the dP chain started from -delta
-      if constexpr ((r & 7) == 7) {
-#pragma unroll
-        for (int i = 0; i < 8; i++) d8[hh][j][r >> 3][i] = static_cast<bf16>(dsv[hh][j][(r & 8) + i]);
-      }
-    };
-    using I0 = std::integral_constant<int, 0>;
-    using I1 = std::integral_constant<int, 1>;
-    // Reads are issued in pairs, the later slot's first: LDS reads complete in
-    // order, so the wait before the earlier slot's MFMA covers both and the
-    // later slot's MFMA needs none.
-    static_for<kSlotAhead / 2>([&](auto pc) __attribute__((always_inline)) {
-      constexpr int q = 2 * decltype(pc)::value;
-      read_for(std::integral_constant<int, q + 1>{});
-      read_for(std::integral_constant<int, q>{});
-    });
-    read_stats(I0{}, I0{}, I0{});
-    read_stats(I0{}, I1{}, I0{});
-    static_for<kSlots>([&](auto mc) __attribute__((always_inline)) {
-      constexpr int M = decltype(mc)::value, hh = M / 64, m = M % 64, j = slot_sub(m), k = slot_pos(m);
-      using H = std::integral_constant<int, hh>;
-      using J = std::integral_constant<int, j>;
-      if constexpr (m % 2 == 0 && M + kSlotAhead + 1 < kSlots) {
-        read_for(std::integral_constant<int, M + kSlotAhead + 1>{});
-        read_for(std::integral_constant<int, M + kSlotAhead>{});
-      }
-      if constexpr (m == 56 && hh + 1 < kHeads) {  // the next head's -lse rows, ahead of its S chains
-        read_stats(std::integral_constant<int, hh + 1>{}, I0{}, I0{});
-        read_stats(std::integral_constant<int, hh + 1>{}, I1{}, I0{});
-      }
-      if constexpr (k == 4) read_stats(H{}, J{}, I1{});  // -delta: the dP chain starts from it at k = 8
-      mfma_at(mc);
-      static_for<16>([&](auto rc) __attribute__((always_inline)) {
-        constexpr int r = decltype(rc)::value;
-        if constexpr (k == 9 + (r * 10) / 16) p_elem(H{}, J{}, rc);   // P: slots 9..18 (pb[0] by 13, pb[1] by 18)
-        if constexpr (k == 19 + (r * 9) / 16) ds_elem(H{}, J{}, rc);  // dS: slots 19..27 (d8[0] by 22, d8[1] by 27)
-      });
-      __builtin_amdgcn_sched_barrier(0);
-    });
-  };
-
-  // Stages [sidx, end) of the stage loop, with (diag) or without the causal
-  // mask in the body.
-  // one stage; the buffer parity is a compile-time constant so that every
-  // LDS address in the stage is a precomputed lane offset plus an immediate
-  auto one_stage = [&](auto diag, auto bufc, int sidx) __attribute__((always_inline)) {
-    constexpr int buf = decltype(bufc)::value;
-    const int tok0 = __builtin_amdgcn_readfirstlane(qtab[cur.blk].y);
-    const StageCursor nxt = advance(cur);
-    if (sidx + 1 < nstage) issue(nxt, buf ^ 1);
-    if (wave_active) {
-      // key kp is visible from query index qi (of the stage) iff qi >= lim;
-      // off this wave's diagonal lim <= -64 (all visible)
-      const int lim = tok0 < kw0 + 31 ? kp - tok0 - 8 * h : -64;
-      stage(diag, bufc, lim);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; i++) {  // accumulators stay in AGPRs across the stage loop
-      settle_acc(dk[i]);
-      settle_acc(dv[i]);
-    }
-#pragma unroll
-    for (int c = 0; c < 8; c++) {  // so do the K/V operands (MFMAs read them there)
       settle_acc(kv[c]);
       settle_acc(vv[c]);
     }
-    cur = nxt;
-    wait_dma();  // stage sidx + 1 has landed
+    wait_dma();
     __syncthreads();
-  };
-  auto run_stages = [&](auto diag, int sidx, int end) __attribute__((always_inline)) {
-    constexpr std::integral_constant<int, 0> b0{};
-    constexpr std::integral_constant<int, 1> b1{};
-    if (sidx < end && (sidx & 1)) one_stage(diag, b1, sidx++);
-    for (; sidx + 1 < end; sidx += 2) {
-      one_stage(diag, b0, sidx);
-      one_stage(diag, b1, sidx + 1);
-    }
-    if (sidx < end) one_stage(diag, b0, sidx);
-  };
-  // (suffix) the leading stages whose query block crosses some wave's causal
-  // diagonal run with the mask, all later ones without it
-  int ndiag = 0;
-  if (!prefix) {
-    int nb = 0;
-    while (nb < qb_hi - qb_lo && qtab[nb].y < key0 + kDkdvKeys - 1) nb++;
-    ndiag = nb * spb;
-  }
-  run_stages(std::true_type{}, 0, ndiag);
-  run_stages(std::false_type{}, ndiag, nstage);
 
-  if (!wave_active) return;
-  // accumulator register r of lane l: key 8*(r/4) + 4*h + r%4 of the wave, d = 32*db + n
-  const int slot = item[DK_SLOT];
-  if (slot >= 0) {
-    // split tile: fp32 partial [kDkdvKeys][128] for dK (already scaled) then dV
-    float* pk = a.ws + static_cast<int64_t>(slot) * 2 * kDkdvKeys * kMfmaD;
-    float* pv = pk + kDkdvKeys * kMfmaD;
+    // One stage: 64 queries of each of its kHeads heads against the wave's 32
+    // keys, each head as two 32-query sub-blocks j of 32 MFMAs -- S (8), dP (8),
+    // dV (8), dK (8). The stage is laid out as one fixed sequence of 64 kHeads
+    // slots, one MFMA per slot (head m / 64), fenced so the compiler keeps the
+    // order:
+    //  * the LDS operands of an MFMA are read kAhead MFMAs of the same
+    //    sub-block earlier -- across the boundary between heads too, so the
+    //    second head's first MFMAs do not wait for a fresh pipeline;
+    //  * the S chain starts from -lse*log2e and the K operand is pre-scaled by
+    //    scale*log2e, so the chain ends at the exponent: P = exp2(acc). P of
+    //    sub-block j is computed under its dP and first dV MFMAs, dS = P * acc
+    //    (the dP chain started from -delta) under its dV and first dK MFMAs, so
+    //    the VALU work runs while the matrix core is busy.
+    // On a diagonal stage (diag), key kp is visible from query index qi of
+    // sub-block j iff qi >= lim - 32j; other stages skip the mask. Queries past
+    // the block end carry -lse*log2e = -inf, so their P and dS are exactly 0.
+    constexpr int kAhead = 4;  // MFMAs of the same sub-block between a read and its use
+    constexpr int kSlotAhead = kInterleave ? 2 * kAhead : kAhead;
+    constexpr int kSlots = 64 * kHeads;
+    // Lane offsets of the operand reads; the second set carries a 64 KiB bias so
+    // that the reads of stage buffer 1 (at 64 KiB when kHeads is 2) keep their
+    // constant part within the 16-bit LDS instruction offset.
+    constexpr uint32_t kBuf1Bias = kHeads * 2 * kTileBytes >= 65536 ? 65536u : 0u;
+    const FwdLdsOffsets lo0 = make_fwd_lds_offsets(lane);
+    const FwdLdsOffsets lo1 = make_fwd_lds_offsets(lane, kBuf1Bias);
+    auto stage = [&](auto diag, auto bufc, int lim) __attribute__((always_inline)) {
+      constexpr int buf = decltype(bufc)::value;
+      const FwdLdsOffsets& lo = buf ? lo1 : lo0;
+      bf16x8 rq[kHeads][2][8], rg[kHeads][2][8], cg[kHeads][2][2][4], cq[kHeads][2][2][4];
+      f32x4 l2v[kHeads][2][4], dlv[kHeads][2][4];
+      f32x16 sc[kHeads][2], dpv[kHeads][2];
+      float p[kHeads][2][16], dsv[kHeads][2][16];
+      bf16x8 pb[kHeads][2][2], d8[kHeads][2][2];
+      // Q tile of head hh (minus the bias of the offset set used for this
+      // buffer); its dO tile follows it
+      auto qtile = [&](int hh) __attribute__((always_inline)) {
+        return smem + (buf * kHeads + hh) * 2 * kTileBytes - (buf ? kBuf1Bias : 0u);
+      };
+      // operands of slot M (head M / 64; sub-block and position of M % 64)
+      auto read_for = [&](auto mc) __attribute__((always_inline)) {
+        constexpr int M = decltype(mc)::value, hh = M / 64, m = M % 64, j = slot_sub(m), k = slot_pos(m);
+        const char* qt = qtile(hh);
+        const char* gt = qt + kTileBytes;
+        // rows 32j + sigma32(n) and the 16-row groups of the column reads are
+        // the lane offsets of lo plus 8192j / 4096(2j + cc) (immediates)
+        if constexpr (k < 8) {
+          rq[hh][j][k] = *reinterpret_cast<const bf16x8*>(qt + 8192 * j + lo.k[k]);
+        } else if constexpr (k < 16) {
+          rg[hh][j][k - 8] = *reinterpret_cast<const bf16x8*>(gt + 8192 * j + lo.k[k - 8]);
+        } else if constexpr (k < 24) {
+          constexpr int cc = (k - 16) >> 2, db = (k - 16) & 3;
+          cg[hh][j][cc][db] = lds_col8_at(gt + 4096 * (2 * j + cc), lo.v[db][0], lo.v[db][1]);
+        } else {
+          constexpr int cc = (k - 24) >> 2, db = (k - 24) & 3;
+          cq[hh][j][cc][db] = lds_col8_at(qt + 4096 * (2 * j + cc), lo.v[db][0], lo.v[db][1]);
+        }
+      };
+      // -lse*log2e (which 0) or -delta (which 1) of the lane's 16 queries of
+      // sub-block j of head hh, in the accumulator layout: register 4i + e holds
+      // query 16 (i / 2) + 4 (i % 2) + e of the lane's 8-row group
+      auto read_stats = [&](auto hc, auto jc, auto wc) __attribute__((always_inline)) {
+        constexpr int hh = decltype(hc)::value, j = decltype(jc)::value, which = decltype(wc)::value;
+        const float* src = &stats[buf][hh][which][0] + 32 * j + 8 * h;
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int key = 32 * wave + 8 * (r >> 2) + 4 * h + (r & 3);
+        for (int i = 0; i < 4; i++) {
+          const f32x4 v = *reinterpret_cast<const f32x4*>(src + 16 * (i >> 1) + 4 * (i & 1));
+          if constexpr (which) dlv[hh][j][i] = v;
+          else l2v[hh][j][i] = v;
+        }
+      };
+      auto acc_of = [&](const f32x4 (&x)[4]) __attribute__((always_inline)) {
+        f32x16 c;
 #pragma unroll
-      for (int db = 0; db < 4; db++) {
-        pk[key * kMfmaD + 32 * db + n] = dk[db][r] * a.scale;
-        pv[key * kMfmaD + 32 * db + n] = dv[db][r];
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+          for (int e = 0; e < 4; e++) c[4 * i + e] = x[i][e];
+        return c;
+      };
+      auto mfma_at = [&](auto mc) __attribute__((always_inline)) {
+        constexpr int M = decltype(mc)::value, hh = M / 64, m = M % 64, j = slot_sub(m), k = slot_pos(m);
+        if constexpr (k < 8) {
+          if constexpr (!TPR_DKDV_VGPR_SP) sc[hh][j] = mfma(rq[hh][j][k], kv[k], k == 0 ? acc_of(l2v[hh][j]) : sc[hh][j]);
+          else if constexpr (k == 0) sc[hh][j] = mfma_vsp_init(rq[hh][j][k], kv[k], acc_of(l2v[hh][j]));
+          else mfma_vsp_acc(sc[hh][j], rq[hh][j][k], kv[k]);
+        } else if constexpr (k < 16) {
+          if constexpr (!TPR_DKDV_VGPR_SP)
+            dpv[hh][j] = mfma(rg[hh][j][k - 8], vv[k - 8], k == 8 ? acc_of(dlv[hh][j]) : dpv[hh][j]);
+          else if constexpr (k == 8) dpv[hh][j] = mfma_vsp_init(rg[hh][j][k - 8], vv[k - 8], acc_of(dlv[hh][j]));
+          else mfma_vsp_acc(dpv[hh][j], rg[hh][j][k - 8], vv[k - 8]);
+        } else if constexpr (k < 24) {
+          constexpr int cc = (k - 16) >> 2, db = (k - 16) & 3;
+          dv[db] = mfma(pb[hh][j][cc], cg[hh][j][cc][db], dv[db]);
+        } else {
+          constexpr int cc = (k - 24) >> 2, db = (k - 24) & 3;
+          dk[db] = mfma(d8[hh][j][cc], cq[hh][j][cc][db], dk[db]);
+        }
+      };
+      // register r of a sub-block holds query 16*(r/8) + r%8 of the lane's 8-row group
+      auto p_elem = [&](auto hc, auto jc, auto rc) __attribute__((always_inline)) {
+        constexpr int hh = decltype(hc)::value, j = decltype(jc)::value, r = decltype(rc)::value;
+        constexpr int qi = 16 * (r >> 3) + (r & 7);
+        float x = sc[hh][j][r];  // scale*log2e*S - lse*log2e
+        if constexpr (decltype(diag)::value) x = qi >= lim - 32 * j ? x : -INFINITY;
+        p[hh][j][r] = fast_exp2(x);
+        if constexpr ((r & 7) == 7) {
+#pragma unroll
+          for (int i = 0; i < 8; i++) pb[hh][j][r >> 3][i] = static_cast<bf16>(p[hh][j][(r & 8) + i]);
+        }
+      };
+      auto ds_elem = [&](auto hc, auto jc, auto rc) __attribute__((always_inline)) {
+        constexpr int hh = decltype(hc)::value, j = decltype(jc)::value, r = decltype(rc)::value;
+        dsv[hh][j][r] = p[hh][j][r] * dpv[hh][j][r];  // the dP chain started from -delta
+        if constexpr ((r & 7) == 7) {
+#pragma unroll
+          for (int i = 0; i < 8; i++) d8[hh][j][r >> 3][i] = static_cast<bf16>(dsv[hh][j][(r & 8) + i]);
+        }
+      };
+      using I0 = std::integral_constant<int, 0>;
+      using I1 = std::integral_constant<int, 1>;
+      // Reads are issued in pairs, the later slot's first: LDS reads complete in
+      // order, so the wait before the earlier slot's MFMA covers both and the
+      // later slot's MFMA needs none.
+      static_for<kSlotAhead / 2>([&](auto pc) __attribute__((always_inline)) {
+        constexpr int q = 2 * decltype(pc)::value;
+        read_for(std::integral_constant<int, q + 1>{});
+        read_for(std::integral_constant<int, q>{});
+      });
+      read_stats(I0{}, I0{}, I0{});
+      read_stats(I0{}, I1{}, I0{});
+      static_for<kSlots>([&](auto mc) __attribute__((always_inline)) {
+        constexpr int M = decltype(mc)::value, hh = M / 64, m = M % 64, j = slot_sub(m), k = slot_pos(m);
+        using H = std::integral_constant<int, hh>;
+        using J = std::integral_constant<int, j>;
+        if constexpr (m % 2 == 0 && M + kSlotAhead + 1 < kSlots) {
+          read_for(std::integral_constant<int, M + kSlotAhead + 1>{});
+          read_for(std::integral_constant<int, M + kSlotAhead>{});
+        }
+        if constexpr (m == 56 && hh + 1 < kHeads) {  // the next head's -lse rows, ahead of its S chains
+          read_stats(std::integral_constant<int, hh + 1>{}, I0{}, I0{});
+          read_stats(std::integral_constant<int, hh + 1>{}, I1{}, I0{});
+        }
+        if constexpr (k == 4) read_stats(H{}, J{}, I1{});  // -delta: the dP chain starts from it at k = 8
+        mfma_at(mc);
+        static_for<16>([&](auto rc) __attribute__((always_inline)) {
+          constexpr int r = decltype(rc)::value;
+          if constexpr (k == 9 + (r * 10) / 16) p_elem(H{}, J{}, rc);   // P: slots 9..18 (pb[0] by 13, pb[1] by 18)
+          if constexpr (k == 19 + (r * 9) / 16) ds_elem(H{}, J{}, rc);  // dS: slots 19..27 (d8[0] by 22, d8[1] by 27)
+        });
+        __builtin_amdgcn_sched_barrier(0);
+      });
+    };
+
+    // Stages [sidx, end) of the stage loop, with (diag) or without the causal
+    // mask in the body.
+    // one stage; the buffer parity is a compile-time constant so that every
+    // LDS address in the stage is a precomputed lane offset plus an immediate
+    auto one_stage = [&](auto diag, auto bufc, int sidx) __attribute__((always_inline)) {
+      constexpr int buf = decltype(bufc)::value;
+      const int tok0 = __builtin_amdgcn_readfirstlane(qtab[cur.blk].y);
+      const StageCursor nxt = advance(cur);
+      if (sidx + 1 < nstage) issue(nxt, buf ^ 1);
+      if (wave_active) {
+        // key kp is visible from query index qi (of the stage) iff qi >= lim;
+        // off this wave's diagonal lim <= -64 (all visible)
+        const int lim = tok0 < kw0 + 31 ? kp - tok0 - 8 * h : -64;
+        stage(diag, bufc, lim);
       }
+#pragma unroll
+      for (int i = 0; i < 4; i++) {  // accumulators stay in AGPRs across the stage loop
+        settle_acc(dk[i]);
+        settle_acc(dv[i]);
+      }
+#pragma unroll
+      for (int c = 0; c < 8; c++) {  // so do the K/V operands (MFMAs read them there)
+        settle_acc(kv[c]);
+        settle_acc(vv[c]);
+      }
+      cur = nxt;
+      wait_dma();  // stage sidx + 1 has landed
+      __syncthreads();
+    };
+    auto run_stages = [&](auto diag, int sidx, int end) __attribute__((always_inline)) {
+      constexpr std::integral_constant<int, 0> b0{};
+      constexpr std::integral_constant<int, 1> b1{};
+      if (sidx < end && (sidx & 1)) one_stage(diag, b1, sidx++);
+      for (; sidx + 1 < end; sidx += 2) {
+        one_stage(diag, b0, sidx);
+        one_stage(diag, b1, sidx + 1);
+      }
+      if (sidx < end) one_stage(diag, b0, sidx);
+    };
+    // (suffix) the stages whose query block crosses some wave's causal diagonal
+    // run with the mask -- the leading ones in first-last order, the trailing
+    // ones in last-first order -- all others without it
+    int ndiag = 0;
+    if (!prefix) {
+      int nb = 0;
+      while (nb < nblk && qtab[first_last ? nb : nblk - 1 - nb].y < key0 + kDkdvKeys - 1) nb++;
+      ndiag = nb * spb;
     }
-    return;
-  }
-  if (prefix && a.acc_prefix) {
-    // fp32 relay accumulators: add this (unsplit) tile's gradient, the scaled
-    // product rounded as the ordinary path rounds it, then one add (no fma)
+    const int lead = first_last ? ndiag : 0, trail = first_last ? nstage : nstage - ndiag;
+    run_stages(std::true_type{}, 0, lead);
+    run_stages(std::false_type{}, lead, trail);
+    run_stages(std::true_type{}, trail, nstage);
+
+    if (wave_active) {
+      // accumulator register r of lane l: key 8*(r/4) + 4*h + r%4 of the wave,
+      // d = 32*db + n. The lane index is laundered so the store addresses are
+      // formed here, not hoisted out of the tile loop (where they would stay
+      // live across the stage loop).
+      int el = lane;
+      asm volatile("" : "+v"(el));
+      const int n = el & 31, h = el >> 5;
+      const int slot = item[DK_SLOT];  // -1 for a pair: its tiles are never split
+      if (slot >= 0) {
+        // split tile: fp32 partial [kDkdvKeys][128] for dK (already scaled) then dV
+        float* pk = a.ws + static_cast<int64_t>(slot) * 2 * kDkdvKeys * kMfmaD;
+        float* pv = pk + kDkdvKeys * kMfmaD;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const int key = 32 * wave + 8 * (r >> 2) + 4 * h + (r & 3);
+#pragma unroll
+          for (int db = 0; db < 4; db++) {
+            pk[key * kMfmaD + 32 * db + n] = dk[db][r] * a.scale;
+            pv[key * kMfmaD + 32 * db + n] = dv[db][r];
+          }
+        }
+      } else if (prefix && a.acc_prefix) {
+        // fp32 relay accumulators: add this (unsplit) tile's gradient, the scaled
+        // product rounded as the ordinary path rounds it, then one add (no fma)
 #pragma clang fp contract(off)
-    float* dkf = static_cast<float*>(a.dpk);
-    float* dvf = static_cast<float*>(a.dpv);
+        float* dkf = static_cast<float*>(a.dpk);
+        float* dvf = static_cast<float*>(a.dpv);
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int key = kw0 + 8 * (r >> 2) + 4 * h + (r & 3);
-      if (key >= seg_len) continue;
-      const int64_t off = static_cast<int64_t>(seg_row0 + key) * kstride + kvh * kMfmaD + n;
+        for (int r = 0; r < 16; r++) {
+          const int key = kw0 + 8 * (r >> 2) + 4 * h + (r & 3);
+          if (key >= seg_len) continue;
+          const int64_t off = static_cast<int64_t>(seg_row0 + key) * kstride + kvh * kMfmaD + n;
 #pragma unroll
-      for (int db = 0; db < 4; db++) {
-        dkf[off + 32 * db] += dk[db][r] * a.scale;
-        dvf[off + 32 * db] += dv[db][r];
+          for (int db = 0; db < 4; db++) {
+            dkf[off + 32 * db] += dk[db][r] * a.scale;
+            dvf[off + 32 * db] += dv[db][r];
+          }
+        }
+      } else {
+        bf16* dkd = static_cast<bf16*>(prefix ? a.dpk : a.dk);
+        bf16* dvd = static_cast<bf16*>(prefix ? a.dpv : a.dv);
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const int key = kw0 + 8 * (r >> 2) + 4 * h + (r & 3);
+          if (key >= seg_len) continue;
+          const int64_t off = static_cast<int64_t>(seg_row0 + key) * kstride + kvh * kMfmaD + n;
+#pragma unroll
+          for (int db = 0; db < 4; db++) {
+            dkd[off + 32 * db] = static_cast<bf16>(dk[db][r] * a.scale);
+            dvd[off + 32 * db] = static_cast<bf16>(dv[db][r]);
+          }
+        }
       }
     }
-    return;
-  }
-  bf16* dkd = static_cast<bf16*>(prefix ? a.dpk : a.dk);
-  bf16* dvd = static_cast<bf16*>(prefix ? a.dpv : a.dv);
-#pragma unroll
-  for (int r = 0; r < 16; r++) {
-    const int key = kw0 + 8 * (r >> 2) + 4 * h + (r & 3);
-    if (key >= seg_len) continue;
-    const int64_t off = static_cast<int64_t>(seg_row0 + key) * kstride + kvh * kMfmaD + n;
-#pragma unroll
-    for (int db = 0; db < 4; db++) {
-      dkd[off + 32 * db] = static_cast<bf16>(dk[db][r] * a.scale);
-      dvd[off + 32 * db] = static_cast<bf16>(dv[db][r]);
-    }
-  }
+  }  // tiles
 }
 
 // ---------------------------------------------------------------------------

@@ -581,9 +581,12 @@ __global__ __launch_bounds__(256) void m16_dkdv(KernelArgs a) {
 
   __shared__ __attribute__((aligned(1024))) char smem[2 * 2 * T::TB];           // [buf][Q | dO]
   __shared__ __attribute__((aligned(256))) float stats[2][2][kTileRows];       // [buf][-lse*log2e | -delta][row]
+  // query-block table; a suffix tile streams its blocks last-first, so the
+  // tiles of one leaf that run together start on the same block and share
+  // its copies in L2
   __shared__ int4 qtab[kDkdvMaxBlocks];
   for (int i = threadIdx.x; i < qb_hi - qb_lo; i += blockDim.x) {
-    const int qb = qb_lo + i;
+    const int qb = prefix ? qb_lo + i : qb_hi - 1 - i;
     const int lf = qblk[2 * qb], tok = qblk[2 * qb + 1];
     const int r0 = cu[lf];
     qtab[i] = int4{r0 + tok, tok, min(kTileRows, cu[lf + 1] - r0 - tok), 0};

@@ -296,10 +296,34 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
     for (int k0 = 0; k0 < len; k0 += KT)
       for (int h = 0; h < Hkv; h++) add_tile(0, n, k0, h, lo, hi);
   }
+  // Suffix tiles: on the head_dim-128 MFMA path, tile j of a leaf with T
+  // tiles is paired with its mirror T-1-j in one item (DK_PAIR) when neither
+  // is split: the pair streams the mirror's blocks last-first, then tile j's
+  // first-last, so all pairs of a leaf take about the same time and read the
+  // same query block at the same time (the copies are shared in L2).
+  const bool pair_tiles = path == PATH_MFMA;
   for (int s = 0; s < N; s++) {
     const int len = cu[s + 1] - cu[s];
-    for (int k0 = 0; k0 < len; k0 += KT)
-      for (int h = 0; h < Hkv; h++) add_tile(1, s, k0, h, leaf_qblk[s] + k0 / BQ, leaf_qblk[s + 1]);
+    const int tiles = (len + KT - 1) / KT;
+    auto first_block = [&](int j) { return leaf_qblk[s] + j * KT / BQ; };
+    for (int j = 0; j < tiles; j++) {
+      const int mirror = tiles - 1 - j;
+      const int lo_tile = std::min(j, mirror);   // the longer query range
+      if (pair_tiles && mirror != j && leaf_qblk[s + 1] - first_block(lo_tile) <= kDkdvMaxBlocks) {
+        if (j == lo_tile) {
+          const int32_t blocks = (leaf_qblk[s + 1] - first_block(j)) + (leaf_qblk[s + 1] - first_block(mirror));
+          for (int h = 0; h < Hkv; h++) {
+            Item it;
+            it.words = {1, s, mirror * KT, h, first_block(mirror), leaf_qblk[s + 1], -1, j * KT + 1};
+            it.work = static_cast<int64_t>(blocks) * G + 2;
+            it.kvh = h;
+            dkdv.push_back(std::move(it));
+          }
+        }
+        continue;
+      }
+      for (int h = 0; h < Hkv; h++) add_tile(1, s, j * KT, h, first_block(j), leaf_qblk[s + 1]);
+    }
   }
   int32_t n_dkdv = 0;
   std::vector<int32_t> dkdv_words = order_for_xcds(dkdv, Hkv, DK_WORDS, &n_dkdv);

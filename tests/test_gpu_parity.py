@@ -46,6 +46,10 @@ def _meta_cases():
         "deep_run_list": (M(cu_seqlens_q=(0, 50, 179, 243), node_offsets=_offsets(_DEEP_LENS[::-1]),
                             leaf_ancestors=(tuple(range(11, -1, -1)), tuple(range(11, 2, -1)),
                                             tuple(range(11, 8, -1)))), 8, 2),
+        # suffix dK/dV tiles paired with their mirrors: 3 tiles (a pair and a
+        # lone middle tile), 2 tiles with a 1-key mirror, 4 tiles (two pairs),
+        # 1 tile, 3 tiles with a 4-key last tile
+        "paired_suffix_tiles": (M.shared_prefix(100, [333, 129, 400, 64, 260]), 8, 2),
     }
 
 
@@ -60,7 +64,7 @@ def _offsets(lens):
 
 
 CASES = ["shared_prefix_gqa4", "no_prefix", "tile_aligned", "mha", "gqa2", "gqa3", "depth3_tree",
-         "unused_node", "empty_leaf", "deep_chain_one_run", "deep_run_list"]
+         "unused_node", "empty_leaf", "deep_chain_one_run", "deep_run_list", "paired_suffix_tiles"]
 KEY_RUNS = {"deep_chain_one_run": 1, "deep_run_list": 12}   # plan header word 29: most runs of a leaf
 
 
@@ -105,6 +109,14 @@ def test_mfma_bf16_matches_oracle(name, cuda_device):
         assert rel_l2(g, r) <= BF16_PREFIX_GRAD_REL_L2
     if name == "unused_node":
         assert torch.count_nonzero(grads[3][10:]) == 0 and torch.count_nonzero(grads[4][10:]) == 0
+    # every 128-key dK/dV tile of every leaf on its own: a tile written by the
+    # wrong item, or not at all, hides in a whole-tensor cosine but has a
+    # relative error near 1 (the bound leaves room for a tile of one key,
+    # whose few dS values may cancel)
+    for s, (a, b) in enumerate(zip(meta.cu_seqlens_q[:-1], meta.cu_seqlens_q[1:])):
+        for k0 in range(a, b, 128):
+            for g, r in zip(grads[1:3], rg[1:3]):
+                assert rel_l2(g[k0:min(b, k0 + 128)], r[k0:min(b, k0 + 128)]) <= 0.1, (s, k0 - a)
 
 
 def test_fp32_plumbing_config_matches_oracle(cuda_device):

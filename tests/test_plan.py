@@ -29,6 +29,22 @@ def decode(plan):
     return w, fwd, dkdv, qblk
 
 
+def tiles_of(dkdv, block_rows=64):
+    """The (src, seg, key0, kvh, lo, hi, slot) tiles of dK/dV items, a paired
+    item (last word 1 + second key0) giving both of its suffix tiles; the
+    second tile's query range starts (key0 - key0b) / block_rows blocks
+    earlier and ends at the same block."""
+    out = []
+    for src, seg, key0, kvh, lo, hi, slot, pair in dkdv:
+        if src < 0:
+            continue
+        out.append((src, seg, key0, kvh, lo, hi, slot))
+        if pair > 0:
+            k0b = pair - 1
+            out.append((src, seg, k0b, kvh, lo - (key0 - k0b) // block_rows, hi, slot))
+    return out
+
+
 @pytest.mark.parametrize("hq,hkv", [(32, 8), (8, 2), (4, 4), (6, 2), (4, 2)])
 def test_forward_items_cover_every_query_row_once(hq, hkv):
     meta = TPRPrefixMeta(cu_seqlens_q=(0, 100, 100, 357), node_offsets=(0, 64, 200),
@@ -63,8 +79,11 @@ def test_xcd_ordering_pins_kv_heads_and_is_lpt_per_xcd():
     # the prefix tiles' query range (4 siblings x 64 query blocks) is below one
     # CU's share of the launch (about 388 blocks), so no tile is split
     tpw = 32 * (FWD_WAVES // 4)  # tokens per forward workgroup (4 query heads of the group)
-    assert len(fwd) == 4 * (4096 // tpw) * 8 and len(dkdv) == (32 + 4 * 32) * 8
+    # dK/dV: 32 prefix tiles, and each leaf's 32 suffix tiles as 16 mirror
+    # pairs (tile j with tile 31 - j), per KV head
+    assert len(fwd) == 4 * (4096 // tpw) * 8 and len(dkdv) == (32 + 4 * 16) * 8
     assert all(item[6] == -1 for item in dkdv) and plan.host[23].item() == 0   # no partial slots, no reductions
+    assert len(tiles_of(dkdv)) == (32 + 4 * 32) * 8
     for i, (leaf, tok0, qh0, kvh) in enumerate(fwd):
         assert leaf >= 0 and kvh == i % 8
     for i, item in enumerate(dkdv):
@@ -93,9 +112,7 @@ def test_dkdv_items_cover_every_key_tile_and_query_block():
     w, _, dkdv, qblk = decode(plan)
     leaf_qblk = w[w[PF["OFF_LEAF_QBLK"]]: w[PF["OFF_LEAF_QBLK"]] + 5]
     seen = Counter()
-    for src, seg, key0, kvh, lo, hi, slot, _ in dkdv:
-        if src < 0:
-            continue
+    for src, seg, key0, kvh, lo, hi, slot in tiles_of(dkdv):
         assert slot == -1
         seen[(src, seg, key0, kvh)] += 1
         leaves = {qblk[i][0] for i in range(lo, hi)}
@@ -139,12 +156,70 @@ def test_split_prefix_tiles_have_ordered_partials_and_reductions():
         for a, b in zip(parts, parts[1:]):
             assert a[5] == b[4]
         assert all(p[5] - p[4] <= (64 if src == 0 else 256) for p in parts)
-    # every direct item streams at most 256 query blocks (its LDS table)
-    assert all(item[5] - item[4] <= 256 for item in dkdv if item[0] >= 0)
+    # every direct tile streams at most 256 query blocks (its LDS table)
+    assert all(t[5] - t[4] <= 256 for t in tiles_of(dkdv))
     # each (tile, head) is either direct or reduced, never both
-    direct = {item[:4] for item in dkdv if item[0] >= 0 and item[6] < 0}
+    direct = {t[:4] for t in tiles_of(dkdv) if t[6] < 0}
     reduced = {r[:4] for r in reds}
     assert not direct & reduced
+
+
+def test_suffix_tiles_pair_with_their_mirror():
+    """head_dim-128 MFMA path: suffix tile j of a leaf with T tiles shares an
+    item with tile T-1-j (the shorter one named first), so all pairs of a leaf
+    stream the same number of query blocks; the middle tile of an odd count,
+    and tiles whose query range is split (and their mirrors), stay alone; every
+    (tile, KV head) is covered once."""
+    lens = [4096, 4000, 333, 100, 20000]
+    meta = TPRPrefixMeta.shared_prefix(256, lens)
+    plan = meta.plan(8, 2, 128, torch.bfloat16, CPU)
+    w, _, dkdv, qblk = decode(plan)
+    leaf_qblk = w[w[PF["OFF_LEAF_QBLK"]]: w[PF["OFF_LEAF_QBLK"]] + len(lens) + 1]
+    items = [it for it in dkdv if it[0] >= 0]
+    pair_blocks = {}
+    paired = set()
+    for src, seg, key0, kvh, lo, hi, slot, pair in items:
+        if pair == 0:
+            continue
+        ntiles = -(-lens[seg] // 128)
+        k0b = pair - 1
+        assert src == 1 and slot == -1 and key0 > k0b and key0 // 128 == ntiles - 1 - k0b // 128
+        assert lo == leaf_qblk[seg] + key0 // 64 and hi == leaf_qblk[seg + 1]
+        long_range = hi - (leaf_qblk[seg] + k0b // 64)
+        assert long_range <= 256
+        pair_blocks.setdefault(seg, set()).add((hi - lo) + long_range)
+        paired |= {(seg, key0 // 128, kvh), (seg, k0b // 128, kvh)}
+    # all pairs of a leaf stream the same number of blocks
+    assert all(len(v) == 1 for v in pair_blocks.values())
+    singles = {(it[1], it[2] // 128, it[3]) for it in items if it[0] == 1 and it[7] == 0}
+    for seg, n in enumerate(lens):
+        ntiles = -(-n // 128)
+        blocks = leaf_qblk[seg + 1] - leaf_qblk[seg]
+        for j in range(ntiles):
+            mirror = ntiles - 1 - j
+            long_j = min(j, mirror)
+            pairable = mirror != j and blocks - 2 * long_j <= 256
+            for h in range(2):
+                assert ((seg, j, h) in paired) == pairable, (seg, j)
+                assert ((seg, j, h) in singles) != pairable, (seg, j)
+    # the 20000-token leaf: tiles 0..28 stream more than 256 blocks (split), so
+    # they and their mirrors 128..156 stay alone, and so does the middle tile 78
+    assert {j for (seg, j, h) in singles if seg == 4 and h == 0} == set(range(29)) | set(range(128, 157)) | {78}
+    assert {j for (seg, j, h) in singles if seg == 2 and h == 0} == {1} and (3, 0, 0) in singles
+    # coverage of every (tile, head) once, prefix and suffix
+    seen = Counter(t[:4] for t in tiles_of(dkdv) if t[6] < 0)
+    reds = [tuple(w[w[24] + 8 * i: w[24] + 8 * i + 8]) for i in range(w[PF["N_RED"]])]
+    seen.update(r[:4] for r in reds)
+    expected = {(0, 0, k0, h) for k0 in (0, 128) for h in range(2)}
+    expected |= {(1, s, k0, h) for s, n in enumerate(lens) for k0 in range(0, n, 128) for h in range(2)}
+    assert set(seen) == expected and set(seen.values()) == {1}
+
+
+def test_suffix_tiles_stay_single_off_the_head_dim_128_path():
+    meta = TPRPrefixMeta.shared_prefix(64, [1000, 700])
+    for d, dtype in ((64, torch.bfloat16), (256, torch.bfloat16), (128, torch.float32)):
+        _, _, dkdv, _ = decode(meta.plan(8, 2, d, dtype, CPU))
+        assert all(it[7] == 0 for it in dkdv)
 
 
 def key_runs(plan):
