@@ -439,8 +439,8 @@ def main() -> int:
     total_flops = 7.0 * unit            # fwd (2 GEMMs) + bwd (5 GEMMs)
     value = total_flops / (ms_per_step * 1e-3) / 1e12
     # the SIMT kernels compute in fp32 on the vector ALUs, whatever the I/O dtype
-    peak = BF16_PEAK_TFLOPS if plan.path in ("mfma", "mfma16") else FP32_PEAK_TFLOPS
-    prefix = {"mfma": "tpr::mfma_", "mfma16": "tpr::m16_", "simt": "tpr::simt_"}[plan.path]
+    peak = BF16_PEAK_TFLOPS if plan.path == "mfma" else FP32_PEAK_TFLOPS
+    prefix = {"32x32x16": "tpr::mfma_", "16x16x32": "tpr::m16_", None: "tpr::simt_"}[plan.mfma_shape]
     kernels = {
         "fwd": (fwd_ms, 2.0 * unit, prefix + "fwd"),
         "dkdv": (dkdv_ms, 4.0 * unit, prefix + "dkdv"),

@@ -563,8 +563,7 @@ __global__ __launch_bounds__(256) void m16_dkdv(KernelArgs a) {
   const int32_t* item = a.plan + a.off_dkdv + DK_WORDS * blockIdx.x;
   if (item[DK_SRC] < 0) return;
   const bool prefix = item[DK_SRC] == 0;
-  const int seg = item[DK_SEG], key0 = item[DK_KEY0], kvh = item[DK_KVH];
-  const int qb_lo = item[DK_QB_LO], qb_hi = item[DK_QB_HI];
+  const int seg = item[DK_SEG], kvh = item[DK_KVH];
   const int32_t* cu = a.plan + a.off_cu;
   const int32_t* no = a.plan + a.off_node_off;
   const int32_t* qblk = a.plan + a.off_qblk;
@@ -573,207 +572,224 @@ __global__ __launch_bounds__(256) void m16_dkdv(KernelArgs a) {
 
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int i16 = lane & 15, g = lane >> 4;
-  const int kw0 = key0 + kWaveKeys * wave;  // first key position of this wave
-  const bool wave_active = kw0 < seg_len;
 
   const int64_t kstride = static_cast<int64_t>(a.hkv) * kD;
   const uint32_t qrow_bytes = static_cast<uint32_t>(a.hq) * kD * 2;
 
   __shared__ __attribute__((aligned(1024))) char smem[2 * 2 * T::TB];           // [buf][Q | dO]
   __shared__ __attribute__((aligned(256))) float stats[2][2][kTileRows];       // [buf][-lse*log2e | -delta][row]
-  // query-block table; a suffix tile streams its blocks last-first, so the
-  // tiles of one leaf that run together start on the same block and share
-  // its copies in L2
   __shared__ int4 qtab[kDkdvMaxBlocks];
-  for (int i = threadIdx.x; i < qb_hi - qb_lo; i += blockDim.x) {
-    const int qb = prefix ? qb_lo + i : qb_hi - 1 - i;
-    const int lf = qblk[2 * qb], tok = qblk[2 * qb + 1];
-    const int r0 = cu[lf];
-    qtab[i] = int4{r0 + tok, tok, min(kTileRows, cu[lf + 1] - r0 - tok), 0};
-  }
-  __syncthreads();
 
-  const int group = a.group;
-  const int nstage = (qb_hi - qb_lo) * group;  // stage s: query block s / group, head s % group
-  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(smem));
-  const uint32_t stats0 = __builtin_amdgcn_readfirstlane(lds_address(stats));
-  auto issue = [&](int blk, int hh, int buf) {
-    const int4 e = qtab[blk];
-    const int row = __builtin_amdgcn_readfirstlane(e.x), nq = __builtin_amdgcn_readfirstlane(e.z);
-    const int qh = kvh * group + hh;
-    const int64_t off = static_cast<int64_t>(qh) * kD * 2 + static_cast<int64_t>(row) * qrow_bytes;
-    const uint32_t tile = lds0 + buf * 2 * T::TB;
-    copy_tile<kD>(reinterpret_cast<const char*>(a.q) + off, qrow_bytes, nq, tile, wave, lane);
-    copy_tile<kD>(reinterpret_cast<const char*>(a.dout) + off, qrow_bytes, nq, tile + T::TB, wave, lane);
-    if (wave < 2) {  // wave 0: -lse*log2e, wave 1: -delta; rows past the block end copy -inf / 0
-      const int64_t at = static_cast<int64_t>(qh) * a.total_q + row + lane;
-      const float* rows = wave == 0 ? a.stat_ws + kStatRowsOffset : a.ndelta_ws;
-      dma4_lane(lane < nq ? rows + at : a.stat_ws + wave, stats0 + (buf * 2 + wave) * kTileRows * 4);
-    }
-  };
-  if (nstage > 0) issue(0, 0, 0);
+  // An item is one key tile, or two suffix tiles of one leaf (DK_PAIR), a
+  // tile and its mirror: the first streams its query blocks last-first, the
+  // second first-last, so the pairs of a leaf that run together read the
+  // same block at the same time and share its copies in L2. A lone suffix
+  // tile streams last-first (all tiles of a leaf end at its last block);
+  // prefix tiles first-last.
+  const int ntiles = item[DK_PAIR] > 0 ? 2 : 1;
+  for (int tile = 0; tile < ntiles; tile++) {
+    const int key0 = tile == 0 ? item[DK_KEY0] : item[DK_PAIR] - 1;
+    const int qb_hi = item[DK_QB_HI];
+    const int qb_lo = tile == 0 ? item[DK_QB_LO] : item[DK_QB_LO] - (item[DK_KEY0] - key0) / kTileRows;
+    const bool first_last = prefix || tile == 1;
+    const int kw0 = key0 + kWaveKeys * wave;  // first key position of this wave
+    const bool wave_active = kw0 < seg_len;
 
-  // K / V of the lane's key kw0 + 16 kb + l % 16: the B operands of
-  // S = Q K^T and dP = dO V^T
-  bf16x8 kv[KB][T::NS], vv[KB][T::NS];
-#pragma unroll
-  for (int kb = 0; kb < KB; kb++) {
-    const bf16* kbase = static_cast<const bf16*>(prefix ? a.pk : a.k);
-    const bf16* vbase = static_cast<const bf16*>(prefix ? a.pv : a.v);
-    const int key = min(kw0 + 16 * kb + i16, seg_len - 1);
-    const int64_t off = static_cast<int64_t>(seg_row0 + key) * kstride + kvh * kD + 8 * g;
-#pragma unroll
-    for (int s = 0; s < T::NS; s++) {
-      kv[kb][s] = *reinterpret_cast<const bf16x8*>(kbase + off + 32 * s);
-      vv[kb][s] = *reinterpret_cast<const bf16x8*>(vbase + off + 32 * s);
+    if (tile > 0) __syncthreads();  // every wave is done with the previous tile's table
+    for (int i = threadIdx.x; i < qb_hi - qb_lo; i += blockDim.x) {
+      const int qb = first_last ? qb_lo + i : qb_hi - 1 - i;
+      const int lf = qblk[2 * qb], tok = qblk[2 * qb + 1];
+      const int r0 = cu[lf];
+      qtab[i] = int4{r0 + tok, tok, min(kTileRows, cu[lf + 1] - r0 - tok), 0};
     }
-  }
-  // register r of block [kb][db]: key 16 kb + 4 g + r of the wave, head dim 16 db + l % 16
-  f32x4 dk[KB][T::ND], dv[KB][T::ND];
-#pragma unroll
-  for (int kb = 0; kb < KB; kb++)
-#pragma unroll
-    for (int db = 0; db < T::ND; db++) {
-      dk[kb][db] = f32x4{};
-      dv[kb][db] = f32x4{};
-    }
-  const float c2 = a.scale * kLog2e;
-#pragma unroll
-  for (int kb = 0; kb < KB; kb++)
-#pragma unroll
-    for (int s = 0; s < T::NS; s++) {
-      settle(kv[kb][s]);
-      settle(vv[kb][s]);
-    }
-  wait_dma();
-  __syncthreads();
+    __syncthreads();
 
-  for (int sidx = 0; sidx < nstage; sidx++) {
-    const int buf = sidx & 1;
-    const int blk = sidx / group;
-    if (sidx + 1 < nstage) issue((sidx + 1) / group, (sidx + 1) % group, buf ^ 1);
-    if (wave_active) {
-      const int tok0 = __builtin_amdgcn_readfirstlane(qtab[blk].y);
-      const char* qt = smem + buf * 2 * T::TB;
-      const char* gt = qt + T::TB;
-      const float* nlse = &stats[buf][0][0];
-      const float* ndel = &stats[buf][1][0];
-      // query q of the block visible from key kp iff kp <= tok0 + q (suffix tiles)
-      const bool diag = !prefix && tok0 < kw0 + kWaveKeys - 1;
+    const int group = a.group;
+    const int nstage = (qb_hi - qb_lo) * group;  // stage s: query block s / group, head s % group
+    const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(smem));
+    const uint32_t stats0 = __builtin_amdgcn_readfirstlane(lds_address(stats));
+    auto issue = [&](int blk, int hh, int buf) {
+      const int4 e = qtab[blk];
+      const int row = __builtin_amdgcn_readfirstlane(e.x), nq = __builtin_amdgcn_readfirstlane(e.z);
+      const int qh = kvh * group + hh;
+      const int64_t off = static_cast<int64_t>(qh) * kD * 2 + static_cast<int64_t>(row) * qrow_bytes;
+      const uint32_t tile = lds0 + buf * 2 * T::TB;
+      copy_tile<kD>(reinterpret_cast<const char*>(a.q) + off, qrow_bytes, nq, tile, wave, lane);
+      copy_tile<kD>(reinterpret_cast<const char*>(a.dout) + off, qrow_bytes, nq, tile + T::TB, wave, lane);
+      if (wave < 2) {  // wave 0: -lse*log2e, wave 1: -delta; rows past the block end copy -inf / 0
+        const int64_t at = static_cast<int64_t>(qh) * a.total_q + row + lane;
+        const float* rows = wave == 0 ? a.stat_ws + kStatRowsOffset : a.ndelta_ws;
+        dma4_lane(lane < nq ? rows + at : a.stat_ws + wave, stats0 + (buf * 2 + wave) * kTileRows * 4);
+      }
+    };
+    if (nstage > 0) issue(0, 0, 0);
+
+    // K / V of the lane's key kw0 + 16 kb + l % 16: the B operands of
+    // S = Q K^T and dP = dO V^T
+    bf16x8 kv[KB][T::NS], vv[KB][T::NS];
 #pragma unroll
-      for (int t = 0; t < 2; t++) {
-        float pf[KB][2][4], df[KB][2][4];  // [key block][query block 2t + e][register]
+    for (int kb = 0; kb < KB; kb++) {
+      const bf16* kbase = static_cast<const bf16*>(prefix ? a.pk : a.k);
+      const bf16* vbase = static_cast<const bf16*>(prefix ? a.pv : a.v);
+      const int key = min(kw0 + 16 * kb + i16, seg_len - 1);
+      const int64_t off = static_cast<int64_t>(seg_row0 + key) * kstride + kvh * kD + 8 * g;
 #pragma unroll
-        for (int e = 0; e < 2; e++) {
-          const int b = 2 * t + e;
-          f32x4 sa[KB], pa[KB];
+      for (int s = 0; s < T::NS; s++) {
+        kv[kb][s] = *reinterpret_cast<const bf16x8*>(kbase + off + 32 * s);
+        vv[kb][s] = *reinterpret_cast<const bf16x8*>(vbase + off + 32 * s);
+      }
+    }
+    // register r of block [kb][db]: key 16 kb + 4 g + r of the wave, head dim 16 db + l % 16
+    f32x4 dk[KB][T::ND], dv[KB][T::ND];
 #pragma unroll
-          for (int kb = 0; kb < KB; kb++) {
-            sa[kb] = f32x4{};
-            pa[kb] = f32x4{};
-          }
+    for (int kb = 0; kb < KB; kb++)
 #pragma unroll
-          for (int s = 0; s < T::NS; s++) {
-            const bf16x8 qop = row_operand<kD>(qt, b, s, lane);
-            const bf16x8 gop = row_operand<kD>(gt, b, s, lane);
+      for (int db = 0; db < T::ND; db++) {
+        dk[kb][db] = f32x4{};
+        dv[kb][db] = f32x4{};
+      }
+    const float c2 = a.scale * kLog2e;
+#pragma unroll
+    for (int kb = 0; kb < KB; kb++)
+#pragma unroll
+      for (int s = 0; s < T::NS; s++) {
+        settle(kv[kb][s]);
+        settle(vv[kb][s]);
+      }
+    wait_dma();
+    __syncthreads();
+
+    for (int sidx = 0; sidx < nstage; sidx++) {
+      const int buf = sidx & 1;
+      const int blk = sidx / group;
+      if (sidx + 1 < nstage) issue((sidx + 1) / group, (sidx + 1) % group, buf ^ 1);
+      if (wave_active) {
+        const int tok0 = __builtin_amdgcn_readfirstlane(qtab[blk].y);
+        const char* qt = smem + buf * 2 * T::TB;
+        const char* gt = qt + T::TB;
+        const float* nlse = &stats[buf][0][0];
+        const float* ndel = &stats[buf][1][0];
+        // query q of the block visible from key kp iff kp <= tok0 + q (suffix tiles)
+        const bool diag = !prefix && tok0 < kw0 + kWaveKeys - 1;
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+          float pf[KB][2][4], df[KB][2][4];  // [key block][query block 2t + e][register]
+#pragma unroll
+          for (int e = 0; e < 2; e++) {
+            const int b = 2 * t + e;
+            f32x4 sa[KB], pa[KB];
 #pragma unroll
             for (int kb = 0; kb < KB; kb++) {
-              sa[kb] = mfma16(qop, kv[kb][s], sa[kb]);
-              pa[kb] = mfma16(gop, vv[kb][s], pa[kb]);
+              sa[kb] = f32x4{};
+              pa[kb] = f32x4{};
+            }
+#pragma unroll
+            for (int s = 0; s < T::NS; s++) {
+              const bf16x8 qop = row_operand<kD>(qt, b, s, lane);
+              const bf16x8 gop = row_operand<kD>(gt, b, s, lane);
+#pragma unroll
+              for (int kb = 0; kb < KB; kb++) {
+                sa[kb] = mfma16(qop, kv[kb][s], sa[kb]);
+                pa[kb] = mfma16(gop, vv[kb][s], pa[kb]);
+              }
+              __builtin_amdgcn_sched_barrier(0);
+            }
+            // register r: query q0 + r of the block
+            const int q0 = 32 * t + 8 * g + 4 * e;
+            const f32x4 ls = *reinterpret_cast<const f32x4*>(nlse + q0);
+            const f32x4 dl = *reinterpret_cast<const f32x4*>(ndel + q0);
+#pragma unroll
+            for (int kb = 0; kb < KB; kb++) {
+              const int kp = kw0 + 16 * kb + i16;
+#pragma unroll
+              for (int r = 0; r < 4; r++) {
+                float x = fmaf(sa[kb][r], c2, ls[r]);
+                if (diag) x = kp <= tok0 + q0 + r ? x : -INFINITY;
+                pf[kb][e][r] = fast_exp2(x);
+                df[kb][e][r] = pf[kb][e][r] * (pa[kb][r] + dl[r]);
+              }
+            }
+          }
+          bf16x8 pT[KB], dT[KB];  // queries 32 t + 8 g + 0..7 of key 16 kb + l % 16
+#pragma unroll
+          for (int kb = 0; kb < KB; kb++) {
+            pT[kb] = pack8(pf[kb][0], pf[kb][1]);
+            dT[kb] = pack8(df[kb][0], df[kb][1]);
+          }
+#pragma unroll
+          for (int db = 0; db < T::ND; db++) {
+            const bf16x8 gcol = col_operand<kD>(gt, 32 * t, 16 * db, lane);
+            const bf16x8 qcol = col_operand<kD>(qt, 32 * t, 16 * db, lane);
+#pragma unroll
+            for (int kb = 0; kb < KB; kb++) {
+              dv[kb][db] = mfma16(pT[kb], gcol, dv[kb][db]);
+              dk[kb][db] = mfma16(dT[kb], qcol, dk[kb][db]);
             }
             __builtin_amdgcn_sched_barrier(0);
           }
-          // register r: query q0 + r of the block
-          const int q0 = 32 * t + 8 * g + 4 * e;
-          const f32x4 ls = *reinterpret_cast<const f32x4*>(nlse + q0);
-          const f32x4 dl = *reinterpret_cast<const f32x4*>(ndel + q0);
+        }
+      }
+      wait_dma();  // stage sidx + 1 has landed
+      __syncthreads();
+    }
+
+    if (wave_active) {
+      // lane index laundered so the store addresses are formed here, not
+      // hoisted out of the tile loop
+      int el = lane;
+      asm volatile("" : "+v"(el));
+      const int i16 = el & 15, g = el >> 4;
+      const int slot = item[DK_SLOT];  // -1 for a pair: its tiles are never split
+      if (slot >= 0) {  // split tile: fp32 partial [kKeys][kD] for dK (already scaled) then dV
+        float* pk = a.ws + static_cast<int64_t>(slot) * 2 * kKeys * kD;
+        float* pv = pk + kKeys * kD;
 #pragma unroll
-          for (int kb = 0; kb < KB; kb++) {
-            const int kp = kw0 + 16 * kb + i16;
+        for (int kb = 0; kb < KB; kb++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-              float x = fmaf(sa[kb][r], c2, ls[r]);
-              if (diag) x = kp <= tok0 + q0 + r ? x : -INFINITY;
-              pf[kb][e][r] = fast_exp2(x);
-              df[kb][e][r] = pf[kb][e][r] * (pa[kb][r] + dl[r]);
+          for (int r = 0; r < 4; r++) {
+            const int key = kWaveKeys * wave + 16 * kb + 4 * g + r;
+#pragma unroll
+            for (int db = 0; db < T::ND; db++) {
+              pk[key * kD + 16 * db + i16] = dk[kb][db][r] * a.scale;
+              pv[key * kD + 16 * db + i16] = dv[kb][db][r];
             }
           }
-        }
-        bf16x8 pT[KB], dT[KB];  // queries 32 t + 8 g + 0..7 of key 16 kb + l % 16
-#pragma unroll
-        for (int kb = 0; kb < KB; kb++) {
-          pT[kb] = pack8(pf[kb][0], pf[kb][1]);
-          dT[kb] = pack8(df[kb][0], df[kb][1]);
-        }
-#pragma unroll
-        for (int db = 0; db < T::ND; db++) {
-          const bf16x8 gcol = col_operand<kD>(gt, 32 * t, 16 * db, lane);
-          const bf16x8 qcol = col_operand<kD>(qt, 32 * t, 16 * db, lane);
-#pragma unroll
-          for (int kb = 0; kb < KB; kb++) {
-            dv[kb][db] = mfma16(pT[kb], gcol, dv[kb][db]);
-            dk[kb][db] = mfma16(dT[kb], qcol, dk[kb][db]);
-          }
-          __builtin_amdgcn_sched_barrier(0);
-        }
-      }
-    }
-    wait_dma();  // stage sidx + 1 has landed
-    __syncthreads();
-  }
-
-  if (!wave_active) return;
-  const int slot = item[DK_SLOT];
-  if (slot >= 0) {  // split tile: fp32 partial [kKeys][kD] for dK (already scaled) then dV
-    float* pk = a.ws + static_cast<int64_t>(slot) * 2 * kKeys * kD;
-    float* pv = pk + kKeys * kD;
-#pragma unroll
-    for (int kb = 0; kb < KB; kb++)
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int key = kWaveKeys * wave + 16 * kb + 4 * g + r;
-#pragma unroll
-        for (int db = 0; db < T::ND; db++) {
-          pk[key * kD + 16 * db + i16] = dk[kb][db][r] * a.scale;
-          pv[key * kD + 16 * db + i16] = dv[kb][db][r];
-        }
-      }
-    return;
-  }
-  if (prefix && a.acc_prefix) {
+      } else if (prefix && a.acc_prefix) {
 #pragma clang fp contract(off)
-    float* dkf = static_cast<float*>(a.dpk);
-    float* dvf = static_cast<float*>(a.dpv);
+        float* dkf = static_cast<float*>(a.dpk);
+        float* dvf = static_cast<float*>(a.dpv);
 #pragma unroll
-    for (int kb = 0; kb < KB; kb++)
+        for (int kb = 0; kb < KB; kb++)
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int key = kw0 + 16 * kb + 4 * g + r;
-        if (key >= seg_len) continue;
-        const int64_t off = static_cast<int64_t>(seg_row0 + key) * kstride + kvh * kD + i16;
+          for (int r = 0; r < 4; r++) {
+            const int key = kw0 + 16 * kb + 4 * g + r;
+            if (key >= seg_len) continue;
+            const int64_t off = static_cast<int64_t>(seg_row0 + key) * kstride + kvh * kD + i16;
 #pragma unroll
-        for (int db = 0; db < T::ND; db++) {
-          dkf[off + 16 * db] += dk[kb][db][r] * a.scale;
-          dvf[off + 16 * db] += dv[kb][db][r];
-        }
-      }
-    return;
-  }
-  bf16* dkd = static_cast<bf16*>(prefix ? a.dpk : a.dk);
-  bf16* dvd = static_cast<bf16*>(prefix ? a.dpv : a.dv);
+            for (int db = 0; db < T::ND; db++) {
+              dkf[off + 16 * db] += dk[kb][db][r] * a.scale;
+              dvf[off + 16 * db] += dv[kb][db][r];
+            }
+          }
+      } else {
+        bf16* dkd = static_cast<bf16*>(prefix ? a.dpk : a.dk);
+        bf16* dvd = static_cast<bf16*>(prefix ? a.dpv : a.dv);
 #pragma unroll
-  for (int kb = 0; kb < KB; kb++)
+        for (int kb = 0; kb < KB; kb++)
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int key = kw0 + 16 * kb + 4 * g + r;
-      if (key >= seg_len) continue;
-      const int64_t off = static_cast<int64_t>(seg_row0 + key) * kstride + kvh * kD + i16;
+          for (int r = 0; r < 4; r++) {
+            const int key = kw0 + 16 * kb + 4 * g + r;
+            if (key >= seg_len) continue;
+            const int64_t off = static_cast<int64_t>(seg_row0 + key) * kstride + kvh * kD + i16;
 #pragma unroll
-      for (int db = 0; db < T::ND; db++) {
-        dkd[off + 16 * db] = static_cast<bf16>(dk[kb][db][r] * a.scale);
-        dvd[off + 16 * db] = static_cast<bf16>(dv[kb][db][r]);
+            for (int db = 0; db < T::ND; db++) {
+              dkd[off + 16 * db] = static_cast<bf16>(dk[kb][db][r] * a.scale);
+              dvd[off + 16 * db] = static_cast<bf16>(dv[kb][db][r]);
+            }
+          }
       }
     }
+  }  // tiles
 }
 
 // Second pass of split dK/dV tiles: the fp32 partial slots of one (segment

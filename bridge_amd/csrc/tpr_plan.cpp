@@ -296,12 +296,15 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
     for (int k0 = 0; k0 < len; k0 += KT)
       for (int h = 0; h < Hkv; h++) add_tile(0, n, k0, h, lo, hi);
   }
-  // Suffix tiles: on the head_dim-128 MFMA path, tile j of a leaf with T
-  // tiles is paired with its mirror T-1-j in one item (DK_PAIR) when neither
-  // is split: the pair streams the mirror's blocks last-first, then tile j's
-  // first-last, so all pairs of a leaf take about the same time and read the
-  // same query block at the same time (the copies are shared in L2).
-  const bool pair_tiles = path == PATH_MFMA;
+  // Suffix tiles: where one dK/dV workgroup fills a CU (the MFMA kernels at
+  // head_dim 128 and 256), tile j of a leaf with T tiles is paired with its
+  // mirror T-1-j in one item (DK_PAIR) when neither is split: the pair
+  // streams the mirror's blocks last-first, then tile j's first-last, so all
+  // pairs of a leaf take about the same time and read the same query block
+  // at the same time (the copies are shared in L2). At head_dim 64 three
+  // dK/dV workgroups share a CU and hide each other's start; pairs measured
+  // slower there (2.29 -> 2.38 ms at prefix 4096 + 4 x 4096, GQA 32/8).
+  const bool pair_tiles = path == PATH_MFMA || (path == PATH_MFMA16 && D == 256);
   for (int s = 0; s < N; s++) {
     const int len = cu[s + 1] - cu[s];
     const int tiles = (len + KT - 1) / KT;

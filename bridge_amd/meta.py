@@ -45,9 +45,16 @@ class LaunchPlan:
 
     @property
     def path(self) -> str:
-        """Kernel family: "mfma" (bf16, head_dim 128), "mfma16" (bf16, head_dim
-        64 or 256) or "simt" (fp32, and bf16 with other head sizes)."""
-        return {1: "mfma", 2: "mfma16"}.get(int(self.host[_PF_PATH]), "simt")
+        """Kernel path: "mfma" (bf16 matrix-core kernels: head_dim 64, 128 and
+        256) or "simt" (fp32, and bf16 with other head sizes)."""
+        return "mfma" if int(self.host[_PF_PATH]) in (1, 2) else "simt"
+
+    @property
+    def mfma_shape(self) -> Optional[str]:
+        """The MFMA instruction the kernels are built on: "32x32x16" (bf16,
+        head_dim 128), "16x16x32" (bf16, head_dim 64 and 256), None off the
+        MFMA path."""
+        return {1: "32x32x16", 2: "16x16x32"}.get(int(self.host[_PF_PATH]))
 
     @property
     def num_forward_items(self) -> int:

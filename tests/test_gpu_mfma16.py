@@ -61,6 +61,9 @@ def _cases():
         "deep_run_list": (M(cu_seqlens_q=(0, 50, 179, 243), node_offsets=_offsets(_DEEP_LENS[::-1]),
                             leaf_ancestors=(tuple(range(11, -1, -1)), tuple(range(11, 2, -1)),
                                             tuple(range(11, 8, -1)))), 8, 2),
+        # 64-key tiles: 6 (three pairs at head_dim 256), 3 (a pair and a lone
+        # middle tile), 2 with a 1-key mirror, and 5 tiles
+        "paired_suffix_tiles": (M.shared_prefix(100, [333, 150, 65, 260]), 8, 2),
     }
 
 
@@ -77,8 +80,8 @@ def _check(tag, meta, hq, hkv, d, seed, device):
     scale = 1.0 / math.sqrt(d)
     plan = meta.plan(hq, hkv, d, torch.bfloat16, device)
     print(f"[mfma16 {tag}] d={d} hq={hq} hkv={hkv} tq={meta.total_q} tp={meta.total_prefix} "
-          f"path={plan.path} slots={int(plan.host[25])}", flush=True)
-    assert plan.path == "mfma16"
+          f"path={plan.path} mfma={plan.mfma_shape} slots={int(plan.host[25])}", flush=True)
+    assert plan.path == "mfma" and plan.mfma_shape == "16x16x32"
     q, k, v, pk, pv, dout = make_inputs(meta, hq, hkv, d, torch.bfloat16, seed=seed, device=device)
     out, lse, grads = _run(meta, q, k, v, pk, pv, dout, scale)
     ro, rl, rg = oracle(meta, q, k, v, pk, pv, dout, scale)
@@ -92,6 +95,13 @@ def _check(tag, meta, hq, hkv, d, seed, device):
         assert cosine(g, r) >= BF16_GRAD_COS
     for g, r in zip(grads[3:], rg[3:]):
         assert rel_l2(g, r) <= BF16_PREFIX_GRAD_REL_L2
+    # every 64-key dK/dV tile of every leaf on its own (at head_dim 256 a
+    # leaf's tiles are paired with their mirrors): a tile written by the wrong
+    # item, or not at all, has a relative error near 1
+    for s, (a, b) in enumerate(zip(meta.cu_seqlens_q[:-1], meta.cu_seqlens_q[1:])):
+        for k0 in range(a, b, 64):
+            for g, r in zip(grads[1:3], rg[1:3]):
+                assert rel_l2(g[k0:min(b, k0 + 64)], r[k0:min(b, k0 + 64)]) <= 0.1, (s, k0 - a)
     return grads
 
 

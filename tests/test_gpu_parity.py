@@ -163,11 +163,14 @@ def test_simt_matches_oracle(name, cuda_device):
     scale = 1.0 / math.sqrt(d)
     q, k, v, pk, pv, dout = make_inputs(meta, hq, hkv, d, dtype, seed=3, device=cuda_device)
     # bf16 at head_dim 64 and 256 runs on the 16-wide MFMA kernels, the rest on SIMT
-    family = "mfma16" if dtype == torch.bfloat16 and d in (64, 256) else "simt"
-    assert meta.plan(hq, hkv, d, dtype, cuda_device).path == family
+    plan = meta.plan(hq, hkv, d, dtype, cuda_device)
+    if dtype == torch.bfloat16 and d in (64, 256):
+        assert plan.path == "mfma" and plan.mfma_shape == "16x16x32"
+    else:
+        assert plan.path == "simt" and plan.mfma_shape is None
     out, lse, grads = _run(meta, q, k, v, pk, pv, dout, scale)
     ref = oracle(meta, q, k, v, pk, pv, dout, scale)
-    _report(family + "_" + name, out, lse, grads, ref)
+    _report(f"{plan.path}{plan.mfma_shape or ''}_{name}", out, lse, grads, ref)
     ro, rl, rg = ref
     if dtype == torch.float32:
         assert max_abs(out, ro) <= FP32_TOL and max_abs(lse, rl) <= FP32_TOL

@@ -164,16 +164,19 @@ def test_split_prefix_tiles_have_ordered_partials_and_reductions():
     assert not direct & reduced
 
 
-def test_suffix_tiles_pair_with_their_mirror():
-    """head_dim-128 MFMA path: suffix tile j of a leaf with T tiles shares an
-    item with tile T-1-j (the shorter one named first), so all pairs of a leaf
-    stream the same number of query blocks; the middle tile of an odd count,
-    and tiles whose query range is split (and their mirrors), stay alone; every
-    (tile, KV head) is covered once."""
+@pytest.mark.parametrize("d,kt", [(128, 128), (256, 64)])
+def test_suffix_tiles_pair_with_their_mirror(d, kt):
+    """bf16 MFMA at head_dim 128 and 256 (kt keys per dK/dV tile, 64-query
+    blocks), where one dK/dV workgroup fills a CU: suffix tile j of a
+    leaf with T tiles shares an item with tile T-1-j (the shorter one named
+    first), so all pairs of a leaf stream the same number of query blocks; the
+    middle tile of an odd count, and tiles whose query range is split (and
+    their mirrors), stay alone; every (tile, KV head) is covered once."""
     lens = [4096, 4000, 333, 100, 20000]
     meta = TPRPrefixMeta.shared_prefix(256, lens)
-    plan = meta.plan(8, 2, 128, torch.bfloat16, CPU)
+    plan = meta.plan(8, 2, d, torch.bfloat16, CPU)
     w, _, dkdv, qblk = decode(plan)
+    per = kt // 64  # query blocks per tile
     leaf_qblk = w[w[PF["OFF_LEAF_QBLK"]]: w[PF["OFF_LEAF_QBLK"]] + len(lens) + 1]
     items = [it for it in dkdv if it[0] >= 0]
     pair_blocks = {}
@@ -181,44 +184,55 @@ def test_suffix_tiles_pair_with_their_mirror():
     for src, seg, key0, kvh, lo, hi, slot, pair in items:
         if pair == 0:
             continue
-        ntiles = -(-lens[seg] // 128)
+        ntiles = -(-lens[seg] // kt)
         k0b = pair - 1
-        assert src == 1 and slot == -1 and key0 > k0b and key0 // 128 == ntiles - 1 - k0b // 128
+        assert src == 1 and slot == -1 and key0 > k0b and key0 // kt == ntiles - 1 - k0b // kt
         assert lo == leaf_qblk[seg] + key0 // 64 and hi == leaf_qblk[seg + 1]
         long_range = hi - (leaf_qblk[seg] + k0b // 64)
         assert long_range <= 256
         pair_blocks.setdefault(seg, set()).add((hi - lo) + long_range)
-        paired |= {(seg, key0 // 128, kvh), (seg, k0b // 128, kvh)}
+        paired |= {(seg, key0 // kt, kvh), (seg, k0b // kt, kvh)}
     # all pairs of a leaf stream the same number of blocks
     assert all(len(v) == 1 for v in pair_blocks.values())
-    singles = {(it[1], it[2] // 128, it[3]) for it in items if it[0] == 1 and it[7] == 0}
+    singles = {(it[1], it[2] // kt, it[3]) for it in items if it[0] == 1 and it[7] == 0}
     for seg, n in enumerate(lens):
-        ntiles = -(-n // 128)
+        ntiles = -(-n // kt)
         blocks = leaf_qblk[seg + 1] - leaf_qblk[seg]
         for j in range(ntiles):
             mirror = ntiles - 1 - j
             long_j = min(j, mirror)
-            pairable = mirror != j and blocks - 2 * long_j <= 256
+            pairable = mirror != j and blocks - per * long_j <= 256
             for h in range(2):
                 assert ((seg, j, h) in paired) == pairable, (seg, j)
                 assert ((seg, j, h) in singles) != pairable, (seg, j)
-    # the 20000-token leaf: tiles 0..28 stream more than 256 blocks (split), so
-    # they and their mirrors 128..156 stay alone, and so does the middle tile 78
-    assert {j for (seg, j, h) in singles if seg == 4 and h == 0} == set(range(29)) | set(range(128, 157)) | {78}
-    assert {j for (seg, j, h) in singles if seg == 2 and h == 0} == {1} and (3, 0, 0) in singles
+    if kt == 128:
+        # the 20000-token leaf (313 blocks): tiles 0..28 stream more than 256
+        # blocks (split), so they and their mirrors 128..156 stay alone, and
+        # so does the middle tile 78
+        assert {j for (seg, j, h) in singles if seg == 4 and h == 0} == set(range(29)) | set(range(128, 157)) | {78}
+        assert {j for (seg, j, h) in singles if seg == 2 and h == 0} == {1} and (3, 0, 0) in singles
+    else:
+        # 313 tiles of 64 keys: tiles 0..56 split, their mirrors 256..312 alone,
+        # middle 156; the 333- and 100-token leaves (6 and 2 tiles) pair fully
+        assert {j for (seg, j, h) in singles if seg == 4 and h == 0} == set(range(57)) | set(range(256, 313)) | {156}
+        assert not {j for (seg, j, h) in singles if seg in (2, 3)}
     # coverage of every (tile, head) once, prefix and suffix
     seen = Counter(t[:4] for t in tiles_of(dkdv) if t[6] < 0)
     reds = [tuple(w[w[24] + 8 * i: w[24] + 8 * i + 8]) for i in range(w[PF["N_RED"]])]
     seen.update(r[:4] for r in reds)
-    expected = {(0, 0, k0, h) for k0 in (0, 128) for h in range(2)}
-    expected |= {(1, s, k0, h) for s, n in enumerate(lens) for k0 in range(0, n, 128) for h in range(2)}
+    expected = {(0, 0, k0, h) for k0 in range(0, 256, kt) for h in range(2)}
+    expected |= {(1, s, k0, h) for s, n in enumerate(lens) for k0 in range(0, n, kt) for h in range(2)}
     assert set(seen) == expected and set(seen.values()) == {1}
 
 
-def test_suffix_tiles_stay_single_off_the_head_dim_128_path():
+def test_suffix_tiles_stay_single_where_dkdv_workgroups_share_a_cu():
+    """head_dim 64 (several dK/dV workgroups per CU) and the SIMT kernels."""
     meta = TPRPrefixMeta.shared_prefix(64, [1000, 700])
-    for d, dtype in ((64, torch.bfloat16), (256, torch.bfloat16), (128, torch.float32)):
-        _, _, dkdv, _ = decode(meta.plan(8, 2, d, dtype, CPU))
+    for d, dtype, path in ((64, torch.bfloat16, "mfma"), (128, torch.float32, "simt"),
+                           (96, torch.bfloat16, "simt"), (256, torch.float32, "simt")):
+        plan = meta.plan(8, 2, d, dtype, CPU)
+        assert plan.path == path
+        _, _, dkdv, _ = decode(plan)
         assert all(it[7] == 0 for it in dkdv)
 
 
@@ -270,13 +284,16 @@ def test_key_runs_merge_adjacent_ancestors_and_drop_empty_nodes():
 
 def test_kernel_family_by_dtype_and_head_dim():
     meta = TPRPrefixMeta.shared_prefix(512, [512, 512])
-    assert meta.plan(4, 4, 64, torch.float32, CPU).path == "simt"
-    assert meta.plan(4, 4, 64, torch.bfloat16, CPU).path == "mfma16"
-    assert meta.plan(4, 4, 128, torch.float32, CPU).path == "simt"
-    assert meta.plan(4, 4, 128, torch.bfloat16, CPU).path == "mfma"
-    assert meta.plan(8, 2, 256, torch.bfloat16, CPU).path == "mfma16"
-    assert meta.plan(8, 2, 256, torch.float32, CPU).path == "simt"
-    assert meta.plan(6, 2, 96, torch.bfloat16, CPU).path == "simt"
+    def kind(hq, hkv, d, dtype):
+        plan = meta.plan(hq, hkv, d, dtype, CPU)
+        return plan.path, plan.mfma_shape
+    assert kind(4, 4, 64, torch.float32) == ("simt", None)
+    assert kind(4, 4, 64, torch.bfloat16) == ("mfma", "16x16x32")
+    assert kind(4, 4, 128, torch.float32) == ("simt", None)
+    assert kind(4, 4, 128, torch.bfloat16) == ("mfma", "32x32x16")
+    assert kind(8, 2, 256, torch.bfloat16) == ("mfma", "16x16x32")
+    assert kind(8, 2, 256, torch.float32) == ("simt", None)
+    assert kind(6, 2, 96, torch.bfloat16) == ("simt", None)
 
 
 def test_mfma16_work_items():
