@@ -196,6 +196,10 @@ __device__ __forceinline__ void dma_tile4_fwd(const char* src, uint32_t row_byte
 // row-linear 16-byte reads spread over all banks.
 __device__ __forceinline__ void store_tile_rows(char* stage, const f32x16 (&acc)[4], float mul, bf16* dst,
                                                 int64_t row_stride, int nrows, int lane) {
+  // The lane index is laundered so that the per-lane LDS offsets are formed
+  // here: hoisted above the caller's tile loop they stay live through it and
+  // take the registers its pipelined operand reads need.
+  asm volatile("" : "+v"(lane));
   const int n = lane & 31, h = lane >> 5;
 #pragma unroll
   for (int db = 0; db < 4; db++)
@@ -278,6 +282,7 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
   const uint32_t row_bytes = static_cast<uint32_t>(a.hkv) * kMfmaD * 2;
 
   __shared__ __attribute__((aligned(1024))) char smem[4 * kTileBytes];  // K0 K1 V0 V1
+  static_assert(sizeof(smem) >= kFwdWaves * 8192, "the output rows are staged in the tile buffers");
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(smem));
 
   const char* kbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.k) + kvh * kMfmaD);
@@ -480,21 +485,16 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
   }
 
   const float lt = wave_sum32(l);  // all 64 lanes take part in the exchange
-  if (tw0 >= len || t >= len) return;
+  if (tw0 >= len) return;
   const float inv = 1.f / lt;
-  // ordinary (cacheable) stores: L2 merges the 8-byte pieces into whole lines,
-  // and the workgroup retires without waiting on write-through stores
-  bf16* op = static_cast<bf16*>(a.out) + static_cast<int64_t>(row0 + t) * qstride + head * kMfmaD;
-#pragma unroll
-  for (int db = 0; db < 4; db++)
-#pragma unroll
-    for (int g = 0; g < 4; g++) {
-      bf16x4 v4;
-#pragma unroll
-      for (int b = 0; b < 4; b++) v4[b] = static_cast<bf16>(o[db][4 * g + b] * inv);
-      *reinterpret_cast<bf16x4*>(op + 32 * db + 8 * g + 4 * h) = v4;
-    }
-  if (h == 0) a.lse[static_cast<int64_t>(head) * a.total_q + row0 + t] = m * a.scale + logf(lt);
+  if (h == 0 && t < len) a.lse[static_cast<int64_t>(head) * a.total_q + row0 + t] = m * a.scale + logf(lt);
+  // O as whole non-temporal rows: cacheable stores would park the output in
+  // L2 and evict the shared prefix K/V the other workgroups of the XCD still
+  // read. Every tile read finished before the last barrier, so the tile
+  // buffers are free for the row staging.
+  store_tile_rows(smem + wave * 8192, o, inv,
+                  static_cast<bf16*>(a.out) + static_cast<int64_t>(row0 + tw0) * qstride + head * kMfmaD, qstride,
+                  len - tw0, lane);
 }
 
 // ---------------------------------------------------------------------------
