@@ -4,8 +4,8 @@
 // Same math, key streams, work lists and fixed-order sibling sum as the
 // head_dim-128 family (tpr_mfma.hip); the tiling is built on the 16-wide MFMA
 // so that head_dim 256 fits the register file: a forward / dQ wave owns 32
-// query tokens of one head as two 16-query sub-blocks, a dK/dV wave owns 32
-// keys as two 16-key blocks (16 keys at head_dim 256). One wave per SIMD, 4 waves per workgroup; K/V (forward, dQ) and Q/dO
+// query tokens of one head as two 16-query sub-blocks, a dK/dV wave owns one
+// 16-key block. One wave per SIMD, 4 waves per workgroup; K/V (forward, dQ) and Q/dO
 // (dK/dV) tiles of 64 rows are staged in LDS by the gfx950 DMA, double
 // buffered, one workgroup barrier per tile.
 //
@@ -542,17 +542,17 @@ __global__ __launch_bounds__(256) void m16_dq(KernelArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// dK/dV. One workgroup = 4 waves x 32 keys (two 16-key blocks kb; one block
-// of 16 at head_dim 256) of one KV segment tile and KV head; it streams every 64-query block that
+// dK/dV. One workgroup = 4 waves x 16 keys (KB 16-key blocks kb per wave) of
+// one KV segment tile and KV head; it streams every 64-query block that
 // sees the tile -- for a prefix node every descendant leaf and every query
 // head of the group -- in the plan's fixed order, so a prefix node's gradient
 // is the sum over its leaves in registers, without atomics. Per stage (one
 // block, one head), for each pair of 16-query blocks t:
-//   S = Q K^T, dP = dO V^T (Q, dO rows from LDS, permuted; K, V of both key
-//   blocks in registers, so every row read feeds two MFMAs),
+//   S = Q K^T, dP = dO V^T (Q, dO rows from LDS, permuted; K, V of the key
+//   blocks in registers, so every row read feeds KB MFMAs),
 //   P = exp2(scale*log2e S - lse*log2e), dS = P (dP - delta),
 //   dV += P^T dO, dK += dS^T Q (dO, Q read transposed from LDS, again shared
-//   by the two key blocks).
+//   by the key blocks).
 // ---------------------------------------------------------------------------
 template <int kD>
 __global__ __launch_bounds__(256) void m16_dkdv(KernelArgs a) {
