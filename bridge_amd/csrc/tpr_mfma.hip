@@ -389,8 +389,13 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
     for (int kb = 0; kb < 2; kb++)
 #pragma unroll
       for (int r = 0; r < 16; r++) mt = fmaxf(mt, s[kb][r]);
-    mt = wave_max32(mt);
+    // Lanes n and n + 32 hold the same query row (different keys) and share
+    // its reference max m. A row outgrew m iff one of its two halves did, so
+    // the test needs no exchange; the row max over both halves is formed only
+    // on the (rare) rescale path, which keeps the cross-lane round trip off
+    // the common path.
     if (__any(mt > m + slack)) {  // some row outgrew its reference max: rescale
+      mt = wave_max32(mt);
       const float m_new = fmaxf(m, mt);
       const float alpha = fast_exp2((m - m_new) * c2);
       m = m_new;
