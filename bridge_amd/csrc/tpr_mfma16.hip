@@ -21,9 +21,9 @@
 // dS.K, P^T.dO, dS^T.Q) reads as an operand from registers.
 //
 // LDS tiles are row-major, 2*D bytes per row, with the 16-byte chunk index
-// XOR-swizzled by the row (row % 16 for D = 256, (row / 2) % 8 for D = 64) so
-// that the row reads of 16 consecutive (permuted) rows and the transposed
-// reads (ds_read_tr16_b64) spread over the banks.
+// XOR-swizzled by bits of the row (Geo::swz) so that the row reads of 16
+// permuted rows and the transposed reads (ds_read_tr16_b64) are free of bank
+// conflicts.
 
 #include "tpr_kernel_util.h"
 
@@ -46,7 +46,21 @@ struct Geo {
   static constexpr int ND = kD / 16;             // 16-wide head_dim blocks
   static constexpr int RPB = 1024 / RB;          // tile rows per 1 KiB DMA block
   static constexpr int BPW = TB / 1024 / kM16Waves;  // DMA blocks per wave per tile
-  __device__ static __forceinline__ int swz(int row) { return kD == 256 ? (row & 15) : ((row >> 1) & 7); }
+  // Physical 16-byte chunk = logical chunk ^ swz(row), chosen so that no tile
+  // read has a bank conflict (bank = byte address / 4 mod 64). One pass of a
+  // 16-byte row read (row_operand) serves lanes 0-7 and 32-39 (and the like):
+  // 8 permuted rows, varying in row bits 0, 1 and 3, at logical chunks c and
+  // c + 2. One pass of a transposed read (col_operand) serves 32 lanes: 8 rows
+  // varying in the same bits, at chunks c and c + 1 (c even). Both passes
+  // cover all 64 banks when the XOR is a bijection of row bits (0, 1, 3) onto
+  // the bank-group bits other than chunk bit 1, and onto those other than
+  // chunk bit 0. At 512-byte rows (head_dim 256, bank group = chunk mod 16)
+  // swz = 3 r0 + 4 r1 + 8 r3; at 128-byte rows (head_dim 64) row bit 0 already
+  // picks the bank half, and swz = 3 r3 + 4 r1.
+  __device__ static __forceinline__ int swz(int row) {
+    if constexpr (kD == 256) return ((row & 1) * 3) | ((row & 2) << 1) | (row & 8);
+    else return (((row >> 3) & 1) * 3) | ((row & 2) << 1);
+  }
   // byte offset of element (row, col) of a swizzled tile
   __device__ static __forceinline__ uint32_t off(int row, int col) {
     return static_cast<uint32_t>(row * RB + (((col >> 3) ^ swz(row)) << 4) + ((col & 7) << 1));
