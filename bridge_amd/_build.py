@@ -18,7 +18,20 @@ BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_PATH = os.path.join(PKG_DIR, "libtpr_attn.so")
 ARCH = os.environ.get("TPR_OFFLOAD_ARCH", "gfx950")
 
-HIP_SOURCES = ["tpr_abi.hip", "tpr_simt.hip", "tpr_mfma.hip", "tpr_mfma16.hip"]
+# (source, object, extra flags). The 16x16x32 family is compiled once per head
+# size. At head_dim 64 every kernel fits 256 VGPRs, and the MFMAs are built
+# with their accumulators in VGPRs (-amdgpu-mfma-vgpr-form): the default form
+# puts them in AGPRs and copies each score tile out for the softmax (forward
+# 1.17 -> 0.93 ms at prefix 4096 + 4 x 4096, GQA 32/8). At head_dim 256 the
+# kernels need more than 256 registers, and the VGPR form measured slower
+# (dQ 1.59 -> 1.72 ms, Qwen3.5 shape).
+HIP_UNITS = [
+    ("tpr_abi.hip", "tpr_abi", []),
+    ("tpr_simt.hip", "tpr_simt", []),
+    ("tpr_mfma.hip", "tpr_mfma", []),
+    ("tpr_mfma16.hip", "tpr_mfma16_d64", ["-DTPR_M16_HEAD_DIM=64", "-mllvm", "-amdgpu-mfma-vgpr-form"]),
+    ("tpr_mfma16.hip", "tpr_mfma16_d256", ["-DTPR_M16_HEAD_DIM=256"]),
+]
 CXX_SOURCES = ["tpr_plan.cpp"]
 
 
@@ -50,9 +63,9 @@ def build(verbose: bool = False, extra_flags=()) -> str:
     os.makedirs(BUILD_DIR, exist_ok=True)
     hipcc = _hipcc()
     jobs = []
-    for src in HIP_SOURCES:
-        obj = os.path.join(BUILD_DIR, src.rsplit(".", 1)[0] + ".o")
-        jobs.append((obj, [hipcc, *_hip_flags(), *extra_flags, "-c", os.path.join(CSRC, src), "-o", obj]))
+    for src, name, unit_flags in HIP_UNITS:
+        obj = os.path.join(BUILD_DIR, name + ".o")
+        jobs.append((obj, [hipcc, *_hip_flags(), *unit_flags, *extra_flags, "-c", os.path.join(CSRC, src), "-o", obj]))
     for src in CXX_SOURCES:
         obj = os.path.join(BUILD_DIR, src.rsplit(".", 1)[0] + ".o")
         jobs.append((obj, ["g++", "-O2", "-std=c++17", "-fPIC", "-Wall", "-I",

@@ -882,24 +882,29 @@ int launch_bwd_d(const KernelArgs& a, int n_fwd, int n_dkdv, int n_red, hipStrea
 
 }  // namespace
 
-int launch_m16_fwd(const KernelArgs& a, hipStream_t s) {
-  return a.d == 64 ? launch_fwd_d<64>(a, s) : launch_fwd_d<256>(a, s);
-}
+// The file is compiled once per head size (TPR_M16_HEAD_DIM = 64 or 256), so
+// that each gets its own code-generation flags; each object exports the
+// launchers of its head size (launch_m16_*_d64 or launch_m16_*_d256).
+#ifndef TPR_M16_HEAD_DIM
+#error "compile tpr_mfma16.hip with -DTPR_M16_HEAD_DIM=64 or -DTPR_M16_HEAD_DIM=256"
+#endif
+constexpr int kM16HeadDim = TPR_M16_HEAD_DIM;
+static_assert(kM16HeadDim == 64 || kM16HeadDim == 256, "the 16-wide family serves head_dim 64 and 256");
+#define TPR_M16_CAT2(a, b) a##b
+#define TPR_M16_CAT(a, b) TPR_M16_CAT2(a, b)
+#define TPR_M16_NAME(name) TPR_M16_CAT(name, TPR_M16_HEAD_DIM)
 
-int launch_m16_delta(const KernelArgs& a, hipStream_t s) {
+int TPR_M16_NAME(launch_m16_fwd_d)(const KernelArgs& a, hipStream_t s) { return launch_fwd_d<kM16HeadDim>(a, s); }
+
+int TPR_M16_NAME(launch_m16_delta_d)(const KernelArgs& a, hipStream_t s) {
   const int64_t rows = static_cast<int64_t>(a.total_q) * a.hq;
   const int blocks = static_cast<int>((rows + 15) / 16);
-  if (blocks > 0) {
-    if (a.d == 64)
-      hipLaunchKernelGGL(m16_delta<64>, dim3(blocks), dim3(256), 0, s, a);
-    else
-      hipLaunchKernelGGL(m16_delta<256>, dim3(blocks), dim3(256), 0, s, a);
-  }
+  if (blocks > 0) hipLaunchKernelGGL(m16_delta<kM16HeadDim>, dim3(blocks), dim3(256), 0, s, a);
   return hipGetLastError() == hipSuccess ? 0 : 4;
 }
 
-int launch_m16_bwd(const KernelArgs& a, int n_fwd, int n_dkdv, int n_red, hipStream_t s) {
-  return a.d == 64 ? launch_bwd_d<64>(a, n_fwd, n_dkdv, n_red, s) : launch_bwd_d<256>(a, n_fwd, n_dkdv, n_red, s);
+int TPR_M16_NAME(launch_m16_bwd_d)(const KernelArgs& a, int n_fwd, int n_dkdv, int n_red, hipStream_t s) {
+  return launch_bwd_d<kM16HeadDim>(a, n_fwd, n_dkdv, n_red, s);
 }
 
 }  // namespace tpr
