@@ -18,19 +18,24 @@ BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_PATH = os.path.join(PKG_DIR, "libtpr_attn.so")
 ARCH = os.environ.get("TPR_OFFLOAD_ARCH", "gfx950")
 
-# (source, object, extra flags). The 16x16x32 family is compiled once per head
-# size. At head_dim 64 every kernel fits 256 VGPRs, and the MFMAs are built
-# with their accumulators in VGPRs (-amdgpu-mfma-vgpr-form): the default form
-# puts them in AGPRs and copies each score tile out for the softmax (forward
-# 1.17 -> 0.93 ms at prefix 4096 + 4 x 4096, GQA 32/8). At head_dim 256 the
-# kernels need more than 256 registers, and the VGPR form measured slower
-# (dQ 1.59 -> 1.72 ms, Qwen3.5 shape).
+# (source, object, extra flags). The 16x16x32 family is compiled per head size
+# and kernel group (TPR_M16_GROUP bits: 1 = forward and delta, 2 = dK/dV and
+# its reduction, 4 = dQ). -amdgpu-mfma-vgpr-form builds the MFMAs with their
+# accumulators in VGPRs; the default form puts them in AGPRs, and a kernel then
+# copies each score tile out for its softmax. Measured per group (forward /
+# dK/dV / dQ ms, default -> VGPR form): head_dim 64 at prefix 4096 + 4 x 4096,
+# GQA 32/8, every group gains; head_dim 256 at the Qwen3.5 shape, forward 1.08
+# -> 0.96 and dK/dV 2.39 -> 2.03 gain, dQ 1.28 -> 1.39 loses and keeps the
+# default form.
+_VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
 HIP_UNITS = [
     ("tpr_abi.hip", "tpr_abi", []),
     ("tpr_simt.hip", "tpr_simt", []),
     ("tpr_mfma.hip", "tpr_mfma", []),
-    ("tpr_mfma16.hip", "tpr_mfma16_d64", ["-DTPR_M16_HEAD_DIM=64", "-mllvm", "-amdgpu-mfma-vgpr-form"]),
-    ("tpr_mfma16.hip", "tpr_mfma16_d256", ["-DTPR_M16_HEAD_DIM=256"]),
+    ("tpr_mfma16.hip", "tpr_mfma16_d64", ["-DTPR_M16_HEAD_DIM=64", "-DTPR_M16_GROUP=7", *_VGPR_FORM]),
+    ("tpr_mfma16.hip", "tpr_mfma16_d256_fwd", ["-DTPR_M16_HEAD_DIM=256", "-DTPR_M16_GROUP=1", *_VGPR_FORM]),
+    ("tpr_mfma16.hip", "tpr_mfma16_d256_dkdv", ["-DTPR_M16_HEAD_DIM=256", "-DTPR_M16_GROUP=2", *_VGPR_FORM]),
+    ("tpr_mfma16.hip", "tpr_mfma16_d256_dq", ["-DTPR_M16_HEAD_DIM=256", "-DTPR_M16_GROUP=4"]),
 ]
 CXX_SOURCES = ["tpr_plan.cpp"]
 

@@ -19,21 +19,26 @@ int launch_simt_bwd(const KernelArgs& a, int n_fwd, int n_dkdv, bool fp32, hipSt
 int launch_mfma_fwd(const KernelArgs& a, hipStream_t s);
 int launch_mfma_bwd(const KernelArgs& a, int n_fwd, int n_dkdv, int n_red, hipStream_t s);
 int launch_mfma_delta(const KernelArgs& a, hipStream_t s);
-// the 16x16x32 family, one object per head size (tpr_mfma16.hip)
+// the 16x16x32 family (tpr_mfma16.hip), one object per head size and kernel group
 int launch_m16_fwd_d64(const KernelArgs& a, hipStream_t s);
 int launch_m16_fwd_d256(const KernelArgs& a, hipStream_t s);
 int launch_m16_delta_d64(const KernelArgs& a, hipStream_t s);
 int launch_m16_delta_d256(const KernelArgs& a, hipStream_t s);
-int launch_m16_bwd_d64(const KernelArgs& a, int n_fwd, int n_dkdv, int n_red, hipStream_t s);
-int launch_m16_bwd_d256(const KernelArgs& a, int n_fwd, int n_dkdv, int n_red, hipStream_t s);
+int launch_m16_dkdv_d64(const KernelArgs& a, int n_dkdv, int n_red, hipStream_t s);
+int launch_m16_dkdv_d256(const KernelArgs& a, int n_dkdv, int n_red, hipStream_t s);
+int launch_m16_dq_d64(const KernelArgs& a, int n_fwd, hipStream_t s);
+int launch_m16_dq_d256(const KernelArgs& a, int n_fwd, hipStream_t s);
 inline int launch_m16_fwd(const KernelArgs& a, hipStream_t s) {
   return a.d == 64 ? launch_m16_fwd_d64(a, s) : launch_m16_fwd_d256(a, s);
 }
 inline int launch_m16_delta(const KernelArgs& a, hipStream_t s) {
   return a.d == 64 ? launch_m16_delta_d64(a, s) : launch_m16_delta_d256(a, s);
 }
+// dK/dV tiles, their reduction, then dQ
 inline int launch_m16_bwd(const KernelArgs& a, int n_fwd, int n_dkdv, int n_red, hipStream_t s) {
-  return a.d == 64 ? launch_m16_bwd_d64(a, n_fwd, n_dkdv, n_red, s) : launch_m16_bwd_d256(a, n_fwd, n_dkdv, n_red, s);
+  const int rc = a.d == 64 ? launch_m16_dkdv_d64(a, n_dkdv, n_red, s) : launch_m16_dkdv_d256(a, n_dkdv, n_red, s);
+  if (rc != 0) return rc;
+  return a.d == 64 ? launch_m16_dq_d64(a, n_fwd, s) : launch_m16_dq_d256(a, n_fwd, s);
 }
 
 namespace {

@@ -220,96 +220,104 @@ __global__ __launch_bounds__(256) void m16_fwd(KernelArgs a) {
     const char* kt = smem + buf * T::TB;
     const char* vt = smem + (2 + buf) * T::TB;
 
-    float sv[2][4][4];  // [sub-block][key block][register]
-    {
-      f32x4 sa[2][4];
+    // mask (register r of key block b holds key 32 (b/2) + 8 g + 4 (b%2) + r of
+    // the tile), online softmax against the running max, P packed for P V
+    auto softmax = [&](f32x4 (&sv)[2][4], bf16x8 (&pb)[2][2]) __attribute__((always_inline)) {
+      const bool partial = tl.len < kTileRows || (tl.suffix && tl.pos0 + kTileRows - 1 > tw0);
+      if (partial) {
 #pragma unroll
-      for (int qs = 0; qs < 2; qs++)
+        for (int qs = 0; qs < 2; qs++) {
+          const int t = tw0 + 16 * qs + i16;
+          int lim = tl.len - 1;
+          if (tl.suffix) lim = min(lim, t - tl.pos0);
 #pragma unroll
-        for (int b = 0; b < 4; b++) sa[qs][b] = f32x4{};
+          for (int b = 0; b < 4; b++)
 #pragma unroll
-      for (int s = 0; s < T::NS; s++) {
-#pragma unroll
-        for (int b = 0; b < 4; b++) {
-          const bf16x8 kop = row_operand<kD>(kt, b, s, lane);
-#pragma unroll
-          for (int qs = 0; qs < 2; qs++) sa[qs][b] = mfma16(kop, qv[qs][s], sa[qs][b]);
+            for (int r = 0; r < 4; r++) {
+              const int key = 32 * (b >> 1) + 8 * g + 4 * (b & 1) + r;
+              sv[qs][b][r] = key <= lim ? sv[qs][b][r] : -INFINITY;
+            }
         }
-        // keep each step's reads next to its MFMAs (measured faster at head_dim 64, slower at 256)
-        if constexpr (kD == 64) __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
-      for (int qs = 0; qs < 2; qs++)
+      for (int qs = 0; qs < 2; qs++) {
+        float mt = sv[qs][0][0];
 #pragma unroll
         for (int b = 0; b < 4; b++)
 #pragma unroll
-          for (int r = 0; r < 4; r++) sv[qs][b][r] = sa[qs][b][r];
-    }
-    // mask: register r of key block b holds key 32 (b/2) + 8 g + 4 (b%2) + r of the tile
-    const bool partial = tl.len < kTileRows || (tl.suffix && tl.pos0 + kTileRows - 1 > tw0);
-    if (partial) {
+          for (int r = 0; r < 4; r++) mt = fmaxf(mt, sv[qs][b][r]);
+        // The four lanes of a query share its reference max: one of them
+        // outgrew it iff the query did, so at head_dim 64 the exchange waits
+        // for the rescale (forward 1.25 -> 1.16 ms at prefix 4096 + 4 x 4096,
+        // GQA 32/8). At head_dim 256 that form measured slower (1.30 -> 1.33
+        // ms, GQA 8/2), and the exchange stays in front of the test.
+        if constexpr (kD == 256) mt = xmax16(mt);
+        if (__any(mt > m[qs] + slack)) {  // some query outgrew its reference max: rescale
+          if constexpr (kD != 256) mt = xmax16(mt);
+          const float m_new = fmaxf(m[qs], mt);
+          const float alpha = fast_exp2((m[qs] - m_new) * c2);
+          m[qs] = m_new;
+          l[qs] *= alpha;
 #pragma unroll
-      for (int qs = 0; qs < 2; qs++) {
-        const int t = tw0 + 16 * qs + i16;
-        int lim = tl.len - 1;
-        if (tl.suffix) lim = min(lim, t - tl.pos0);
+          for (int db = 0; db < T::ND; db++) o[qs][db] *= alpha;
+        }
+        const float mc2 = m[qs] * c2;
+        float pf[4][4];
+        float ls = 0.f;
 #pragma unroll
         for (int b = 0; b < 4; b++)
 #pragma unroll
           for (int r = 0; r < 4; r++) {
-            const int key = 32 * (b >> 1) + 8 * g + 4 * (b & 1) + r;
-            sv[qs][b][r] = key <= lim ? sv[qs][b][r] : -INFINITY;
+            pf[b][r] = fast_exp2(fmaf(sv[qs][b][r], c2, -mc2));
+            ls += pf[b][r];
           }
+        l[qs] += ls;
+        pb[qs][0] = pack8(pf[0], pf[1]);
+        pb[qs][1] = pack8(pf[2], pf[3]);
       }
-    }
+    };
+    // The tile is one fixed sequence of fenced slots: the S slots (k-step s,
+    // key block b), then the P V slots (head-dim block db, key step t). Each
+    // slot reads one operand from LDS (a K row block, or V read transposed)
+    // for two MFMAs (the wave's two query sub-blocks), and each read is
+    // issued kRead slots ahead of its use, so the MFMAs do not wait on LDS
+    // latency. The softmax runs after the last S slot, while the first P V
+    // operands are already in flight.
+    constexpr int kS = 4 * T::NS;             // S slots
+    constexpr int kSlots = kS + 2 * T::ND;    // + P V slots
+    constexpr int kRead = 4, kRing = kRead + 1;
+    bf16x8 ring[kRing];                       // slot i's operand sits at i % kRing
+    auto read_slot = [&](auto ic) __attribute__((always_inline)) {
+      constexpr int i = decltype(ic)::value;
+      if constexpr (i < kS) {
+        ring[i % kRing] = row_operand<kD>(kt, i % 4, i / 4, lane);
+      } else {
+        constexpr int k = i - kS;
+        ring[i % kRing] = col_operand<kD>(vt, 32 * (k % 2), 16 * (k / 2), lane);
+      }
+    };
+    static_for<kRead>([&](auto ic) { read_slot(ic); });
+    f32x4 sa[2][4];
+#pragma unroll
+    for (int qs = 0; qs < 2; qs++)
+#pragma unroll
+      for (int b = 0; b < 4; b++) sa[qs][b] = f32x4{};
     bf16x8 pb[2][2];
+    static_for<kSlots>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      if constexpr (i + kRead < kSlots) read_slot(std::integral_constant<int, i + kRead>{});
+      if constexpr (i < kS) {
+        constexpr int b = i % 4, s = i / 4;
 #pragma unroll
-    for (int qs = 0; qs < 2; qs++) {
-      float mt = sv[qs][0][0];
+        for (int qs = 0; qs < 2; qs++) sa[qs][b] = mfma16(ring[i % kRing], qv[qs][s], sa[qs][b]);
+        if constexpr (i == kS - 1) softmax(sa, pb);
+      } else {
+        constexpr int k = i - kS, db = k / 2, t = k % 2;
 #pragma unroll
-      for (int b = 0; b < 4; b++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) mt = fmaxf(mt, sv[qs][b][r]);
-      // The four lanes of a query share its reference max: one of them
-      // outgrew it iff the query did, so at head_dim 64 the exchange waits
-      // for the rescale (forward 1.25 -> 1.16 ms at prefix 4096 + 4 x 4096,
-      // GQA 32/8). At head_dim 256 that form measured slower (1.30 -> 1.33
-      // ms, GQA 8/2), and the exchange stays in front of the test.
-      if constexpr (kD == 256) mt = xmax16(mt);
-      if (__any(mt > m[qs] + slack)) {  // some query outgrew its reference max: rescale
-        if constexpr (kD != 256) mt = xmax16(mt);
-        const float m_new = fmaxf(m[qs], mt);
-        const float alpha = fast_exp2((m[qs] - m_new) * c2);
-        m[qs] = m_new;
-        l[qs] *= alpha;
-#pragma unroll
-        for (int db = 0; db < T::ND; db++) o[qs][db] *= alpha;
+        for (int qs = 0; qs < 2; qs++) o[qs][db] = mfma16(ring[i % kRing], pb[qs][t], o[qs][db]);
       }
-      const float mc2 = m[qs] * c2;
-      float pf[4][4];
-      float ls = 0.f;
-#pragma unroll
-      for (int b = 0; b < 4; b++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-          pf[b][r] = fast_exp2(fmaf(sv[qs][b][r], c2, -mc2));
-          ls += pf[b][r];
-        }
-      l[qs] += ls;
-      pb[qs][0] = pack8(pf[0], pf[1]);
-      pb[qs][1] = pack8(pf[2], pf[3]);
-    }
-    // O^T += V^T P^T: A = V^T (16 head dims x 32 keys of step t), B = P^T
-#pragma unroll
-    for (int db = 0; db < T::ND; db++) {
-#pragma unroll
-      for (int t = 0; t < 2; t++) {
-        const bf16x8 vop = col_operand<kD>(vt, 32 * t, 16 * db, lane);
-#pragma unroll
-        for (int qs = 0; qs < 2; qs++) o[qs][db] = mfma16(vop, pb[qs][t], o[qs][db]);
-      }
-      if constexpr (kD == 64) __builtin_amdgcn_sched_barrier(0);
-    }
+      __builtin_amdgcn_sched_barrier(0);
+    });
     if (j + 1 < ntiles) {
       cursor_next(seg, mc);
       tl = cursor_tile(mc);
@@ -473,71 +481,75 @@ __global__ __launch_bounds__(256) void m16_dq(KernelArgs a) {
     const char* kt = smem + buf * T::TB;
     const char* vt = smem + (2 + buf) * T::TB;
 
-    float sv[2][4][4], pv[2][4][4];
-    {
-      f32x4 sa[2][4], pa[2][4];
-#pragma unroll
-      for (int qs = 0; qs < 2; qs++)
-#pragma unroll
-        for (int b = 0; b < 4; b++) {
-          sa[qs][b] = f32x4{};
-          pa[qs][b] = f32x4{};
-        }
-#pragma unroll
-      for (int s = 0; s < T::NS; s++) {
-#pragma unroll
-        for (int b = 0; b < 4; b++) {
-          const bf16x8 kop = row_operand<kD>(kt, b, s, lane);
-          const bf16x8 vop = row_operand<kD>(vt, b, s, lane);
-#pragma unroll
-          for (int qs = 0; qs < 2; qs++) {
-            sa[qs][b] = mfma16(kop, qv[qs][s], sa[qs][b]);
-            pa[qs][b] = mfma16(vop, gv[qs][s], pa[qs][b]);
-          }
-        }
-        if constexpr (kD == 64) __builtin_amdgcn_sched_barrier(0);
+    // One fixed sequence of fenced slots, as in the forward: the S / dP slots
+    // (k-step s, key block b: a K and a V row block, four MFMAs), dS after the
+    // last of them, then the dQ slots (head-dim block db, key step t: K read
+    // transposed, two MFMAs). Operand reads run kRead slots ahead of use.
+    constexpr int kS = 4 * T::NS;
+    constexpr int kSlots = kS + 2 * T::ND;
+    constexpr int kRead = 4, kRing = kRead + 1;
+    bf16x8 ra[kRing], rb[kRing];
+    auto read_slot = [&](auto ic) __attribute__((always_inline)) {
+      constexpr int i = decltype(ic)::value;
+      if constexpr (i < kS) {
+        ra[i % kRing] = row_operand<kD>(kt, i % 4, i / 4, lane);
+        rb[i % kRing] = row_operand<kD>(vt, i % 4, i / 4, lane);
+      } else {
+        constexpr int k = i - kS;
+        ra[i % kRing] = col_operand<kD>(kt, 32 * (k % 2), 16 * (k / 2), lane);
       }
+    };
+    static_for<kRead>([&](auto ic) { read_slot(ic); });
+    f32x4 sa[2][4], pa[2][4];
 #pragma unroll
-      for (int qs = 0; qs < 2; qs++)
+    for (int qs = 0; qs < 2; qs++)
+#pragma unroll
+      for (int b = 0; b < 4; b++) {
+        sa[qs][b] = f32x4{};
+        pa[qs][b] = f32x4{};
+      }
+    bf16x8 dsb[2][2];
+    // dS = P (dP - delta), P = exp2(S scale log2e - lse log2e), masked
+    auto grad_scores = [&]() __attribute__((always_inline)) {
+      const bool partial = tl.len < kTileRows || (tl.suffix && tl.pos0 + kTileRows - 1 > tw0);
+#pragma unroll
+      for (int qs = 0; qs < 2; qs++) {
+        const int t = tw0 + 16 * qs + i16;
+        int lim = tl.len - 1;
+        if (tl.suffix) lim = min(lim, t - tl.pos0);
+        float df[4][4];
 #pragma unroll
         for (int b = 0; b < 4; b++)
 #pragma unroll
           for (int r = 0; r < 4; r++) {
-            sv[qs][b][r] = sa[qs][b][r];
-            pv[qs][b][r] = pa[qs][b][r];
+            const int key = 32 * (b >> 1) + 8 * g + 4 * (b & 1) + r;
+            float x = fmaf(sa[qs][b][r], c2, -lse2[qs]);
+            if (partial) x = key <= lim ? x : -INFINITY;
+            df[b][r] = fast_exp2(x) * (pa[qs][b][r] - delta[qs]);
           }
-    }
-    const bool partial = tl.len < kTileRows || (tl.suffix && tl.pos0 + kTileRows - 1 > tw0);
-    bf16x8 dsb[2][2];
-#pragma unroll
-    for (int qs = 0; qs < 2; qs++) {
-      const int t = tw0 + 16 * qs + i16;
-      int lim = tl.len - 1;
-      if (tl.suffix) lim = min(lim, t - tl.pos0);
-      float df[4][4];
-#pragma unroll
-      for (int b = 0; b < 4; b++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-          const int key = 32 * (b >> 1) + 8 * g + 4 * (b & 1) + r;
-          float x = fmaf(sv[qs][b][r], c2, -lse2[qs]);
-          if (partial) x = key <= lim ? x : -INFINITY;
-          df[b][r] = fast_exp2(x) * (pv[qs][b][r] - delta[qs]);
-        }
-      dsb[qs][0] = pack8(df[0], df[1]);
-      dsb[qs][1] = pack8(df[2], df[3]);
-    }
-    // dQ^T += K^T dS^T: A = K^T (16 head dims x 32 keys of step t), B = dS^T
-#pragma unroll
-    for (int db = 0; db < T::ND; db++) {
-#pragma unroll
-      for (int t = 0; t < 2; t++) {
-        const bf16x8 kop = col_operand<kD>(kt, 32 * t, 16 * db, lane);
-#pragma unroll
-        for (int qs = 0; qs < 2; qs++) dq[qs][db] = mfma16(kop, dsb[qs][t], dq[qs][db]);
+        dsb[qs][0] = pack8(df[0], df[1]);
+        dsb[qs][1] = pack8(df[2], df[3]);
       }
-      if constexpr (kD == 64) __builtin_amdgcn_sched_barrier(0);
-    }
+    };
+    static_for<kSlots>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      if constexpr (i + kRead < kSlots) read_slot(std::integral_constant<int, i + kRead>{});
+      if constexpr (i < kS) {
+        constexpr int b = i % 4, s = i / 4;
+#pragma unroll
+        for (int qs = 0; qs < 2; qs++) {
+          sa[qs][b] = mfma16(ra[i % kRing], qv[qs][s], sa[qs][b]);
+          pa[qs][b] = mfma16(rb[i % kRing], gv[qs][s], pa[qs][b]);
+        }
+        if constexpr (i == kS - 1) grad_scores();
+      } else {
+        constexpr int k = i - kS, db = k / 2, t = k % 2;
+        // dQ^T += K^T dS^T: A = K^T (16 head dims x 32 keys of step t), B = dS^T
+#pragma unroll
+        for (int qs = 0; qs < 2; qs++) dq[qs][db] = mfma16(ra[i % kRing], dsb[qs][t], dq[qs][db]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    });
     if (j + 1 < ntiles) {
       cursor_next(seg, mc);
       tl = cursor_tile(mc);
@@ -691,63 +703,88 @@ __global__ __launch_bounds__(256) void m16_dkdv(KernelArgs a) {
         const float* ndel = &stats[buf][1][0];
         // query q of the block visible from key kp iff kp <= tok0 + q (suffix tiles)
         const bool diag = !prefix && tok0 < kw0 + kWaveKeys - 1;
-#pragma unroll
-        for (int t = 0; t < 2; t++) {
-          float pf[KB][2][4], df[KB][2][4];  // [key block][query block 2t + e][register]
-#pragma unroll
-          for (int e = 0; e < 2; e++) {
-            const int b = 2 * t + e;
-            f32x4 sa[KB], pa[KB];
-#pragma unroll
-            for (int kb = 0; kb < KB; kb++) {
-              sa[kb] = f32x4{};
-              pa[kb] = f32x4{};
-            }
-#pragma unroll
-            for (int s = 0; s < T::NS; s++) {
-              const bf16x8 qop = row_operand<kD>(qt, b, s, lane);
-              const bf16x8 gop = row_operand<kD>(gt, b, s, lane);
+        // The stage is one fixed sequence of slots, each fenced: per query-block
+        // pair t, the S / dP slots (e = 0, 1; k-steps s) and then the dV / dK
+        // slots (head-dim blocks db). Every slot takes two operands from LDS
+        // (Q and dO rows, or dO and Q read transposed), and those reads are
+        // issued kRead slots ahead of the slot that uses them, so the MFMAs do
+        // not wait on LDS latency; the softmax of block (t, e) runs after its
+        // last S / dP slot, and its statistics are read at the block's first.
+        constexpr int kSD = 2 * T::NS;       // S / dP slots per t
+        constexpr int kPT = kSD + T::ND;     // slots per t
+        constexpr int kSlots = 2 * kPT;
+        constexpr int kRead = 4, kRing = kRead + 1;
+        bf16x8 ra[kRing], rb[kRing];         // slot i's operands sit at i % kRing
+        auto read_slot = [&](auto ic) __attribute__((always_inline)) {
+          constexpr int i = decltype(ic)::value;
+          constexpr int t = i / kPT, j = i % kPT;
+          if constexpr (j < kSD) {
+            constexpr int b = 2 * t + j / T::NS, s = j % T::NS;
+            ra[i % kRing] = row_operand<kD>(qt, b, s, lane);
+            rb[i % kRing] = row_operand<kD>(gt, b, s, lane);
+          } else {
+            constexpr int db = j - kSD;
+            ra[i % kRing] = col_operand<kD>(gt, 32 * t, 16 * db, lane);
+            rb[i % kRing] = col_operand<kD>(qt, 32 * t, 16 * db, lane);
+          }
+        };
+        static_for<kRead>([&](auto ic) { read_slot(ic); });
+        f32x4 sa[KB], pa[KB];
+        f32x4 ls, dl;                                  // -lse*log2e, -delta of the block's queries
+        float pf[KB][2][4], df[KB][2][4];              // [key block][query block 2t + e][register]
+        bf16x8 pT[KB], dT[KB];                         // queries 32 t + 8 g + 0..7 of key 16 kb + l % 16
+        static_for<kSlots>([&](auto ic) {
+          constexpr int i = decltype(ic)::value;
+          constexpr int t = i / kPT, j = i % kPT;
+          if constexpr (i + kRead < kSlots) read_slot(std::integral_constant<int, i + kRead>{});
+          if constexpr (j < kSD) {
+            constexpr int e = j / T::NS, s = j % T::NS;
+            if constexpr (s == 0) {
 #pragma unroll
               for (int kb = 0; kb < KB; kb++) {
-                sa[kb] = mfma16(qop, kv[kb][s], sa[kb]);
-                pa[kb] = mfma16(gop, vv[kb][s], pa[kb]);
+                sa[kb] = f32x4{};
+                pa[kb] = f32x4{};
               }
-              __builtin_amdgcn_sched_barrier(0);
+              // register r: query 32 t + 8 g + 4 e + r of the block
+              ls = *reinterpret_cast<const f32x4*>(nlse + 32 * t + 8 * g + 4 * e);
+              dl = *reinterpret_cast<const f32x4*>(ndel + 32 * t + 8 * g + 4 * e);
             }
-            // register r: query q0 + r of the block
-            const int q0 = 32 * t + 8 * g + 4 * e;
-            const f32x4 ls = *reinterpret_cast<const f32x4*>(nlse + q0);
-            const f32x4 dl = *reinterpret_cast<const f32x4*>(ndel + q0);
 #pragma unroll
             for (int kb = 0; kb < KB; kb++) {
-              const int kp = kw0 + 16 * kb + i16;
+              sa[kb] = mfma16(ra[i % kRing], kv[kb][s], sa[kb]);
+              pa[kb] = mfma16(rb[i % kRing], vv[kb][s], pa[kb]);
+            }
+            if constexpr (s == T::NS - 1) {
+              const int q0 = 32 * t + 8 * g + 4 * e;
 #pragma unroll
-              for (int r = 0; r < 4; r++) {
-                float x = fmaf(sa[kb][r], c2, ls[r]);
-                if (diag) x = kp <= tok0 + q0 + r ? x : -INFINITY;
-                pf[kb][e][r] = fast_exp2(x);
-                df[kb][e][r] = pf[kb][e][r] * (pa[kb][r] + dl[r]);
+              for (int kb = 0; kb < KB; kb++) {
+                const int kp = kw0 + 16 * kb + i16;
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                  float x = fmaf(sa[kb][r], c2, ls[r]);
+                  if (diag) x = kp <= tok0 + q0 + r ? x : -INFINITY;
+                  pf[kb][e][r] = fast_exp2(x);
+                  df[kb][e][r] = pf[kb][e][r] * (pa[kb][r] + dl[r]);
+                }
+              }
+              if constexpr (e == 1) {
+#pragma unroll
+                for (int kb = 0; kb < KB; kb++) {
+                  pT[kb] = pack8(pf[kb][0], pf[kb][1]);
+                  dT[kb] = pack8(df[kb][0], df[kb][1]);
+                }
               }
             }
-          }
-          bf16x8 pT[KB], dT[KB];  // queries 32 t + 8 g + 0..7 of key 16 kb + l % 16
-#pragma unroll
-          for (int kb = 0; kb < KB; kb++) {
-            pT[kb] = pack8(pf[kb][0], pf[kb][1]);
-            dT[kb] = pack8(df[kb][0], df[kb][1]);
-          }
-#pragma unroll
-          for (int db = 0; db < T::ND; db++) {
-            const bf16x8 gcol = col_operand<kD>(gt, 32 * t, 16 * db, lane);
-            const bf16x8 qcol = col_operand<kD>(qt, 32 * t, 16 * db, lane);
+          } else {
+            constexpr int db = j - kSD;
 #pragma unroll
             for (int kb = 0; kb < KB; kb++) {
-              dv[kb][db] = mfma16(pT[kb], gcol, dv[kb][db]);
-              dk[kb][db] = mfma16(dT[kb], qcol, dk[kb][db]);
+              dv[kb][db] = mfma16(pT[kb], ra[i % kRing], dv[kb][db]);
+              dk[kb][db] = mfma16(dT[kb], rb[i % kRing], dk[kb][db]);
             }
-            __builtin_amdgcn_sched_barrier(0);
           }
-        }
+          __builtin_amdgcn_sched_barrier(0);
+        });
       }
       wait_dma();  // stage sidx + 1 has landed
       __syncthreads();
@@ -861,7 +898,7 @@ int launch_fwd_d(const KernelArgs& a, hipStream_t s) {
 }
 
 template <int kD>
-int launch_bwd_d(const KernelArgs& a, int n_fwd, int n_dkdv, int n_red, hipStream_t s) {
+int launch_dkdv_d(const KernelArgs& a, int n_dkdv, int n_red, hipStream_t s) {
   if (n_dkdv > 0) {
     hipLaunchKernelGGL((m16_dkdv<kD>), dim3(n_dkdv), dim3(64 * kM16Waves), 0, s, a);
     if (hipGetLastError() != hipSuccess) return 4;
@@ -870,6 +907,11 @@ int launch_bwd_d(const KernelArgs& a, int n_fwd, int n_dkdv, int n_red, hipStrea
     hipLaunchKernelGGL((m16_reduce<kD>), dim3(n_red), dim3(256), 0, s, a);
     if (hipGetLastError() != hipSuccess) return 4;
   }
+  return 0;
+}
+
+template <int kD>
+int launch_dq_d(const KernelArgs& a, int n_fwd, hipStream_t s) {
   if (n_fwd > 0) {
     if (a.max_runs > kMfmaRegRuns)
       hipLaunchKernelGGL((m16_dq<kD, true>), dim3(n_fwd), dim3(64 * kM16Waves), 0, s, a);
@@ -882,11 +924,16 @@ int launch_bwd_d(const KernelArgs& a, int n_fwd, int n_dkdv, int n_red, hipStrea
 
 }  // namespace
 
-// The file is compiled once per head size (TPR_M16_HEAD_DIM = 64 or 256), so
-// that each gets its own code-generation flags; each object exports the
-// launchers of its head size (launch_m16_*_d64 or launch_m16_*_d256).
+// The file is compiled once per head size (TPR_M16_HEAD_DIM = 64 or 256) and
+// kernel group (TPR_M16_GROUP, bits: 1 = forward and delta, 2 = dK/dV and its
+// reduction, 4 = dQ), so that each gets its own code-generation flags. Each
+// object exports the launchers of its head size and groups
+// (launch_m16_<kernel>_d64 or _d256).
 #ifndef TPR_M16_HEAD_DIM
 #error "compile tpr_mfma16.hip with -DTPR_M16_HEAD_DIM=64 or -DTPR_M16_HEAD_DIM=256"
+#endif
+#ifndef TPR_M16_GROUP
+#define TPR_M16_GROUP 7
 #endif
 constexpr int kM16HeadDim = TPR_M16_HEAD_DIM;
 static_assert(kM16HeadDim == 64 || kM16HeadDim == 256, "the 16-wide family serves head_dim 64 and 256");
@@ -894,6 +941,7 @@ static_assert(kM16HeadDim == 64 || kM16HeadDim == 256, "the 16-wide family serve
 #define TPR_M16_CAT(a, b) TPR_M16_CAT2(a, b)
 #define TPR_M16_NAME(name) TPR_M16_CAT(name, TPR_M16_HEAD_DIM)
 
+#if TPR_M16_GROUP & 1
 int TPR_M16_NAME(launch_m16_fwd_d)(const KernelArgs& a, hipStream_t s) { return launch_fwd_d<kM16HeadDim>(a, s); }
 
 int TPR_M16_NAME(launch_m16_delta_d)(const KernelArgs& a, hipStream_t s) {
@@ -903,8 +951,18 @@ int TPR_M16_NAME(launch_m16_delta_d)(const KernelArgs& a, hipStream_t s) {
   return hipGetLastError() == hipSuccess ? 0 : 4;
 }
 
-int TPR_M16_NAME(launch_m16_bwd_d)(const KernelArgs& a, int n_fwd, int n_dkdv, int n_red, hipStream_t s) {
-  return launch_bwd_d<kM16HeadDim>(a, n_fwd, n_dkdv, n_red, s);
+#endif
+
+#if TPR_M16_GROUP & 4
+int TPR_M16_NAME(launch_m16_dq_d)(const KernelArgs& a, int n_fwd, hipStream_t s) {
+  return launch_dq_d<kM16HeadDim>(a, n_fwd, s);
 }
+#endif
+
+#if TPR_M16_GROUP & 2
+int TPR_M16_NAME(launch_m16_dkdv_d)(const KernelArgs& a, int n_dkdv, int n_red, hipStream_t s) {
+  return launch_dkdv_d<kM16HeadDim>(a, n_dkdv, n_red, s);
+}
+#endif
 
 }  // namespace tpr
