@@ -323,6 +323,7 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
 #pragma unroll
   for (int i = 0; i < 4; i++) o[i] = f32x16{};
   float m = -1e30f, l = 0.f;  // running max (raw score units) the O/l are referenced to
+  float s_max = -1e30f;       // the lane's max over the scores of the tile in s (unmasked)
   const float c2 = a.scale * kLog2e;
   const float slack = kRescaleSlack / c2;
   f32x16 s[2];
@@ -357,6 +358,16 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
           for (int db = 0; db < 4; db++) o[db] = mfma(lds_col8_at(vr, lo.v[db][0], lo.v[db][1]), pb[kb][cc], o[db]);
         }
     }
+    if constexpr (decltype(with_s)::value) {
+      // the lane's max over the new scores, taken while the P V MFMAs run
+      // (the softmax phase uses it unless the tile is masked)
+      s_max = s[0][0];
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) s_max = fmaxf(s_max, s[kb][r]);
+      asm volatile("" : "+v"(s_max));  // formed in this phase, not sunk past its barrier
+    }
     if constexpr (decltype(with_s)::value && decltype(with_pv)::value) {
       // 48 LDS reads (16 K rows, 32 transposed V halves) for 32 MFMAs: keep
       // kMphaseAhead reads in flight ahead of the MFMA that consumes them
@@ -372,6 +383,7 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
   auto vphase = [&](int j) {
     // visibility: key kb*32 + 16*(r/8) + 8*h + r%8 <= lim. A tile entirely in
     // this wave's future gets lim < 0 (nothing visible).
+    float mt = s_max;
     if (tl_m.len < kTileRows || (tl_m.suffix && tl_m.pos0 + kTileRows - 1 > tw0)) {
       int lim = tl_m.len - 1 - 8 * h;
       if (tl_m.suffix) lim = min(lim, t - tl_m.pos0 - 8 * h);
@@ -379,16 +391,16 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
       for (int kb = 0; kb < 2; kb++)
 #pragma unroll
         for (int r = 0; r < 16; r++) s[kb][r] = (kb * 32 + 16 * (r >> 3) + (r & 7) <= lim) ? s[kb][r] : -INFINITY;
+      mt = s[0][0];
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) mt = fmaxf(mt, s[kb][r]);
     }
     if (j + 2 < ntiles) {
       cursor_next(seg, mc);
       tl_m = cursor_tile(mc);
     }
-    float mt = s[0][0];
-#pragma unroll
-    for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) mt = fmaxf(mt, s[kb][r]);
     // Lanes n and n + 32 hold the same query row (different keys) and share
     // its reference max m. A row outgrew m iff one of its two halves did, so
     // the test needs no exchange; the row max over both halves is formed only
