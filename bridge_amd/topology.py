@@ -319,56 +319,36 @@ def build_prompt_sibling_trees(keys: Sequence[str], batch: Any) -> Tuple[Traject
 
 
 # ---- turn-unit trie (trajectory_tree_turn.py) ----------------------------------------------
-def _turn_units(tokens: np.ndarray, *, prompt_length: Optional[int], min_segment_tokens: int,
-                end_token_id: int) -> Tuple[Tuple[bytes, int], ...]:
-    """Units ending at complete messages or the prompt end (trajectory_tree_turn.py:46-75).
-
-    A boundary closer than ``min_segment_tokens`` to the previous one is
-    dropped unless it is the end of the row. Unit signatures are the raw
-    token bytes (equal tokens <=> equal bytes)."""
+def _unit_ends(tokens: np.ndarray, *, prompt_length: Optional[int], min_segment_tokens: int,
+               end_token_id: int) -> np.ndarray:
+    """Token positions where a row's units end (the unit rule of
+    trajectory_tree_turn.py:46-75): after every end-of-message token and at
+    the prompt end, dropping a boundary closer than ``min_segment_tokens`` to
+    the one kept before it; the row's end always closes the last unit."""
     length = int(tokens.size)
-    candidates = set((np.flatnonzero(tokens == end_token_id) + 1).tolist())
+    cuts = np.flatnonzero(tokens == end_token_id) + 1
     if prompt_length is not None and 0 < prompt_length < length:
-        candidates.add(prompt_length)
-    candidates.add(length)
-    previous, units = 0, []
-    for end in sorted(candidates):
-        if end < length and end - previous < min_segment_tokens:
-            continue
-        units.append((tokens[previous:end].tobytes(), end))
-        previous = end
-    return tuple(units)
-
-
-@dataclass
-class _TurnNode:
-    end: int
-    source_row: int
-    members: List[int] = field(default_factory=list)
-    terminals: List[int] = field(default_factory=list)
-    children: Dict[bytes, "_TurnNode"] = field(default_factory=dict)
-
-
-def _emit_turn(node: _TurnNode, parent_id: Optional[int], nodes: Dict[int, TrajectoryNode], start: int) -> int:
-    """Compress single-child chains of equal membership (trajectory_tree_turn.py:93-117)."""
-    current = node
-    while not current.terminals and len(current.children) == 1:
-        candidate = next(iter(current.children.values()))
-        if current.members != candidate.members:
-            break
-        current = candidate
-    node_id = len(nodes)
-    seg = SegmentRef(row=node.source_row, start=start, end=current.end)
-    nodes[node_id] = None
-    child_ids = tuple(_emit_turn(c, node_id, nodes, current.end) for c in current.children.values())
-    nodes[node_id] = TrajectoryNode(node_id, parent_id, seg, tuple(current.members), tuple(current.terminals),
-                                    child_ids)
-    return node_id
+        cuts = np.union1d(cuts, [prompt_length])
+    kept, previous = [], 0
+    for end in cuts.tolist():
+        if end < length and end - previous >= min_segment_tokens:
+            kept.append(end)
+            previous = end
+    kept.append(length)
+    return np.asarray(kept, dtype=np.int64)
 
 
 def build_trajectory_trees_turn(keys: Sequence[str], batch: Any, *, min_segment_tokens: int = 128,
                                 end_token_id: int = QWEN3_IM_END_TOKEN_ID) -> Tuple[TrajectoryTree, ...]:
-    """Tries that share only complete message units (trajectory_tree_turn.py:120-186)."""
+    """Tries that share only complete message units (trajectory_tree_turn.py:120-186).
+
+    Each row is cut into units, every distinct unit (its exact tokens) gets
+    an integer id, and the rows' id sequences go through the same radix trie
+    as the token-exact builder: rows share a node while they share whole
+    units, and a node ends where rows branch or end. Node spans are mapped
+    back from unit indices to token positions (equal unit prefixes end at
+    equal positions).
+    """
     if not _is_int(min_segment_tokens) or min_segment_tokens < 1:
         raise ValueError("min_segment_tokens must be a positive integer")
     if not _is_int(end_token_id) or end_token_id < 0:
@@ -385,8 +365,8 @@ def build_trajectory_trees_turn(keys: Sequence[str], batch: Any, *, min_segment_
         prompts = None
     if prompts is not None and len(prompts) != len(keys):
         raise ValueError("turn builder prompt rows and trajectory keys disagree")
-    groups = _group_rows(keys)
-    units = []
+    unit_id: Dict[bytes, int] = {}
+    ends, seqs = [], []
     for row in range(len(keys)):
         tokens = _as_token_array(inputs[row], row=row)
         prompt_length = None
@@ -395,25 +375,26 @@ def build_trajectory_trees_turn(keys: Sequence[str], batch: Any, *, min_segment_
             prompt_length = int(prompt.size)
             if prompt_length > tokens.size or not np.array_equal(tokens[:prompt_length], prompt):
                 raise ValueError(f"turn builder prompt is not an exact input prefix for row={row}")
-        units.append(_turn_units(tokens, prompt_length=prompt_length, min_segment_tokens=min_segment_tokens,
-                                 end_token_id=end_token_id))
+        cut = _unit_ends(tokens, prompt_length=prompt_length, min_segment_tokens=min_segment_tokens,
+                         end_token_id=end_token_id)
+        starts = np.concatenate(([0], cut[:-1]))
+        seqs.append(np.asarray([unit_id.setdefault(tokens[a:b].tobytes(), len(unit_id))
+                                for a, b in zip(starts.tolist(), cut.tolist())], dtype=np.int64))
+        ends.append(cut)
     forest = []
-    for uid, rows in groups.items():
-        dummy = _TurnNode(0, rows[0])
+    for uid, rows in _group_rows(keys).items():
+        dummy = _Radix(0, 0, -1)
         for row in rows:
-            current = dummy
-            for signature, end in units[row]:
-                # the same unit tokens under the same parent end at the same position
-                child = current.children.get(signature)
-                if child is None:
-                    child = _TurnNode(end, row)
-                    current.children[signature] = child
-                child.members.append(row)
-                current = child
-            current.terminals.append(row)
-        for tree_index, child in enumerate(dummy.children.values()):
-            nodes: Dict[int, TrajectoryNode] = {}
-            root_id = _emit_turn(child, None, nodes, 0)
+            _insert_tokens(dummy, row, seqs[row], seqs)
+        for tree_index, real_root in enumerate(dummy.children.values()):
+            unit_nodes: Dict[int, TrajectoryNode] = {}
+            root_id = _emit(real_root, unit_nodes)
+            nodes = {}
+            for nid, nd in unit_nodes.items():
+                e = ends[nd.segment.row]
+                span = SegmentRef(row=nd.segment.row, start=int(e[nd.segment.start - 1]) if nd.segment.start else 0,
+                                  end=int(e[nd.segment.end - 1]))
+                nodes[nid] = TrajectoryNode(nid, nd.parent_id, span, nd.member_rows, nd.terminal_rows, nd.children)
             forest.append(TrajectoryTree(uid, tree_index, root_id, nodes[root_id].member_rows, nodes))
     return tuple(forest)
 

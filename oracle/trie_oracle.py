@@ -11,8 +11,16 @@ token) is compressed by following single-child chains of equal membership
 with no terminal rows, numbering nodes in preorder. The result is plain
 tuples, so tests compare it field by field with ``bridge_amd.topology``.
 
+``turn_trie`` restates the reference's message-unit trie
+(trajectory_tree_turn.py:46-186) in its plain form: each row is cut into
+units after every end-of-message token and at the prompt end (a boundary
+closer than ``min_segment_tokens`` to the previous kept one is dropped,
+except the row end), one trie node per unit keyed by the unit's tokens under
+its parent, then compressed and numbered like ``token_trie``.
+
 Pins: ``token_trie`` reproduces the known answers of the reference's own
 trie tests (unit/test_trajectory_tree.py:23-151, in tests/test_topology.py);
+``turn_trie`` those of its turn-trie tests (unit/test_trajectory_tree_turn.py:64-172);
 ``segment_visits`` is built on ``prefix_attention`` (pinned in
 tests/test_oracle.py) and is checked against the oracle's independent
 ``tree_forward`` / ``tree_backward`` formulation on lowered layouts.
@@ -78,6 +86,70 @@ def token_trie(groups: Sequence[Tuple[str, Sequence[int]]], rows: Sequence[Seque
         for index, real_root in enumerate(dummy.children.values()):
             nodes: Dict[int, Node] = {}
             root_id = _compress(real_root, None, nodes)
+            trees.append((uid, index, root_id, nodes))
+    return trees
+
+
+def _units(tokens: Sequence[int], prompt_length, min_segment_tokens: int, end_token_id: int):
+    """[(unit tokens, end position)] of one row (trajectory_tree_turn.py:46-75)."""
+    length = len(tokens)
+    candidates = {i + 1 for i, t in enumerate(tokens) if int(t) == end_token_id}
+    if prompt_length is not None and 0 < prompt_length < length:
+        candidates.add(prompt_length)
+    candidates.add(length)
+    previous, units = 0, []
+    for end in sorted(candidates):
+        if end < length and end - previous < min_segment_tokens:
+            continue
+        units.append((tuple(int(t) for t in tokens[previous:end]), end))
+        previous = end
+    return units
+
+
+class _UnitNode:
+    __slots__ = ("position", "members", "terminals", "children")
+
+    def __init__(self, end: int):
+        self.position = end - 1          # last token of the unit, as in _TokenNode
+        self.members: List[int] = []
+        self.terminals: List[int] = []
+        self.children: Dict[tuple, "_UnitNode"] = {}
+
+
+def _compress_units(first: "_UnitNode", parent, start: int, out: Dict[int, Node]) -> int:
+    cur = first
+    while not cur.terminals and len(cur.children) == 1:
+        nxt = next(iter(cur.children.values()))
+        if cur.members != nxt.members:
+            break
+        cur = nxt
+    node_id = len(out)
+    out[node_id] = None
+    kids = tuple(_compress_units(c, node_id, cur.position + 1, out) for c in cur.children.values())
+    out[node_id] = (parent, (first.members[0], start, cur.position + 1), tuple(cur.members), tuple(cur.terminals), kids)
+    return node_id
+
+
+def turn_trie(groups: Sequence[Tuple[str, Sequence[int]]], rows: Sequence[Sequence[int]], prompt_lengths,
+              min_segment_tokens: int, end_token_id: int):
+    """The ``token_trie`` result format for the message-unit trie."""
+    trees = []
+    for uid, members in groups:
+        dummy = _UnitNode(0)
+        for row in members:
+            node = dummy
+            plen = None if prompt_lengths is None else prompt_lengths[row]
+            for unit, end in _units(rows[row], plen, min_segment_tokens, end_token_id):
+                child = node.children.get(unit)
+                if child is None:
+                    child = _UnitNode(end)
+                    node.children[unit] = child
+                child.members.append(row)
+                node = child
+            node.terminals.append(row)
+        for index, real_root in enumerate(dummy.children.values()):
+            nodes: Dict[int, Node] = {}
+            root_id = _compress_units(real_root, None, 0, nodes)
             trees.append((uid, index, root_id, nodes))
     return trees
 

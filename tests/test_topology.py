@@ -198,6 +198,63 @@ def test_radix_builder_equals_the_one_token_trie(seed):
     _paths_reconstruct(trees, batch)
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_turn_builder_equals_the_unit_trie(seed):
+    """The radix-based turn builder against the reference's unit trie restated
+    in the oracle, field by field, on random batches with message ends,
+    prompts and several minimum unit lengths."""
+    from oracle.trie_oracle import turn_trie
+    rng = random.Random(seed)
+    end = 7
+    groups_n = rng.randint(1, 3)
+    keys, rows, prompts = [], [], []
+    for gi in range(groups_n):
+        base_prompt = [rng.randint(0, 9) for _ in range(rng.randint(1, 12))]
+        turns = [[rng.randint(0, 9) for _ in range(rng.randint(1, 6))] + [end] for _ in range(rng.randint(0, 4))]
+        for _ in range(rng.randint(1, 5)):
+            row = list(base_prompt)
+            prompt_len = len(row)
+            for t in turns[:rng.randint(0, len(turns))]:
+                row += t
+            row += [rng.randint(0, 9) for _ in range(rng.randint(0, 8))]
+            if rng.random() < 0.3:
+                row += [end]
+            keys.append(f"g{gi}_tpr_{len(keys)}")
+            rows.append(row)
+            prompts.append(prompt_len)
+    for min_len in (1, 2, 5, 128):
+        batch = {"input_ids": [torch.tensor(r) for r in rows], "prompts": [torch.tensor(r[:p]) for r, p in zip(rows, prompts)]}
+        trees = build_trajectory_trees_turn(keys, batch, min_segment_tokens=min_len, end_token_id=end)
+        groups = {}
+        for r, key in enumerate(keys):
+            groups.setdefault(key.rsplit("_", 2)[0], []).append(r)
+        expected = turn_trie(list(groups.items()), rows, prompts, min_len, end)
+        assert len(trees) == len(expected)
+        for tree, (uid, index, root_id, nodes) in zip(trees, expected):
+            assert (tree.uid, tree.tree_index, tree.root_id) == (uid, index, root_id)
+            assert set(tree.nodes) == set(nodes)
+            for node_id, (parent, (row, start, stop), members, terminals, children) in nodes.items():
+                n = tree.get(node_id)
+                assert n.parent_id == parent
+                assert (n.segment.row, n.segment.start, n.segment.end) == (row, start, stop), (seed, min_len, node_id)
+                assert n.member_rows == members and n.terminal_rows == terminals and n.children == children
+
+
+def test_oracle_turn_trie_reproduces_the_reference_known_answers():
+    # unit/test_trajectory_tree_turn.py:64-172 applied to the oracle: complete
+    # shared turns share a node, a short partial message does not
+    from oracle.trie_oracle import turn_trie
+    end = 151645
+    prompt = [1, 2, 3]
+    rows = [prompt + [10, 11, end] + [20, 21], prompt + [10, 11, end] + [30], prompt + [10, 12, end]]
+    ((_, _, root, nodes),) = turn_trie([("s", [0, 1, 2])], rows, [3, 3, 3], 2, end)
+    parent, (row, start, stop), members, terminals, children = nodes[root]
+    assert (start, stop) == (0, 3) and members == (0, 1, 2) and len(children) == 2
+    shared = nodes[children[0]]
+    assert shared[1][1:] == (3, 6) and shared[2] == (0, 1) and len(shared[4]) == 2
+    assert nodes[children[1]][1][1:] == (3, 6) and nodes[children[1]][2] == (2,)
+
+
 def test_radix_builder_handles_long_rows():
     # 8 rollouts of 20k tokens sharing a 12k-token prompt and pairwise longer prefixes
     g = torch.Generator().manual_seed(0)
