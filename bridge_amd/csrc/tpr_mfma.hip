@@ -863,11 +863,6 @@ __global__ __launch_bounds__(512) void mfma_dq(KernelArgs a) {
 // last MFMA (the stage schedule puts it at least 4 MFMA slots later), and a
 // chained MFMA reads its predecessor's result as srcC with the other
 // sub-block's MFMA between them, the spacing the builtin form also uses.
-__device__ __forceinline__ f32x16 mfma_vsp_first(bf16x8 a, bf16x8 b_agpr) {
-  f32x16 d;
-  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "a"(b_agpr));
-  return d;
-}
 __device__ __forceinline__ f32x16 mfma_vsp_init(bf16x8 a, bf16x8 b_agpr, f32x16 c) {
   f32x16 d;
   asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %3" : "=&v"(d) : "v"(a), "a"(b_agpr), "v"(c));
@@ -901,7 +896,6 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 31, h = lane >> 5;
 
-  const int64_t qstride = static_cast<int64_t>(a.hq) * kMfmaD;
   const int64_t kstride = static_cast<int64_t>(a.hkv) * kMfmaD;
 
   // two stage buffers of kHeads (Q, dO) tile pairs: the copies of stage s + 1
