@@ -12,7 +12,7 @@ import threading
 
 LIB_NAME = "libtpr_attn.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 TPR_OK = 0
 TPR_ERR_INVALID_ARGUMENT = 1
@@ -77,6 +77,9 @@ class TprFwdParams(ctypes.Structure):
         ("prefix_v", _p),
         ("out", _p),
         ("lse", _p),
+        ("q_row_stride", ctypes.c_int64),
+        ("k_row_stride", ctypes.c_int64),
+        ("v_row_stride", ctypes.c_int64),
     ]
 
 
@@ -104,6 +107,9 @@ class TprBwdParams(ctypes.Structure):
         ("dprefix_v", _p),
         ("workspace", _p),
         ("workspace_bytes", ctypes.c_size_t),
+        ("q_row_stride", ctypes.c_int64),
+        ("k_row_stride", ctypes.c_int64),
+        ("v_row_stride", ctypes.c_int64),
     ]
 
 

@@ -91,6 +91,31 @@ KernelArgs args_from_plan(const int32_t* ph, const int32_t* pd, float scale) {
   return a;
 }
 
+// Row strides of q, k and v (0 = packed), validated into the kernel arguments.
+int set_row_strides(KernelArgs& a, const int32_t* ph, int64_t q_rs, int64_t k_rs, int64_t v_rs) {
+  const int64_t elem = ph[PF_DTYPE] == TPR_DTYPE_FP32 ? 4 : 2;
+  const int64_t packed_q = static_cast<int64_t>(a.hq) * a.d, packed_kv = static_cast<int64_t>(a.hkv) * a.d;
+  const struct {
+    int64_t given, packed;
+    const char* name;
+    int64_t* out;
+  } rows[3] = {{q_rs, packed_q, "q", &a.q_rs}, {k_rs, packed_kv, "k", &a.k_rs}, {v_rs, packed_kv, "v", &a.v_rs}};
+  for (const auto& r : rows) {
+    const int64_t stride = r.given == 0 ? r.packed : r.given;
+    if (stride < r.packed)
+      return fail(TPR_ERR_INVALID_ARGUMENT, "%s_row_stride must be 0 or at least %lld elements, got %lld", r.name,
+                  static_cast<long long>(r.packed), static_cast<long long>(r.given));
+    if ((stride * elem) % 16 != 0)
+      return fail(TPR_ERR_INVALID_ARGUMENT, "%s_row_stride must give rows of a multiple of 16 bytes, got %lld",
+                  r.name, static_cast<long long>(stride));
+    if (stride * elem > (int64_t{1} << 25))
+      return fail(TPR_ERR_UNSUPPORTED, "%s_row_stride must give rows of at most 32 MiB, got %lld elements", r.name,
+                  static_cast<long long>(stride));
+    *r.out = stride;
+  }
+  return TPR_OK;
+}
+
 int check_tensor(const void* p, const char* name, bool needed, bool mfma) {
   if (!needed) return TPR_OK;
   if (!p) return fail(TPR_ERR_INVALID_ARGUMENT, "%s must not be NULL", name);
@@ -160,6 +185,7 @@ extern "C" int tpr_attn_fwd(const TprFwdParams* p, void* stream) {
       (rc = check_tensor(p->prefix_v, "prefix_v", any_p, mfma)))
     return rc;
   KernelArgs a = args_from_plan(ph, p->plan_device, p->softmax_scale);
+  if ((rc = set_row_strides(a, ph, p->q_row_stride, p->k_row_stride, p->v_row_stride))) return rc;
   a.q = p->q;
   a.k = p->k;
   a.v = p->v;
@@ -219,6 +245,7 @@ int bwd_phases(const TprBwdParams* p, int phases, void* stream, void* workspace,
   if (need > 0 && (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
     return fail(TPR_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
   KernelArgs a = args_from_plan(ph, p->plan_device, p->softmax_scale);
+  if ((rc = set_row_strides(a, ph, p->q_row_stride, p->k_row_stride, p->v_row_stride))) return rc;
   a.q = p->q;
   a.k = p->k;
   a.v = p->v;

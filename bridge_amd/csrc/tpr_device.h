@@ -51,6 +51,10 @@ struct KernelArgs {
   float* ws;       // fp32 partial dK/dV slots of split tiles
   float* stat_ws;  // MFMA backward: [0] = +inf, [1] = 0, then lse*log2e rows from kStatRowsOffset
   float* ndelta_ws;  // MFMA backward: -delta rows [Hq, Tq] (the dK/dV kernel's dP accumulator start)
+  // token (row) strides of q, k and v in elements (the packed Hq*D / Hkv*D
+  // unless the caller reads them out of a wider buffer); every other tensor
+  // is packed
+  int64_t q_rs, k_rs, v_rs;
 };
 
 __device__ __forceinline__ float to_f32(float x) { return x; }

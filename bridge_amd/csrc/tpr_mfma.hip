@@ -140,11 +140,13 @@ __device__ __forceinline__ TileLanes4 make_tile_lanes4(int wave, int lane, uint3
 
 // Copy rows [0, 64) of the tile starting at `src` (uniform; rows at or beyond
 // `len` re-read row len - 1) into the swizzled LDS tile at `lds_tile`; this
-// wave moves its four 1 KiB blocks (one asm group).
+// wave moves its four 1 KiB blocks (one asm group). A full tile whose row
+// stride is the one p.full was made for (`full_ok`) uses those offsets;
+// other tiles compute them.
 __device__ __forceinline__ void dma_tile4(const char* src, uint32_t row_bytes, int len, uint32_t lds_tile,
-                                          const TileLanes4& p, int wave) {
+                                          const TileLanes4& p, int wave, bool full_ok) {
   const uint32_t dst = lds_tile + wave * 4096;
-  if (len >= kTileRows) {
+  if (len >= kTileRows && full_ok) {
     dma_blocks4(src, p.full[0], p.full[1], p.full[2], p.full[3], dst);
   } else {
     const uint32_t last = static_cast<uint32_t>(len - 1);
@@ -278,8 +280,11 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
   const int n = lane & 31, h = lane >> 5;
   const int t = tw0 + n;                             // this lane's query token
 
-  const int64_t qstride = static_cast<int64_t>(a.hq) * kMfmaD;
-  const uint32_t row_bytes = static_cast<uint32_t>(a.hkv) * kMfmaD * 2;
+  const int64_t qstride = static_cast<int64_t>(a.hq) * kMfmaD;  // output rows (packed)
+  // row bytes of the suffix K and V (views of a wider buffer allowed) and of
+  // the packed prefix K/V
+  const uint32_t k_rb = static_cast<uint32_t>(a.k_rs) * 2, v_rb = static_cast<uint32_t>(a.v_rs) * 2;
+  const uint32_t p_rb = static_cast<uint32_t>(a.hkv) * kMfmaD * 2;
 
   __shared__ __attribute__((aligned(1024))) char smem[4 * kTileBytes];  // K0 K1 V0 V1
   static_assert(sizeof(smem) >= kFwdWaves * 8192, "the output rows are staged in the tile buffers");
@@ -294,14 +299,15 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
 
   const auto seg = load_keys<kRunList>(a, leaf, suffix_keys);
   const int ntiles = seg.ntiles;
+  auto kv_rb = [&](const TileLoc& x, bool is_k) { return x.suffix ? (is_k ? k_rb : v_rb) : p_rb; };
   auto kv_src = [&](const TileLoc& x, bool is_k) {
     const char* b = x.suffix ? (is_k ? kbase : vbase) : (is_k ? pkbase : pvbase);
-    return b + x.row * static_cast<int64_t>(row_bytes);
+    return b + x.row * static_cast<int64_t>(kv_rb(x, is_k));
   };
   // group B's copy cursor: the next K tile (tl_k) and the next V tile (tl_v)
   Cursor dc = cursor_begin(seg);
   TileLoc tl_k = cursor_tile(dc), tl_v = tl_k;
-  if (grp) dma_tile4_fwd(kv_src(tl_k, true), row_bytes, tl_k.len, lds0, dl, wave & 3);  // K[0]
+  if (grp) dma_tile4_fwd(kv_src(tl_k, true), kv_rb(tl_k, true), tl_k.len, lds0, dl, wave & 3);  // K[0]
   if (ntiles > 1) {
     cursor_next(seg, dc);
     tl_k = cursor_tile(dc);
@@ -313,7 +319,7 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
   // Q as the B operand of S^T = K Q^T: lane holds Q[t][16c + 8h .. +7]
   bf16x8 qv[8];
   {
-    const bf16* qp = static_cast<const bf16*>(a.q) + static_cast<int64_t>(row0 + min(t, len - 1)) * qstride +
+    const bf16* qp = static_cast<const bf16*>(a.q) + static_cast<int64_t>(row0 + min(t, len - 1)) * a.q_rs +
                      head * kMfmaD + 8 * h;
 #pragma unroll
     for (int c = 0; c < 8; c++) qv[c] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(qp + 16 * c));
@@ -333,9 +339,11 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
   // into V buffer (j+1)&1
   auto issue = [&](int j) {
     if (j + 2 < ntiles)
-      dma_tile4_fwd(kv_src(tl_k, true), row_bytes, tl_k.len, lds0 + ((j + 2) & 1) * kTileBytes, dl, wave & 3);
+      dma_tile4_fwd(kv_src(tl_k, true), kv_rb(tl_k, true), tl_k.len, lds0 + ((j + 2) & 1) * kTileBytes, dl,
+                    wave & 3);
     if (j + 1 < ntiles)
-      dma_tile4_fwd(kv_src(tl_v, false), row_bytes, tl_v.len, lds0 + (2 + ((j + 1) & 1)) * kTileBytes, dl, wave & 3);
+      dma_tile4_fwd(kv_src(tl_v, false), kv_rb(tl_v, false), tl_v.len, lds0 + (2 + ((j + 1) & 1)) * kTileBytes, dl,
+                    wave & 3);
     tl_v = tl_k;
     if (j + 3 < ntiles) {
       cursor_next(seg, dc);
@@ -597,8 +605,11 @@ __global__ __launch_bounds__(512) void mfma_dq(KernelArgs a) {
   const int t = tw0 + n;
   const int tc = min(t, len - 1);
 
-  const int64_t qstride = static_cast<int64_t>(a.hq) * kMfmaD;
-  const uint32_t row_bytes = static_cast<uint32_t>(a.hkv) * kMfmaD * 2;
+  const int64_t qstride = static_cast<int64_t>(a.hq) * kMfmaD;  // dO and dQ rows (packed)
+  // row bytes of the suffix K and V (views of a wider buffer allowed) and of
+  // the packed prefix K/V; the full-tile copy offsets are made for the latter
+  const uint32_t k_rb = static_cast<uint32_t>(a.k_rs) * 2, v_rb = static_cast<uint32_t>(a.v_rs) * 2;
+  const uint32_t p_rb = static_cast<uint32_t>(a.hkv) * kMfmaD * 2;
 
   // K0 K1 V0 V1 (row-major, swizzled) | T0 T1 (K^T)
   __shared__ __attribute__((aligned(1024))) char smem[6 * kTileBytes];
@@ -609,7 +620,7 @@ __global__ __launch_bounds__(512) void mfma_dq(KernelArgs a) {
   const char* vbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.v) + kvh * kMfmaD);
   const char* pkbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.pk) + kvh * kMfmaD);
   const char* pvbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.pv) + kvh * kMfmaD);
-  const TileLanes4 dl = make_tile_lanes4(wave & 3, lane, row_bytes);
+  const TileLanes4 dl = make_tile_lanes4(wave & 3, lane, p_rb);
   // K/V row reads (A operands of S, dP) and, for group A, the transposing reads
   const FwdLdsOffsets lo = make_fwd_lds_offsets(lane);
   // K^T reads (A operand of dQ^T): row 32db + n, keys 32kb + 16cc + 8h: the
@@ -629,16 +640,20 @@ __global__ __launch_bounds__(512) void mfma_dq(KernelArgs a) {
 
   const auto seg = load_keys<kRunList>(a, leaf, suffix_keys);
   const int ntiles = seg.ntiles;
+  auto kv_rb = [&](const TileLoc& x, bool is_k) __attribute__((always_inline)) {
+    return x.suffix ? (is_k ? k_rb : v_rb) : p_rb;
+  };
   auto kv_src = [&](const TileLoc& x, bool is_k) __attribute__((always_inline)) {
     const char* b = x.suffix ? (is_k ? kbase : vbase) : (is_k ? pkbase : pvbase);
-    return b + x.row * static_cast<int64_t>(row_bytes);
+    return b + x.row * static_cast<int64_t>(kv_rb(x, is_k));
   };
   // group B's copy cursor: the next tile whose K and V it copies
   Cursor dc = cursor_begin(seg);
   TileLoc tl_c = cursor_tile(dc);
   if (grp) {
-    dma_tile4(kv_src(tl_c, true), row_bytes, tl_c.len, lds0, dl, wave & 3);
-    dma_tile4(kv_src(tl_c, false), row_bytes, tl_c.len, lds0 + 2 * kTileBytes, dl, wave & 3);
+    dma_tile4(kv_src(tl_c, true), kv_rb(tl_c, true), tl_c.len, lds0, dl, wave & 3, kv_rb(tl_c, true) == p_rb);
+    dma_tile4(kv_src(tl_c, false), kv_rb(tl_c, false), tl_c.len, lds0 + 2 * kTileBytes, dl, wave & 3,
+              kv_rb(tl_c, false) == p_rb);
   }
   if (ntiles > 1) {
     cursor_next(seg, dc);
@@ -649,9 +664,9 @@ __global__ __launch_bounds__(512) void mfma_dq(KernelArgs a) {
 
   bf16x8 qv[8], gv[8];
   {
-    const int64_t off = static_cast<int64_t>(row0 + tc) * qstride + head * kMfmaD + 8 * h;
-    const bf16* qp = static_cast<const bf16*>(a.q) + off;
-    const bf16* gp = static_cast<const bf16*>(a.dout) + off;
+    const int64_t col = head * kMfmaD + 8 * h;
+    const bf16* qp = static_cast<const bf16*>(a.q) + static_cast<int64_t>(row0 + tc) * a.q_rs + col;
+    const bf16* gp = static_cast<const bf16*>(a.dout) + static_cast<int64_t>(row0 + tc) * qstride + col;
 #pragma unroll
     for (int c = 0; c < 8; c++) {
       qv[c] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(qp + 16 * c));
@@ -673,8 +688,10 @@ __global__ __launch_bounds__(512) void mfma_dq(KernelArgs a) {
   auto issue = [&](int j) __attribute__((always_inline)) {
     if (j + 2 < ntiles) {
       const int b = j & 1;
-      dma_tile4(kv_src(tl_c, true), row_bytes, tl_c.len, lds0 + b * kTileBytes, dl, wave & 3);
-      dma_tile4(kv_src(tl_c, false), row_bytes, tl_c.len, lds0 + (2 + b) * kTileBytes, dl, wave & 3);
+      dma_tile4(kv_src(tl_c, true), kv_rb(tl_c, true), tl_c.len, lds0 + b * kTileBytes, dl, wave & 3,
+                kv_rb(tl_c, true) == p_rb);
+      dma_tile4(kv_src(tl_c, false), kv_rb(tl_c, false), tl_c.len, lds0 + (2 + b) * kTileBytes, dl, wave & 3,
+                kv_rb(tl_c, false) == p_rb);
     }
     if (j + 3 < ntiles) {
       cursor_next(seg, dc);
@@ -896,7 +913,7 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 31, h = lane >> 5;
 
-  const int64_t kstride = static_cast<int64_t>(a.hkv) * kMfmaD;
+  const int64_t kstride = static_cast<int64_t>(a.hkv) * kMfmaD;  // packed K/V rows: prefix inputs, every output
 
   // two stage buffers of kHeads (Q, dO) tile pairs: the copies of stage s + 1
   // run during stage s
@@ -951,24 +968,32 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
     auto advance = [&](StageCursor c) __attribute__((always_inline)) {
       return c.sub + 1 == spb ? StageCursor{c.blk + 1, 0} : StageCursor{c.blk, c.sub + 1};
     };
-    const uint32_t qrow_bytes = static_cast<uint32_t>(a.hq) * kMfmaD * 2;
-    const DmaLanes<kDkdvWaves> dl = make_dma_lanes<kDkdvWaves>(qrow_bytes, wave, lane);
+    // row bytes of dO (packed; the full-block lane offsets are made for it)
+    // and of Q (a view of a wider buffer allowed)
+    const uint32_t g_rb = static_cast<uint32_t>(a.hq) * kMfmaD * 2;
+    const uint32_t q_rb = static_cast<uint32_t>(a.q_rs) * 2;
+    const bool q_packed = q_rb == g_rb;
+    const DmaLanes<kDkdvWaves> dl = make_dma_lanes<kDkdvWaves>(g_rb, wave, lane);
     const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(smem));
     // copy the Q and dO rows [row, row + 64) of query head qh into the stage buffer at byte `tile`
     auto issue_stage = [&](int row, int nq, int qh, uint32_t tile) __attribute__((always_inline)) {
-      const int64_t off = static_cast<int64_t>(qh) * kMfmaD * 2 + static_cast<int64_t>(row) * qrow_bytes;
+      const int64_t col = static_cast<int64_t>(qh) * kMfmaD * 2;
       const uint32_t dst = lds0 + tile + wave * 4096;
-      const char* qs = reinterpret_cast<const char*>(qbase) + off;
-      const char* gs = reinterpret_cast<const char*>(gbase) + off;
-      if (nq >= kTileRows) {
+      const char* qs = reinterpret_cast<const char*>(qbase) + col + static_cast<int64_t>(row) * q_rb;
+      const char* gs = reinterpret_cast<const char*>(gbase) + col + static_cast<int64_t>(row) * g_rb;
+      if (nq >= kTileRows && q_packed) {
         dma_blocks4(qs, dl.voff[0], dl.voff[1], dl.voff[2], dl.voff[3], dst);
         dma_blocks4(gs, dl.voff[0], dl.voff[1], dl.voff[2], dl.voff[3], dst + kTileBytes);
       } else {  // rows at or beyond nq re-read row nq - 1
-        uint32_t v[4];
+        uint32_t vq[4], vg[4];
 #pragma unroll
-        for (int j = 0; j < 4; j++) v[j] = static_cast<uint32_t>(min(dl.row[j], nq - 1)) * qrow_bytes + dl.cbytes[j];
-        dma_blocks4_m0(qs, v[0], v[1], v[2], v[3], dst);
-        dma_blocks4_m0(gs, v[0], v[1], v[2], v[3], dst + kTileBytes);
+        for (int j = 0; j < 4; j++) {
+          const uint32_t r = static_cast<uint32_t>(min(dl.row[j], nq - 1));
+          vq[j] = r * q_rb + dl.cbytes[j];
+          vg[j] = r * g_rb + dl.cbytes[j];
+        }
+        dma_blocks4_m0(qs, vq[0], vq[1], vq[2], vq[3], dst);
+        dma_blocks4_m0(gs, vg[0], vg[1], vg[2], vg[3], dst + kTileBytes);
       }
     };
 
@@ -1002,11 +1027,12 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
     {
       const bf16* kb = static_cast<const bf16*>(prefix ? a.pk : a.k);
       const bf16* vb = static_cast<const bf16*>(prefix ? a.pv : a.v);
-      const int64_t off = static_cast<int64_t>(seg_row0 + min(kp, seg_len - 1)) * kstride + kvh * kMfmaD + 8 * h;
+      const int64_t key = seg_row0 + min(kp, seg_len - 1), col = kvh * kMfmaD + 8 * h;
+      const int64_t koff = key * (prefix ? kstride : a.k_rs) + col, voff = key * (prefix ? kstride : a.v_rs) + col;
 #pragma unroll
       for (int c = 0; c < 8; c++) {
-        kv[c] = *reinterpret_cast<const bf16x8*>(kb + off + 16 * c);
-        vv[c] = *reinterpret_cast<const bf16x8*>(vb + off + 16 * c);
+        kv[c] = *reinterpret_cast<const bf16x8*>(kb + koff + 16 * c);
+        vv[c] = *reinterpret_cast<const bf16x8*>(vb + voff + 16 * c);
       }
     }
     f32x16 dk[4], dv[4];

@@ -170,9 +170,12 @@ __global__ __launch_bounds__(256) void m16_fwd(KernelArgs a) {
   const char* vbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.v) + kvh * kD);
   const char* pkbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.pk) + kvh * kD);
   const char* pvbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.pv) + kvh * kD);
+  // row bytes of a tile's source: prefix K/V packed, suffix K/V as the caller's views
+  const uint32_t k_rb = static_cast<uint32_t>(a.k_rs) * 2, v_rb = static_cast<uint32_t>(a.v_rs) * 2;
+  auto kv_rb = [&](const TileLoc& x, bool is_k) { return x.suffix ? (is_k ? k_rb : v_rb) : row_bytes; };
   auto kv_src = [&](const TileLoc& x, bool is_k) {
     const char* b = x.suffix ? (is_k ? kbase : vbase) : (is_k ? pkbase : pvbase);
-    return b + x.row * static_cast<int64_t>(row_bytes);
+    return b + x.row * static_cast<int64_t>(kv_rb(x, is_k));
   };
 
   const auto seg = load_keys<kRunList>(a, leaf, suffix_keys);
@@ -181,15 +184,15 @@ __global__ __launch_bounds__(256) void m16_fwd(KernelArgs a) {
   TileLoc tl_c = cursor_tile(cc);
   Cursor mc = cursor_begin(seg);  // the tile being computed
   TileLoc tl = cursor_tile(mc);
-  copy_tile<kD>(kv_src(tl_c, true), row_bytes, tl_c.len, lds0, wave, lane);
-  copy_tile<kD>(kv_src(tl_c, false), row_bytes, tl_c.len, lds0 + 2 * T::TB, wave, lane);
+  copy_tile<kD>(kv_src(tl_c, true), kv_rb(tl_c, true), tl_c.len, lds0, wave, lane);
+  copy_tile<kD>(kv_src(tl_c, false), kv_rb(tl_c, false), tl_c.len, lds0 + 2 * T::TB, wave, lane);
 
   // Q of the lane's query l % 16 of each sub-block: the B operand of S^T
   bf16x8 qv[2][T::NS];
 #pragma unroll
   for (int qs = 0; qs < 2; qs++) {
     const int t = min(tw0 + 16 * qs + i16, len - 1);
-    const bf16* qp = static_cast<const bf16*>(a.q) + static_cast<int64_t>(row0 + t) * qstride + head * kD + 8 * g;
+    const bf16* qp = static_cast<const bf16*>(a.q) + static_cast<int64_t>(row0 + t) * a.q_rs + head * kD + 8 * g;
 #pragma unroll
     for (int s = 0; s < T::NS; s++) qv[qs][s] = *reinterpret_cast<const bf16x8*>(qp + 32 * s);
   }
@@ -214,8 +217,8 @@ __global__ __launch_bounds__(256) void m16_fwd(KernelArgs a) {
     if (j + 1 < ntiles) {  // copy tile j+1 into the other buffer (read by tile j-1, released by the last barrier)
       cursor_next(seg, cc);
       tl_c = cursor_tile(cc);
-      copy_tile<kD>(kv_src(tl_c, true), row_bytes, tl_c.len, lds0 + (1 - buf) * T::TB, wave, lane);
-      copy_tile<kD>(kv_src(tl_c, false), row_bytes, tl_c.len, lds0 + (3 - buf) * T::TB, wave, lane);
+      copy_tile<kD>(kv_src(tl_c, true), kv_rb(tl_c, true), tl_c.len, lds0 + (1 - buf) * T::TB, wave, lane);
+      copy_tile<kD>(kv_src(tl_c, false), kv_rb(tl_c, false), tl_c.len, lds0 + (3 - buf) * T::TB, wave, lane);
     }
     const char* kt = smem + buf * T::TB;
     const char* vt = smem + (2 + buf) * T::TB;
@@ -421,9 +424,12 @@ __global__ __launch_bounds__(256) void m16_dq(KernelArgs a) {
   const char* vbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.v) + kvh * kD);
   const char* pkbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.pk) + kvh * kD);
   const char* pvbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.pv) + kvh * kD);
+  // row bytes of a tile's source: prefix K/V packed, suffix K/V as the caller's views
+  const uint32_t k_rb = static_cast<uint32_t>(a.k_rs) * 2, v_rb = static_cast<uint32_t>(a.v_rs) * 2;
+  auto kv_rb = [&](const TileLoc& x, bool is_k) { return x.suffix ? (is_k ? k_rb : v_rb) : row_bytes; };
   auto kv_src = [&](const TileLoc& x, bool is_k) {
     const char* b = x.suffix ? (is_k ? kbase : vbase) : (is_k ? pkbase : pvbase);
-    return b + x.row * static_cast<int64_t>(row_bytes);
+    return b + x.row * static_cast<int64_t>(kv_rb(x, is_k));
   };
 
   const auto seg = load_keys<kRunList>(a, leaf, suffix_keys);
@@ -432,8 +438,8 @@ __global__ __launch_bounds__(256) void m16_dq(KernelArgs a) {
   TileLoc tl_c = cursor_tile(cc);
   Cursor mc = cursor_begin(seg);
   TileLoc tl = cursor_tile(mc);
-  copy_tile<kD>(kv_src(tl_c, true), row_bytes, tl_c.len, lds0, wave, lane);
-  copy_tile<kD>(kv_src(tl_c, false), row_bytes, tl_c.len, lds0 + 2 * T::TB, wave, lane);
+  copy_tile<kD>(kv_src(tl_c, true), kv_rb(tl_c, true), tl_c.len, lds0, wave, lane);
+  copy_tile<kD>(kv_src(tl_c, false), kv_rb(tl_c, false), tl_c.len, lds0 + 2 * T::TB, wave, lane);
 
   bf16x8 qv[2][T::NS], gv[2][T::NS];
   float lse2[2], delta[2];
@@ -441,9 +447,10 @@ __global__ __launch_bounds__(256) void m16_dq(KernelArgs a) {
   for (int qs = 0; qs < 2; qs++) {
     const int t = min(tw0 + 16 * qs + i16, len - 1);
     const int64_t off = static_cast<int64_t>(row0 + t) * qstride + head * kD + 8 * g;
+    const int64_t qoff = static_cast<int64_t>(row0 + t) * a.q_rs + head * kD + 8 * g;
 #pragma unroll
     for (int s = 0; s < T::NS; s++) {
-      qv[qs][s] = *reinterpret_cast<const bf16x8*>(static_cast<const bf16*>(a.q) + off + 32 * s);
+      qv[qs][s] = *reinterpret_cast<const bf16x8*>(static_cast<const bf16*>(a.q) + qoff + 32 * s);
       gv[qs][s] = *reinterpret_cast<const bf16x8*>(static_cast<const bf16*>(a.dout) + off + 32 * s);
     }
     const int64_t at = static_cast<int64_t>(head) * a.total_q + row0 + t;
@@ -475,8 +482,8 @@ __global__ __launch_bounds__(256) void m16_dq(KernelArgs a) {
     if (j + 1 < ntiles) {
       cursor_next(seg, cc);
       tl_c = cursor_tile(cc);
-      copy_tile<kD>(kv_src(tl_c, true), row_bytes, tl_c.len, lds0 + (1 - buf) * T::TB, wave, lane);
-      copy_tile<kD>(kv_src(tl_c, false), row_bytes, tl_c.len, lds0 + (3 - buf) * T::TB, wave, lane);
+      copy_tile<kD>(kv_src(tl_c, true), kv_rb(tl_c, true), tl_c.len, lds0 + (1 - buf) * T::TB, wave, lane);
+      copy_tile<kD>(kv_src(tl_c, false), kv_rb(tl_c, false), tl_c.len, lds0 + (3 - buf) * T::TB, wave, lane);
     }
     const char* kt = smem + buf * T::TB;
     const char* vt = smem + (2 + buf) * T::TB;
@@ -605,8 +612,9 @@ __global__ __launch_bounds__(256) void m16_dkdv(KernelArgs a) {
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int i16 = lane & 15, g = lane >> 4;
 
-  const int64_t kstride = static_cast<int64_t>(a.hkv) * kD;
-  const uint32_t qrow_bytes = static_cast<uint32_t>(a.hq) * kD * 2;
+  const int64_t kstride = static_cast<int64_t>(a.hkv) * kD;  // packed K/V rows: prefix inputs, every output
+  const uint32_t g_rb = static_cast<uint32_t>(a.hq) * kD * 2;  // dO row bytes (packed)
+  const uint32_t q_rb = static_cast<uint32_t>(a.q_rs) * 2;     // Q row bytes
 
   __shared__ __attribute__((aligned(1024))) char smem[2 * 2 * T::TB];           // [buf][Q | dO]
   __shared__ __attribute__((aligned(256))) float stats[2][2][kTileRows];       // [buf][-lse*log2e | -delta][row]
@@ -644,10 +652,11 @@ __global__ __launch_bounds__(256) void m16_dkdv(KernelArgs a) {
       const int4 e = qtab[blk];
       const int row = __builtin_amdgcn_readfirstlane(e.x), nq = __builtin_amdgcn_readfirstlane(e.z);
       const int qh = kvh * group + hh;
-      const int64_t off = static_cast<int64_t>(qh) * kD * 2 + static_cast<int64_t>(row) * qrow_bytes;
+      const int64_t col = static_cast<int64_t>(qh) * kD * 2;
       const uint32_t tile = lds0 + buf * 2 * T::TB;
-      copy_tile<kD>(reinterpret_cast<const char*>(a.q) + off, qrow_bytes, nq, tile, wave, lane);
-      copy_tile<kD>(reinterpret_cast<const char*>(a.dout) + off, qrow_bytes, nq, tile + T::TB, wave, lane);
+      copy_tile<kD>(reinterpret_cast<const char*>(a.q) + col + static_cast<int64_t>(row) * q_rb, q_rb, nq, tile, wave, lane);
+      copy_tile<kD>(reinterpret_cast<const char*>(a.dout) + col + static_cast<int64_t>(row) * g_rb, g_rb, nq, tile + T::TB,
+                    wave, lane);
       if (wave < 2) {  // wave 0: -lse*log2e, wave 1: -delta; rows past the block end copy -inf / 0
         const int64_t at = static_cast<int64_t>(qh) * a.total_q + row + lane;
         const float* rows = wave == 0 ? a.stat_ws + kStatRowsOffset : a.ndelta_ws;
@@ -663,12 +672,12 @@ __global__ __launch_bounds__(256) void m16_dkdv(KernelArgs a) {
     for (int kb = 0; kb < KB; kb++) {
       const bf16* kbase = static_cast<const bf16*>(prefix ? a.pk : a.k);
       const bf16* vbase = static_cast<const bf16*>(prefix ? a.pv : a.v);
-      const int key = min(kw0 + 16 * kb + i16, seg_len - 1);
-      const int64_t off = static_cast<int64_t>(seg_row0 + key) * kstride + kvh * kD + 8 * g;
+      const int64_t key = seg_row0 + min(kw0 + 16 * kb + i16, seg_len - 1), col = kvh * kD + 8 * g;
+      const int64_t koff = key * (prefix ? kstride : a.k_rs) + col, voff = key * (prefix ? kstride : a.v_rs) + col;
 #pragma unroll
       for (int s = 0; s < T::NS; s++) {
-        kv[kb][s] = *reinterpret_cast<const bf16x8*>(kbase + off + 32 * s);
-        vv[kb][s] = *reinterpret_cast<const bf16x8*>(vbase + off + 32 * s);
+        kv[kb][s] = *reinterpret_cast<const bf16x8*>(kbase + koff + 32 * s);
+        vv[kb][s] = *reinterpret_cast<const bf16x8*>(vbase + voff + 32 * s);
       }
     }
     // register r of block [kb][db]: key 16 kb + 4 g + r of the wave, head dim 16 db + l % 16

@@ -208,15 +208,18 @@ __device__ __forceinline__ void stage_tile(float* tile, const T* base, int64_t s
 
 // Segment sg of a forward / dQ workgroup's key stream: 0 = the leaf's suffix
 // (the first `suffix_keys` keys, causal), 1 + r = key run r of the leaf.
-// Returns false past the last run.
+// Sets the segment's K and V row strides (elements): the caller's for the
+// suffix, packed for the prefix. Returns false past the last run.
 template <typename T>
 __device__ __forceinline__ bool key_segment(const KernelArgs& a, int leaf, int sg, int suffix_keys, int kvh,
-                                            const T*& kb, const T*& vb, int& seg_len) {
+                                            const T*& kb, const T*& vb, int64_t& kst, int64_t& vst, int& seg_len) {
   const int64_t ks = static_cast<int64_t>(a.hkv) * a.d;
   if (sg == 0) {
     const int row0 = a.plan[a.off_cu + leaf];
-    kb = static_cast<const T*>(a.k) + static_cast<int64_t>(row0) * ks + kvh * a.d;
-    vb = static_cast<const T*>(a.v) + static_cast<int64_t>(row0) * ks + kvh * a.d;
+    kb = static_cast<const T*>(a.k) + static_cast<int64_t>(row0) * a.k_rs + kvh * a.d;
+    vb = static_cast<const T*>(a.v) + static_cast<int64_t>(row0) * a.v_rs + kvh * a.d;
+    kst = a.k_rs;
+    vst = a.v_rs;
     seg_len = suffix_keys;
     return true;
   }
@@ -226,6 +229,7 @@ __device__ __forceinline__ bool key_segment(const KernelArgs& a, int leaf, int s
   if (seg_len == 0) return false;  // {0, 0} pads the run list
   kb = static_cast<const T*>(a.pk) + static_cast<int64_t>(run[0]) * ks + kvh * a.d;
   vb = static_cast<const T*>(a.pv) + static_cast<int64_t>(run[0]) * ks + kvh * a.d;
+  kst = vst = ks;
   return true;
 }
 
@@ -244,7 +248,7 @@ __global__ __launch_bounds__(kSimtQ * DMAX / 32) void simt_fwd(KernelArgs a) {
   const int c = threadIdx.x % kL;
   const int t = tok0 + static_cast<int>(threadIdx.x) / kL;
   const bool valid = t < len;
-  const int64_t qs = static_cast<int64_t>(a.hq) * d, ks = static_cast<int64_t>(a.hkv) * d;
+  const int64_t qs = static_cast<int64_t>(a.hq) * d;
 
   constexpr bool kBf = __is_same(T, bf16);  // bf16 dot operands (K tile in bf16)
   __shared__ __attribute__((aligned(16))) float Ks[kBf ? 4 : kTile * DMAX];
@@ -254,7 +258,7 @@ __global__ __launch_bounds__(kSimtQ * DMAX / 32) void simt_fwd(KernelArgs a) {
   const float cs = a.scale * kLog2e;
   f32x4 q[8], o[8];
   bf16x8 qb[4];
-  const T* qrow = static_cast<const T*>(a.q) + static_cast<int64_t>(row0 + (valid ? t : 0)) * qs + qh * d;
+  const T* qrow = static_cast<const T*>(a.q) + static_cast<int64_t>(row0 + (valid ? t : 0)) * a.q_rs + qh * d;
   if constexpr (kBf) load_slice_bf<kL>(qrow, d, c, qb);
   else load_slice<kL>(qrow, d, c, cs, q);
 #pragma unroll
@@ -263,15 +267,16 @@ __global__ __launch_bounds__(kSimtQ * DMAX / 32) void simt_fwd(KernelArgs a) {
 
   const int suffix_keys = min(len, tok0 + kSimtQ);
   const T *kb, *vb;
+  int64_t ks, vs;
   int seg_len;
-  for (int sg = 0; key_segment<T>(a, leaf, sg, suffix_keys, kvh, kb, vb, seg_len); sg++) {
+  for (int sg = 0; key_segment<T>(a, leaf, sg, suffix_keys, kvh, kb, vb, ks, vs, seg_len); sg++) {
     const bool causal = sg == 0;
     for (int j0 = 0; j0 < seg_len; j0 += kTile) {
       const int nk = min(kTile, seg_len - j0);
       __syncthreads();
       if constexpr (kBf) stage_tile_bf<DMAX>(Kb, kb, ks, j0, kTile, nk, d);
       else stage_tile<DMAX>(Ks, kb, ks, j0, kTile, nk, d);
-      stage_tile<DMAX>(Vs, vb, ks, j0, kTile, nk, d);
+      stage_tile<DMAX>(Vs, vb, vs, j0, kTile, nk, d);
       __syncthreads();
       float s[kTile];
       float mt = m;
@@ -335,7 +340,7 @@ __global__ __launch_bounds__(kSimtQ * DMAX / 32) void simt_dq(KernelArgs a) {
   const int t = tok0 + static_cast<int>(threadIdx.x) / kL;
   const bool valid = t < len;
   const int tr = valid ? t : 0;
-  const int64_t qs = static_cast<int64_t>(a.hq) * d, ks = static_cast<int64_t>(a.hkv) * d;
+  const int64_t qs = static_cast<int64_t>(a.hq) * d;
 
   constexpr bool kBf = __is_same(T, bf16);  // bf16 dot operands (K, V tiles also in bf16)
   __shared__ __attribute__((aligned(16))) float Ks[kTile * DMAX];
@@ -346,7 +351,7 @@ __global__ __launch_bounds__(kSimtQ * DMAX / 32) void simt_dq(KernelArgs a) {
   const float cs = a.scale * kLog2e;
   f32x4 q[8], g[8], dq[8];
   bf16x8 qb[4], gb[4];
-  const T* qrow = static_cast<const T*>(a.q) + static_cast<int64_t>(row0 + tr) * qs + qh * d;
+  const T* qrow = static_cast<const T*>(a.q) + static_cast<int64_t>(row0 + tr) * a.q_rs + qh * d;
   const T* grow = static_cast<const T*>(a.dout) + static_cast<int64_t>(row0 + tr) * qs + qh * d;
   if constexpr (kBf) {
     load_slice_bf<kL>(qrow, d, c, qb);
@@ -363,8 +368,9 @@ __global__ __launch_bounds__(kSimtQ * DMAX / 32) void simt_dq(KernelArgs a) {
 
   const int suffix_keys = min(len, tok0 + kSimtQ);
   const T *kb, *vb;
+  int64_t ks, vs;
   int seg_len;
-  for (int sg = 0; key_segment<T>(a, leaf, sg, suffix_keys, kvh, kb, vb, seg_len); sg++) {
+  for (int sg = 0; key_segment<T>(a, leaf, sg, suffix_keys, kvh, kb, vb, ks, vs, seg_len); sg++) {
     const bool causal = sg == 0;
     for (int j0 = 0; j0 < seg_len; j0 += kTile) {
       const int nk = min(kTile, seg_len - j0);
@@ -372,9 +378,9 @@ __global__ __launch_bounds__(kSimtQ * DMAX / 32) void simt_dq(KernelArgs a) {
       stage_tile<DMAX>(Ks, kb, ks, j0, kTile, nk, d);
       if constexpr (kBf) {
         stage_tile_bf<DMAX>(Kb, kb, ks, j0, kTile, nk, d);
-        stage_tile_bf<DMAX>(Vb, vb, ks, j0, kTile, nk, d);
+        stage_tile_bf<DMAX>(Vb, vb, vs, j0, kTile, nk, d);
       } else {
-        stage_tile<DMAX>(Vs, vb, ks, j0, kTile, nk, d);
+        stage_tile<DMAX>(Vs, vb, vs, j0, kTile, nk, d);
       }
       __syncthreads();
       for (int j = 0; j < nk; j++) {
@@ -432,8 +438,8 @@ __global__ __launch_bounds__(kSimtKeys * DMAX / 32) void simt_dkdv(KernelArgs a)
   __shared__ float Ls[kTile], Ds[kTile];  // lse * log2e, delta
 
   f32x4 kr[8], vr[8], dk[8], dv[8];
-  load_slice<kL>(kbase + krow * ks + kvh * d, d, c, a.scale * kLog2e, kr);
-  load_slice<kL>(vbase + krow * ks + kvh * d, d, c, 1.f, vr);
+  load_slice<kL>(kbase + krow * (prefix ? ks : a.k_rs) + kvh * d, d, c, a.scale * kLog2e, kr);
+  load_slice<kL>(vbase + krow * (prefix ? ks : a.v_rs) + kvh * d, d, c, 1.f, vr);
 #pragma unroll
   for (int j = 0; j < 8; j++) {
     dk[j] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -449,7 +455,7 @@ __global__ __launch_bounds__(kSimtKeys * DMAX / 32) void simt_dkdv(KernelArgs a)
         const int nq = min(kTile, nblk - sub);
         const int64_t r0 = static_cast<int64_t>(row0) + tok0 + sub;
         __syncthreads();
-        stage_tile<DMAX>(Qs, static_cast<const T*>(a.q) + qh * d, qs, r0, kTile, nq, d);
+        stage_tile<DMAX>(Qs, static_cast<const T*>(a.q) + qh * d, a.q_rs, r0, kTile, nq, d);
         stage_tile<DMAX>(Gs, static_cast<const T*>(a.dout) + qh * d, qs, r0, kTile, nq, d);
         for (int i = threadIdx.x; i < kTile; i += blockDim.x) {
           const int64_t at = static_cast<int64_t>(qh) * a.total_q + r0 + (i < nq ? i : 0);

@@ -47,6 +47,37 @@ def _stream_handle(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+_MAX_ROW_BYTES = 1 << 25
+
+
+def _rows(t: torch.Tensor) -> torch.Tensor:
+    """``t`` itself when the kernels can read it through a row stride (heads
+    and head_dim packed, rows 16-byte aligned: a slice of a fused
+    [tokens, (Hq + 2 Hkv) * D] projection is one), else a packed copy."""
+    _, h, d = t.shape
+    es = t.element_size()
+    rs = t.stride(0)
+    if ((t.stride(2) == 1 or d == 1) and (t.stride(1) == d or h == 1) and rs >= h * d and (rs * es) % 16 == 0
+            and rs * es <= _MAX_ROW_BYTES and t.data_ptr() % 16 == 0):
+        return t
+    return t.contiguous()
+
+
+def _row_stride(t: torch.Tensor) -> int:
+    """Row stride (elements) for the ABI: 0 when packed."""
+    _, h, d = t.shape
+    return 0 if t.shape[0] <= 1 or t.stride(0) == h * d else t.stride(0)
+
+
+def _inputs(q, k, v, prefix_k, prefix_v):
+    """q, k, v as strided row views where possible; the prefix packed."""
+    return _rows(q), _rows(k), _rows(v), prefix_k.contiguous(), prefix_v.contiguous()
+
+
+def _empty(t: torch.Tensor) -> torch.Tensor:
+    return torch.empty(t.shape, dtype=t.dtype, device=t.device)
+
+
 def validate(q, k, v, prefix_k, prefix_v, meta: TPRPrefixMeta, softmax_scale):
     """Contract checks with the reference's exception types and wording
     (rectangular_attention.py:51-83, 165-172). Returns the resolved scale."""
@@ -101,7 +132,7 @@ def validate(q, k, v, prefix_k, prefix_v, meta: TPRPrefixMeta, softmax_scale):
 
 def _forward(q, k, v, prefix_k, prefix_v, meta, scale):
     plan = meta.plan(q.shape[1], k.shape[1], q.shape[2], q.dtype, q.device)
-    out = torch.empty_like(q)
+    out = _empty(q)
     lse = torch.empty((q.shape[1], q.shape[0]), dtype=torch.float32, device=q.device)
     if q.shape[0] == 0:
         return out, lse
@@ -109,7 +140,8 @@ def _forward(q, k, v, prefix_k, prefix_v, meta, scale):
     params = _lib.TprFwdParams(
         _lib.ABI_VERSION, 0, scale, 0.0,
         plan.host.data_ptr(), plan.device.data_ptr(),
-        _ptr(q), _ptr(k), _ptr(v), _ptr(prefix_k), _ptr(prefix_v), _ptr(out), _ptr(lse))
+        _ptr(q), _ptr(k), _ptr(v), _ptr(prefix_k), _ptr(prefix_v), _ptr(out), _ptr(lse),
+        _row_stride(q), _row_stride(k), _row_stride(v))
     _lib.check(lib.tpr_attn_fwd(ctypes.byref(params), ctypes.c_void_p(_stream_handle(q.device))), "tpr_attn_fwd")
     return out, lse
 
@@ -143,9 +175,12 @@ def _backward(q, k, v, prefix_k, prefix_v, out, lse, dout, meta, scale, *, phase
     also what is returned for them."""
     plan = meta.plan(q.shape[1], k.shape[1], q.shape[2], q.dtype, q.device)
     b = dict(buffers or {})
-    dq = b.get("dq") if b.get("dq") is not None else torch.empty_like(q)
-    dk = b.get("dk") if b.get("dk") is not None else torch.empty_like(k)
-    dv = b.get("dv") if b.get("dv") is not None else torch.empty_like(v)
+    dq = b.get("dq") if b.get("dq") is not None else _empty(q)
+    dk = b.get("dk") if b.get("dk") is not None else _empty(k)
+    dv = b.get("dv") if b.get("dv") is not None else _empty(v)
+    for name, t in (("dq", dq), ("dk", dk), ("dv", dv)):
+        if not t.is_contiguous():
+            raise ValueError(f"buffer {name} must be contiguous (gradients are written packed)")
     flags = 0
     if prefix_grad_accumulators is not None:
         dpk, dpv = _check_accumulators(prefix_grad_accumulators, prefix_k)
@@ -166,7 +201,8 @@ def _backward(q, k, v, prefix_k, prefix_v, out, lse, dout, meta, scale, *, phase
         _lib.ABI_VERSION, flags, scale, 0.0,
         plan.host.data_ptr(), plan.device.data_ptr(),
         _ptr(q), _ptr(k), _ptr(v), _ptr(prefix_k), _ptr(prefix_v), _ptr(out), _ptr(dout), _ptr(lse),
-        _ptr(delta), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dpk), _ptr(dpv), _ptr(ws), plan.workspace_bytes)
+        _ptr(delta), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dpk), _ptr(dpv), _ptr(ws), plan.workspace_bytes,
+        _row_stride(q), _row_stride(k), _row_stride(v))
     mask = phases if phases is not None else (_lib.TPR_BWD_DELTA | _lib.TPR_BWD_DKDV | _lib.TPR_BWD_DQ)
     _lib.check(lib.tpr_attn_bwd_phases(ctypes.byref(params), int(mask), ctypes.c_void_p(_stream_handle(q.device))),
                "tpr_attn_bwd")
@@ -189,7 +225,7 @@ class TPRPrefixAttention(torch.autograd.Function):
             if prefix_k.requires_grad or prefix_v.requires_grad:
                 raise ValueError("prefix_k/prefix_v must not require grad when prefix_grad_accumulators is given")
             _check_accumulators(prefix_grad_accumulators, prefix_k)
-        q, k, v, prefix_k, prefix_v = (t.contiguous() for t in (q, k, v, prefix_k, prefix_v))
+        q, k, v, prefix_k, prefix_v = _inputs(q, k, v, prefix_k, prefix_v)
         out, lse = _forward(q, k, v, prefix_k, prefix_v, meta, scale)
         ctx.save_for_backward(q, k, v, prefix_k, prefix_v, out, lse)
         ctx.meta = meta
@@ -220,7 +256,7 @@ def tpr_prefix_attention(q, k, v, prefix_k, prefix_v, meta: TPRPrefixMeta, softm
 def prefix_attention_forward(q, k, v, prefix_k, prefix_v, meta: TPRPrefixMeta, softmax_scale=None):
     """Forward only, no autograd graph: (out, lse)."""
     scale = validate(q, k, v, prefix_k, prefix_v, meta, softmax_scale)
-    q, k, v, prefix_k, prefix_v = (t.contiguous() for t in (q, k, v, prefix_k, prefix_v))
+    q, k, v, prefix_k, prefix_v = _inputs(q, k, v, prefix_k, prefix_v)
     return _forward(q, k, v, prefix_k, prefix_v, meta, scale)
 
 
@@ -236,6 +272,6 @@ def prefix_attention_backward(q, k, v, prefix_k, prefix_v, out, lse, dout, meta:
     ``prefix_grad_accumulators``: a (dK, dV) pair of fp32 tensors shaped like
     prefix_k into which the prefix gradients are added (and returned)."""
     scale = validate(q, k, v, prefix_k, prefix_v, meta, softmax_scale)
-    tensors = [t.contiguous() for t in (q, k, v, prefix_k, prefix_v, out, lse, dout)]
+    tensors = [*_inputs(q, k, v, prefix_k, prefix_v), *(t.contiguous() for t in (out, lse, dout))]
     return _backward(*tensors[:7], tensors[7], meta, scale, phases=phases, buffers=buffers,
                      prefix_grad_accumulators=prefix_grad_accumulators)

@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define TPR_ATTN_ABI_VERSION 2
+#define TPR_ATTN_ABI_VERSION 3
 
 typedef enum TprStatus {
   TPR_OK = 0,
@@ -57,8 +57,9 @@ typedef enum TprStatus {
 } TprStatus;
 
 /* head_dim: a multiple of 8, at most 256. bf16 with head_dim 128 runs on the
- * MFMA kernels (any tree depth); fp32 and the other head sizes on the SIMT
- * kernels. Both accumulate in fp32. */
+ * 32x32x16 MFMA kernels, bf16 with head_dim 64 or 256 on the 16x16x32 MFMA
+ * kernels (any tree depth); fp32 and the other head sizes on the SIMT
+ * kernels. All accumulate in fp32. */
 typedef enum TprDtype {
   TPR_DTYPE_BF16 = 0, /* bf16 in/out, fp32 accumulation */
   TPR_DTYPE_FP32 = 1  /* fp32 in/out, fp32 accumulation */
@@ -105,6 +106,15 @@ typedef struct TprFwdParams {
   const void* prefix_v;
   void* out;
   float* lse;
+  /* Token (row) strides of q, k and v in elements; 0 = packed (Hq*D for q,
+   * Hkv*D for k and v). They let q, k and v be read as views of a wider
+   * buffer, e.g. the column slices of a fused QKV projection
+   * [tokens, (Hq + 2 Hkv) * D], without a copy. A stride must be at least the
+   * packed one, give rows of a multiple of 16 bytes and at most 32 MiB; the
+   * heads of a row stay packed (head stride D). Every other tensor is packed. */
+  int64_t q_row_stride;
+  int64_t k_row_stride;
+  int64_t v_row_stride;
 } TprFwdParams;
 
 /* Backward: dq, dk, dv for the suffix tokens, and dprefix_k/dprefix_v summed
@@ -145,6 +155,11 @@ typedef struct TprBwdParams {
   void* dprefix_v;
   void* workspace;
   size_t workspace_bytes;
+  /* row strides of q, k and v, as in TprFwdParams (0 = packed); the
+   * gradients dq, dk, dv are written packed */
+  int64_t q_row_stride;
+  int64_t k_row_stride;
+  int64_t v_row_stride;
 } TprBwdParams;
 
 /* ABI version compiled into the library (TPR_ATTN_ABI_VERSION). */

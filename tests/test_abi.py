@@ -26,7 +26,7 @@ def _declared_functions():
 
 def test_library_loads_and_reports_abi_version():
     lib = _lib.load()
-    assert lib.tpr_attn_abi_version() == _lib.ABI_VERSION == 2
+    assert lib.tpr_attn_abi_version() == _lib.ABI_VERSION == 3
 
 
 def test_every_declared_symbol_is_exported_and_bound():
@@ -132,3 +132,68 @@ def test_misaligned_workspace_is_rejected_before_any_launch():
     b.workspace_bytes = need + 256
     assert lib.tpr_attn_bwd(ctypes.byref(b), None) == _lib.TPR_ERR_INVALID_ARGUMENT
     assert b"256-byte aligned" in lib.tpr_attn_last_error()
+
+
+def _fake_fwd_params(plan):
+    p = _lib.TprFwdParams(_lib.ABI_VERSION, 0, 0.1, 0.0, plan.host.data_ptr(), plan.host.data_ptr())
+    fake = 1 << 20
+    for name in ("q", "k", "v", "prefix_k", "prefix_v", "out", "lse"):
+        setattr(p, name, fake)
+        fake += 1 << 20
+    return p
+
+
+def test_bad_row_strides_are_rejected_before_any_launch():
+    """q/k/v row strides: 0 (packed) or at least the packed stride, rows a
+    multiple of 16 bytes, at most 32 MiB. The checks run on the host before
+    anything is enqueued (the pointers below are never dereferenced)."""
+    import torch
+
+    from bridge_amd import TPRPrefixMeta
+    lib = _lib.load()
+    for dtype, d, elem in ((torch.bfloat16, 128, 2), (torch.bfloat16, 64, 2), (torch.float32, 96, 4)):
+        hq, hkv = 4, 2
+        plan = TPRPrefixMeta.shared_prefix(8, [4]).plan(hq, hkv, d, dtype, torch.device("cpu"))
+        cases = [("q_row_stride", hq * d - 8, "at least"), ("k_row_stride", hkv * d - 8, "at least"),
+                 ("v_row_stride", hkv * d + 8 // elem + 1, "16 bytes"), ("q_row_stride", (1 << 25) // elem + 8,
+                                                                        "32 MiB")]
+        for field, value, words in cases:
+            p = _fake_fwd_params(plan)
+            setattr(p, field, value)
+            assert lib.tpr_attn_fwd(ctypes.byref(p), None) != 0, (dtype, field, value)
+            msg = lib.tpr_attn_last_error()
+            assert field.encode() in msg and words.encode() in msg, msg
+        b = _lib.TprBwdParams()
+        b.abi_version = _lib.ABI_VERSION
+        b.softmax_scale = 0.1
+        b.plan_host = b.plan_device = plan.host.data_ptr()
+        b.k_row_stride = hkv * d - 8
+        assert lib.tpr_attn_bwd(ctypes.byref(b), None) != 0
+        assert b"k_row_stride" in lib.tpr_attn_last_error() or b"must not be NULL" in lib.tpr_attn_last_error()
+
+
+def test_fused_projection_views_pass_through_with_their_row_stride():
+    """Slices of one [tokens, (Hq + 2 Hkv) * D] projection reach the kernels
+    as views with the projection's row stride; layouts the kernels cannot read
+    (head stride not D, misaligned rows) are copied packed."""
+    import torch
+
+    from bridge_amd.prefix_attention import _inputs, _row_stride, _rows
+    t, hq, hkv, d = 10, 4, 2, 64
+    qkv = torch.zeros(t, (hq + 2 * hkv) * d, dtype=torch.bfloat16)
+    q = qkv[:, :hq * d].view(t, hq, d)
+    k = qkv[:, hq * d:(hq + hkv) * d].view(t, hkv, d)
+    v = qkv[:, (hq + hkv) * d:].view(t, hkv, d)
+    pk = torch.zeros(3, hkv, d, dtype=torch.bfloat16)
+    q2, k2, v2, pk2, pv2 = _inputs(q, k, v, pk, pk)
+    for a, b in ((q, q2), (k, k2), (v, v2)):
+        assert b.data_ptr() == a.data_ptr() and _row_stride(b) == (hq + 2 * hkv) * d
+    assert _row_stride(pk2) == 0
+    assert _row_stride(torch.zeros(t, hq, d)) == 0
+    heads_strided = torch.zeros(t, hq, 2 * d, dtype=torch.bfloat16)[:, :, :d]
+    assert _rows(heads_strided).is_contiguous()
+    odd_rows = torch.zeros(t * (hq * d + 4), dtype=torch.bfloat16).as_strided((t, hq, d), (hq * d + 4, d, 1))
+    assert _rows(odd_rows).is_contiguous()
+    head_major = torch.zeros(hq, t, d, dtype=torch.bfloat16).transpose(0, 1)
+    assert _rows(head_major).is_contiguous()
+
