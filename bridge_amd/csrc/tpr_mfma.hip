@@ -260,7 +260,10 @@ constexpr float kRescaleSlack = 8.f;
 #endif
 constexpr int kMphaseAhead = TPR_MPHASE_AHEAD;  // LDS reads issued ahead in a forward M phase (even)
 
-template <bool kRunList>  // key runs read from the plan (more than kMfmaRegRuns)
+// kRunList: key runs read from the plan (more than kMfmaRegRuns); kStrided:
+// q, k or v rows wider than packed (the packed instance folds every row
+// stride to a constant)
+template <bool kRunList, bool kStrided>
 __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
   const int32_t* item = a.plan + a.off_fwd + 4 * blockIdx.x;
   const int leaf = item[0];
@@ -283,8 +286,10 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
   const int64_t qstride = static_cast<int64_t>(a.hq) * kMfmaD;  // output rows (packed)
   // row bytes of the suffix K and V (views of a wider buffer allowed) and of
   // the packed prefix K/V
-  const uint32_t k_rb = static_cast<uint32_t>(a.k_rs) * 2, v_rb = static_cast<uint32_t>(a.v_rs) * 2;
   const uint32_t p_rb = static_cast<uint32_t>(a.hkv) * kMfmaD * 2;
+  const uint32_t k_rb = kStrided ? static_cast<uint32_t>(a.k_rs) * 2 : p_rb;
+  const uint32_t v_rb = kStrided ? static_cast<uint32_t>(a.v_rs) * 2 : p_rb;
+  const int64_t q_rs = kStrided ? a.q_rs : qstride;
 
   __shared__ __attribute__((aligned(1024))) char smem[4 * kTileBytes];  // K0 K1 V0 V1
   static_assert(sizeof(smem) >= kFwdWaves * 8192, "the output rows are staged in the tile buffers");
@@ -319,7 +324,7 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
   // Q as the B operand of S^T = K Q^T: lane holds Q[t][16c + 8h .. +7]
   bf16x8 qv[8];
   {
-    const bf16* qp = static_cast<const bf16*>(a.q) + static_cast<int64_t>(row0 + min(t, len - 1)) * a.q_rs +
+    const bf16* qp = static_cast<const bf16*>(a.q) + static_cast<int64_t>(row0 + min(t, len - 1)) * q_rs +
                      head * kMfmaD + 8 * h;
 #pragma unroll
     for (int c = 0; c < 8; c++) qv[c] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(qp + 16 * c));
@@ -584,7 +589,7 @@ __device__ __forceinline__ uint32_t kt_off(int d, int chunk) {
 #endif
 constexpr int kDqAhead = TPR_DQ_AHEAD;  // LDS reads issued ahead in a dQ M phase
 
-template <bool kRunList>  // key runs read from the plan (more than kMfmaRegRuns)
+template <bool kRunList, bool kStrided>  // as mfma_fwd
 __global__ __launch_bounds__(512) void mfma_dq(KernelArgs a) {
   static_assert(kFwdWaves == 8, "two groups of one wave per SIMD");
   const int32_t* item = a.plan + a.off_fwd + 4 * blockIdx.x;
@@ -608,8 +613,10 @@ __global__ __launch_bounds__(512) void mfma_dq(KernelArgs a) {
   const int64_t qstride = static_cast<int64_t>(a.hq) * kMfmaD;  // dO and dQ rows (packed)
   // row bytes of the suffix K and V (views of a wider buffer allowed) and of
   // the packed prefix K/V; the full-tile copy offsets are made for the latter
-  const uint32_t k_rb = static_cast<uint32_t>(a.k_rs) * 2, v_rb = static_cast<uint32_t>(a.v_rs) * 2;
   const uint32_t p_rb = static_cast<uint32_t>(a.hkv) * kMfmaD * 2;
+  const uint32_t k_rb = kStrided ? static_cast<uint32_t>(a.k_rs) * 2 : p_rb;
+  const uint32_t v_rb = kStrided ? static_cast<uint32_t>(a.v_rs) * 2 : p_rb;
+  const int64_t q_rs = kStrided ? a.q_rs : qstride;
 
   // K0 K1 V0 V1 (row-major, swizzled) | T0 T1 (K^T)
   __shared__ __attribute__((aligned(1024))) char smem[6 * kTileBytes];
@@ -664,9 +671,10 @@ __global__ __launch_bounds__(512) void mfma_dq(KernelArgs a) {
 
   bf16x8 qv[8], gv[8];
   {
-    const int64_t col = head * kMfmaD + 8 * h;
-    const bf16* qp = static_cast<const bf16*>(a.q) + static_cast<int64_t>(row0 + tc) * a.q_rs + col;
-    const bf16* gp = static_cast<const bf16*>(a.dout) + static_cast<int64_t>(row0 + tc) * qstride + col;
+    const int64_t off = static_cast<int64_t>(row0 + tc) * qstride + head * kMfmaD + 8 * h;
+    const int64_t qoff = kStrided ? static_cast<int64_t>(row0 + tc) * q_rs + head * kMfmaD + 8 * h : off;
+    const bf16* qp = static_cast<const bf16*>(a.q) + qoff;
+    const bf16* gp = static_cast<const bf16*>(a.dout) + off;
 #pragma unroll
     for (int c = 0; c < 8; c++) {
       qv[c] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(qp + 16 * c));
@@ -898,7 +906,7 @@ constexpr bool kInterleave = TPR_DKDV_INTERLEAVE;
 constexpr int slot_sub(int m) { return kInterleave ? (m & 1) : (m >> 5); }
 constexpr int slot_pos(int m) { return kInterleave ? (m >> 1) : (m & 31); }
 
-template <int kHeads>
+template <int kHeads, bool kStrided>  // kStrided as in mfma_fwd
 __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
   const int32_t* item = a.plan + a.off_dkdv + DK_WORDS * blockIdx.x;
   if (item[DK_SRC] < 0) return;
@@ -971,16 +979,18 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
     // row bytes of dO (packed; the full-block lane offsets are made for it)
     // and of Q (a view of a wider buffer allowed)
     const uint32_t g_rb = static_cast<uint32_t>(a.hq) * kMfmaD * 2;
-    const uint32_t q_rb = static_cast<uint32_t>(a.q_rs) * 2;
-    const bool q_packed = q_rb == g_rb;
+    const uint32_t q_rb = kStrided ? static_cast<uint32_t>(a.q_rs) * 2 : g_rb;
+    const bool q_packed = !kStrided || q_rb == g_rb;
     const DmaLanes<kDkdvWaves> dl = make_dma_lanes<kDkdvWaves>(g_rb, wave, lane);
     const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(smem));
     // copy the Q and dO rows [row, row + 64) of query head qh into the stage buffer at byte `tile`
     auto issue_stage = [&](int row, int nq, int qh, uint32_t tile) __attribute__((always_inline)) {
       const int64_t col = static_cast<int64_t>(qh) * kMfmaD * 2;
+      const int64_t goff = col + static_cast<int64_t>(row) * g_rb;
+      const int64_t qoff = kStrided ? col + static_cast<int64_t>(row) * q_rb : goff;
       const uint32_t dst = lds0 + tile + wave * 4096;
-      const char* qs = reinterpret_cast<const char*>(qbase) + col + static_cast<int64_t>(row) * q_rb;
-      const char* gs = reinterpret_cast<const char*>(gbase) + col + static_cast<int64_t>(row) * g_rb;
+      const char* qs = reinterpret_cast<const char*>(qbase) + qoff;
+      const char* gs = reinterpret_cast<const char*>(gbase) + goff;
       if (nq >= kTileRows && q_packed) {
         dma_blocks4(qs, dl.voff[0], dl.voff[1], dl.voff[2], dl.voff[3], dst);
         dma_blocks4(gs, dl.voff[0], dl.voff[1], dl.voff[2], dl.voff[3], dst + kTileBytes);
@@ -988,9 +998,8 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
         uint32_t vq[4], vg[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-          const uint32_t r = static_cast<uint32_t>(min(dl.row[j], nq - 1));
-          vq[j] = r * q_rb + dl.cbytes[j];
-          vg[j] = r * g_rb + dl.cbytes[j];
+          vg[j] = static_cast<uint32_t>(min(dl.row[j], nq - 1)) * g_rb + dl.cbytes[j];
+          vq[j] = kStrided ? static_cast<uint32_t>(min(dl.row[j], nq - 1)) * q_rb + dl.cbytes[j] : vg[j];
         }
         dma_blocks4_m0(qs, vq[0], vq[1], vq[2], vq[3], dst);
         dma_blocks4_m0(gs, vg[0], vg[1], vg[2], vg[3], dst + kTileBytes);
@@ -1027,8 +1036,10 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
     {
       const bf16* kb = static_cast<const bf16*>(prefix ? a.pk : a.k);
       const bf16* vb = static_cast<const bf16*>(prefix ? a.pv : a.v);
-      const int64_t key = seg_row0 + min(kp, seg_len - 1), col = kvh * kMfmaD + 8 * h;
-      const int64_t koff = key * (prefix ? kstride : a.k_rs) + col, voff = key * (prefix ? kstride : a.v_rs) + col;
+      const int key = seg_row0 + min(kp, seg_len - 1);
+      const int64_t off = static_cast<int64_t>(key) * kstride + kvh * kMfmaD + 8 * h;
+      const int64_t koff = prefix || !kStrided ? off : static_cast<int64_t>(key) * a.k_rs + kvh * kMfmaD + 8 * h;
+      const int64_t voff = prefix || !kStrided ? off : static_cast<int64_t>(key) * a.v_rs + kvh * kMfmaD + 8 * h;
 #pragma unroll
       for (int c = 0; c < 8; c++) {
         kv[c] = *reinterpret_cast<const bf16x8*>(kb + koff + 16 * c);
@@ -1366,14 +1377,36 @@ __global__ __launch_bounds__(256) void mfma_reduce(KernelArgs a) {
   }
 }
 
+// Whether any of q, k, v has rows wider than packed.
+bool strided_rows(const KernelArgs& a) {
+  return a.q_rs != static_cast<int64_t>(a.hq) * kMfmaD || a.k_rs != static_cast<int64_t>(a.hkv) * kMfmaD ||
+         a.v_rs != static_cast<int64_t>(a.hkv) * kMfmaD;
+}
+
+template <bool kRunList>
+void launch_fwd_tile(const KernelArgs& a, hipStream_t s) {
+  if (strided_rows(a))
+    hipLaunchKernelGGL((mfma_fwd<kRunList, true>), dim3(a.n_items), dim3(64 * kFwdWaves), 0, s, a);
+  else
+    hipLaunchKernelGGL((mfma_fwd<kRunList, false>), dim3(a.n_items), dim3(64 * kFwdWaves), 0, s, a);
+}
+
+template <bool kRunList>
+void launch_dq_tile(const KernelArgs& a, int n_fwd, hipStream_t s) {
+  if (strided_rows(a))
+    hipLaunchKernelGGL((mfma_dq<kRunList, true>), dim3(n_fwd), dim3(64 * kFwdWaves), 0, s, a);
+  else
+    hipLaunchKernelGGL((mfma_dq<kRunList, false>), dim3(n_fwd), dim3(64 * kFwdWaves), 0, s, a);
+}
+
 }  // namespace
 
 int launch_mfma_fwd(const KernelArgs& a, hipStream_t s) {
   if (a.n_items > 0) {
     if (a.max_runs > kMfmaRegRuns)
-      hipLaunchKernelGGL(mfma_fwd<true>, dim3(a.n_items), dim3(64 * kFwdWaves), 0, s, a);
+      launch_fwd_tile<true>(a, s);
     else
-      hipLaunchKernelGGL(mfma_fwd<false>, dim3(a.n_items), dim3(64 * kFwdWaves), 0, s, a);
+      launch_fwd_tile<false>(a, s);
   }
   return hipGetLastError() == hipSuccess ? 0 : 4;
 }
@@ -1387,10 +1420,15 @@ int launch_mfma_delta(const KernelArgs& a, hipStream_t s) {
 
 int launch_mfma_bwd(const KernelArgs& a, int n_fwd, int n_dkdv, int n_red, hipStream_t s) {
   if (n_dkdv > 0) {
-    if (a.group % 2 == 0)
-      hipLaunchKernelGGL(mfma_dkdv<2>, dim3(n_dkdv), dim3(256), 0, s, a);
+    const bool st = strided_rows(a);
+    if (a.group % 2 == 0 && st)
+      hipLaunchKernelGGL((mfma_dkdv<2, true>), dim3(n_dkdv), dim3(256), 0, s, a);
+    else if (a.group % 2 == 0)
+      hipLaunchKernelGGL((mfma_dkdv<2, false>), dim3(n_dkdv), dim3(256), 0, s, a);
+    else if (st)
+      hipLaunchKernelGGL((mfma_dkdv<1, true>), dim3(n_dkdv), dim3(256), 0, s, a);
     else
-      hipLaunchKernelGGL(mfma_dkdv<1>, dim3(n_dkdv), dim3(256), 0, s, a);
+      hipLaunchKernelGGL((mfma_dkdv<1, false>), dim3(n_dkdv), dim3(256), 0, s, a);
     if (hipGetLastError() != hipSuccess) return 4;
   }
   if (n_red > 0) {
@@ -1399,9 +1437,9 @@ int launch_mfma_bwd(const KernelArgs& a, int n_fwd, int n_dkdv, int n_red, hipSt
   }
   if (n_fwd > 0) {
     if (a.max_runs > kMfmaRegRuns)
-      hipLaunchKernelGGL(mfma_dq<true>, dim3(n_fwd), dim3(64 * kFwdWaves), 0, s, a);
+      launch_dq_tile<true>(a, n_fwd, s);
     else
-      hipLaunchKernelGGL(mfma_dq<false>, dim3(n_fwd), dim3(64 * kFwdWaves), 0, s, a);
+      launch_dq_tile<false>(a, n_fwd, s);
     if (hipGetLastError() != hipSuccess) return 4;
   }
   return 0;

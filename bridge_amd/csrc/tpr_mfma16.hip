@@ -143,8 +143,10 @@ constexpr float kSlack16 = 8.f;  // lazy-rescale slack in log2 units (as the hea
 // (B); online softmax in registers (lane l holds 16 keys of query l % 16; the
 // other 48 keys of the tile sit in lanes l ^ 16, l ^ 32, l ^ 48); then
 // O^T += V^T P^T with V^T read transposed from LDS (A) and P^T from registers.
+// kRunList: key runs read from the plan; kStrided: q, k or v rows wider than
+// packed (the packed instance folds every row stride to a constant).
 // ---------------------------------------------------------------------------
-template <int kD, bool kRunList>
+template <int kD, bool kRunList, bool kStrided>
 __global__ __launch_bounds__(256) void m16_fwd(KernelArgs a) {
   using T = Geo<kD>;
   const int32_t* item = a.plan + a.off_fwd + 4 * blockIdx.x;
@@ -171,7 +173,9 @@ __global__ __launch_bounds__(256) void m16_fwd(KernelArgs a) {
   const char* pkbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.pk) + kvh * kD);
   const char* pvbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.pv) + kvh * kD);
   // row bytes of a tile's source: prefix K/V packed, suffix K/V as the caller's views
-  const uint32_t k_rb = static_cast<uint32_t>(a.k_rs) * 2, v_rb = static_cast<uint32_t>(a.v_rs) * 2;
+  const uint32_t k_rb = kStrided ? static_cast<uint32_t>(a.k_rs) * 2 : row_bytes;
+  const uint32_t v_rb = kStrided ? static_cast<uint32_t>(a.v_rs) * 2 : row_bytes;
+  const int64_t q_rs = kStrided ? a.q_rs : qstride;
   auto kv_rb = [&](const TileLoc& x, bool is_k) { return x.suffix ? (is_k ? k_rb : v_rb) : row_bytes; };
   auto kv_src = [&](const TileLoc& x, bool is_k) {
     const char* b = x.suffix ? (is_k ? kbase : vbase) : (is_k ? pkbase : pvbase);
@@ -192,7 +196,7 @@ __global__ __launch_bounds__(256) void m16_fwd(KernelArgs a) {
 #pragma unroll
   for (int qs = 0; qs < 2; qs++) {
     const int t = min(tw0 + 16 * qs + i16, len - 1);
-    const bf16* qp = static_cast<const bf16*>(a.q) + static_cast<int64_t>(row0 + t) * a.q_rs + head * kD + 8 * g;
+    const bf16* qp = static_cast<const bf16*>(a.q) + static_cast<int64_t>(row0 + t) * q_rs + head * kD + 8 * g;
 #pragma unroll
     for (int s = 0; s < T::NS; s++) qv[qs][s] = *reinterpret_cast<const bf16x8*>(qp + 32 * s);
   }
@@ -398,7 +402,7 @@ __global__ __launch_bounds__(256) void m16_delta(KernelArgs a) {
 // P = exp2(scale*log2e S - lse*log2e), dS = P (dP - delta), then
 // dQ^T += K^T dS^T with K^T read transposed from the K tile.
 // ---------------------------------------------------------------------------
-template <int kD, bool kRunList>
+template <int kD, bool kRunList, bool kStrided>
 __global__ __launch_bounds__(256) void m16_dq(KernelArgs a) {
   using T = Geo<kD>;
   const int32_t* item = a.plan + a.off_fwd + 4 * blockIdx.x;
@@ -425,7 +429,9 @@ __global__ __launch_bounds__(256) void m16_dq(KernelArgs a) {
   const char* pkbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.pk) + kvh * kD);
   const char* pvbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.pv) + kvh * kD);
   // row bytes of a tile's source: prefix K/V packed, suffix K/V as the caller's views
-  const uint32_t k_rb = static_cast<uint32_t>(a.k_rs) * 2, v_rb = static_cast<uint32_t>(a.v_rs) * 2;
+  const uint32_t k_rb = kStrided ? static_cast<uint32_t>(a.k_rs) * 2 : row_bytes;
+  const uint32_t v_rb = kStrided ? static_cast<uint32_t>(a.v_rs) * 2 : row_bytes;
+  const int64_t q_rs = kStrided ? a.q_rs : qstride;
   auto kv_rb = [&](const TileLoc& x, bool is_k) { return x.suffix ? (is_k ? k_rb : v_rb) : row_bytes; };
   auto kv_src = [&](const TileLoc& x, bool is_k) {
     const char* b = x.suffix ? (is_k ? kbase : vbase) : (is_k ? pkbase : pvbase);
@@ -447,7 +453,7 @@ __global__ __launch_bounds__(256) void m16_dq(KernelArgs a) {
   for (int qs = 0; qs < 2; qs++) {
     const int t = min(tw0 + 16 * qs + i16, len - 1);
     const int64_t off = static_cast<int64_t>(row0 + t) * qstride + head * kD + 8 * g;
-    const int64_t qoff = static_cast<int64_t>(row0 + t) * a.q_rs + head * kD + 8 * g;
+    const int64_t qoff = static_cast<int64_t>(row0 + t) * q_rs + head * kD + 8 * g;
 #pragma unroll
     for (int s = 0; s < T::NS; s++) {
       qv[qs][s] = *reinterpret_cast<const bf16x8*>(static_cast<const bf16*>(a.q) + qoff + 32 * s);
@@ -593,7 +599,7 @@ __global__ __launch_bounds__(256) void m16_dq(KernelArgs a) {
 //   dV += P^T dO, dK += dS^T Q (dO, Q read transposed from LDS, again shared
 //   by the key blocks).
 // ---------------------------------------------------------------------------
-template <int kD>
+template <int kD, bool kStrided>  // kStrided as in m16_fwd
 __global__ __launch_bounds__(256) void m16_dkdv(KernelArgs a) {
   using T = Geo<kD>;
   constexpr int kWaveKeys = m16_wave_keys(kD);
@@ -614,7 +620,7 @@ __global__ __launch_bounds__(256) void m16_dkdv(KernelArgs a) {
 
   const int64_t kstride = static_cast<int64_t>(a.hkv) * kD;  // packed K/V rows: prefix inputs, every output
   const uint32_t g_rb = static_cast<uint32_t>(a.hq) * kD * 2;  // dO row bytes (packed)
-  const uint32_t q_rb = static_cast<uint32_t>(a.q_rs) * 2;     // Q row bytes
+  const uint32_t q_rb = kStrided ? static_cast<uint32_t>(a.q_rs) * 2 : g_rb;  // Q row bytes
 
   __shared__ __attribute__((aligned(1024))) char smem[2 * 2 * T::TB];           // [buf][Q | dO]
   __shared__ __attribute__((aligned(256))) float stats[2][2][kTileRows];       // [buf][-lse*log2e | -delta][row]
@@ -653,10 +659,11 @@ __global__ __launch_bounds__(256) void m16_dkdv(KernelArgs a) {
       const int row = __builtin_amdgcn_readfirstlane(e.x), nq = __builtin_amdgcn_readfirstlane(e.z);
       const int qh = kvh * group + hh;
       const int64_t col = static_cast<int64_t>(qh) * kD * 2;
+      const int64_t goff = col + static_cast<int64_t>(row) * g_rb;
+      const int64_t qoff = kStrided ? col + static_cast<int64_t>(row) * q_rb : goff;
       const uint32_t tile = lds0 + buf * 2 * T::TB;
-      copy_tile<kD>(reinterpret_cast<const char*>(a.q) + col + static_cast<int64_t>(row) * q_rb, q_rb, nq, tile, wave, lane);
-      copy_tile<kD>(reinterpret_cast<const char*>(a.dout) + col + static_cast<int64_t>(row) * g_rb, g_rb, nq, tile + T::TB,
-                    wave, lane);
+      copy_tile<kD>(reinterpret_cast<const char*>(a.q) + qoff, q_rb, nq, tile, wave, lane);
+      copy_tile<kD>(reinterpret_cast<const char*>(a.dout) + goff, g_rb, nq, tile + T::TB, wave, lane);
       if (wave < 2) {  // wave 0: -lse*log2e, wave 1: -delta; rows past the block end copy -inf / 0
         const int64_t at = static_cast<int64_t>(qh) * a.total_q + row + lane;
         const float* rows = wave == 0 ? a.stat_ws + kStatRowsOffset : a.ndelta_ws;
@@ -672,8 +679,10 @@ __global__ __launch_bounds__(256) void m16_dkdv(KernelArgs a) {
     for (int kb = 0; kb < KB; kb++) {
       const bf16* kbase = static_cast<const bf16*>(prefix ? a.pk : a.k);
       const bf16* vbase = static_cast<const bf16*>(prefix ? a.pv : a.v);
-      const int64_t key = seg_row0 + min(kw0 + 16 * kb + i16, seg_len - 1), col = kvh * kD + 8 * g;
-      const int64_t koff = key * (prefix ? kstride : a.k_rs) + col, voff = key * (prefix ? kstride : a.v_rs) + col;
+      const int key = min(kw0 + 16 * kb + i16, seg_len - 1);
+      const int64_t off = static_cast<int64_t>(seg_row0 + key) * kstride + kvh * kD + 8 * g;
+      const int64_t koff = prefix || !kStrided ? off : static_cast<int64_t>(seg_row0 + key) * a.k_rs + kvh * kD + 8 * g;
+      const int64_t voff = prefix || !kStrided ? off : static_cast<int64_t>(seg_row0 + key) * a.v_rs + kvh * kD + 8 * g;
 #pragma unroll
       for (int s = 0; s < T::NS; s++) {
         kv[kb][s] = *reinterpret_cast<const bf16x8*>(kbase + koff + 32 * s);
@@ -895,13 +904,28 @@ __global__ __launch_bounds__(256) void m16_reduce(KernelArgs a) {
   }
 }
 
+// Whether any of q, k, v has rows wider than packed.
+template <int kD>
+bool strided_rows(const KernelArgs& a) {
+  return a.q_rs != static_cast<int64_t>(a.hq) * kD || a.k_rs != static_cast<int64_t>(a.hkv) * kD ||
+         a.v_rs != static_cast<int64_t>(a.hkv) * kD;
+}
+
+template <int kD, bool kRunList>
+void launch_fwd_runs(const KernelArgs& a, hipStream_t s) {
+  if (strided_rows<kD>(a))
+    hipLaunchKernelGGL((m16_fwd<kD, kRunList, true>), dim3(a.n_items), dim3(64 * kM16Waves), 0, s, a);
+  else
+    hipLaunchKernelGGL((m16_fwd<kD, kRunList, false>), dim3(a.n_items), dim3(64 * kM16Waves), 0, s, a);
+}
+
 template <int kD>
 int launch_fwd_d(const KernelArgs& a, hipStream_t s) {
   if (a.n_items > 0) {
     if (a.max_runs > kMfmaRegRuns)
-      hipLaunchKernelGGL((m16_fwd<kD, true>), dim3(a.n_items), dim3(64 * kM16Waves), 0, s, a);
+      launch_fwd_runs<kD, true>(a, s);
     else
-      hipLaunchKernelGGL((m16_fwd<kD, false>), dim3(a.n_items), dim3(64 * kM16Waves), 0, s, a);
+      launch_fwd_runs<kD, false>(a, s);
   }
   return hipGetLastError() == hipSuccess ? 0 : 4;
 }
@@ -909,7 +933,10 @@ int launch_fwd_d(const KernelArgs& a, hipStream_t s) {
 template <int kD>
 int launch_dkdv_d(const KernelArgs& a, int n_dkdv, int n_red, hipStream_t s) {
   if (n_dkdv > 0) {
-    hipLaunchKernelGGL((m16_dkdv<kD>), dim3(n_dkdv), dim3(64 * kM16Waves), 0, s, a);
+    if (strided_rows<kD>(a))
+      hipLaunchKernelGGL((m16_dkdv<kD, true>), dim3(n_dkdv), dim3(64 * kM16Waves), 0, s, a);
+    else
+      hipLaunchKernelGGL((m16_dkdv<kD, false>), dim3(n_dkdv), dim3(64 * kM16Waves), 0, s, a);
     if (hipGetLastError() != hipSuccess) return 4;
   }
   if (n_red > 0) {
@@ -919,13 +946,21 @@ int launch_dkdv_d(const KernelArgs& a, int n_dkdv, int n_red, hipStream_t s) {
   return 0;
 }
 
+template <int kD, bool kRunList>
+void launch_dq_runs(const KernelArgs& a, int n_fwd, hipStream_t s) {
+  if (strided_rows<kD>(a))
+    hipLaunchKernelGGL((m16_dq<kD, kRunList, true>), dim3(n_fwd), dim3(64 * kM16Waves), 0, s, a);
+  else
+    hipLaunchKernelGGL((m16_dq<kD, kRunList, false>), dim3(n_fwd), dim3(64 * kM16Waves), 0, s, a);
+}
+
 template <int kD>
 int launch_dq_d(const KernelArgs& a, int n_fwd, hipStream_t s) {
   if (n_fwd > 0) {
     if (a.max_runs > kMfmaRegRuns)
-      hipLaunchKernelGGL((m16_dq<kD, true>), dim3(n_fwd), dim3(64 * kM16Waves), 0, s, a);
+      launch_dq_runs<kD, true>(a, n_fwd, s);
     else
-      hipLaunchKernelGGL((m16_dq<kD, false>), dim3(n_fwd), dim3(64 * kM16Waves), 0, s, a);
+      launch_dq_runs<kD, false>(a, n_fwd, s);
     if (hipGetLastError() != hipSuccess) return 4;
   }
   return 0;
