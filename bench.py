@@ -346,6 +346,8 @@ def main() -> int:
                     choices=["qwen3-4b", "plumbing-fp32", "long-session", "ragged", "turn-tree", "qwen35-attn", "head64",
                              "qwen3-4b-1sibling", "qwen3-4b-noprefix"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--recompute-dq", action="store_true",
+                    help="use the plan without a dS store (head_dim 128: dQ recomputes S and dP; small workspace)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="before the timed steps, run one plain device copy of MIB MiB (read MIB, write MIB): "
                          "the calibration dispatch for rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -385,7 +387,7 @@ def main() -> int:
     pk = torch.randn(tp, hkv, d, device=device, generator=gen).to(dtype)
     pv = torch.randn(tp, hkv, d, device=device, generator=gen).to(dtype)
     dout = torch.randn(tq, hq, d, device=device, generator=gen).to(dtype)
-    plan = meta.plan(hq, hkv, d, dtype, device)
+    plan = meta.plan(hq, hkv, d, dtype, device, recompute_dq=args.recompute_dq)
 
     buffers = {"dq": torch.empty_like(q), "dk": torch.empty_like(k), "dv": torch.empty_like(v),
                "dprefix_k": torch.empty_like(pk), "dprefix_v": torch.empty_like(pv),
@@ -406,7 +408,8 @@ def main() -> int:
             if ph is None:
                 out, lse = prefix_attention_forward(q, k, v, pk, pv, meta, scale)
             else:
-                prefix_attention_backward(q, k, v, pk, pv, out, lse, dout, meta, scale, phases=ph, buffers=buffers)
+                prefix_attention_backward(q, k, v, pk, pv, out, lse, dout, meta, scale, phases=ph, buffers=buffers,
+                                          recompute_dq=args.recompute_dq)
         if events:
             events[len(phases)].record(stream)
 
@@ -441,10 +444,12 @@ def main() -> int:
     # the SIMT kernels compute in fp32 on the vector ALUs, whatever the I/O dtype
     peak = BF16_PEAK_TFLOPS if plan.path == "mfma" else FP32_PEAK_TFLOPS
     prefix = {"32x32x16": "tpr::mfma_", "16x16x32": "tpr::m16_", None: "tpr::simt_"}[plan.mfma_shape]
+    # executed MFMA work per kernel: the forward 2 GEMMs, dK/dV 4; dQ 1 from
+    # the dS store, 3 when it recomputes S and dP
     kernels = {
         "fwd": (fwd_ms, 2.0 * unit, prefix + "fwd"),
         "dkdv": (dkdv_ms, 4.0 * unit, prefix + "dkdv"),
-        "dq": (dq_ms, 3.0 * unit, prefix + "dq"),
+        "dq": (dq_ms, (1.0 if plan.dq_from_ds else 3.0) * unit, prefix + ("dqs" if plan.dq_from_ds else "dq")),
     }
     dom = max(kernels, key=lambda n: kernels[n][0])
     dom_ms, dom_flops, dom_name = kernels[dom]
@@ -475,6 +480,8 @@ def main() -> int:
             "head_dim": d,
             "visible_pairs_per_head": pairs,
             "fwd_bwd_flop": total_flops,
+            "dq": "from the dS store" if plan.dq_from_ds else "recomputed",
+            "workspace_bytes": plan.workspace_bytes,
         },
         "fraction_of_peak": round(value / peak, 4),
         "fwd_tflops": round(2.0 * unit / (fwd_ms * 1e-3) / 1e12, 2),

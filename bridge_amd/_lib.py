@@ -12,7 +12,7 @@ import threading
 
 LIB_NAME = "libtpr_attn.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 TPR_OK = 0
 TPR_ERR_INVALID_ARGUMENT = 1
@@ -22,6 +22,8 @@ TPR_ERR_LAUNCH = 4
 
 TPR_DTYPE_BF16 = 0
 TPR_DTYPE_FP32 = 1
+
+TPR_PLAN_RECOMPUTE_DQ = 1
 
 EXPORTED_SYMBOLS = (
     "tpr_attn_abi_version",
@@ -55,7 +57,7 @@ class TprTreeDesc(ctypes.Structure):
         ("num_kv_heads", ctypes.c_int32),
         ("head_dim", ctypes.c_int32),
         ("dtype", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("flags", ctypes.c_int32),
         ("cu_seqlens_q", _p),
         ("node_offsets", _p),
         ("leaf_ancestors", _p),

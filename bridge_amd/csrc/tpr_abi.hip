@@ -159,11 +159,25 @@ size_t stat_floats(const int32_t* ph) {
 }  // namespace
 }  // namespace tpr
 
+namespace tpr {
+namespace {
+// bytes before the dS store: the stat area and the fp32 partial slots
+// (a multiple of 256: the stat rows are padded to 64 floats, a slot is
+// keys x D x 2 floats)
+size_t ws_fp32_bytes(const int32_t* ph) {
+  const size_t slots = static_cast<size_t>(ph[PF_N_SLOTS]);
+  const size_t keys = ph[PF_PATH] == PATH_MFMA16 ? m16_keys(ph[PF_D]) : kDkdvKeys;  // per partial slot
+  return (stat_floats(ph) + slots * keys * static_cast<size_t>(ph[PF_D]) * 2) * sizeof(float);
+}
+size_t ds_bytes(const int32_t* ph) {
+  return static_cast<size_t>(ph[PF_DS_SLOTS]) * static_cast<size_t>(ph[PF_HQ]) * kDsHeadBytes;
+}
+}  // namespace
+}  // namespace tpr
+
 extern "C" size_t tpr_attn_bwd_workspace_bytes(const int32_t* plan_host) {
   if (!plan_host || plan_host[PF_MAGIC] != kPlanMagic) return 0;
-  const size_t slots = static_cast<size_t>(plan_host[PF_N_SLOTS]);
-  const size_t keys = plan_host[PF_PATH] == PATH_MFMA16 ? m16_keys(plan_host[PF_D]) : kDkdvKeys;  // per partial slot
-  return (stat_floats(plan_host) + slots * keys * static_cast<size_t>(plan_host[PF_D]) * 2) * sizeof(float);
+  return ws_fp32_bytes(plan_host) + ds_bytes(plan_host);
 }
 
 extern "C" int tpr_attn_fwd(const TprFwdParams* p, void* stream) {
@@ -264,6 +278,10 @@ int bwd_phases(const TprBwdParams* p, int phases, void* stream, void* workspace,
   a.stat_ws = static_cast<float*>(workspace);
   a.ndelta_ws = a.stat_ws ? a.stat_ws + kStatRowsOffset + stat_row_floats(ph) : nullptr;
   a.ws = a.stat_ws + stat_floats(ph);
+  a.ds = ds_bytes(ph) ? static_cast<char*>(workspace) + ws_fp32_bytes(ph) : nullptr;
+  a.off_ds = ph[PF_OFF_DS];
+  a.off_ds_tiles = ph[PF_OFF_DS] + ph[PF_NUM_NODES] + ph[PF_NUM_LEAVES] + 1;
+  a.num_nodes = ph[PF_NUM_NODES];
   const bool fp32 = ph[PF_DTYPE] == TPR_DTYPE_FP32;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int n_dkdv = (phases & (TPR_BWD_DKDV | TPR_BWD_DKDV_TILES)) ? ph[PF_N_DKDV] : 0;
@@ -334,7 +352,8 @@ extern "C" int tpr_attn_bwd_noalloc(const TprBwdParams* p, void* stream) {
     if (need > kScratchBytes)
       return fail(TPR_ERR_UNSUPPORTED,
                   "backward workspace needs %zu bytes, more than the %zu bytes of the library's static scratch; "
-                  "use tpr_attn_bwd with a caller-allocated workspace", need, kScratchBytes);
+                  "build the plan with TPR_PLAN_RECOMPUTE_DQ (no dS store), or use tpr_attn_bwd with a "
+                  "caller-allocated workspace", need, kScratchBytes);
   }
   void* ws = nullptr;
   int rc = scratch_for_current_device(&ws);

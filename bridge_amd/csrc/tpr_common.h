@@ -9,7 +9,7 @@
 namespace tpr {
 
 constexpr int32_t kPlanMagic = 0x31525054;  // "TPR1"
-constexpr int32_t kPlanVersion = 2;
+constexpr int32_t kPlanVersion = 3;
 
 // Header word indices.
 enum PlanField : int {
@@ -45,7 +45,10 @@ enum PlanField : int {
                      // ancestor nodes root first, nodes adjacent in prefix_k/v merged, empty
                      // nodes dropped; {0, 0} pads a leaf with fewer runs
   PF_MAX_RUNS,       // most key runs of any leaf
-  PF_HEADER_WORDS = 32
+  PF_DS_SLOTS,       // dS slots of the head_dim-128 backward (0: dQ recomputes the scores)
+  PF_OFF_DS,         // dS tile table: [M + N + 1] first tile of each segment (nodes, then leaf
+                     // suffixes), then [tiles][2] = {first slot, first query block}
+  PF_HEADER_WORDS = 40
 };
 
 enum KernelPath : int32_t {
@@ -99,6 +102,13 @@ constexpr int kDkdvQ = 64;            // queries per staged query block
 constexpr int kDkdvMaxBlocks = 256;   // query blocks one dK/dV item may stream (LDS table size)
 constexpr int kDkdvPrefixChunk = 64;  // smallest chunk a prefix tile is split into
 constexpr int kPlanCus = 256;         // compute units the dK/dV work is balanced over (MI355X)
+// dS store (head_dim 128): the dK/dV kernel writes each dS block it computes,
+// bf16, and dQ = scale dS K reads them instead of recomputing S and dP. One
+// slot per (128-key tile, query block it is visible to) holds, per query
+// head, the 128 x 64 block as four 4 KiB wave blocks (32 keys each) in the
+// dK/dV kernel's register order.
+constexpr int kDsHeadBytes = kDkdvKeys * kDkdvQ * 2;          // 16 KiB per query head per slot
+constexpr int64_t kDsMaxBytes = int64_t{32} << 30;           // larger dS areas fall back to recomputation
 // MFMA backward workspace, ahead of the partial slots: two constants (+inf,
 // 0) that rows past a query block's end are copied from, then lse * log2e per
 // (query head, token) in the lse layout, then -delta in the same layout.

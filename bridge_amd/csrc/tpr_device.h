@@ -55,6 +55,11 @@ struct KernelArgs {
   // unless the caller reads them out of a wider buffer); every other tensor
   // is packed
   int64_t q_rs, k_rs, v_rs;
+  // dS store of the head_dim-128 backward (null: dQ recomputes the scores):
+  // slot s, query head h at byte (s * hq + h) * kDsHeadBytes; the plan's tile
+  // table at off_ds, segment ids nodes first, then num_nodes + leaf
+  void* ds;
+  int32_t off_ds, off_ds_tiles, num_nodes;
 };
 
 __device__ __forceinline__ float to_f32(float x) { return x; }

@@ -169,6 +169,24 @@ __device__ __forceinline__ void dma_blocks4(const char* sbase, uint32_t v0, uint
       : "v"(v0), "v"(v1 - 1024u), "v"(v2 - 2048u), "v"(v3 - 3072u), "s"(lds_dst), "s"(sbase));
 }
 
+// dma_blocks4 with the streaming (nt) hint, for data read once: it keeps
+// the last-level cache for the data that is read again.
+__device__ __forceinline__ void dma_blocks4_nt(const char* sbase, uint32_t v0, uint32_t v1, uint32_t v2, uint32_t v3,
+                                               uint32_t lds_dst) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %5\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %6 nt\n\t"
+      "global_load_lds_dwordx4 %2, %6 offset:1024 nt\n\t"
+      "global_load_lds_dwordx4 %3, %6 offset:2048 nt\n\t"
+      "global_load_lds_dwordx4 %4, %6 offset:3072 nt\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(v0), "v"(v1 - 1024u), "v"(v2 - 2048u), "v"(v3 - 3072u), "s"(lds_dst), "s"(sbase));
+}
+
 __device__ __forceinline__ void dma_blocks4_m0(const char* sbase, uint32_t v0, uint32_t v1, uint32_t v2, uint32_t v3,
                                                uint32_t lds_dst) {
   uint32_t saved;
@@ -266,6 +284,21 @@ __device__ __forceinline__ void cursor_next(const Keys& t, Cursor& c) {
 __device__ __forceinline__ TileLoc cursor_tile(const Cursor& c) {
   return TileLoc{static_cast<int64_t>(c.row) + c.lt * kTileRows, min(kTileRows, c.len - c.lt * kTileRows),
                  c.lt * kTileRows, c.d == 0};
+}
+
+// A plan word read through the scalar cache (s_load_dword) at a uniform
+// address, waited for here. The compiler reads plan words it cannot prove
+// unclobbered with vector loads, and its vmcnt(0) wait for one of those also
+// drains every global->LDS copy in flight; a scalar load is counted by
+// lgkmcnt instead.
+__device__ __forceinline__ int plan_word(const int32_t* p) {
+  const uint64_t b = reinterpret_cast<uint64_t>(p);
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(b >> 32)));
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(b & 0xffffffffu)));
+  const uint64_t bs = (static_cast<uint64_t>(hi) << 32) | static_cast<uint64_t>(lo);
+  int v;
+  asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(bs));
+  return v;
 }
 
 // Wait until this wave's outstanding global->LDS copies have landed.

@@ -868,6 +868,213 @@ __global__ __launch_bounds__(512) void mfma_dq(KernelArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// dQ from the dS store: dQ^T = K^T dS^T, times scale -- the forward's P V
+// product with V -> K and P -> dS, the dS blocks read from what the dK/dV
+// kernel stored instead of recomputed from Q, K, dO and V. Work items are the
+// forward's. The key stream follows the dK/dV kernel's tiling: the leaf's
+// ancestor nodes root first, then its suffix, each in 128-key tiles of two
+// 64-key halves, so every half lies in one dS slot. Per half: every wave
+// copies two 1 KiB blocks of the K rows (swizzled like the forward's V tile,
+// read column-wise as the A operand) and its own 64 x 32 dS block (4 KiB),
+// then runs 16 MFMAs.
+// A slot holds a head's 128 x 64 block as four 4 KiB wave blocks of 32 keys,
+// each [32-query half j][16-query quarter qc][lane L] x 8 queries, lane L
+// holding key L % 32 and queries 32 j + 16 qc + 8 (L / 32) .. +7 (the dK/dV
+// kernel's register order). The copy puts chunk L of each 1 KiB block at
+// L ^ (8 (L / 32) + 4 qc), which spreads every 32-lane pass of the
+// transposed operand reads over all 64 banks. The kernel streams 2 bytes of
+// dS per MFMA multiply-add pair from HBM, so it is bound by memory latency
+// and bandwidth: three buffers keep two halves in flight behind the one
+// being computed.
+// ---------------------------------------------------------------------------
+template <bool kStrided>
+__global__ __launch_bounds__(512) void mfma_dqs(KernelArgs a) {
+  const int32_t* item = a.plan + a.off_fwd + 4 * blockIdx.x;
+  const int leaf = item[0];
+  if (leaf < 0) return;
+  const int tok0 = item[1], qh0 = item[2], kvh = item[3];
+  const int32_t* cu = a.plan + a.off_cu;
+  const int32_t* no = a.plan + a.off_node_off;
+  const int row0 = cu[leaf], len = cu[leaf + 1] - cu[leaf];
+
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hpw = a.hpw;
+  const int head = qh0 + wave % hpw;
+  const int tw0 = tok0 + kFwdTokens * (wave / hpw);  // first token of this wave
+  const int tpw = kFwdTokens * (kFwdWaves / hpw);
+  const int suffix_keys = min(len, tok0 + tpw);
+  const bool wave_ok = tw0 < len;
+  const int qb = a.plan[a.off_leaf_qblk + leaf] + tw0 / kDkdvQ;  // the wave's query block
+  const int jq = (tw0 / kFwdTokens) & 1;                          // and its 32-query half of it
+  const int h = lane >> 5;
+
+  const int64_t qstride = static_cast<int64_t>(a.hq) * kMfmaD;
+  const uint32_t p_rb = static_cast<uint32_t>(a.hkv) * kMfmaD * 2;
+  const uint32_t k_rb = kStrided ? static_cast<uint32_t>(a.k_rs) * 2 : p_rb;
+
+  constexpr int kBufs = 3;
+  constexpr int kDsWave = 4096;                   // one wave's dS block per half
+  constexpr int kDsOff = kBufs * kTileBytes;      // K [buffer] | dS [buffer][wave]
+  __shared__ __attribute__((aligned(1024))) char smem[kBufs * (kTileBytes + kFwdWaves * kDsWave)];
+  static_assert(sizeof(smem) >= kFwdWaves * 8192, "the output rows are staged in the tile buffers");
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(smem));
+
+  const char* kbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.k) + kvh * kMfmaD);
+  const char* pkbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.pk) + kvh * kMfmaD);
+  // K copy: wave w moves blocks 2w, 2w + 1 of the tile (rows 8w + 4j + l / 16)
+  const uint32_t krow0 = static_cast<uint32_t>(8 * wave + (lane >> 4));
+  const uint32_t kcb0 = static_cast<uint32_t>(16 * ((lane & 15) ^ ((lane >> 4) << 2)));
+  const FwdLdsOffsets lo = make_fwd_lds_offsets(lane);
+  // dS copy, block (kb, qc) = 2 kb + qc: lane l fetches the chunk that lands
+  // at l (the swizzle is its own inverse)
+  uint32_t dsv[4];
+#pragma unroll
+  for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+    for (int qc = 0; qc < 2; qc++)
+      dsv[2 * kb + qc] = kb * 4096 + qc * 1024 + 16 * (lane ^ (8 * (lane >> 5) + 4 * qc));
+  // dS^T operand reads (B: lane l gets query l % 32, keys 8 (l / 32) + 0..7
+  // of a 16-key step). As a source row of ds_read_tr16_b64, lane l (group
+  // g = l / 16, e = (l % 16) / 4, m = l % 4) addresses key 8 (g / 2) + 4 t + e,
+  // queries 16 (g % 2) + 4 m .. +3; t = 0 / 1 gives keys +0..3 / +4..7.
+  uint32_t dso[2];
+  {
+    const int g = lane >> 4, e = (lane & 15) >> 2, m = lane & 3, qc = g & 1;
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+      const int L = 8 * (g >> 1) + 4 * t + e + 32 * (m >> 1);
+      dso[t] = qc * 1024 + 16 * (L ^ (8 * (L >> 5) + 4 * qc)) + 8 * (m & 1);
+    }
+  }
+
+  // Key stream cursor (uniform): ancestor index cd (max_depth = the suffix,
+  // past it = the end), first row, length, key limit, first dS tile of the
+  // segment, tile key, half. Plan words inside the stream are scalar loads.
+  const int depth = a.max_depth;
+  const int32_t* anc = a.plan + a.off_anc + static_cast<int64_t>(leaf) * depth;
+  int cd = -1, crow = 0, clen = 0, clim = 0, ctile = 0, ckey = 0, chalf = 0;
+  auto next_segment = [&]() {
+    for (;;) {
+      cd++;
+      if (cd < depth) {
+        const int nd = plan_word(anc + cd);
+        if (nd >= 0) {
+          crow = plan_word(no + nd);
+          const int l = plan_word(no + nd + 1) - crow;
+          if (l == 0) continue;
+          clen = clim = l;
+          ctile = plan_word(a.plan + a.off_ds + nd);
+          break;
+        }
+        cd = depth;  // -1 pads the list: the suffix is next
+      }
+      if (cd == depth) {
+        crow = row0;
+        clen = len;
+        clim = suffix_keys;
+        ctile = plan_word(a.plan + a.off_ds + a.num_nodes + leaf);
+      } else {
+        clen = clim = 0;  // past the end
+      }
+      break;
+    }
+    ckey = 0;
+    chalf = 0;
+  };
+  auto advance = [&]() {
+    chalf++;
+    if (chalf == 2 || ckey + kTileRows * chalf >= clim) {
+      chalf = 0;
+      ckey += kDkdvKeys;
+      if (ckey >= clim) next_segment();
+    }
+  };
+  // copy the current half into buffer b; returns its rows, and whether this
+  // wave reads it (prefix halves: every wave; suffix halves: those not
+  // entirely in the wave's future). A wave issues 2 copies for K and 4 for
+  // its dS block (if it reads the half).
+  auto issue = [&](int b, int& rows, bool& vis) __attribute__((always_inline)) {
+    const int k0 = ckey + kTileRows * chalf;
+    const bool suffix = cd == depth;
+    rows = min(kTileRows, clen - k0);
+    vis = wave_ok && (!suffix || k0 <= tw0 + kFwdTokens - 1);
+    {
+      const uint32_t rb = suffix ? k_rb : p_rb;
+      const char* src = (suffix ? kbase : pkbase) + static_cast<int64_t>(crow + k0) * rb;
+      const uint32_t last = static_cast<uint32_t>(rows - 1);
+#pragma unroll
+      for (int j = 0; j < 2; j++)  // block 2w + j: rows 8w + 4j + l / 16; the swizzle's row term is (2w + j) % 4
+        dma16s(src, min(krow0 + 4u * j, last) * rb + (kcb0 ^ (16u * ((2 * wave + j) & 3))),
+               lds0 + b * kTileBytes + (2 * wave + j) * 1024);
+    }
+    if (vis) {
+      const int32_t* te = a.plan + a.off_ds_tiles + 2 * (ctile + ckey / kDkdvKeys);
+      const int slot = plan_word(te) + qb - plan_word(te + 1);
+      const char* src = static_cast<const char*>(a.ds) +
+                        (static_cast<int64_t>(slot) * a.hq + head) * kDsHeadBytes + 2 * chalf * 4096 + jq * 2048;
+      dma_blocks4_nt(src, dsv[0], dsv[1], dsv[2], dsv[3], lds0 + kDsOff + (b * kFwdWaves + wave) * kDsWave);
+    }
+  };
+
+  f32x16 dq[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) dq[i] = f32x16{};
+  // 16 MFMAs on buffer b: key step (kb, kc) covers keys 32 kb + 16 kc ..
+  // +15; keys at or past `rows` (the segment's end) read as zero dS
+  auto compute = [&](int b, int rows) __attribute__((always_inline)) {
+    const char* kt = smem + b * kTileBytes;
+    const char* dt = smem + kDsOff + (b * kFwdWaves + wave) * kDsWave;
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+      for (int kc = 0; kc < 2; kc++) {
+        bf16x8 f = lds_col8_at(dt + kb * 2048 + kc * 256, dso[0], dso[1]);
+        if (rows < kTileRows) {
+#pragma unroll
+          for (int i = 0; i < 8; i++)
+            if (32 * kb + 16 * kc + 8 * h + i >= rows) f[i] = static_cast<bf16>(0.f);
+        }
+        const char* kr = kt + (32 * kb + 16 * kc) * 256;
+#pragma unroll
+        for (int db = 0; db < 4; db++) dq[db] = mfma(lds_col8_at(kr, lo.v[db][0], lo.v[db][1]), f, dq[db]);
+      }
+  };
+
+  // halves i (computed), i + 1 and i + 2 (in flight) sit in buffers i % 3,
+  // (i + 1) % 3, (i + 2) % 3; loads complete in issue order, so waiting
+  // until at most half i + 1's copies are outstanding means half i landed
+  next_segment();
+  int rows[kBufs];
+  bool vis[kBufs];
+  issue(0, rows[0], vis[0]);
+  advance();
+  bool more1 = clim > 0;  // half i + 1 exists
+  if (more1) issue(1, rows[1], vis[1]);
+  for (int b = 0;;) {
+    const int b1 = b == kBufs - 1 ? 0 : b + 1, b2 = b1 == kBufs - 1 ? 0 : b1 + 1;
+    if (!more1) wait_dma();
+    else if (vis[b1]) asm volatile("s_waitcnt vmcnt(6)");
+    else asm volatile("s_waitcnt vmcnt(2)");
+    __syncthreads();  // half i has landed; every wave is done with buffer b2 (half i - 1)
+    bool more2 = false;
+    if (more1) {
+      advance();
+      more2 = clim > 0;
+      if (more2) issue(b2, rows[b2], vis[b2]);
+    }
+    if (vis[b]) compute(b, rows[b]);
+    if (!more1) break;
+    more1 = more2;
+    b = b1;
+  }
+  __syncthreads();  // every LDS read is done: the buffers are free for the row staging
+  if (!wave_ok) return;
+  store_tile_rows(smem + wave * 8192, dq, a.scale,
+                  static_cast<bf16*>(a.dq) + static_cast<int64_t>(row0 + tw0) * qstride + head * kMfmaD, qstride,
+                  len - tw0, lane);
+}
+
+// ---------------------------------------------------------------------------
 // dK/dV
 //   S = Q K^T (query rows permuted by sigma32), P = exp(scale S - lse),
 //   dP = dO V^T, dS = P (dP - delta), dV += P^T dO, dK += dS^T Q, dK *= scale.
@@ -877,6 +1084,15 @@ __global__ __launch_bounds__(512) void mfma_dq(KernelArgs a) {
 // block of kHeads query heads of the GQA group (2 when the group size is even:
 // half the stages, and with them half the per-stage barriers and copy waits).
 // ---------------------------------------------------------------------------
+// MFMA slots (position k within a head's sub-block sequence) at which the
+// dK/dV stage stores the two 16-query halves of a dS block: the first half
+// is complete at k = 22, the second at k = 27
+#ifndef TPR_DS_STORE_K1
+#define TPR_DS_STORE_K1 23
+#endif
+#ifndef TPR_DS_STORE_K2
+#define TPR_DS_STORE_K2 28
+#endif
 #ifndef TPR_DKDV_INTERLEAVE
 #define TPR_DKDV_INTERLEAVE 1
 #endif
@@ -906,7 +1122,9 @@ constexpr bool kInterleave = TPR_DKDV_INTERLEAVE;
 constexpr int slot_sub(int m) { return kInterleave ? (m & 1) : (m >> 5); }
 constexpr int slot_pos(int m) { return kInterleave ? (m >> 1) : (m & 31); }
 
-template <int kHeads, bool kStrided>  // kStrided as in mfma_fwd
+// kStrided as in mfma_fwd; kStoreDs: also store every dS block to the dS
+// store (a.ds) for the dQ kernel
+template <int kHeads, bool kStrided, bool kStoreDs>
 __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
   const int32_t* item = a.plan + a.off_dkdv + DK_WORDS * blockIdx.x;
   if (item[DK_SRC] < 0) return;
@@ -928,7 +1146,7 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
   __shared__ __attribute__((aligned(1024))) char smem[2 * kHeads * 2 * kTileBytes];
   __shared__ __attribute__((aligned(256))) float stats[2][kHeads][2][kTileRows];  // [buf][head][-lse*log2e | -delta][row]
   // query-block table of the current tile: {first packed row, token start
-  // within the leaf, valid rows}
+  // within the leaf, valid rows, dS slot}
   __shared__ int4 qtab[kDkdvMaxBlocks];
 
   const int spb = a.group / kHeads;  // stages per query block
@@ -959,11 +1177,18 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
     // from the plan once, so the stage loop touches no plan memory
     if (tile > 0) __syncthreads();  // every wave is done with the previous tile's table
     const int nblk = qb_hi - qb_lo;
+    int ds_first = 0, ds_lo = 0;  // the tile's first dS slot and first query block
+    if constexpr (kStoreDs) {
+      const int32_t* seg_tiles = a.plan + a.off_ds;
+      const int32_t* te = a.plan + a.off_ds_tiles + 2 * (seg_tiles[prefix ? seg : a.num_nodes + seg] + key0 / kDkdvKeys);
+      ds_first = te[0];
+      ds_lo = te[1];
+    }
     for (int i = threadIdx.x; i < nblk; i += blockDim.x) {
       const int qb = first_last ? qb_lo + i : qb_hi - 1 - i;
       const int lf = qblk[2 * qb], tok = qblk[2 * qb + 1];
       const int r0 = cu[lf];
-      qtab[i] = int4{r0 + tok, tok, min(kTileRows, cu[lf + 1] - r0 - tok), 0};
+      qtab[i] = int4{r0 + tok, tok, min(kTileRows, cu[lf + 1] - r0 - tok), kStoreDs ? ds_first + qb - ds_lo : 0};
     }
     __syncthreads();
 
@@ -1031,6 +1256,7 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
     };
     StageCursor cur{0, 0};
     if (nstage > 0) issue(cur, 0);
+    char* ds_stage = nullptr;  // this stage's dS blocks (dS store only)
 
     bf16x8 kv[8], vv[8];
     {
@@ -1216,6 +1442,15 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
         }
         if constexpr (k == 4) read_stats(H{}, J{}, I1{});  // -delta: the dP chain starts from it at k = 8
         mfma_at(mc);
+        // dS of head hh, sub-block j (complete at k = 27): whole 1 KiB lines
+        if constexpr (kStoreDs && k == TPR_DS_STORE_K1) {
+          __builtin_nontemporal_store(d8[hh][j][0], reinterpret_cast<bf16x8*>(ds_stage + hh * kDsHeadBytes +
+                                                                              (2 * j) * 1024 + 16 * lane));
+        }
+        if constexpr (kStoreDs && k == TPR_DS_STORE_K2) {
+          __builtin_nontemporal_store(d8[hh][j][1], reinterpret_cast<bf16x8*>(ds_stage + hh * kDsHeadBytes +
+                                                                              (2 * j + 1) * 1024 + 16 * lane));
+        }
         static_for<16>([&](auto rc) __attribute__((always_inline)) {
           constexpr int r = decltype(rc)::value;
           if constexpr (k == 9 + (r * 10) / 16) p_elem(H{}, J{}, rc);   // P: slots 9..18 (pb[0] by 13, pb[1] by 18)
@@ -1232,6 +1467,12 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
     auto one_stage = [&](auto diag, auto bufc, int sidx) __attribute__((always_inline)) {
       constexpr int buf = decltype(bufc)::value;
       const int tok0 = __builtin_amdgcn_readfirstlane(qtab[cur.blk].y);
+      if constexpr (kStoreDs) {
+        // this stage's dS blocks: slot, heads kvh G + sub kHeads + hh, this wave's 32 keys
+        const int slot = __builtin_amdgcn_readfirstlane(qtab[cur.blk].w);
+        ds_stage = static_cast<char*>(a.ds) +
+                   (static_cast<int64_t>(slot) * a.hq + kvh * a.group + cur.sub * kHeads) * kDsHeadBytes + wave * 4096;
+      }
       const StageCursor nxt = advance(cur);
       if (sidx + 1 < nstage) issue(nxt, buf ^ 1);
       if (wave_active) {
@@ -1391,6 +1632,19 @@ void launch_fwd_tile(const KernelArgs& a, hipStream_t s) {
     hipLaunchKernelGGL((mfma_fwd<kRunList, false>), dim3(a.n_items), dim3(64 * kFwdWaves), 0, s, a);
 }
 
+template <int kHeads>
+void launch_dkdv_heads(const KernelArgs& a, int n_dkdv, hipStream_t s) {
+  const bool st = strided_rows(a), ds = a.ds != nullptr;
+  if (st && ds)
+    hipLaunchKernelGGL((mfma_dkdv<kHeads, true, true>), dim3(n_dkdv), dim3(256), 0, s, a);
+  else if (st)
+    hipLaunchKernelGGL((mfma_dkdv<kHeads, true, false>), dim3(n_dkdv), dim3(256), 0, s, a);
+  else if (ds)
+    hipLaunchKernelGGL((mfma_dkdv<kHeads, false, true>), dim3(n_dkdv), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((mfma_dkdv<kHeads, false, false>), dim3(n_dkdv), dim3(256), 0, s, a);
+}
+
 template <bool kRunList>
 void launch_dq_tile(const KernelArgs& a, int n_fwd, hipStream_t s) {
   if (strided_rows(a))
@@ -1420,15 +1674,10 @@ int launch_mfma_delta(const KernelArgs& a, hipStream_t s) {
 
 int launch_mfma_bwd(const KernelArgs& a, int n_fwd, int n_dkdv, int n_red, hipStream_t s) {
   if (n_dkdv > 0) {
-    const bool st = strided_rows(a);
-    if (a.group % 2 == 0 && st)
-      hipLaunchKernelGGL((mfma_dkdv<2, true>), dim3(n_dkdv), dim3(256), 0, s, a);
-    else if (a.group % 2 == 0)
-      hipLaunchKernelGGL((mfma_dkdv<2, false>), dim3(n_dkdv), dim3(256), 0, s, a);
-    else if (st)
-      hipLaunchKernelGGL((mfma_dkdv<1, true>), dim3(n_dkdv), dim3(256), 0, s, a);
+    if (a.group % 2 == 0)
+      launch_dkdv_heads<2>(a, n_dkdv, s);
     else
-      hipLaunchKernelGGL((mfma_dkdv<1, false>), dim3(n_dkdv), dim3(256), 0, s, a);
+      launch_dkdv_heads<1>(a, n_dkdv, s);
     if (hipGetLastError() != hipSuccess) return 4;
   }
   if (n_red > 0) {
@@ -1436,7 +1685,11 @@ int launch_mfma_bwd(const KernelArgs& a, int n_fwd, int n_dkdv, int n_red, hipSt
     if (hipGetLastError() != hipSuccess) return 4;
   }
   if (n_fwd > 0) {
-    if (a.max_runs > kMfmaRegRuns)
+    if (a.ds && strided_rows(a))
+      hipLaunchKernelGGL((mfma_dqs<true>), dim3(n_fwd), dim3(64 * kFwdWaves), 0, s, a);
+    else if (a.ds)
+      hipLaunchKernelGGL((mfma_dqs<false>), dim3(n_fwd), dim3(64 * kFwdWaves), 0, s, a);
+    else if (a.max_runs > kMfmaRegRuns)
       launch_dq_tile<true>(a, n_fwd, s);
     else
       launch_dq_tile<false>(a, n_fwd, s);

@@ -97,6 +97,8 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
     return fail(TPR_ERR_UNSUPPORTED, "head_dim must be a multiple of 8 and at most 256, got %d", D);
   if (t->dtype != TPR_DTYPE_BF16 && t->dtype != TPR_DTYPE_FP32)
     return fail(TPR_ERR_INVALID_ARGUMENT, "unknown dtype %d", t->dtype);
+  if (t->flags & ~TPR_PLAN_RECOMPUTE_DQ)
+    return fail(TPR_ERR_INVALID_ARGUMENT, "unknown plan flags 0x%x", static_cast<unsigned>(t->flags));
   if (!t->cu_seqlens_q || !t->node_offsets || (N * depth > 0 && !t->leaf_ancestors))
     return fail(TPR_ERR_INVALID_ARGUMENT, "tree metadata pointers must not be NULL");
 
@@ -331,6 +333,41 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
   int32_t n_dkdv = 0;
   std::vector<int32_t> dkdv_words = order_for_xcds(dkdv, Hkv, DK_WORDS, &n_dkdv);
 
+  // ---- dS store (head_dim 128) ------------------------------------------------
+  // Every (128-key tile, query block) pair the dK/dV items stream gets one
+  // slot; a tile's query blocks are one contiguous range (a node's descendant
+  // leaves, or a leaf's blocks from the tile's first key on), so its slots
+  // are {first slot + (block - first block)}. Tiles are numbered per segment
+  // in key order, nodes first, then the leaf suffixes; the table gives each
+  // segment's first tile and each tile's {first slot, first block}.
+  std::vector<int32_t> ds_table;
+  int64_t ds_slots = 0;
+  if (path == PATH_MFMA && !(t->flags & TPR_PLAN_RECOMPUTE_DQ)) {
+    std::vector<int32_t> first(static_cast<size_t>(M) + N + 1), tiles;
+    int32_t ntile = 0;
+    auto add = [&](int32_t lo, int32_t hi) {
+      tiles.push_back(static_cast<int32_t>(std::min<int64_t>(ds_slots, INT32_MAX)));
+      tiles.push_back(lo);
+      ds_slots += hi - lo;
+      ntile++;
+    };
+    for (int n = 0; n < M; n++) {
+      first[n] = ntile;
+      for (int k0 = 0; k0 < no[n + 1] - no[n]; k0 += KT) add(leaf_qblk[leaf_lo[n]], leaf_qblk[leaf_hi[n]]);
+    }
+    for (int s = 0; s < N; s++) {
+      first[M + s] = ntile;
+      for (int k0 = 0; k0 < cu[s + 1] - cu[s]; k0 += KT) add(leaf_qblk[s] + k0 / BQ, leaf_qblk[s + 1]);
+    }
+    first[M + N] = ntile;
+    if (ds_slots > 0 && ds_slots < INT32_MAX && ds_slots * Hq * kDsHeadBytes <= kDsMaxBytes) {
+      ds_table = std::move(first);
+      ds_table.insert(ds_table.end(), tiles.begin(), tiles.end());
+    } else {
+      ds_slots = 0;
+    }
+  }
+
   // ---- assemble ----------------------------------------------------------------
   plan.assign(PF_HEADER_WORDS, 0);
   auto append = [&](const int32_t* src, size_t count) {
@@ -369,6 +406,8 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
   plan[PF_MAX_SPLIT] = max_split;
   plan[PF_OFF_RUNS] = append(runs_flat.data(), runs_flat.size());
   plan[PF_MAX_RUNS] = std::max(max_runs, 1);
+  plan[PF_DS_SLOTS] = static_cast<int32_t>(ds_slots);
+  plan[PF_OFF_DS] = ds_table.empty() ? 0 : append(ds_table.data(), ds_table.size());
   plan[PF_TOTAL_WORDS] = static_cast<int32_t>(plan.size());
   return TPR_OK;
 }

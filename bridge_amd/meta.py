@@ -33,6 +33,7 @@ _PF_PATH = 11
 _PF_N_FWD = 19
 _PF_N_DKDV = 21
 _PF_TOTAL_WORDS = 27
+_PF_DS_SLOTS = 30
 
 
 @dataclass(frozen=True)
@@ -55,6 +56,13 @@ class LaunchPlan:
         head_dim 128), "16x16x32" (bf16, head_dim 64 and 256), None off the
         MFMA path."""
         return {1: "32x32x16", 2: "16x16x32"}.get(int(self.host[_PF_PATH]))
+
+    @property
+    def dq_from_ds(self) -> bool:
+        """Whether the backward stores dS and computes dQ from it (bf16
+        head_dim 128 unless the plan was built with recompute_dq=True or the
+        store would exceed 32 GiB); the workspace then holds the store."""
+        return int(self.host[_PF_DS_SLOTS]) > 0
 
     @property
     def num_forward_items(self) -> int:
@@ -190,15 +198,22 @@ class TPRPrefixMeta:
 
     # ---- launch plan -------------------------------------------------------
     def plan(self, num_q_heads: int, num_kv_heads: int, head_dim: int, dtype: torch.dtype,
-             device: torch.device) -> LaunchPlan:
-        """Build (once per configuration) the native launch plan and upload it."""
+             device: torch.device, *, recompute_dq: bool = False) -> LaunchPlan:
+        """Build (once per configuration) the native launch plan and upload it.
+
+        ``recompute_dq``: the dQ kernel recomputes the scores instead of
+        reading a dS store (TPR_PLAN_RECOMPUTE_DQ): a backward workspace of a
+        few MB instead of 2 bytes per visible (query, key) pair and query head,
+        at the cost of a slower dQ (bf16 head_dim 128 only; the other paths
+        always recompute)."""
         if dtype == torch.bfloat16:
             code = _lib.TPR_DTYPE_BF16
         elif dtype == torch.float32:
             code = _lib.TPR_DTYPE_FP32
         else:
             raise ValueError(f"prefix attention supports torch.bfloat16 and torch.float32, got {dtype}")
-        key = (num_q_heads, num_kv_heads, head_dim, code, str(device))
+        flags = _lib.TPR_PLAN_RECOMPUTE_DQ if recompute_dq else 0
+        key = (num_q_heads, num_kv_heads, head_dim, code, str(device), flags)
         cached = self._plans.get(key)
         if cached is not None:
             return cached
@@ -209,7 +224,7 @@ class TPRPrefixMeta:
         no = (ctypes.c_int32 * len(self.node_offsets))(*self.node_offsets)
         an = (ctypes.c_int32 * max(1, len(anc)))(*anc) if anc else (ctypes.c_int32 * 1)(-1)
         desc = _lib.TprTreeDesc(self.num_leaves, self.num_nodes, depth, num_q_heads, num_kv_heads, head_dim,
-                                code, 0, ctypes.cast(cu, ctypes.c_void_p), ctypes.cast(no, ctypes.c_void_p),
+                                code, flags, ctypes.cast(cu, ctypes.c_void_p), ctypes.cast(no, ctypes.c_void_p),
                                 ctypes.cast(an, ctypes.c_void_p))
         words = ctypes.c_int64(0)
         _lib.check(lib.tpr_attn_plan(ctypes.byref(desc), None, 0, ctypes.byref(words)), "tpr_attn_plan")

@@ -166,14 +166,15 @@ def _check_accumulators(accumulators, prefix_k) -> Tuple[torch.Tensor, torch.Ten
 
 
 def _backward(q, k, v, prefix_k, prefix_v, out, lse, dout, meta, scale, *, phases=None, buffers=None,
-              prefix_grad_accumulators=None):
+              prefix_grad_accumulators=None, recompute_dq=False):
     """Enqueue the backward. ``buffers`` may supply preallocated dq, dk, dv,
     dprefix_k, dprefix_v and delta tensors; ``phases`` is a mask of
     _lib.TPR_BWD_* bits (default: all). With ``prefix_grad_accumulators`` (a
     pair of fp32 tensors shaped like prefix_k) the prefix gradients are added
     into that pair by the kernels (TPR_BWD_ACCUMULATE_PREFIX_F32), which is
-    also what is returned for them."""
-    plan = meta.plan(q.shape[1], k.shape[1], q.shape[2], q.dtype, q.device)
+    also what is returned for them. ``recompute_dq`` selects the plan without
+    a dS store (TPRPrefixMeta.plan)."""
+    plan = meta.plan(q.shape[1], k.shape[1], q.shape[2], q.dtype, q.device, recompute_dq=recompute_dq)
     b = dict(buffers or {})
     dq = b.get("dq") if b.get("dq") is not None else _empty(q)
     dk = b.get("dk") if b.get("dk") is not None else _empty(k)
@@ -216,10 +217,13 @@ class TPRPrefixAttention(torch.autograd.Function):
     prefix_k, the backward adds the prefix gradients into them (the relay of
     prefix_state.py:546-573, in fp32 and inside the kernel) and gives
     prefix_k / prefix_v no autograd gradient; they must then not require one.
+    ``recompute_dq``: the backward uses the plan without a dS store (a small
+    workspace, a slower dQ; see TPRPrefixMeta.plan).
     """
 
     @staticmethod
-    def forward(ctx, q, k, v, prefix_k, prefix_v, meta, softmax_scale=None, prefix_grad_accumulators=None):
+    def forward(ctx, q, k, v, prefix_k, prefix_v, meta, softmax_scale=None, prefix_grad_accumulators=None,
+                recompute_dq=False):
         scale = validate(q, k, v, prefix_k, prefix_v, meta, softmax_scale)
         if prefix_grad_accumulators is not None:
             if prefix_k.requires_grad or prefix_v.requires_grad:
@@ -231,6 +235,7 @@ class TPRPrefixAttention(torch.autograd.Function):
         ctx.meta = meta
         ctx.scale = scale
         ctx.accumulators = prefix_grad_accumulators
+        ctx.recompute_dq = bool(recompute_dq)
         ctx.mark_non_differentiable(lse)
         return out, lse
 
@@ -241,16 +246,17 @@ class TPRPrefixAttention(torch.autograd.Function):
             dout = torch.zeros_like(out)
         dout = dout.contiguous()
         dq, dk, dv, dpk, dpv = _backward(q, k, v, prefix_k, prefix_v, out, lse, dout, ctx.meta, ctx.scale,
-                                         prefix_grad_accumulators=ctx.accumulators)
+                                         prefix_grad_accumulators=ctx.accumulators, recompute_dq=ctx.recompute_dq)
         if ctx.accumulators is not None:
             dpk = dpv = None
-        return dq, dk, dv, dpk, dpv, None, None, None
+        return dq, dk, dv, dpk, dpv, None, None, None, None
 
 
 def tpr_prefix_attention(q, k, v, prefix_k, prefix_v, meta: TPRPrefixMeta, softmax_scale=None, *,
-                         prefix_grad_accumulators=None):
+                         prefix_grad_accumulators=None, recompute_dq=False):
     """Functional form of TPRPrefixAttention; returns (out, lse)."""
-    return TPRPrefixAttention.apply(q, k, v, prefix_k, prefix_v, meta, softmax_scale, prefix_grad_accumulators)
+    return TPRPrefixAttention.apply(q, k, v, prefix_k, prefix_v, meta, softmax_scale, prefix_grad_accumulators,
+                                    recompute_dq)
 
 
 def prefix_attention_forward(q, k, v, prefix_k, prefix_v, meta: TPRPrefixMeta, softmax_scale=None):
@@ -261,7 +267,8 @@ def prefix_attention_forward(q, k, v, prefix_k, prefix_v, meta: TPRPrefixMeta, s
 
 
 def prefix_attention_backward(q, k, v, prefix_k, prefix_v, out, lse, dout, meta: TPRPrefixMeta,
-                              softmax_scale=None, *, phases=None, buffers=None, prefix_grad_accumulators=None):
+                              softmax_scale=None, *, phases=None, buffers=None, prefix_grad_accumulators=None,
+                              recompute_dq=False):
     """Backward only: (dq, dk, dv, dprefix_k, dprefix_v) from saved out/lse.
 
     ``phases`` selects backward phases (mask of TPR_BWD_DELTA / _DKDV / _DQ,
@@ -270,8 +277,10 @@ def prefix_attention_backward(q, k, v, prefix_k, prefix_v, out, lse, dout, meta:
     ``workspace``); ``buffers`` may hold preallocated outputs, the fp32
     ``delta`` scratch and the ``workspace``, keyed by name.
     ``prefix_grad_accumulators``: a (dK, dV) pair of fp32 tensors shaped like
-    prefix_k into which the prefix gradients are added (and returned)."""
+    prefix_k into which the prefix gradients are added (and returned).
+    ``recompute_dq``: use the plan without a dS store (TPRPrefixMeta.plan);
+    with a dS store the dQ phase reads what the dK/dV phase wrote."""
     scale = validate(q, k, v, prefix_k, prefix_v, meta, softmax_scale)
     tensors = [*_inputs(q, k, v, prefix_k, prefix_v), *(t.contiguous() for t in (out, lse, dout))]
     return _backward(*tensors[:7], tensors[7], meta, scale, phases=phases, buffers=buffers,
-                     prefix_grad_accumulators=prefix_grad_accumulators)
+                     prefix_grad_accumulators=prefix_grad_accumulators, recompute_dq=recompute_dq)

@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define TPR_ATTN_ABI_VERSION 3
+#define TPR_ATTN_ABI_VERSION 4
 
 typedef enum TprStatus {
   TPR_OK = 0,
@@ -74,7 +74,17 @@ typedef enum TprDtype {
  *       root first, padded with -1 at the end (kv_stack.py:139-154 order).
  * Every node must be the ancestor of a contiguous range of leaves (true when
  * leaves are numbered in DFS order, segment_plan.py:266-275), and a node that
- * appears in a path must appear at the same depth in every path. */
+ * appears in a path must appear at the same depth in every path.
+ *
+ * flags: 0, or TPR_PLAN_RECOMPUTE_DQ. By default a bf16 head_dim-128 plan
+ * has the dK/dV kernel store every dS block it computes (bf16, 2 bytes per
+ * visible (query, key) pair and query head) in the backward workspace, and
+ * the dQ kernel reads them: dQ = scale dS K then costs one matrix product
+ * instead of three (the scores S and dP recomputed). The workspace grows by
+ * that store; a plan whose store would exceed 32 GiB recomputes instead.
+ * TPR_PLAN_RECOMPUTE_DQ asks for the recomputing dQ and the small workspace
+ * (needed by tpr_attn_bwd_noalloc for such shapes). Other paths ignore it. */
+#define TPR_PLAN_RECOMPUTE_DQ 1
 typedef struct TprTreeDesc {
   int32_t num_leaves;
   int32_t num_nodes;
@@ -83,7 +93,7 @@ typedef struct TprTreeDesc {
   int32_t num_kv_heads;
   int32_t head_dim;
   int32_t dtype; /* TprDtype */
-  int32_t reserved;
+  int32_t flags; /* 0 or TPR_PLAN_RECOMPUTE_DQ */
   const int32_t* cu_seqlens_q;
   const int32_t* node_offsets;
   const int32_t* leaf_ancestors;
@@ -174,7 +184,8 @@ const char* tpr_attn_last_error(void);
 int tpr_attn_plan(const TprTreeDesc* tree, int32_t* plan, int64_t capacity_words,
                   int64_t* words_needed);
 
-/* Bytes of fp32 workspace the backward needs for this plan. */
+/* Bytes of workspace the backward needs for this plan (fp32 statistics and
+ * partial sums, and the dS store of a plan that has one). */
 size_t tpr_attn_bwd_workspace_bytes(const int32_t* plan_host);
 
 /* Enqueue the forward on `stream` (a hipStream_t; NULL = default stream). */
@@ -184,8 +195,10 @@ int tpr_attn_fwd(const TprFwdParams* params, void* stream);
 int tpr_attn_bwd(const TprBwdParams* params, void* stream);
 
 /* Backward phases, for callers that time them separately or run dK/dV and dQ
- * on two streams: TPR_BWD_DELTA must complete before the other two, which
- * are independent of each other. tpr_attn_bwd == all three in this order.
+ * on two streams: TPR_BWD_DELTA must complete before the other two. Those are
+ * independent of each other when the plan recomputes dQ; with a dS store
+ * (see TprTreeDesc.flags) TPR_BWD_DQ reads what TPR_BWD_DKDV (its tiles step)
+ * wrote, so it must run after it. tpr_attn_bwd == all three in this order.
  * TPR_BWD_DKDV is the two steps TPR_BWD_DKDV_TILES then TPR_BWD_DKDV_REDUCE,
  * which may also be enqueued separately (in that order, same workspace). */
 #define TPR_BWD_DELTA 1        /* delta = rowsum(dout * out), fp32 [Hq, Tq] */

@@ -55,7 +55,8 @@ def test_accumulate_mode_adds_the_prefix_gradient(case, cuda_device):
         # whose fp32 partials a reduction item sums (4 partial slots)
         meta, hq, hkv, d, dtype = TPRPrefixMeta.shared_prefix(256, [300] * 16), 4, 1, 128, torch.bfloat16
         stat_bytes = (64 + 2 * ((hq * meta.total_q + 63) // 64 * 64)) * 4   # constants + lse and -delta rows
-        assert meta.plan(hq, hkv, d, dtype, cuda_device).workspace_bytes == stat_bytes + 4 * 2 * 128 * 128 * 4
+        compact = meta.plan(hq, hkv, d, dtype, cuda_device, recompute_dq=True)  # no dS store
+        assert compact.workspace_bytes == stat_bytes + 4 * 2 * 128 * 128 * 4
     elif case == "simt_fp32":
         meta, hq, hkv, d, dtype = TPRPrefixMeta.shared_prefix(96, [40, 17, 33]), 4, 2, 64, torch.float32
     elif case == "mfma16_bf16_d64":  # bf16 with head_dim 64: the 16-wide MFMA kernels

@@ -15,7 +15,7 @@ CPU = torch.device("cpu")
 PF = dict(MAGIC=0, NUM_LEAVES=2, NUM_NODES=3, MAX_DEPTH=4, TOTAL_Q=5, TOTAL_PREFIX=6, HQ=7, HKV=8, D=9,
           PATH=11, OFF_CU=12, OFF_NODE_OFF=13, OFF_ANC=14, OFF_NODE_LEAF=15, N_QBLK=16, OFF_QBLK=17,
           OFF_LEAF_QBLK=18, N_FWD=19, OFF_FWD=20, N_DKDV=21, OFF_DKDV=22, N_RED=23, TOTAL_WORDS=27,
-          OFF_RUNS=28, MAX_RUNS=29)
+          OFF_RUNS=28, MAX_RUNS=29, DS_SLOTS=30, OFF_DS=31)
 
 FWD_WAVES = 8  # waves per forward / dQ workgroup (kFwdWaves)
 
@@ -143,10 +143,13 @@ def test_split_prefix_tiles_have_ordered_partials_and_reductions():
     n_slots = w[25]
     # workspace: stat area (2 constants padded to 64 floats, then lse*log2e and
     # -delta per (query head, token), each rounded up to 64 floats), then the
-    # fp32 partial slots
+    # fp32 partial slots, then the dS store (16 KiB per slot and query head)
     total_q = 4096 * 3 + 100
     stat_floats = 64 + 2 * ((8 * total_q + 63) // 64 * 64)
-    assert n_slots > 0 and plan.workspace_bytes == (stat_floats + n_slots * 2 * 128 * 128) * 4
+    fp32_bytes = (stat_floats + n_slots * 2 * 128 * 128) * 4
+    assert n_slots > 0 and plan.dq_from_ds and plan.workspace_bytes == fp32_bytes + w[PF["DS_SLOTS"]] * 8 * 16384
+    compact = meta.plan(8, 2, 128, torch.bfloat16, CPU, recompute_dq=True)
+    assert not compact.dq_from_ds and compact.workspace_bytes == fp32_bytes
     by_slot = {item[6]: item for item in dkdv if item[0] >= 0 and item[6] >= 0}
     assert sorted(by_slot) == list(range(n_slots))
     for src, seg, key0, kvh, slot0, nslots, _, _ in reds:
@@ -399,3 +402,103 @@ def test_empty_leaves_and_prefixless_trees_plan():
     _, fwd, dkdv, _ = decode(plan)
     assert {item[0] for item in fwd if item[0] >= 0} == {1}
     assert all(item[0] == 1 for item in dkdv if item[0] >= 0)
+
+
+def _ds_tables(w):
+    m, n = w[PF["NUM_NODES"]], w[PF["NUM_LEAVES"]]
+    off = w[PF["OFF_DS"]]
+    first = w[off:off + m + n + 1]
+    tiles = w[off + m + n + 1: off + m + n + 1 + 2 * first[-1]]
+    return first, [(tiles[2 * i], tiles[2 * i + 1]) for i in range(first[-1])]
+
+
+def _ds_reads_and_writes(meta, hq, hkv):
+    """Emulate the slot arithmetic of the head_dim-128 backward with a dS
+    store: the (slot, query head, 32-key wave block) triples every dK/dV stage
+    writes, and those every dQ wave reads (a block wholly past its segment's
+    end is masked, not read)."""
+    plan = meta.plan(hq, hkv, 128, torch.bfloat16, CPU)
+    assert plan.dq_from_ds
+    w, fwd, dkdv, qblk = decode(plan)
+    g = hq // hkv
+    n_slots = w[PF["DS_SLOTS"]]
+    first, tiles = _ds_tables(w)
+    m = meta.num_nodes
+    cu, no = meta.cu_seqlens_q, meta.node_offsets
+    leaf_qblk = w[w[PF["OFF_LEAF_QBLK"]]: w[PF["OFF_LEAF_QBLK"]] + meta.num_leaves + 1]
+
+    def seg_len(src, seg):
+        return no[seg + 1] - no[seg] if src == 0 else cu[seg + 1] - cu[seg]
+
+    writes = Counter()
+    for src, seg, key0, kvh, lo, hi, _ in tiles_of(dkdv):
+        t_first, t_lo = tiles[first[seg if src == 0 else m + seg] + key0 // 128]
+        for qb in range(lo, hi):
+            slot = t_first + qb - t_lo
+            assert 0 <= slot < n_slots
+            for wv in range(4):
+                if key0 + 32 * wv < seg_len(src, seg):  # active waves only
+                    for head in range(kvh * g, kvh * g + g):
+                        writes[(slot, head, wv)] += 1
+    reads = set()
+    hpw = math.gcd(g, FWD_WAVES)
+    tpw = 32 * (FWD_WAVES // hpw)
+    for leaf, tok0, qh0, kvh in fwd:
+        if leaf < 0:
+            continue
+        length = cu[leaf + 1] - cu[leaf]
+        segs = [(0, nd, no[nd + 1] - no[nd], no[nd + 1] - no[nd]) for nd in meta.leaf_ancestors[leaf]
+                if no[nd + 1] > no[nd]]
+        segs.append((1, leaf, length, min(length, tok0 + tpw)))
+        for wave in range(FWD_WAVES):
+            head, tw0 = qh0 + wave % hpw, tok0 + 32 * (wave // hpw)
+            if tw0 >= length:
+                continue
+            qb = leaf_qblk[leaf] + tw0 // 64
+            for src, seg, slen, lim in segs:
+                for key0 in range(0, lim, 128):
+                    for half in range(2):
+                        k0 = key0 + 64 * half
+                        if k0 >= lim or (src == 1 and k0 > tw0 + 31):
+                            continue
+                        t_first, t_lo = tiles[first[seg if src == 0 else m + seg] + key0 // 128]
+                        slot = t_first + qb - t_lo
+                        assert 0 <= slot < n_slots
+                        for kb in range(2):
+                            if k0 + 32 * kb < slen:
+                                reads.add((slot, head, 2 * half + kb))
+    return n_slots, writes, reads
+
+
+@pytest.mark.parametrize("case", ["split_prefix", "depth3_ragged", "empty_leaves", "gqa8", "gqa3", "mha"])
+def test_ds_store_is_written_once_before_every_dq_read(case):
+    trees = {
+        "split_prefix": (TPRPrefixMeta.shared_prefix(300, [4096, 4096, 100, 4096]), 8, 2),
+        "depth3_ragged": (TPRPrefixMeta(cu_seqlens_q=(0, 33, 98, 138, 155, 420), node_offsets=(0, 130, 200, 270),
+                                        leaf_ancestors=((0, 1), (0, 1), (0, 2), (0, 2), (0,))), 8, 2),
+        "empty_leaves": (TPRPrefixMeta.shared_prefix(50, [0, 260, 0, 64]), 4, 1),
+        "gqa8": (TPRPrefixMeta.shared_prefix(130, [70, 300]), 16, 2),
+        "gqa3": (TPRPrefixMeta.shared_prefix(200, [129, 20, 257]), 6, 2),
+        "mha": (TPRPrefixMeta.shared_prefix(0, [200, 65]), 4, 4),
+    }
+    meta, hq, hkv = trees[case]
+    n_slots, writes, reads = _ds_reads_and_writes(meta, hq, hkv)
+    assert set(writes.values()) == {1}  # no block is written twice
+    assert reads <= set(writes)         # every read block was written
+    # the store holds exactly the visible (tile, query block) pairs: each slot is read
+    assert {r[0] for r in reads} == set(range(n_slots))
+
+
+def test_ds_store_size_at_the_qwen3_layer_shape():
+    """Prefix 4096 + 4 x 4096, GQA 32/8: 32 prefix tiles x 256 query blocks
+    plus, per leaf, sum over its 32 suffix tiles of (64 - 2 j) blocks."""
+    meta = TPRPrefixMeta.shared_prefix(4096, [4096] * 4)
+    plan = meta.plan(32, 8, 128, torch.bfloat16, CPU)
+    w = plan.host.tolist()
+    slots = 32 * 256 + 4 * sum(64 - 2 * j for j in range(32))
+    assert w[PF["DS_SLOTS"]] == slots == 12416
+    fp32 = meta.plan(32, 8, 128, torch.bfloat16, CPU, recompute_dq=True).workspace_bytes
+    assert plan.workspace_bytes == fp32 + slots * 32 * 16384  # 6.5 GB
+    # other paths never store dS
+    assert not meta.plan(32, 8, 64, torch.bfloat16, CPU).dq_from_ds
+    assert not meta.plan(32, 8, 128, torch.float32, CPU).dq_from_ds

@@ -59,15 +59,18 @@ def test_noalloc_backward_equals_the_workspace_backward(cuda_device):
     lib = _lib.load()
     stream = ctypes.c_void_p(torch.cuda.current_stream(cuda_device).cuda_stream)
     # first: split prefix tiles (fp32 partial slots + ordered reduction in the
-    # workspace); second, smaller: stat rows only, in the same scratch
-    cases = [(TPRPrefixMeta.shared_prefix(300, [4100, 4100, 100, 4200]), 8, 2),
-             (TPRPrefixMeta.shared_prefix(200, [100, 37]), 8, 2)]
-    for i, (meta, hq, hkv) in enumerate(cases):
+    # workspace), dQ recomputed (its dS store would not fit the scratch);
+    # second, smaller: stat rows and a dS store, in the same scratch
+    cases = [(TPRPrefixMeta.shared_prefix(300, [4100, 4100, 100, 4200]), 8, 2, True),
+             (TPRPrefixMeta.shared_prefix(200, [100, 37]), 8, 2, False)]
+    for i, (meta, hq, hkv, recompute) in enumerate(cases):
         d = 128
         scale = 1.0 / math.sqrt(d)
-        plan = meta.plan(hq, hkv, d, torch.bfloat16, cuda_device)
+        plan = meta.plan(hq, hkv, d, torch.bfloat16, cuda_device, recompute_dq=recompute)
+        assert plan.dq_from_ds != recompute
         print(f"[noalloc call {i}] tq={meta.total_q} tp={meta.total_prefix} hq={hq} hkv={hkv} "
-              f"workspace_bytes={plan.workspace_bytes} slots={int(plan.host[25])}", flush=True)
+              f"workspace_bytes={plan.workspace_bytes} slots={int(plan.host[25])} dS store={plan.dq_from_ds}",
+              flush=True)
         assert plan.path == "mfma" and 0 < plan.workspace_bytes <= lib.tpr_attn_bwd_noalloc_max_workspace_bytes()
         if i == 0:
             assert int(plan.host[25]) > 0  # the first call uses partial slots
