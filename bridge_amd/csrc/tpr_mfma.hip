@@ -33,6 +33,9 @@ namespace tpr {
 namespace {
 
 constexpr int kTileBytes = kTileRows * 256;   // 64 rows x 128 bf16
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+constexpr int kBufferRsrcWord3 = 0x00020000;  // raw (untyped) buffer resource, gfx9 data format field
+constexpr int kCachePolicyNt = 2;             // buffer access cache policy: non-temporal (streaming)
 
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
@@ -1442,15 +1445,17 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
         }
         if constexpr (k == 4) read_stats(H{}, J{}, I1{});  // -delta: the dP chain starts from it at k = 8
         mfma_at(mc);
-        // dS of head hh, sub-block j (complete at k = 27): whole 1 KiB lines
-        if constexpr (kStoreDs && k == TPR_DS_STORE_K1) {
-          __builtin_nontemporal_store(d8[hh][j][0], reinterpret_cast<bf16x8*>(ds_stage + hh * kDsHeadBytes +
-                                                                              (2 * j) * 1024 + 16 * lane));
-        }
-        if constexpr (kStoreDs && k == TPR_DS_STORE_K2) {
-          __builtin_nontemporal_store(d8[hh][j][1], reinterpret_cast<bf16x8*>(ds_stage + hh * kDsHeadBytes +
-                                                                              (2 * j + 1) * 1024 + 16 * lane));
-        }
+        // dS of head hh, sub-block j, 16-query half cc: whole 1 KiB lines,
+        // streaming (nt) buffer stores from the stage's uniform base (a
+        // 32-bit lane offset, not a 64-bit address per lane)
+        auto store_ds = [&](int cc) __attribute__((always_inline)) {
+          __builtin_amdgcn_raw_buffer_store_b128(
+              __builtin_bit_cast(i32x4, d8[hh][j][cc]),
+              __builtin_amdgcn_make_buffer_rsrc(ds_stage, 0, kHeads * kDsHeadBytes, kBufferRsrcWord3),
+              hh * kDsHeadBytes + (2 * j + cc) * 1024 + 16 * lane, 0, kCachePolicyNt);
+        };
+        if constexpr (kStoreDs && k == TPR_DS_STORE_K1) store_ds(0);
+        if constexpr (kStoreDs && k == TPR_DS_STORE_K2) store_ds(1);
         static_for<16>([&](auto rc) __attribute__((always_inline)) {
           constexpr int r = decltype(rc)::value;
           if constexpr (k == 9 + (r * 10) / 16) p_elem(H{}, J{}, rc);   // P: slots 9..18 (pb[0] by 13, pb[1] by 18)
