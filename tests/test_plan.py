@@ -358,6 +358,24 @@ def test_planner_rejects_other_dtypes():
         TPRPrefixMeta.shared_prefix(8, [4]).plan(4, 2, 128, torch.float16, CPU)
 
 
+def test_planner_rejects_unknown_plan_flags():
+    import ctypes
+
+    from bridge_amd import _lib
+    lib = _lib.load()
+    cu = (ctypes.c_int32 * 2)(0, 4)
+    no = (ctypes.c_int32 * 2)(0, 8)
+    an = (ctypes.c_int32 * 1)(0)
+    for flags, ok in ((0, True), (_lib.TPR_PLAN_RECOMPUTE_DQ, True), (2, False), (-1, False)):
+        desc = _lib.TprTreeDesc(1, 1, 1, 4, 2, 128, _lib.TPR_DTYPE_BF16, flags, ctypes.cast(cu, ctypes.c_void_p),
+                                ctypes.cast(no, ctypes.c_void_p), ctypes.cast(an, ctypes.c_void_p))
+        words = ctypes.c_int64(0)
+        rc = lib.tpr_attn_plan(ctypes.byref(desc), None, 0, ctypes.byref(words))
+        assert (rc == _lib.TPR_OK) == ok, (flags, rc)
+        if not ok:
+            assert rc == _lib.TPR_ERR_INVALID_ARGUMENT and b"plan flags" in lib.tpr_attn_last_error()
+
+
 def test_segment_tree_lowering_turn_tree():
     # root 2048 -> 4 branches x 1024 -> 4 leaves x 1024 each (turn-boundary tree, depth 3)
     parents = {0: None}
