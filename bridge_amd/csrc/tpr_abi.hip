@@ -170,7 +170,7 @@ size_t ws_fp32_bytes(const int32_t* ph) {
   return (stat_floats(ph) + slots * keys * static_cast<size_t>(ph[PF_D]) * 2) * sizeof(float);
 }
 size_t ds_bytes(const int32_t* ph) {
-  return static_cast<size_t>(ph[PF_DS_SLOTS]) * static_cast<size_t>(ph[PF_HQ]) * kDsHeadBytes;
+  return static_cast<size_t>(ph[PF_DS_SLOTS]) * static_cast<size_t>(ph[PF_HQ]) * ds_head_bytes(ph[PF_PATH], ph[PF_D]);
 }
 }  // namespace
 }  // namespace tpr

@@ -102,12 +102,14 @@ constexpr int kDkdvQ = 64;            // queries per staged query block
 constexpr int kDkdvMaxBlocks = 256;   // query blocks one dK/dV item may stream (LDS table size)
 constexpr int kDkdvPrefixChunk = 64;  // smallest chunk a prefix tile is split into
 constexpr int kPlanCus = 256;         // compute units the dK/dV work is balanced over (MI355X)
-// dS store (head_dim 128): the dK/dV kernel writes each dS block it computes,
-// bf16, and dQ = scale dS K reads them instead of recomputing S and dP. One
-// slot per (128-key tile, query block it is visible to) holds, per query
-// head, the 128 x 64 block as four 4 KiB wave blocks (32 keys each) in the
-// dK/dV kernel's register order.
-constexpr int kDsHeadBytes = kDkdvKeys * kDkdvQ * 2;          // 16 KiB per query head per slot
+// dS store (bf16 head_dim 128 and 256): the dK/dV kernel writes each dS block
+// it computes, bf16, and dQ = scale dS K reads them instead of recomputing S
+// and dP. One slot per (dK/dV key tile, query block it is visible to) holds,
+// per query head, the tile x 64 block as four wave blocks in the dK/dV
+// kernel's register order: at head_dim 128 a 128-key tile of 4 KiB wave
+// blocks (32 keys each), at head_dim 256 a 64-key tile of 2 KiB wave blocks
+// (16 keys each).
+constexpr int kDsHeadBytes = kDkdvKeys * kDkdvQ * 2;          // 16 KiB per query head per slot (head_dim 128)
 constexpr int64_t kDsMaxBytes = int64_t{32} << 30;           // larger dS areas fall back to recomputation
 // MFMA backward workspace, ahead of the partial slots: two constants (+inf,
 // 0) that rows past a query block's end are copied from, then lse * log2e per
@@ -120,6 +122,10 @@ constexpr int kM16Tokens = 32;        // forward / dQ tokens per wave (two 16-qu
 // two would not fit the register file; at 64 two measured no faster)
 constexpr int m16_wave_keys(int /*head_dim*/) { return 16; }
 constexpr int m16_keys(int d) { return m16_wave_keys(d) * kM16Waves; }  // keys per dK/dV workgroup
+// bytes per query head per slot of a plan's dS store
+constexpr int ds_head_bytes(int path, int d) {
+  return (path == PATH_MFMA ? kDkdvKeys : m16_keys(d)) * kDkdvQ * 2;
+}
 constexpr int kMfmaRegRuns = 8;       // key runs a forward / dQ workgroup holds in registers; a
                                       // launch with longer run lists reads them from the plan
 

@@ -31,6 +31,9 @@ namespace tpr {
 namespace {
 
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4_m16;
+typedef int i32x4_m16 __attribute__((ext_vector_type(4)));
+// bytes per query head per dS slot: the 64-key dK/dV tile x 64 queries
+constexpr int m16_ds_head_bytes(int d) { return m16_keys(d) * kDkdvQ * 2; }
 
 __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -587,6 +590,218 @@ __global__ __launch_bounds__(256) void m16_dq(KernelArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// dQ from the dS store (head_dim 256): dQ^T += K^T dS^T over the dS blocks
+// the dK/dV kernel stored, instead of recomputing S and dP. Work items and
+// waves as the forward's. The key stream follows the dK/dV tiling: the leaf's
+// ancestor nodes root first, then its suffix, in 64-key tiles, one dS slot
+// each. A slot holds a head's 64 x 64 block as four 2 KiB wave blocks (16
+// keys each) of [32-query half][lane L] x 8 queries, lane L holding key L %
+// 16 and queries 32 t + 8 (L / 16) .. +7. Per tile every wave copies its
+// share of the K rows (read transposed as the A operand) and its own 4 KiB
+// of dS (the four wave blocks' halves of its 32 queries), then runs 64 MFMAs.
+// The copy puts chunk L of each 1 KiB block at L ^ (4 ((L >> 4) & 1)), which
+// spreads every 32-lane pass of the transposed dS reads over all 64 banks.
+// Three buffers keep two tiles in flight behind the one being computed.
+// ---------------------------------------------------------------------------
+template <int kD, bool kStrided>
+__global__ __launch_bounds__(256) void m16_dqs(KernelArgs a) {
+  using T = Geo<kD>;
+  static_assert(kD == 256, "the dS store serves head_dim 256 on this family");
+  const int32_t* item = a.plan + a.off_fwd + 4 * blockIdx.x;
+  const int leaf = item[0];
+  if (leaf < 0) return;
+  const int tok0 = item[1], qh0 = item[2], kvh = item[3];
+  const int32_t* cu = a.plan + a.off_cu;
+  const int32_t* no = a.plan + a.off_node_off;
+  const int row0 = cu[leaf], len = cu[leaf + 1] - cu[leaf];
+
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hpw = a.hpw;
+  const int head = qh0 + wave % hpw;
+  const int tw0 = tok0 + kM16Tokens * (wave / hpw);
+  const int tpw = kM16Tokens * (kM16Waves / hpw);
+  const int suffix_keys = min(len, tok0 + tpw);
+  const int i16 = lane & 15, g = lane >> 4;
+  const bool wave_ok = tw0 < len;
+  const int qb = a.plan[a.off_leaf_qblk + leaf] + tw0 / kDkdvQ;  // the wave's query block
+  const int jq = (tw0 / kM16Tokens) & 1;                          // and its 32-query half of it
+
+  const int64_t qstride = static_cast<int64_t>(a.hq) * kD;
+  const uint32_t p_rb = static_cast<uint32_t>(a.hkv) * kD * 2;
+  const uint32_t k_rb = kStrided ? static_cast<uint32_t>(a.k_rs) * 2 : p_rb;
+  constexpr int kKeys = m16_keys(kD);                 // keys per tile (= per dS slot)
+  constexpr int kSlotHead = m16_ds_head_bytes(kD);    // 8 KiB per head per slot
+  constexpr int kBufs = 3, kDsWave = 4096;
+  constexpr int kDsOff = kBufs * T::TB;               // K [buffer] | dS [buffer][wave]
+  __shared__ __attribute__((aligned(1024))) char smem[kBufs * (T::TB + kM16Waves * kDsWave)];
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(smem));
+  const char* kbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.k) + kvh * kD);
+  const char* pkbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.pk) + kvh * kD);
+
+  // dS copy: block w (wave block w of the slot, this wave's query half) lands
+  // at 1024 w; lane l fetches the chunk that lands at l (the swizzle is its own inverse)
+  const uint32_t dsl = 16u * static_cast<uint32_t>(lane ^ (4 * ((lane >> 4) & 1)));
+  // dS^T operand reads (B: lane l gets query 16 qs + l % 16, keys 32 t + 8 (l / 16) + 0..7).
+  // As a source row of ds_read_tr16_b64, lane l (group g, e = (l % 16) / 4,
+  // m = l % 4) addresses key 8 g + 4 h + e of the 32-key step (wave block
+  // 2 t + g / 2, its key 8 (g % 2) + 4 h + e), queries 16 qs + 4 m .. +3;
+  // h = 0 / 1 gives keys +0..3 / +4..7, qs adds 512 bytes, t 2048.
+  uint32_t dso[2];
+  {
+    const int e = (lane & 15) >> 2, m = lane & 3;
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {
+      const int L = 8 * (g & 1) + 4 * hh + e + 16 * (m >> 1);
+      dso[hh] = 1024u * (g >> 1) + 16u * (L ^ (4 * ((L >> 4) & 1))) + 8u * (m & 1);
+    }
+  }
+
+  // key stream cursor (uniform; plan words through the scalar cache)
+  const int depth = a.max_depth;
+  const int32_t* anc = a.plan + a.off_anc + static_cast<int64_t>(leaf) * depth;
+  int cd = -1, crow = 0, clen = 0, clim = 0, ctile = 0, ckey = 0;
+  auto next_segment = [&]() {
+    for (;;) {
+      cd++;
+      if (cd < depth) {
+        const int nd = plan_word(anc + cd);
+        if (nd >= 0) {
+          crow = plan_word(no + nd);
+          const int l = plan_word(no + nd + 1) - crow;
+          if (l == 0) continue;
+          clen = clim = l;
+          ctile = plan_word(a.plan + a.off_ds + nd);
+          break;
+        }
+        cd = depth;  // -1 pads the list: the suffix is next
+      }
+      if (cd == depth) {
+        crow = row0;
+        clen = len;
+        clim = suffix_keys;
+        ctile = plan_word(a.plan + a.off_ds + a.num_nodes + leaf);
+      } else {
+        clen = clim = 0;  // past the end
+      }
+      break;
+    }
+    ckey = 0;
+  };
+  auto advance = [&]() {
+    ckey += kKeys;
+    if (ckey >= clim) next_segment();
+  };
+  // copy the current tile into buffer b (K: this wave's T::BPW blocks; dS: 4
+  // blocks if the wave reads the tile -- prefix tiles: every wave; suffix
+  // tiles: those not entirely in the wave's future)
+  auto issue = [&](int b, int& rows, bool& vis) __attribute__((always_inline)) {
+    const bool suffix = cd == depth;
+    rows = min(kKeys, clen - ckey);
+    vis = wave_ok && (!suffix || ckey <= tw0 + kM16Tokens - 1);
+    const uint32_t rb = suffix ? k_rb : p_rb;
+    copy_tile<kD>((suffix ? kbase : pkbase) + static_cast<int64_t>(crow + ckey) * rb, rb, rows, lds0 + b * T::TB,
+                  wave, lane);
+    if (vis) {
+      const int32_t* te = a.plan + a.off_ds_tiles + 2 * (ctile + ckey / kKeys);
+      const int slot = plan_word(te) + qb - plan_word(te + 1);
+      const char* src = static_cast<const char*>(a.ds) + (static_cast<int64_t>(slot) * a.hq + head) * kSlotHead +
+                        jq * 1024;
+      dma_blocks4_nt(src, dsl, 2048 + dsl, 4096 + dsl, 6144 + dsl, lds0 + kDsOff + (b * kM16Waves + wave) * kDsWave);
+    }
+  };
+
+  f32x4 dq[2][T::ND];
+#pragma unroll
+  for (int qs = 0; qs < 2; qs++)
+#pragma unroll
+    for (int db = 0; db < T::ND; db++) dq[qs][db] = f32x4{};
+  // 64 MFMAs on buffer b; keys at or past `rows` (the segment's end) read as zero dS
+  auto compute = [&](int b, int rows) __attribute__((always_inline)) {
+    const char* kt = smem + b * T::TB;
+    const char* dt = smem + kDsOff + (b * kM16Waves + wave) * kDsWave;
+    bf16x8 f[2][2];  // [qs][t]
+#pragma unroll
+    for (int qs = 0; qs < 2; qs++)
+#pragma unroll
+      for (int t = 0; t < 2; t++) {
+        const char* base = dt + 2048 * t + 512 * qs;
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_m16*)(base + dso[0]));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_m16*)(base + dso[1]));
+        const bf16x4 l4 = __builtin_bit_cast(bf16x4, lo), h4 = __builtin_bit_cast(bf16x4, hi);
+        bf16x8 r;
+        r[0] = l4[0]; r[1] = l4[1]; r[2] = l4[2]; r[3] = l4[3];
+        r[4] = h4[0]; r[5] = h4[1]; r[6] = h4[2]; r[7] = h4[3];
+        if (rows < kKeys) {
+#pragma unroll
+          for (int i = 0; i < 8; i++)
+            if (32 * t + 8 * g + i >= rows) r[i] = static_cast<bf16>(0.f);
+        }
+        f[qs][t] = r;
+      }
+    // one fenced slot per (key step t, head-dim block db): the K^T operand
+    // (head dims 16 db.., keys 32 t..), read kRead slots ahead, and two MFMAs
+    constexpr int kSlots = 2 * T::ND;
+    constexpr int kRead = 4, kRing = kRead + 1;
+    bf16x8 ra[kRing];
+    auto read_slot = [&](auto ic) __attribute__((always_inline)) {
+      constexpr int i = decltype(ic)::value;
+      ra[i % kRing] = col_operand<kD>(kt, 32 * (i / T::ND), 16 * (i % T::ND), lane);
+    };
+    static_for<kRead>([&](auto ic) { read_slot(ic); });
+    static_for<kSlots>([&](auto ic) {
+      constexpr int i = decltype(ic)::value, t = i / T::ND, db = i % T::ND;
+      if constexpr (i + kRead < kSlots) read_slot(std::integral_constant<int, i + kRead>{});
+#pragma unroll
+      for (int qs = 0; qs < 2; qs++) dq[qs][db] = mfma16(ra[i % kRing], f[qs][t], dq[qs][db]);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+
+  // copies complete in issue order: waiting until at most tile i + 1's copies
+  // are outstanding means tile i landed
+  next_segment();
+  int rows[kBufs];
+  bool vis[kBufs];
+  issue(0, rows[0], vis[0]);
+  advance();
+  bool more1 = clim > 0;
+  if (more1) issue(1, rows[1], vis[1]);
+  static_assert(T::BPW == 8, "8 K copies per wave per tile");
+  for (int b = 0;;) {
+    const int b1 = b == kBufs - 1 ? 0 : b + 1, b2 = b1 == kBufs - 1 ? 0 : b1 + 1;
+    if (!more1) wait_dma();
+    else if (vis[b1]) asm volatile("s_waitcnt vmcnt(12)");
+    else asm volatile("s_waitcnt vmcnt(8)");
+    __syncthreads();  // tile i has landed; every wave is done with buffer b2 (tile i - 1)
+    bool more2 = false;
+    if (more1) {
+      advance();
+      more2 = clim > 0;
+      if (more2) issue(b2, rows[b2], vis[b2]);
+    }
+    if (vis[b]) compute(b, rows[b]);
+    if (!more1) break;
+    more1 = more2;
+    b = b1;
+  }
+
+  if (!wave_ok) return;
+#pragma unroll
+  for (int qs = 0; qs < 2; qs++) {
+    const int t = tw0 + 16 * qs + i16;
+    if (tw0 + 16 * qs >= len || t >= len) continue;
+    bf16* dp = static_cast<bf16*>(a.dq) + static_cast<int64_t>(row0 + t) * qstride + head * kD + 4 * g;
+#pragma unroll
+    for (int db = 0; db < T::ND; db++) {
+      bf16x4 v4;
+#pragma unroll
+      for (int r = 0; r < 4; r++) v4[r] = static_cast<bf16>(dq[qs][db][r] * a.scale);
+      *reinterpret_cast<bf16x4*>(dp + 16 * db) = v4;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // dK/dV. One workgroup = 4 waves x 16 keys (KB 16-key blocks kb per wave) of
 // one KV segment tile and KV head; it streams every 64-query block that
 // sees the tile -- for a prefix node every descendant leaf and every query
@@ -599,7 +814,9 @@ __global__ __launch_bounds__(256) void m16_dq(KernelArgs a) {
 //   dV += P^T dO, dK += dS^T Q (dO, Q read transposed from LDS, again shared
 //   by the key blocks).
 // ---------------------------------------------------------------------------
-template <int kD, bool kStrided>  // kStrided as in m16_fwd
+// kStrided as in m16_fwd; kStoreDs: also store every dS block to the dS store
+// (a.ds, head_dim 256) for the dQ kernel
+template <int kD, bool kStrided, bool kStoreDs>
 __global__ __launch_bounds__(256) void m16_dkdv(KernelArgs a) {
   using T = Geo<kD>;
   constexpr int kWaveKeys = m16_wave_keys(kD);
@@ -642,11 +859,18 @@ __global__ __launch_bounds__(256) void m16_dkdv(KernelArgs a) {
     const bool wave_active = kw0 < seg_len;
 
     if (tile > 0) __syncthreads();  // every wave is done with the previous tile's table
+    int ds_first = 0, ds_lo = 0;  // the tile's first dS slot and first query block
+    if constexpr (kStoreDs) {
+      const int32_t* seg_tiles = a.plan + a.off_ds;
+      const int32_t* te = a.plan + a.off_ds_tiles + 2 * (seg_tiles[prefix ? seg : a.num_nodes + seg] + key0 / kKeys);
+      ds_first = te[0];
+      ds_lo = te[1];
+    }
     for (int i = threadIdx.x; i < qb_hi - qb_lo; i += blockDim.x) {
       const int qb = first_last ? qb_lo + i : qb_hi - 1 - i;
       const int lf = qblk[2 * qb], tok = qblk[2 * qb + 1];
       const int r0 = cu[lf];
-      qtab[i] = int4{r0 + tok, tok, min(kTileRows, cu[lf + 1] - r0 - tok), 0};
+      qtab[i] = int4{r0 + tok, tok, min(kTileRows, cu[lf + 1] - r0 - tok), kStoreDs ? ds_first + qb - ds_lo : 0};
     }
     __syncthreads();
 
@@ -715,6 +939,14 @@ __global__ __launch_bounds__(256) void m16_dkdv(KernelArgs a) {
       if (sidx + 1 < nstage) issue((sidx + 1) / group, (sidx + 1) % group, buf ^ 1);
       if (wave_active) {
         const int tok0 = __builtin_amdgcn_readfirstlane(qtab[blk].y);
+        // dS store: this stage's block (slot, head kvh G + sidx % G, this wave's 16 keys)
+        char* ds_stage = nullptr;
+        if constexpr (kStoreDs) {
+          const int slot = __builtin_amdgcn_readfirstlane(qtab[blk].w);
+          ds_stage = static_cast<char*>(a.ds) +
+                     (static_cast<int64_t>(slot) * a.hq + kvh * group + sidx % group) * m16_ds_head_bytes(kD) +
+                     wave * (m16_ds_head_bytes(kD) / kM16Waves);
+        }
         const char* qt = smem + buf * 2 * T::TB;
         const char* gt = qt + T::TB;
         const float* nlse = &stats[buf][0][0];
@@ -790,6 +1022,15 @@ __global__ __launch_bounds__(256) void m16_dkdv(KernelArgs a) {
                 for (int kb = 0; kb < KB; kb++) {
                   pT[kb] = pack8(pf[kb][0], pf[kb][1]);
                   dT[kb] = pack8(df[kb][0], df[kb][1]);
+                }
+                if constexpr (kStoreDs) {
+                  // dS of the 32-query half t, lane l: key l % 16, queries 32 t + 8 (l / 16) .. +7:
+                  // one whole 1 KiB line, streaming buffer store from the stage's uniform base
+                  static_assert(KB == 1, "one 16-key block per wave");
+                  __builtin_amdgcn_raw_buffer_store_b128(
+                      __builtin_bit_cast(i32x4_m16, dT[0]),
+                      __builtin_amdgcn_make_buffer_rsrc(ds_stage, 0, m16_ds_head_bytes(kD) / kM16Waves, 0x00020000),
+                      t * 1024 + 16 * lane, 0, 2 /* non-temporal */);
                 }
               }
             }
@@ -933,10 +1174,15 @@ int launch_fwd_d(const KernelArgs& a, hipStream_t s) {
 template <int kD>
 int launch_dkdv_d(const KernelArgs& a, int n_dkdv, int n_red, hipStream_t s) {
   if (n_dkdv > 0) {
-    if (strided_rows<kD>(a))
-      hipLaunchKernelGGL((m16_dkdv<kD, true>), dim3(n_dkdv), dim3(64 * kM16Waves), 0, s, a);
+    const bool st = strided_rows<kD>(a), ds = kD == 256 && a.ds != nullptr;
+    if (st && ds)
+      hipLaunchKernelGGL((m16_dkdv<kD, true, kD == 256>), dim3(n_dkdv), dim3(64 * kM16Waves), 0, s, a);
+    else if (st)
+      hipLaunchKernelGGL((m16_dkdv<kD, true, false>), dim3(n_dkdv), dim3(64 * kM16Waves), 0, s, a);
+    else if (ds)
+      hipLaunchKernelGGL((m16_dkdv<kD, false, kD == 256>), dim3(n_dkdv), dim3(64 * kM16Waves), 0, s, a);
     else
-      hipLaunchKernelGGL((m16_dkdv<kD, false>), dim3(n_dkdv), dim3(64 * kM16Waves), 0, s, a);
+      hipLaunchKernelGGL((m16_dkdv<kD, false, false>), dim3(n_dkdv), dim3(64 * kM16Waves), 0, s, a);
     if (hipGetLastError() != hipSuccess) return 4;
   }
   if (n_red > 0) {
@@ -956,6 +1202,15 @@ void launch_dq_runs(const KernelArgs& a, int n_fwd, hipStream_t s) {
 
 template <int kD>
 int launch_dq_d(const KernelArgs& a, int n_fwd, hipStream_t s) {
+  if constexpr (kD == 256) {
+    if (n_fwd > 0 && a.ds) {  // dQ from the dS store
+      if (strided_rows<kD>(a))
+        hipLaunchKernelGGL((m16_dqs<kD, true>), dim3(n_fwd), dim3(64 * kM16Waves), 0, s, a);
+      else
+        hipLaunchKernelGGL((m16_dqs<kD, false>), dim3(n_fwd), dim3(64 * kM16Waves), 0, s, a);
+      return hipGetLastError() != hipSuccess ? 4 : 0;
+    }
+  }
   if (n_fwd > 0) {
     if (a.max_runs > kMfmaRegRuns)
       launch_dq_runs<kD, true>(a, n_fwd, s);

@@ -333,7 +333,7 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
   int32_t n_dkdv = 0;
   std::vector<int32_t> dkdv_words = order_for_xcds(dkdv, Hkv, DK_WORDS, &n_dkdv);
 
-  // ---- dS store (head_dim 128) ------------------------------------------------
+  // ---- dS store (bf16 head_dim 128 and 256) -------------------------------------
   // Every (128-key tile, query block) pair the dK/dV items stream gets one
   // slot; a tile's query blocks are one contiguous range (a node's descendant
   // leaves, or a leaf's blocks from the tile's first key on), so its slots
@@ -342,7 +342,8 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
   // segment's first tile and each tile's {first slot, first block}.
   std::vector<int32_t> ds_table;
   int64_t ds_slots = 0;
-  if (path == PATH_MFMA && !(t->flags & TPR_PLAN_RECOMPUTE_DQ)) {
+  const bool ds_path = path == PATH_MFMA || (path == PATH_MFMA16 && D == 256);
+  if (ds_path && !(t->flags & TPR_PLAN_RECOMPUTE_DQ)) {
     std::vector<int32_t> first(static_cast<size_t>(M) + N + 1), tiles;
     int32_t ntile = 0;
     auto add = [&](int32_t lo, int32_t hi) {
@@ -360,7 +361,7 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
       for (int k0 = 0; k0 < cu[s + 1] - cu[s]; k0 += KT) add(leaf_qblk[s] + k0 / BQ, leaf_qblk[s + 1]);
     }
     first[M + N] = ntile;
-    if (ds_slots > 0 && ds_slots < INT32_MAX && ds_slots * Hq * kDsHeadBytes <= kDsMaxBytes) {
+    if (ds_slots > 0 && ds_slots < INT32_MAX && ds_slots * Hq * ds_head_bytes(path, D) <= kDsMaxBytes) {
       ds_table = std::move(first);
       ds_table.insert(ds_table.end(), tiles.begin(), tiles.end());
     } else {

@@ -1,6 +1,6 @@
-"""GPU checks of the dS store (bf16, head_dim 128): the dK/dV kernel stores
-every dS block it computes and the dQ kernel (mfma_dqs) computes
-dQ = scale dS K from them, instead of recomputing S and dP.
+"""GPU checks of the dS store (bf16, head_dim 128 and 256): the dK/dV kernel
+stores every dS block it computes and the dQ kernel (mfma_dqs, m16_dqs)
+computes dQ = scale dS K from them, instead of recomputing S and dP.
 
 * dK, dV and the prefix gradients are those of the recomputing plan bit for
   bit (the same dK/dV kernel, the stores only add writes);
@@ -46,14 +46,15 @@ def _backward(meta, q, k, v, pk, pv, out, lse, dout, scale, recompute, phases=No
     return grads
 
 
+@pytest.mark.parametrize("d", [128, 256])
 @pytest.mark.parametrize("case", list(_cases()))
-def test_ds_store_backward_matches_recomputed_dq_and_oracle(case, cuda_device):
+def test_ds_store_backward_matches_recomputed_dq_and_oracle(case, d, cuda_device):
     from bridge_amd import prefix_attention_forward
     meta, hq, hkv = _cases()[case]
-    d, scale = 128, 0.09
+    scale = 0.09
     assert meta.plan(hq, hkv, d, torch.bfloat16, cuda_device).dq_from_ds
     q, k, v, pk, pv, dout = make_inputs(meta, hq, hkv, d, torch.bfloat16, seed=5, device=cuda_device)
-    print(f"ds_store case={case} hq={hq} hkv={hkv} tq={meta.total_q} tp={meta.total_prefix}", flush=True)
+    print(f"ds_store case={case} d={d} hq={hq} hkv={hkv} tq={meta.total_q} tp={meta.total_prefix}", flush=True)
     out, lse = prefix_attention_forward(q, k, v, pk, pv, meta, scale)
     ds = _backward(meta, q, k, v, pk, pv, out, lse, dout, scale, recompute=False)
     rc = _backward(meta, q, k, v, pk, pv, out, lse, dout, scale, recompute=True)
@@ -87,12 +88,13 @@ def test_ds_store_phase_by_phase_equals_one_call(cuda_device):
         assert torch.equal(a, b), name
 
 
-def test_ds_store_reads_strided_inputs(cuda_device):
+@pytest.mark.parametrize("d", [128, 256])
+def test_ds_store_reads_strided_inputs(d, cuda_device):
     """q/k/v as slices of one fused projection: the dS-store backward equals
     that of packed copies bit for bit."""
     from bridge_amd import tpr_prefix_attention
     meta, hq, hkv = _cases()["depth3_ragged"]
-    d, scale, tq = 128, 0.09, meta.total_q
+    scale, tq = 0.09, meta.total_q
     gen = torch.Generator(device="cpu").manual_seed(3)
     width = (hq + 2 * hkv) * d
     base = torch.randn(tq, width, generator=gen).to(torch.bfloat16).to(cuda_device)

@@ -430,13 +430,16 @@ def _ds_tables(w):
     return first, [(tiles[2 * i], tiles[2 * i + 1]) for i in range(first[-1])]
 
 
-def _ds_reads_and_writes(meta, hq, hkv):
-    """Emulate the slot arithmetic of the head_dim-128 backward with a dS
-    store: the (slot, query head, 32-key wave block) triples every dK/dV stage
-    writes, and those every dQ wave reads (a block wholly past its segment's
-    end is masked, not read)."""
-    plan = meta.plan(hq, hkv, 128, torch.bfloat16, CPU)
+def _ds_reads_and_writes(meta, hq, hkv, d=128):
+    """Emulate the slot arithmetic of the bf16 backward with a dS store: the
+    (slot, query head, wave block) triples every dK/dV stage writes, and those
+    every dQ wave reads (a block wholly past its segment's end is masked, not
+    read). head_dim 128: 128-key tiles of four 32-key wave blocks, dQ
+    workgroups of 8 waves streaming 64-key halves; head_dim 256: 64-key tiles
+    of four 16-key wave blocks, dQ workgroups of 4 waves streaming whole tiles."""
+    plan = meta.plan(hq, hkv, d, torch.bfloat16, CPU)
     assert plan.dq_from_ds
+    kt, wk, waves, step = (128, 32, FWD_WAVES, 64) if d == 128 else (64, 16, 4, 64)
     w, fwd, dkdv, qblk = decode(plan)
     g = hq // hkv
     n_slots = w[PF["DS_SLOTS"]]
@@ -450,17 +453,17 @@ def _ds_reads_and_writes(meta, hq, hkv):
 
     writes = Counter()
     for src, seg, key0, kvh, lo, hi, _ in tiles_of(dkdv):
-        t_first, t_lo = tiles[first[seg if src == 0 else m + seg] + key0 // 128]
+        t_first, t_lo = tiles[first[seg if src == 0 else m + seg] + key0 // kt]
         for qb in range(lo, hi):
             slot = t_first + qb - t_lo
             assert 0 <= slot < n_slots
             for wv in range(4):
-                if key0 + 32 * wv < seg_len(src, seg):  # active waves only
+                if key0 + wk * wv < seg_len(src, seg):  # active waves only
                     for head in range(kvh * g, kvh * g + g):
                         writes[(slot, head, wv)] += 1
     reads = set()
-    hpw = math.gcd(g, FWD_WAVES)
-    tpw = 32 * (FWD_WAVES // hpw)
+    hpw = math.gcd(g, waves)
+    tpw = 32 * (waves // hpw)
     for leaf, tok0, qh0, kvh in fwd:
         if leaf < 0:
             continue
@@ -468,28 +471,28 @@ def _ds_reads_and_writes(meta, hq, hkv):
         segs = [(0, nd, no[nd + 1] - no[nd], no[nd + 1] - no[nd]) for nd in meta.leaf_ancestors[leaf]
                 if no[nd + 1] > no[nd]]
         segs.append((1, leaf, length, min(length, tok0 + tpw)))
-        for wave in range(FWD_WAVES):
+        for wave in range(waves):
             head, tw0 = qh0 + wave % hpw, tok0 + 32 * (wave // hpw)
             if tw0 >= length:
                 continue
             qb = leaf_qblk[leaf] + tw0 // 64
             for src, seg, slen, lim in segs:
-                for key0 in range(0, lim, 128):
-                    for half in range(2):
-                        k0 = key0 + 64 * half
-                        if k0 >= lim or (src == 1 and k0 > tw0 + 31):
+                for key0 in range(0, lim, kt):
+                    for k0 in range(key0, min(key0 + kt, lim), step):  # the dQ kernel's tiles (halves at 128)
+                        if src == 1 and k0 > tw0 + 31:
                             continue
-                        t_first, t_lo = tiles[first[seg if src == 0 else m + seg] + key0 // 128]
+                        t_first, t_lo = tiles[first[seg if src == 0 else m + seg] + key0 // kt]
                         slot = t_first + qb - t_lo
                         assert 0 <= slot < n_slots
-                        for kb in range(2):
-                            if k0 + 32 * kb < slen:
-                                reads.add((slot, head, 2 * half + kb))
+                        for wv in range((k0 - key0) // wk, (k0 - key0 + step) // wk):
+                            if key0 + wk * wv < slen:
+                                reads.add((slot, head, wv))
     return n_slots, writes, reads
 
 
+@pytest.mark.parametrize("d", [128, 256])
 @pytest.mark.parametrize("case", ["split_prefix", "depth3_ragged", "empty_leaves", "gqa8", "gqa3", "mha"])
-def test_ds_store_is_written_once_before_every_dq_read(case):
+def test_ds_store_is_written_once_before_every_dq_read(case, d):
     trees = {
         "split_prefix": (TPRPrefixMeta.shared_prefix(300, [4096, 4096, 100, 4096]), 8, 2),
         "depth3_ragged": (TPRPrefixMeta(cu_seqlens_q=(0, 33, 98, 138, 155, 420), node_offsets=(0, 130, 200, 270),
@@ -500,7 +503,7 @@ def test_ds_store_is_written_once_before_every_dq_read(case):
         "mha": (TPRPrefixMeta.shared_prefix(0, [200, 65]), 4, 4),
     }
     meta, hq, hkv = trees[case]
-    n_slots, writes, reads = _ds_reads_and_writes(meta, hq, hkv)
+    n_slots, writes, reads = _ds_reads_and_writes(meta, hq, hkv, d)
     assert set(writes.values()) == {1}  # no block is written twice
     assert reads <= set(writes)         # every read block was written
     # the store holds exactly the visible (tile, query block) pairs: each slot is read
@@ -517,6 +520,11 @@ def test_ds_store_size_at_the_qwen3_layer_shape():
     assert w[PF["DS_SLOTS"]] == slots == 12416
     fp32 = meta.plan(32, 8, 128, torch.bfloat16, CPU, recompute_dq=True).workspace_bytes
     assert plan.workspace_bytes == fp32 + slots * 32 * 16384  # 6.5 GB
-    # other paths never store dS
+    # head_dim 256 (64-key tiles, 8 KiB per head and slot) stores dS too; other paths never do
+    q35 = meta.plan(8, 2, 256, torch.bfloat16, CPU)
+    slots256 = 64 * 256 + 4 * sum(64 - j for j in range(64))
+    assert q35.dq_from_ds and q35.host.tolist()[PF["DS_SLOTS"]] == slots256
+    assert q35.workspace_bytes == meta.plan(8, 2, 256, torch.bfloat16, CPU, recompute_dq=True).workspace_bytes + \
+        slots256 * 8 * 8192  # 1.6 GB
     assert not meta.plan(32, 8, 64, torch.bfloat16, CPU).dq_from_ds
     assert not meta.plan(32, 8, 128, torch.float32, CPU).dq_from_ds
