@@ -60,8 +60,8 @@ class LaunchPlan:
     @property
     def dq_from_ds(self) -> bool:
         """Whether the backward stores dS and computes dQ from it (bf16
-        head_dim 128 unless the plan was built with recompute_dq=True or the
-        store would exceed 32 GiB); the workspace then holds the store."""
+        head_dim 128 and 256 unless the plan was built with recompute_dq=True
+        or the store would exceed 32 GiB); the workspace then holds the store."""
         return int(self.host[_PF_DS_SLOTS]) > 0
 
     @property
@@ -204,7 +204,7 @@ class TPRPrefixMeta:
         ``recompute_dq``: the dQ kernel recomputes the scores instead of
         reading a dS store (TPR_PLAN_RECOMPUTE_DQ): a backward workspace of a
         few MB instead of 2 bytes per visible (query, key) pair and query head,
-        at the cost of a slower dQ (bf16 head_dim 128 only; the other paths
+        at the cost of a slower dQ (bf16 head_dim 128 and 256; the other paths
         always recompute)."""
         if dtype == torch.bfloat16:
             code = _lib.TPR_DTYPE_BF16

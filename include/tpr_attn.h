@@ -76,8 +76,8 @@ typedef enum TprDtype {
  * leaves are numbered in DFS order, segment_plan.py:266-275), and a node that
  * appears in a path must appear at the same depth in every path.
  *
- * flags: 0, or TPR_PLAN_RECOMPUTE_DQ. By default a bf16 head_dim-128 plan
- * has the dK/dV kernel store every dS block it computes (bf16, 2 bytes per
+ * flags: 0, or TPR_PLAN_RECOMPUTE_DQ. By default a bf16 head_dim-128 or 256
+ * plan has the dK/dV kernel store every dS block it computes (bf16, 2 bytes per
  * visible (query, key) pair and query head) in the backward workspace, and
  * the dQ kernel reads them: dQ = scale dS K then costs one matrix product
  * instead of three (the scores S and dP recomputed). The workspace grows by
