@@ -1027,20 +1027,32 @@ __global__ __launch_bounds__(512) void mfma_dqs(KernelArgs a) {
   auto compute = [&](int b, int rows) __attribute__((always_inline)) {
     const char* kt = smem + b * kTileBytes;
     const char* dt = smem + kDsOff + (b * kFwdWaves + wave) * kDsWave;
+    bf16x8 f[4];  // dS^T operands of the four key steps
 #pragma unroll
-    for (int kb = 0; kb < 2; kb++)
+    for (int st = 0; st < 4; st++) {
+      const int kb = st >> 1, kc = st & 1;
+      f[st] = lds_col8_at(dt + kb * 2048 + kc * 256, dso[0], dso[1]);
+      if (rows < kTileRows) {
 #pragma unroll
-      for (int kc = 0; kc < 2; kc++) {
-        bf16x8 f = lds_col8_at(dt + kb * 2048 + kc * 256, dso[0], dso[1]);
-        if (rows < kTileRows) {
-#pragma unroll
-          for (int i = 0; i < 8; i++)
-            if (32 * kb + 16 * kc + 8 * h + i >= rows) f[i] = static_cast<bf16>(0.f);
-        }
-        const char* kr = kt + (32 * kb + 16 * kc) * 256;
-#pragma unroll
-        for (int db = 0; db < 4; db++) dq[db] = mfma(lds_col8_at(kr, lo.v[db][0], lo.v[db][1]), f, dq[db]);
+        for (int i = 0; i < 8; i++)
+          if (32 * kb + 16 * kc + 8 * h + i >= rows) f[st][i] = static_cast<bf16>(0.f);
       }
+    }
+    // one fenced slot per (key step st, head-dim block db): the K^T operand,
+    // read kRead slots ahead, and its MFMA
+    constexpr int kRead = 4, kRing = kRead + 1;
+    bf16x8 ra[kRing];
+    auto read_slot = [&](auto ic) __attribute__((always_inline)) {
+      constexpr int i = decltype(ic)::value, st = i / 4, db = i % 4;
+      ra[i % kRing] = lds_col8_at(kt + (32 * (st >> 1) + 16 * (st & 1)) * 256, lo.v[db][0], lo.v[db][1]);
+    };
+    static_for<kRead>([&](auto ic) { read_slot(ic); });
+    static_for<16>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      if constexpr (i + kRead < 16) read_slot(std::integral_constant<int, i + kRead>{});
+      dq[i % 4] = mfma(ra[i % kRing], f[i / 4], dq[i % 4]);
+      __builtin_amdgcn_sched_barrier(0);
+    });
   };
 
   // halves i (computed), i + 1 and i + 2 (in flight) sit in buffers i % 3,
