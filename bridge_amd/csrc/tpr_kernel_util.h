@@ -206,7 +206,8 @@ __device__ __forceinline__ void dma_blocks4_m0(const char* sbase, uint32_t v0, u
       "global_load_lds_dwordx4 %4, %6\n\t"
       "s_mov_b32 m0, %0"
       : "=&s"(saved)
-      : "v"(v0), "v"(v1), "v"(v2), "v"(v3), "s"(lds_dst), "s"(sbase));
+      : "v"(v0), "v"(v1), "v"(v2), "v"(v3), "s"(lds_dst), "s"(sbase)
+      : "scc");  // s_add_u32 sets SCC
 }
 
 // One dword per lane from a per-lane address, landing at lds_dst + 4 l
