@@ -528,3 +528,21 @@ def test_ds_store_size_at_the_qwen3_layer_shape():
         slots256 * 8 * 8192  # 1.6 GB
     assert not meta.plan(32, 8, 64, torch.bfloat16, CPU).dq_from_ds
     assert not meta.plan(32, 8, 128, torch.float32, CPU).dq_from_ds
+
+
+def test_ds_store_falls_back_to_recompute_past_its_cap():
+    """A store over 32 GiB is not planned: prefix 32768 + 8 x 2048 at GQA 32/8
+    would need 256 x 256 + 8 x sum(32 - 2 j, j < 16) = 67,712 slots x 32 heads x
+    16 KiB = 35.5 GB, so its plan keeps the recomputing dQ and the small
+    workspace; with 4 siblings (33,856 slots, 17.7 GB) the store is planned."""
+    cap = 32 << 30
+    big = TPRPrefixMeta.shared_prefix(32768, [2048] * 8)
+    slots = 256 * 256 + 8 * sum(32 - 2 * j for j in range(16))
+    assert slots == 67712 and slots * 32 * 16384 > cap
+    plan = big.plan(32, 8, 128, torch.bfloat16, CPU)
+    assert not plan.dq_from_ds and plan.host.tolist()[PF["DS_SLOTS"]] == 0
+    assert plan.workspace_bytes == big.plan(32, 8, 128, torch.bfloat16, CPU, recompute_dq=True).workspace_bytes
+    half = TPRPrefixMeta.shared_prefix(32768, [2048] * 4)
+    hplan = half.plan(32, 8, 128, torch.bfloat16, CPU)
+    hslots = 256 * 128 + 4 * sum(32 - 2 * j for j in range(16))
+    assert hplan.dq_from_ds and hplan.host.tolist()[PF["DS_SLOTS"]] == hslots and hslots * 32 * 16384 <= cap
