@@ -34,6 +34,11 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4_m16;
 typedef int i32x4_m16 __attribute__((ext_vector_type(4)));
 // bytes per query head per dS slot: the 64-key dK/dV tile x 64 queries
 constexpr int m16_ds_head_bytes(int d) { return m16_keys(d) * kDkdvQ * 2; }
+// forward waves per workgroup. head_dim 256 runs 8 waves of 16 queries: about
+// 200 registers, so two waves share a SIMD, and LDS returns operands to each
+// wave at its own rate (one wave of 32 queries needed 342 registers and ran
+// alone). head_dim 64 runs 4 waves of 32 queries (162 registers).
+constexpr int m16_fwd_waves(int d) { return d == 256 ? 8 : kM16Waves; }
 
 __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -103,13 +108,14 @@ __device__ __forceinline__ bf16x8 col_operand(const char* tile, int r0, int c0, 
 // swizzled LDS tile at `lds_tile`: this wave's BPW 1 KiB blocks. Lane l of
 // block b lands at physical chunk l % NC of tile row b*RPB + l/NC, so it
 // fetches the logical chunk that swizzles there.
-template <int kD>
+template <int kD, int kWaves = kM16Waves>
 __device__ __forceinline__ void copy_tile(const char* src, uint32_t stride, int len, uint32_t lds_tile, int wave,
                                           int lane) {
   using T = Geo<kD>;
+  constexpr int kBPW = T::TB / 1024 / kWaves;  // DMA blocks per wave
 #pragma unroll
-  for (int j = 0; j < T::BPW; j++) {
-    const int b = wave * T::BPW + j;
+  for (int j = 0; j < kBPW; j++) {
+    const int b = wave * kBPW + j;
     const int row = b * T::RPB + lane / T::NC;
     const int chunk = (lane % T::NC) ^ T::swz(row);
     const uint32_t voff = static_cast<uint32_t>(min(row, len - 1)) * stride + 16u * chunk;
@@ -140,9 +146,10 @@ __device__ __forceinline__ float xsum16(float x) {
 constexpr float kSlack16 = 8.f;  // lazy-rescale slack in log2 units (as the head_dim-128 forward)
 
 // ---------------------------------------------------------------------------
-// Forward. Wave w: query head qh0 + w % hpw, tokens tw0 .. tw0 + 31 as two
-// 16-query sub-blocks qs. Per 64-key tile: S^T (4 blocks of 16 keys x 16
-// queries per sub-block) = K Q^T with K rows from LDS (A) and Q in registers
+// Forward. Wave w: query head qh0 + w % hpw, tokens tw0 .. tw0 + 16 kQS - 1
+// as kQS 16-query sub-blocks qs (two at head_dim 64, one at 256). Per 64-key
+// tile: S^T (4 blocks of 16 keys x 16 queries per sub-block) = K Q^T with K
+// rows from LDS (A) and Q in registers
 // (B); online softmax in registers (lane l holds 16 keys of query l % 16; the
 // other 48 keys of the tile sit in lanes l ^ 16, l ^ 32, l ^ 48); then
 // O^T += V^T P^T with V^T read transposed from LDS (A) and P^T from registers.
@@ -150,7 +157,7 @@ constexpr float kSlack16 = 8.f;  // lazy-rescale slack in log2 units (as the hea
 // packed (the packed instance folds every row stride to a constant).
 // ---------------------------------------------------------------------------
 template <int kD, bool kRunList, bool kStrided>
-__global__ __launch_bounds__(256) void m16_fwd(KernelArgs a) {
+__global__ __launch_bounds__(64 * m16_fwd_waves(kD)) void m16_fwd(KernelArgs a) {
   using T = Geo<kD>;
   const int32_t* item = a.plan + a.off_fwd + 4 * blockIdx.x;
   const int leaf = item[0];
@@ -160,10 +167,14 @@ __global__ __launch_bounds__(256) void m16_fwd(KernelArgs a) {
   const int row0 = cu[leaf], len = cu[leaf + 1] - cu[leaf];
 
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // kFW waves of kQS 16-query sub-blocks each (the planner's work item is
+  // kM16Waves x kM16Tokens query rows either way)
+  constexpr int kFW = m16_fwd_waves(kD), kQS = kFW * 16 == kM16Waves * kM16Tokens ? 1 : 2, kTokW = 16 * kQS;
+  static_assert(kFW * kTokW == kM16Waves * kM16Tokens, "a workgroup covers the planner's work item");
   const int hpw = a.hpw;
   const int head = qh0 + wave % hpw;
-  const int tw0 = tok0 + kM16Tokens * (wave / hpw);
-  const int tpw = kM16Tokens * (kM16Waves / hpw);
+  const int tw0 = tok0 + kTokW * (wave / hpw);
+  const int tpw = kTokW * (kFW / hpw);
   const int suffix_keys = min(len, tok0 + tpw);
   const int i16 = lane & 15, g = lane >> 4;
 
@@ -191,29 +202,34 @@ __global__ __launch_bounds__(256) void m16_fwd(KernelArgs a) {
   TileLoc tl_c = cursor_tile(cc);
   Cursor mc = cursor_begin(seg);  // the tile being computed
   TileLoc tl = cursor_tile(mc);
-  copy_tile<kD>(kv_src(tl_c, true), kv_rb(tl_c, true), tl_c.len, lds0, wave, lane);
-  copy_tile<kD>(kv_src(tl_c, false), kv_rb(tl_c, false), tl_c.len, lds0 + 2 * T::TB, wave, lane);
+  copy_tile<kD, kFW>(kv_src(tl_c, true), kv_rb(tl_c, true), tl_c.len, lds0, wave, lane);
+  copy_tile<kD, kFW>(kv_src(tl_c, false), kv_rb(tl_c, false), tl_c.len, lds0 + 2 * T::TB, wave, lane);
 
   // Q of the lane's query l % 16 of each sub-block: the B operand of S^T
-  bf16x8 qv[2][T::NS];
+  bf16x8 qv[kQS][T::NS];
 #pragma unroll
-  for (int qs = 0; qs < 2; qs++) {
+  for (int qs = 0; qs < kQS; qs++) {
     const int t = min(tw0 + 16 * qs + i16, len - 1);
     const bf16* qp = static_cast<const bf16*>(a.q) + static_cast<int64_t>(row0 + t) * q_rs + head * kD + 8 * g;
 #pragma unroll
     for (int s = 0; s < T::NS; s++) qv[qs][s] = *reinterpret_cast<const bf16x8*>(qp + 32 * s);
   }
-  f32x4 o[2][T::ND];
+  f32x4 o[kQS][T::ND];
 #pragma unroll
-  for (int qs = 0; qs < 2; qs++)
+  for (int qs = 0; qs < kQS; qs++)
 #pragma unroll
     for (int db = 0; db < T::ND; db++) o[qs][db] = f32x4{};
-  float m[2] = {-1e30f, -1e30f}, l[2] = {0.f, 0.f};  // running max (raw score units), lane-partial sum
+  float m[kQS], l[kQS];  // running max (raw score units), lane-partial sum
+#pragma unroll
+  for (int qs = 0; qs < kQS; qs++) {
+    m[qs] = -1e30f;
+    l[qs] = 0.f;
+  }
   const float c2 = a.scale * kLog2e;
   const float slack = kSlack16 / c2;
 
 #pragma unroll
-  for (int qs = 0; qs < 2; qs++)
+  for (int qs = 0; qs < kQS; qs++)
 #pragma unroll
     for (int s = 0; s < T::NS; s++) settle(qv[qs][s]);
   wait_dma();
@@ -224,19 +240,19 @@ __global__ __launch_bounds__(256) void m16_fwd(KernelArgs a) {
     if (j + 1 < ntiles) {  // copy tile j+1 into the other buffer (read by tile j-1, released by the last barrier)
       cursor_next(seg, cc);
       tl_c = cursor_tile(cc);
-      copy_tile<kD>(kv_src(tl_c, true), kv_rb(tl_c, true), tl_c.len, lds0 + (1 - buf) * T::TB, wave, lane);
-      copy_tile<kD>(kv_src(tl_c, false), kv_rb(tl_c, false), tl_c.len, lds0 + (3 - buf) * T::TB, wave, lane);
+      copy_tile<kD, kFW>(kv_src(tl_c, true), kv_rb(tl_c, true), tl_c.len, lds0 + (1 - buf) * T::TB, wave, lane);
+      copy_tile<kD, kFW>(kv_src(tl_c, false), kv_rb(tl_c, false), tl_c.len, lds0 + (3 - buf) * T::TB, wave, lane);
     }
     const char* kt = smem + buf * T::TB;
     const char* vt = smem + (2 + buf) * T::TB;
 
     // mask (register r of key block b holds key 32 (b/2) + 8 g + 4 (b%2) + r of
     // the tile), online softmax against the running max, P packed for P V
-    auto softmax = [&](f32x4 (&sv)[2][4], bf16x8 (&pb)[2][2]) __attribute__((always_inline)) {
+    auto softmax = [&](f32x4 (&sv)[kQS][4], bf16x8 (&pb)[kQS][2]) __attribute__((always_inline)) {
       const bool partial = tl.len < kTileRows || (tl.suffix && tl.pos0 + kTileRows - 1 > tw0);
       if (partial) {
 #pragma unroll
-        for (int qs = 0; qs < 2; qs++) {
+        for (int qs = 0; qs < kQS; qs++) {
           const int t = tw0 + 16 * qs + i16;
           int lim = tl.len - 1;
           if (tl.suffix) lim = min(lim, t - tl.pos0);
@@ -250,7 +266,7 @@ __global__ __launch_bounds__(256) void m16_fwd(KernelArgs a) {
         }
       }
 #pragma unroll
-      for (int qs = 0; qs < 2; qs++) {
+      for (int qs = 0; qs < kQS; qs++) {
         float mt = sv[qs][0][0];
 #pragma unroll
         for (int b = 0; b < 4; b++)
@@ -307,24 +323,24 @@ __global__ __launch_bounds__(256) void m16_fwd(KernelArgs a) {
       }
     };
     static_for<kRead>([&](auto ic) { read_slot(ic); });
-    f32x4 sa[2][4];
+    f32x4 sa[kQS][4];
 #pragma unroll
-    for (int qs = 0; qs < 2; qs++)
+    for (int qs = 0; qs < kQS; qs++)
 #pragma unroll
       for (int b = 0; b < 4; b++) sa[qs][b] = f32x4{};
-    bf16x8 pb[2][2];
+    bf16x8 pb[kQS][2];
     static_for<kSlots>([&](auto ic) {
       constexpr int i = decltype(ic)::value;
       if constexpr (i + kRead < kSlots) read_slot(std::integral_constant<int, i + kRead>{});
       if constexpr (i < kS) {
         constexpr int b = i % 4, s = i / 4;
 #pragma unroll
-        for (int qs = 0; qs < 2; qs++) sa[qs][b] = mfma16(ring[i % kRing], qv[qs][s], sa[qs][b]);
+        for (int qs = 0; qs < kQS; qs++) sa[qs][b] = mfma16(ring[i % kRing], qv[qs][s], sa[qs][b]);
         if constexpr (i == kS - 1) softmax(sa, pb);
       } else {
         constexpr int k = i - kS, db = k / 2, t = k % 2;
 #pragma unroll
-        for (int qs = 0; qs < 2; qs++) o[qs][db] = mfma16(ring[i % kRing], pb[qs][t], o[qs][db]);
+        for (int qs = 0; qs < kQS; qs++) o[qs][db] = mfma16(ring[i % kRing], pb[qs][t], o[qs][db]);
       }
       __builtin_amdgcn_sched_barrier(0);
     });
@@ -338,7 +354,7 @@ __global__ __launch_bounds__(256) void m16_fwd(KernelArgs a) {
 
   // O^T register r of block db: head dim 16 db + 4 g + r of query l % 16
 #pragma unroll
-  for (int qs = 0; qs < 2; qs++) {
+  for (int qs = 0; qs < kQS; qs++) {
     const float lt = xsum16(l[qs]);
     const int t = tw0 + 16 * qs + i16;
     if (tw0 + 16 * qs >= len || t >= len) continue;
@@ -1155,9 +1171,9 @@ bool strided_rows(const KernelArgs& a) {
 template <int kD, bool kRunList>
 void launch_fwd_runs(const KernelArgs& a, hipStream_t s) {
   if (strided_rows<kD>(a))
-    hipLaunchKernelGGL((m16_fwd<kD, kRunList, true>), dim3(a.n_items), dim3(64 * kM16Waves), 0, s, a);
+    hipLaunchKernelGGL((m16_fwd<kD, kRunList, true>), dim3(a.n_items), dim3(64 * m16_fwd_waves(kD)), 0, s, a);
   else
-    hipLaunchKernelGGL((m16_fwd<kD, kRunList, false>), dim3(a.n_items), dim3(64 * kM16Waves), 0, s, a);
+    hipLaunchKernelGGL((m16_fwd<kD, kRunList, false>), dim3(a.n_items), dim3(64 * m16_fwd_waves(kD)), 0, s, a);
 }
 
 template <int kD>
