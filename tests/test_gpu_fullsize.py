@@ -4,8 +4,10 @@ The kernel runs on the whole workload (every head, every sibling); the fp32
 oracle runs on the GPU for KV-head groups whose outputs and gradients depend
 on that group alone, so the comparison is exact for them: out, lse and dq of
 the group's query heads, dk/dv and the sibling-summed prefix dk/dv of its KV
-head. The Qwen3-4B shape checks KV heads 0, 5 and 7 (the first and last
-query-head groups, and one between); the other configurations KV head 5.
+head. The Qwen3-4B, long-session and ragged shapes check KV heads 0, 5 and 7
+(the first and last query-head groups, and one between; the latter two run
+the dQ kernel that recomputes the scores, their dS store being over its
+budget); the turn tree KV head 5.
 """
 
 from __future__ import annotations
@@ -91,7 +93,7 @@ def _compare_group(meta, hq, hkv, kvh, scale, inputs, out, lse, grads, device):
 
 @pytest.mark.parametrize("name", ["qwen3_4b", "long_session", "ragged_varlen", "turn_tree_depth3"])
 def test_full_size_config_matches_oracle_on_head_groups(name, cuda_device):
-    kvhs = (0, KVH, HKV - 1) if name == "qwen3_4b" else (KVH,)
+    kvhs = (KVH,) if name == "turn_tree_depth3" else (0, KVH, HKV - 1)
     _check_head_group(name, _configs()[name], HQ, HKV, D, kvhs, cuda_device)
 
 

@@ -12,7 +12,11 @@ divides 8. The head pairs below cover those branches:
   (32, 4)  G=8: 8 heads per workgroup (32 tokens), a KV head on two XCDs
   (28, 4)  G=7: 1 head per workgroup (256 tokens), one-head dK/dV stages
 
-each on a ragged shared-prefix case and on a depth-3 tree."""
+each on a ragged shared-prefix case and on a depth-3 tree, at head_dim 128
+(32x32x16 MFMA kernels) and 256 (16x16x32), and with both dQ plans: the
+default one that reads the dS store the dK/dV kernel writes, and the one
+that recomputes the scores (recompute_dq=True; the plan the long-session
+and ragged workloads fall back to when their store exceeds its budget)."""
 
 from __future__ import annotations
 
@@ -49,19 +53,22 @@ def _metas():
     }
 
 
+@pytest.mark.parametrize("recompute_dq", [False, True], ids=["ds_store", "recompute"])
+@pytest.mark.parametrize("d", [128, 256])
 @pytest.mark.parametrize("case", ["ragged", "depth3"])
 @pytest.mark.parametrize("hq,hkv", HEADS)
-def test_every_head_matches_oracle(hq, hkv, case, cuda_device):
+def test_every_head_matches_oracle(hq, hkv, case, d, recompute_dq, cuda_device):
     from bridge_amd import TPRPrefixAttention
     meta = _metas()[case]
-    d = 128
     scale = 1.0 / math.sqrt(d)
-    plan = meta.plan(hq, hkv, d, torch.bfloat16, cuda_device)
-    print(f"[gqa {case}] hq={hq} hkv={hkv} tq={meta.total_q} tp={meta.total_prefix} path={plan.path}", flush=True)
+    plan = meta.plan(hq, hkv, d, torch.bfloat16, cuda_device, recompute_dq=recompute_dq)
+    print(f"[gqa {case}] hq={hq} hkv={hkv} d={d} recompute_dq={recompute_dq} tq={meta.total_q} "
+          f"tp={meta.total_prefix} path={plan.path} shape={plan.mfma_shape} dq_from_ds={plan.dq_from_ds}", flush=True)
     assert plan.path == "mfma"
+    assert plan.dq_from_ds == (not recompute_dq)
     q, k, v, pk, pv, dout = make_inputs(meta, hq, hkv, d, torch.bfloat16, seed=7 * hq + hkv, device=cuda_device)
     tensors = [t.clone().requires_grad_(True) for t in (q, k, v, pk, pv)]
-    out, lse = TPRPrefixAttention.apply(*tensors, meta, scale)
+    out, lse = TPRPrefixAttention.apply(*tensors, meta, scale, None, recompute_dq)
     out.backward(dout)
     torch.cuda.synchronize()
     grads = [t.grad for t in tensors]
