@@ -347,7 +347,10 @@ def main() -> int:
                              "qwen3-4b-1sibling", "qwen3-4b-noprefix"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--recompute-dq", action="store_true",
-                    help="use the plan without a dS store (head_dim 128: dQ recomputes S and dP; small workspace)")
+                    help="use the plan without a dS store (dQ recomputes S and dP; small workspace); "
+                         "the same as --ds-store-budget 0")
+    ap.add_argument("--ds-store-budget", type=int, default=None, metavar="BYTES",
+                    help="bytes the backward's dS store may take (default: the library's, 8 GiB)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="before the timed steps, run one plain device copy of MIB MiB (read MIB, write MIB): "
                          "the calibration dispatch for rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -374,6 +377,7 @@ def main() -> int:
         return tree_launch_bench(args)
 
     from bridge_amd import _lib
+    from bridge_amd.meta import DS_STORE_DEFAULT_BYTES
     from bridge_amd.prefix_attention import prefix_attention_backward, prefix_attention_forward
 
     device = torch.device("cuda", 0)
@@ -387,7 +391,8 @@ def main() -> int:
     pk = torch.randn(tp, hkv, d, device=device, generator=gen).to(dtype)
     pv = torch.randn(tp, hkv, d, device=device, generator=gen).to(dtype)
     dout = torch.randn(tq, hq, d, device=device, generator=gen).to(dtype)
-    plan = meta.plan(hq, hkv, d, dtype, device, recompute_dq=args.recompute_dq)
+    budget = 0 if args.recompute_dq else args.ds_store_budget
+    plan = meta.plan(hq, hkv, d, dtype, device, ds_store_budget=budget)
 
     buffers = {"dq": torch.empty_like(q), "dk": torch.empty_like(k), "dv": torch.empty_like(v),
                "dprefix_k": torch.empty_like(pk), "dprefix_v": torch.empty_like(pv),
@@ -409,7 +414,7 @@ def main() -> int:
                 out, lse = prefix_attention_forward(q, k, v, pk, pv, meta, scale)
             else:
                 prefix_attention_backward(q, k, v, pk, pv, out, lse, dout, meta, scale, phases=ph, buffers=buffers,
-                                          recompute_dq=args.recompute_dq)
+                                          ds_store_budget=budget)
         if events:
             events[len(phases)].record(stream)
 
@@ -426,12 +431,14 @@ def main() -> int:
 
     events = [[torch.cuda.Event(enable_timing=True) for _ in range(len(phases) + 1)] for _ in range(args.steps)]
     torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats(device)
     t0 = time.perf_counter()
     for i in range(args.steps):
         step(events[i])
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_per_step = wall * 1e3 / args.steps
+    peak_bytes = torch.cuda.max_memory_allocated(device)  # of the timed steps: inputs, outputs, workspace
 
     def avg(a, b):
         return statistics.mean(e[a].elapsed_time(e[b]) for e in events)
@@ -482,6 +489,8 @@ def main() -> int:
             "fwd_bwd_flop": total_flops,
             "dq": "from the dS store" if plan.dq_from_ds else "recomputed",
             "workspace_bytes": plan.workspace_bytes,
+            "ds_store_budget_bytes": DS_STORE_DEFAULT_BYTES if budget is None else budget,
+            "peak_memory_bytes": peak_bytes,
         },
         "fraction_of_peak": round(value / peak, 4),
         "fwd_tflops": round(2.0 * unit / (fwd_ms * 1e-3) / 1e12, 2),

@@ -12,7 +12,7 @@ import threading
 
 LIB_NAME = "libtpr_attn.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 TPR_OK = 0
 TPR_ERR_INVALID_ARGUMENT = 1
@@ -24,6 +24,8 @@ TPR_DTYPE_BF16 = 0
 TPR_DTYPE_FP32 = 1
 
 TPR_PLAN_RECOMPUTE_DQ = 1
+TPR_DS_STORE_DEFAULT = -1                 # TprTreeDesc.ds_store_max_bytes: the library's default budget
+TPR_DS_STORE_DEFAULT_BYTES = 8 << 30      # ... which is 8 GiB
 
 EXPORTED_SYMBOLS = (
     "tpr_attn_abi_version",
@@ -61,6 +63,7 @@ class TprTreeDesc(ctypes.Structure):
         ("cu_seqlens_q", _p),
         ("node_offsets", _p),
         ("leaf_ancestors", _p),
+        ("ds_store_max_bytes", ctypes.c_int64),
     ]
 
 

@@ -37,7 +37,7 @@ from typing import Mapping, Optional, Sequence, Tuple
 
 import torch
 
-from .meta import TPRPrefixMeta
+from .meta import TPRPrefixMeta, ds_store_budget_bytes
 from .prefix_attention import TPRPrefixAttention
 
 __all__ = ["TPRKernelBackend"]
@@ -77,12 +77,16 @@ class TPRKernelBackend:
     ``prefix_key_values``: ``{layer_number: (K, V)}``, K and V ``[P, 1, Hkv,
     D]`` (empty mapping when P = 0); ``suffix_lengths``: the token counts of
     the sibling leaves whose tokens are packed, in this order, into each
-    ``attention`` call.
+    ``attention`` call. ``ds_store_budget``: bytes the backward's dS store
+    may take per layer call (``TPRPrefixAttention``; None = the library
+    default of 8 GiB, 0 = none). The store is transient -- allocated by each
+    layer's backward and released after it.
     """
 
     def __init__(self, prefix_key_values: Mapping[int, KVPair], suffix_lengths: Sequence[int], *,
                  prefix_length: Optional[int] = None,
-                 prefix_grad_accumulators: Optional[Mapping[int, KVPair]] = None):
+                 prefix_grad_accumulators: Optional[Mapping[int, KVPair]] = None,
+                 ds_store_budget: Optional[int] = None):
         lengths = tuple(suffix_lengths)
         if not lengths or any(not isinstance(s, int) or isinstance(s, bool) or s <= 0 for s in lengths):
             raise ValueError(f"suffix_lengths must be positive integers, got {suffix_lengths!r}")
@@ -107,13 +111,16 @@ class TPRKernelBackend:
         self._prefix_length = prefix_length
         self._lengths = lengths
         self._meta = TPRPrefixMeta.shared_prefix(prefix_length, lengths)
+        self._ds_store_budget = ds_store_budget_bytes(ds_store_budget)
 
     @classmethod
-    def from_stack(cls, stack, suffix_lengths: Sequence[int]) -> "TPRKernelBackend":
+    def from_stack(cls, stack, suffix_lengths: Sequence[int], *,
+                   ds_store_budget: Optional[int] = None) -> "TPRKernelBackend":
         """The siblings under the top of a ``PrefixKVStack``: prefix = the stack's
         path (views), prefix gradient added into the stack's fp32 rows."""
         return cls(stack.build_past_key_values(), suffix_lengths, prefix_length=stack.prefix_length,
-                   prefix_grad_accumulators=stack.past_gradient_accumulators() if stack.prefix_length else None)
+                   prefix_grad_accumulators=stack.past_gradient_accumulators() if stack.prefix_length else None,
+                   ds_store_budget=ds_store_budget)
 
     # -- the protocol ---------------------------------------------------------
     @property
@@ -157,7 +164,8 @@ class TPRKernelBackend:
         if self._accumulators is not None and self._prefix_length:
             accumulators = self._accumulators[layer_number]
         out, _ = TPRPrefixAttention.apply(query[:, 0], new_key[:, 0], new_value[:, 0], past_key[:, 0],
-                                          past_value[:, 0], self._meta, softmax_scale, accumulators)
+                                          past_value[:, 0], self._meta, softmax_scale, accumulators, False,
+                                          self._ds_store_budget)
         return out.reshape(query.shape[0], 1, query.shape[2] * query.shape[3])
 
     # -- packing helpers --------------------------------------------------------

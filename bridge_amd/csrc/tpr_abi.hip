@@ -280,7 +280,8 @@ int bwd_phases(const TprBwdParams* p, int phases, void* stream, void* workspace,
   a.ws = a.stat_ws + stat_floats(ph);
   a.ds = ds_bytes(ph) ? static_cast<char*>(workspace) + ws_fp32_bytes(ph) : nullptr;
   a.off_ds = ph[PF_OFF_DS];
-  a.off_ds_tiles = ph[PF_OFF_DS] + ph[PF_NUM_NODES] + ph[PF_NUM_LEAVES] + 1;
+  a.off_ds_first = ph[PF_OFF_DS] + ph[PF_NUM_NODES] + ph[PF_NUM_LEAVES];
+  a.ds_slots = ph[PF_DS_SLOTS];
   a.num_nodes = ph[PF_NUM_NODES];
   const bool fp32 = ph[PF_DTYPE] == TPR_DTYPE_FP32;
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -323,13 +324,24 @@ static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
 
-int scratch_for_current_device(void** out) {
+// The lookup may load the library's code object on the device, which a
+// stream capture must not see: the first call on a device has to be made
+// outside capture, and a capturing stream that finds no address yet is
+// refused with a message saying so.
+int scratch_for_current_device(hipStream_t stream, void** out) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0)
     return fail(TPR_ERR_LAUNCH, "hipGetDevice failed: %s", hipGetErrorString(hipGetLastError()));
   if (dev >= kMaxDevices) return fail(TPR_ERR_UNSUPPORTED, "device %d is beyond the %d this library tracks", dev, kMaxDevices);
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &capture) != hipSuccess)
+      return fail(TPR_ERR_LAUNCH, "hipStreamIsCapturing failed: %s", hipGetErrorString(hipGetLastError()));
+    if (capture != hipStreamCaptureStatusNone)
+      return fail(TPR_ERR_INVALID_ARGUMENT,
+                  "the first tpr_attn_bwd_noalloc call on device %d is being captured; make one call on that device "
+                  "outside stream capture first (it looks up the static scratch's address)", dev);
     void* ptr = nullptr;
     const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !ptr)
@@ -356,7 +368,7 @@ extern "C" int tpr_attn_bwd_noalloc(const TprBwdParams* p, void* stream) {
                   "caller-allocated workspace", need, kScratchBytes);
   }
   void* ws = nullptr;
-  int rc = scratch_for_current_device(&ws);
+  int rc = scratch_for_current_device(static_cast<hipStream_t>(stream), &ws);
   if (rc) return rc;
   return bwd_phases(p, TPR_BWD_DELTA | TPR_BWD_DKDV | TPR_BWD_DQ, stream, ws, kScratchBytes);
 }

@@ -9,7 +9,7 @@
 namespace tpr {
 
 constexpr int32_t kPlanMagic = 0x31525054;  // "TPR1"
-constexpr int32_t kPlanVersion = 3;
+constexpr int32_t kPlanVersion = 4;
 
 // Header word indices.
 enum PlanField : int {
@@ -45,9 +45,11 @@ enum PlanField : int {
                      // ancestor nodes root first, nodes adjacent in prefix_k/v merged, empty
                      // nodes dropped; {0, 0} pads a leaf with fewer runs
   PF_MAX_RUNS,       // most key runs of any leaf
-  PF_DS_SLOTS,       // dS slots of the head_dim-128 backward (0: dQ recomputes the scores)
-  PF_OFF_DS,         // dS tile table: [M + N + 1] first tile of each segment (nodes, then leaf
-                     // suffixes), then [tiles][2] = {first slot, first query block}
+  PF_DS_SLOTS,       // dS slots of the head_dim-128 / 256 backward (0: dQ recomputes the scores)
+  PF_OFF_DS,         // dS slot table: [M + N] tiles ahead of each segment (nodes, then leaf
+                     // suffixes) in the dQ walk of a query block below it, then
+                     // [n_qblk + 1] first slot of each query block; slot of (segment, tile t,
+                     // block b) = first[b] + base[segment] + t
   PF_HEADER_WORDS = 40
 };
 
@@ -108,9 +110,11 @@ constexpr int kPlanCus = 256;         // compute units the dK/dV work is balance
 // per query head, the tile x 64 block as four wave blocks in the dK/dV
 // kernel's register order: at head_dim 128 a 128-key tile of 4 KiB wave
 // blocks (32 keys each), at head_dim 256 a 64-key tile of 2 KiB wave blocks
-// (16 keys each).
+// (16 keys each). The store is [KV head][slot][query head of the group]
+// blocks (ds_offset), slots numbered query-block-major in the dQ kernel's key
+// order (PF_OFF_DS), so each dQ work item reads one contiguous stretch. A plan has a store only when it fits the caller's budget
+// (TprTreeDesc.ds_store_max_bytes).
 constexpr int kDsHeadBytes = kDkdvKeys * kDkdvQ * 2;          // 16 KiB per query head per slot (head_dim 128)
-constexpr int64_t kDsMaxBytes = int64_t{32} << 30;           // larger dS areas fall back to recomputation
 // MFMA backward workspace, ahead of the partial slots: two constants (+inf,
 // 0) that rows past a query block's end are copied from, then lse * log2e per
 // (query head, token) in the lse layout, then -delta in the same layout.

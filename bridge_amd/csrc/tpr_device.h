@@ -55,11 +55,14 @@ struct KernelArgs {
   // unless the caller reads them out of a wider buffer); every other tensor
   // is packed
   int64_t q_rs, k_rs, v_rs;
-  // dS store of the head_dim-128 backward (null: dQ recomputes the scores):
-  // slot s, query head h at byte (s * hq + h) * kDsHeadBytes; the plan's tile
-  // table at off_ds, segment ids nodes first, then num_nodes + leaf
+  // dS store of the head_dim-128 / 256 backward (null: dQ recomputes the
+  // scores): slot s of KV head g, query head g * group + e at block
+  // (g * ds_slots + s) * group + e (ds_head_bytes each); the plan's slot
+  // table: tiles ahead of each segment at off_ds (nodes first, then
+  // num_nodes + leaf), first slot of each query block at off_ds_first
   void* ds;
-  int32_t off_ds, off_ds_tiles, num_nodes;
+  int32_t off_ds, off_ds_first, num_nodes;
+  int64_t ds_slots;
 };
 
 __device__ __forceinline__ float to_f32(float x) { return x; }

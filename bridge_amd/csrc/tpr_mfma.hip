@@ -951,11 +951,15 @@ __global__ __launch_bounds__(512) void mfma_dqs(KernelArgs a) {
   }
 
   // Key stream cursor (uniform): ancestor index cd (max_depth = the suffix,
-  // past it = the end), first row, length, key limit, first dS tile of the
-  // segment, tile key, half. Plan words inside the stream are scalar loads.
+  // past it = the end), first row, length, key limit, tile key, half, and the
+  // tile's position in the stream. Plan words inside the stream are scalar
+  // loads. The dS slots of the wave's query block are numbered in this same
+  // order from the block's first slot, so slot = first + cpos; at
+  // [KV head][slot][query head of the group] the wave's blocks follow each
+  // other tile by tile.
   const int depth = a.max_depth;
   const int32_t* anc = a.plan + a.off_anc + static_cast<int64_t>(leaf) * depth;
-  int cd = -1, crow = 0, clen = 0, clim = 0, ctile = 0, ckey = 0, chalf = 0;
+  int cd = -1, crow = 0, clen = 0, clim = 0, ckey = 0, chalf = 0, cpos = 0;
   auto next_segment = [&]() {
     for (;;) {
       cd++;
@@ -966,7 +970,6 @@ __global__ __launch_bounds__(512) void mfma_dqs(KernelArgs a) {
           const int l = plan_word(no + nd + 1) - crow;
           if (l == 0) continue;
           clen = clim = l;
-          ctile = plan_word(a.plan + a.off_ds + nd);
           break;
         }
         cd = depth;  // -1 pads the list: the suffix is next
@@ -975,7 +978,6 @@ __global__ __launch_bounds__(512) void mfma_dqs(KernelArgs a) {
         crow = row0;
         clen = len;
         clim = suffix_keys;
-        ctile = plan_word(a.plan + a.off_ds + a.num_nodes + leaf);
       } else {
         clen = clim = 0;  // past the end
       }
@@ -989,9 +991,19 @@ __global__ __launch_bounds__(512) void mfma_dqs(KernelArgs a) {
     if (chalf == 2 || ckey + kTileRows * chalf >= clim) {
       chalf = 0;
       ckey += kDkdvKeys;
+      cpos++;
       if (ckey >= clim) next_segment();
     }
   };
+  // this wave's dS blocks: its query block's first slot, its head, its 32-query half
+  const char* ds_wave = nullptr;
+  if (wave_ok) {
+    const int first = plan_word(a.plan + a.off_ds_first + qb);
+    ds_wave = static_cast<const char*>(a.ds) +
+              ((static_cast<int64_t>(kvh) * a.ds_slots + first) * a.group + (head - kvh * a.group)) * kDsHeadBytes +
+              jq * 2048;
+  }
+  const int64_t ds_tile_bytes = static_cast<int64_t>(a.group) * kDsHeadBytes;  // one slot of the group
   // copy the current half into buffer b; returns its rows, and whether this
   // wave reads it (prefix halves: every wave; suffix halves: those not
   // entirely in the wave's future). A wave issues 2 copies for K and 4 for
@@ -1011,10 +1023,7 @@ __global__ __launch_bounds__(512) void mfma_dqs(KernelArgs a) {
                lds0 + b * kTileBytes + (2 * wave + j) * 1024);
     }
     if (vis) {
-      const int32_t* te = a.plan + a.off_ds_tiles + 2 * (ctile + ckey / kDkdvKeys);
-      const int slot = plan_word(te) + qb - plan_word(te + 1);
-      const char* src = static_cast<const char*>(a.ds) +
-                        (static_cast<int64_t>(slot) * a.hq + head) * kDsHeadBytes + 2 * chalf * 4096 + jq * 2048;
+      const char* src = ds_wave + cpos * ds_tile_bytes + 2 * chalf * 4096;
       dma_blocks4_nt(src, dsv[0], dsv[1], dsv[2], dsv[3], lds0 + kDsOff + (b * kFwdWaves + wave) * kDsWave);
     }
   };
@@ -1192,18 +1201,15 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
     // from the plan once, so the stage loop touches no plan memory
     if (tile > 0) __syncthreads();  // every wave is done with the previous tile's table
     const int nblk = qb_hi - qb_lo;
-    int ds_first = 0, ds_lo = 0;  // the tile's first dS slot and first query block
-    if constexpr (kStoreDs) {
-      const int32_t* seg_tiles = a.plan + a.off_ds;
-      const int32_t* te = a.plan + a.off_ds_tiles + 2 * (seg_tiles[prefix ? seg : a.num_nodes + seg] + key0 / kDkdvKeys);
-      ds_first = te[0];
-      ds_lo = te[1];
-    }
+    // the tile's dS slot in the numbering of query block qb: first[qb] + the
+    // tiles ahead of it in the dQ walk of any block below its segment
+    const int ds_ahead = kStoreDs ? a.plan[a.off_ds + (prefix ? seg : a.num_nodes + seg)] + key0 / kDkdvKeys : 0;
     for (int i = threadIdx.x; i < nblk; i += blockDim.x) {
       const int qb = first_last ? qb_lo + i : qb_hi - 1 - i;
       const int lf = qblk[2 * qb], tok = qblk[2 * qb + 1];
       const int r0 = cu[lf];
-      qtab[i] = int4{r0 + tok, tok, min(kTileRows, cu[lf + 1] - r0 - tok), kStoreDs ? ds_first + qb - ds_lo : 0};
+      qtab[i] = int4{r0 + tok, tok, min(kTileRows, cu[lf + 1] - r0 - tok),
+                     kStoreDs ? a.plan[a.off_ds_first + qb] + ds_ahead : 0};
     }
     __syncthreads();
 
@@ -1488,7 +1494,8 @@ __global__ __launch_bounds__(256) void mfma_dkdv(KernelArgs a) {
         // this stage's dS blocks: slot, heads kvh G + sub kHeads + hh, this wave's 32 keys
         const int slot = __builtin_amdgcn_readfirstlane(qtab[cur.blk].w);
         ds_stage = static_cast<char*>(a.ds) +
-                   (static_cast<int64_t>(slot) * a.hq + kvh * a.group + cur.sub * kHeads) * kDsHeadBytes + wave * 4096;
+                   ((static_cast<int64_t>(kvh) * a.ds_slots + slot) * a.group + cur.sub * kHeads) * kDsHeadBytes +
+                   wave * 4096;
       }
       const StageCursor nxt = advance(cur);
       if (sidx + 1 < nstage) issue(nxt, buf ^ 1);

@@ -672,10 +672,14 @@ __global__ __launch_bounds__(256) void m16_dqs(KernelArgs a) {
     }
   }
 
-  // key stream cursor (uniform; plan words through the scalar cache)
+  // key stream cursor (uniform; plan words through the scalar cache), with
+  // the tile's position in the stream: the dS slots of the wave's query block
+  // are numbered in this order from the block's first slot (slot = first +
+  // cpos), so at [KV head][slot][query head of the group] the wave's blocks
+  // follow each other tile by tile
   const int depth = a.max_depth;
   const int32_t* anc = a.plan + a.off_anc + static_cast<int64_t>(leaf) * depth;
-  int cd = -1, crow = 0, clen = 0, clim = 0, ctile = 0, ckey = 0;
+  int cd = -1, crow = 0, clen = 0, clim = 0, ckey = 0, cpos = 0;
   auto next_segment = [&]() {
     for (;;) {
       cd++;
@@ -686,7 +690,6 @@ __global__ __launch_bounds__(256) void m16_dqs(KernelArgs a) {
           const int l = plan_word(no + nd + 1) - crow;
           if (l == 0) continue;
           clen = clim = l;
-          ctile = plan_word(a.plan + a.off_ds + nd);
           break;
         }
         cd = depth;  // -1 pads the list: the suffix is next
@@ -695,7 +698,6 @@ __global__ __launch_bounds__(256) void m16_dqs(KernelArgs a) {
         crow = row0;
         clen = len;
         clim = suffix_keys;
-        ctile = plan_word(a.plan + a.off_ds + a.num_nodes + leaf);
       } else {
         clen = clim = 0;  // past the end
       }
@@ -705,8 +707,17 @@ __global__ __launch_bounds__(256) void m16_dqs(KernelArgs a) {
   };
   auto advance = [&]() {
     ckey += kKeys;
+    cpos++;
     if (ckey >= clim) next_segment();
   };
+  const char* ds_wave = nullptr;  // this wave's dS blocks: first slot of its query block, its head and half
+  if (wave_ok) {
+    const int first = plan_word(a.plan + a.off_ds_first + qb);
+    ds_wave = static_cast<const char*>(a.ds) +
+              ((static_cast<int64_t>(kvh) * a.ds_slots + first) * a.group + (head - kvh * a.group)) * kSlotHead +
+              jq * 1024;
+  }
+  const int64_t ds_tile_bytes = static_cast<int64_t>(a.group) * kSlotHead;  // one slot of the group
   // copy the current tile into buffer b (K: this wave's T::BPW blocks; dS: 4
   // blocks if the wave reads the tile -- prefix tiles: every wave; suffix
   // tiles: those not entirely in the wave's future)
@@ -718,10 +729,7 @@ __global__ __launch_bounds__(256) void m16_dqs(KernelArgs a) {
     copy_tile<kD>((suffix ? kbase : pkbase) + static_cast<int64_t>(crow + ckey) * rb, rb, rows, lds0 + b * T::TB,
                   wave, lane);
     if (vis) {
-      const int32_t* te = a.plan + a.off_ds_tiles + 2 * (ctile + ckey / kKeys);
-      const int slot = plan_word(te) + qb - plan_word(te + 1);
-      const char* src = static_cast<const char*>(a.ds) + (static_cast<int64_t>(slot) * a.hq + head) * kSlotHead +
-                        jq * 1024;
+      const char* src = ds_wave + cpos * ds_tile_bytes;
       dma_blocks4_nt(src, dsl, 2048 + dsl, 4096 + dsl, 6144 + dsl, lds0 + kDsOff + (b * kM16Waves + wave) * kDsWave);
     }
   };
@@ -875,18 +883,15 @@ __global__ __launch_bounds__(256) void m16_dkdv(KernelArgs a) {
     const bool wave_active = kw0 < seg_len;
 
     if (tile > 0) __syncthreads();  // every wave is done with the previous tile's table
-    int ds_first = 0, ds_lo = 0;  // the tile's first dS slot and first query block
-    if constexpr (kStoreDs) {
-      const int32_t* seg_tiles = a.plan + a.off_ds;
-      const int32_t* te = a.plan + a.off_ds_tiles + 2 * (seg_tiles[prefix ? seg : a.num_nodes + seg] + key0 / kKeys);
-      ds_first = te[0];
-      ds_lo = te[1];
-    }
+    // the tile's dS slot in the numbering of query block qb: first[qb] + the
+    // tiles ahead of it in the dQ walk of any block below its segment
+    const int ds_ahead = kStoreDs ? a.plan[a.off_ds + (prefix ? seg : a.num_nodes + seg)] + key0 / kKeys : 0;
     for (int i = threadIdx.x; i < qb_hi - qb_lo; i += blockDim.x) {
       const int qb = first_last ? qb_lo + i : qb_hi - 1 - i;
       const int lf = qblk[2 * qb], tok = qblk[2 * qb + 1];
       const int r0 = cu[lf];
-      qtab[i] = int4{r0 + tok, tok, min(kTileRows, cu[lf + 1] - r0 - tok), kStoreDs ? ds_first + qb - ds_lo : 0};
+      qtab[i] = int4{r0 + tok, tok, min(kTileRows, cu[lf + 1] - r0 - tok),
+                     kStoreDs ? a.plan[a.off_ds_first + qb] + ds_ahead : 0};
     }
     __syncthreads();
 
@@ -960,7 +965,7 @@ __global__ __launch_bounds__(256) void m16_dkdv(KernelArgs a) {
         if constexpr (kStoreDs) {
           const int slot = __builtin_amdgcn_readfirstlane(qtab[blk].w);
           ds_stage = static_cast<char*>(a.ds) +
-                     (static_cast<int64_t>(slot) * a.hq + kvh * group + sidx % group) * m16_ds_head_bytes(kD) +
+                     ((static_cast<int64_t>(kvh) * a.ds_slots + slot) * group + sidx % group) * m16_ds_head_bytes(kD) +
                      wave * (m16_ds_head_bytes(kD) / kM16Waves);
         }
         const char* qt = smem + buf * 2 * T::TB;

@@ -99,6 +99,9 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
     return fail(TPR_ERR_INVALID_ARGUMENT, "unknown dtype %d", t->dtype);
   if (t->flags & ~TPR_PLAN_RECOMPUTE_DQ)
     return fail(TPR_ERR_INVALID_ARGUMENT, "unknown plan flags 0x%x", static_cast<unsigned>(t->flags));
+  if (t->ds_store_max_bytes < 0 && t->ds_store_max_bytes != TPR_DS_STORE_DEFAULT)
+    return fail(TPR_ERR_INVALID_ARGUMENT, "ds_store_max_bytes must be 0, TPR_DS_STORE_DEFAULT or positive, got %lld",
+                static_cast<long long>(t->ds_store_max_bytes));
   if (!t->cu_seqlens_q || !t->node_offsets || (N * depth > 0 && !t->leaf_ancestors))
     return fail(TPR_ERR_INVALID_ARGUMENT, "tree metadata pointers must not be NULL");
 
@@ -334,36 +337,43 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
   std::vector<int32_t> dkdv_words = order_for_xcds(dkdv, Hkv, DK_WORDS, &n_dkdv);
 
   // ---- dS store (bf16 head_dim 128 and 256) -------------------------------------
-  // Every (128-key tile, query block) pair the dK/dV items stream gets one
-  // slot; a tile's query blocks are one contiguous range (a node's descendant
-  // leaves, or a leaf's blocks from the tile's first key on), so its slots
-  // are {first slot + (block - first block)}. Tiles are numbered per segment
-  // in key order, nodes first, then the leaf suffixes; the table gives each
-  // segment's first tile and each tile's {first slot, first block}.
+  // Every (key tile, query block) pair the dK/dV items stream gets one slot.
+  // Slots are numbered query-block-major, in the order the dQ kernel walks a
+  // block's keys: the leaf's ancestor nodes root first (each node's tiles in
+  // key order), then the leaf's suffix tiles up to the one holding the
+  // block's last token. So slot(segment, tile t, block b) = first[b] +
+  // base[segment] + t, where base[] counts the tiles ahead of a segment in
+  // that walk -- the same for every block below a node, since they share the
+  // path above it. The store is laid out [KV head][slot][query head of the
+  // group][tile x 64 block] (ds_head_bytes each), so a dQ work item -- one
+  // block of one KV head's group -- reads one contiguous stretch.
   std::vector<int32_t> ds_table;
   int64_t ds_slots = 0;
   const bool ds_path = path == PATH_MFMA || (path == PATH_MFMA16 && D == 256);
-  if (ds_path && !(t->flags & TPR_PLAN_RECOMPUTE_DQ)) {
-    std::vector<int32_t> first(static_cast<size_t>(M) + N + 1), tiles;
-    int32_t ntile = 0;
-    auto add = [&](int32_t lo, int32_t hi) {
-      tiles.push_back(static_cast<int32_t>(std::min<int64_t>(ds_slots, INT32_MAX)));
-      tiles.push_back(lo);
-      ds_slots += hi - lo;
-      ntile++;
-    };
-    for (int n = 0; n < M; n++) {
-      first[n] = ntile;
-      for (int k0 = 0; k0 < no[n + 1] - no[n]; k0 += KT) add(leaf_qblk[leaf_lo[n]], leaf_qblk[leaf_hi[n]]);
-    }
+  const int64_t ds_budget = t->ds_store_max_bytes == TPR_DS_STORE_DEFAULT ? TPR_DS_STORE_DEFAULT_BYTES
+                                                                          : t->ds_store_max_bytes;
+  if (ds_path && ds_budget > 0 && !(t->flags & TPR_PLAN_RECOMPUTE_DQ)) {
+    auto ntiles = [&](int64_t len) { return static_cast<int32_t>((len + KT - 1) / KT); };
+    std::vector<int32_t> base(static_cast<size_t>(M) + N, 0), first(static_cast<size_t>(n_qblk) + 1, 0);
     for (int s = 0; s < N; s++) {
-      first[M + s] = ntile;
-      for (int k0 = 0; k0 < cu[s + 1] - cu[s]; k0 += KT) add(leaf_qblk[s] + k0 / BQ, leaf_qblk[s + 1]);
+      int32_t ahead = 0;
+      for (int d = 0; d < depth; d++) {
+        const int n = anc[s * depth + d];
+        if (n < 0) break;
+        base[n] = ahead;  // the same from every leaf below n
+        ahead += ntiles(no[n + 1] - no[n]);
+      }
+      base[M + s] = ahead;
+      const int len = cu[s + 1] - cu[s];
+      for (int b = leaf_qblk[s]; b < leaf_qblk[s + 1]; b++) {
+        const int last = std::min(len, (b - leaf_qblk[s] + 1) * BQ) - 1;  // the block's last token
+        ds_slots += ahead + last / KT + 1;
+        first[b + 1] = static_cast<int32_t>(std::min<int64_t>(ds_slots, INT32_MAX));
+      }
     }
-    first[M + N] = ntile;
-    if (ds_slots > 0 && ds_slots < INT32_MAX && ds_slots * Hq * ds_head_bytes(path, D) <= kDsMaxBytes) {
-      ds_table = std::move(first);
-      ds_table.insert(ds_table.end(), tiles.begin(), tiles.end());
+    if (ds_slots > 0 && ds_slots < INT32_MAX && ds_slots * Hq * ds_head_bytes(path, D) <= ds_budget) {
+      ds_table = std::move(base);
+      ds_table.insert(ds_table.end(), first.begin(), first.end());
     } else {
       ds_slots = 0;
     }

@@ -35,6 +35,20 @@ _PF_N_DKDV = 21
 _PF_TOTAL_WORDS = 27
 _PF_DS_SLOTS = 30
 
+DS_STORE_DEFAULT_BYTES = 8 << 30  # the library's default dS store budget (TPR_DS_STORE_DEFAULT_BYTES)
+
+
+def ds_store_budget_bytes(ds_store_budget: Optional[int], recompute_dq: bool = False) -> Optional[int]:
+    """The dS store budget a plan is built with: None (the library default),
+    or a byte count >= 0 (0: no store)."""
+    if recompute_dq:
+        return 0
+    if ds_store_budget is None:
+        return None
+    if isinstance(ds_store_budget, bool) or not isinstance(ds_store_budget, int) or ds_store_budget < 0:
+        raise ValueError(f"ds_store_budget must be None or a non-negative integer, got {ds_store_budget!r}")
+    return ds_store_budget
+
 
 @dataclass(frozen=True)
 class LaunchPlan:
@@ -60,8 +74,8 @@ class LaunchPlan:
     @property
     def dq_from_ds(self) -> bool:
         """Whether the backward stores dS and computes dQ from it (bf16
-        head_dim 128 and 256 unless the plan was built with recompute_dq=True
-        or the store would exceed 32 GiB); the workspace then holds the store."""
+        head_dim 128 and 256 when the store fits the plan's dS store budget);
+        the workspace then holds the store."""
         return int(self.host[_PF_DS_SLOTS]) > 0
 
     @property
@@ -198,22 +212,28 @@ class TPRPrefixMeta:
 
     # ---- launch plan -------------------------------------------------------
     def plan(self, num_q_heads: int, num_kv_heads: int, head_dim: int, dtype: torch.dtype,
-             device: torch.device, *, recompute_dq: bool = False) -> LaunchPlan:
+             device: torch.device, *, recompute_dq: bool = False,
+             ds_store_budget: Optional[int] = None) -> LaunchPlan:
         """Build (once per configuration) the native launch plan and upload it.
 
-        ``recompute_dq``: the dQ kernel recomputes the scores instead of
-        reading a dS store (TPR_PLAN_RECOMPUTE_DQ): a backward workspace of a
-        few MB instead of 2 bytes per visible (query, key) pair and query head,
-        at the cost of a slower dQ (bf16 head_dim 128 and 256; the other paths
-        always recompute)."""
+        ``ds_store_budget``: bytes the backward's dS store may take (bf16
+        head_dim 128 and 256). With a store, the dK/dV kernel writes every dS
+        block, 2 bytes per visible (query, key) pair and query head, and the
+        dQ kernel computes dQ = scale dS K from them instead of recomputing S
+        and dP (one matrix product instead of three); without one the
+        workspace is a few MB. ``None``: the library default,
+        ``DS_STORE_DEFAULT_BYTES`` (8 GiB; the Qwen3-4B layer shape, prefix
+        4096 + 4 x 4096 at GQA 32/8, needs 6.5 GB); ``0``: no store.
+        ``recompute_dq=True`` is the same as ``ds_store_budget=0``."""
         if dtype == torch.bfloat16:
             code = _lib.TPR_DTYPE_BF16
         elif dtype == torch.float32:
             code = _lib.TPR_DTYPE_FP32
         else:
             raise ValueError(f"prefix attention supports torch.bfloat16 and torch.float32, got {dtype}")
-        flags = _lib.TPR_PLAN_RECOMPUTE_DQ if recompute_dq else 0
-        key = (num_q_heads, num_kv_heads, head_dim, code, str(device), flags)
+        budget = ds_store_budget_bytes(ds_store_budget, recompute_dq)
+        flags = 0
+        key = (num_q_heads, num_kv_heads, head_dim, code, str(device), budget)
         cached = self._plans.get(key)
         if cached is not None:
             return cached
@@ -225,7 +245,8 @@ class TPRPrefixMeta:
         an = (ctypes.c_int32 * max(1, len(anc)))(*anc) if anc else (ctypes.c_int32 * 1)(-1)
         desc = _lib.TprTreeDesc(self.num_leaves, self.num_nodes, depth, num_q_heads, num_kv_heads, head_dim,
                                 code, flags, ctypes.cast(cu, ctypes.c_void_p), ctypes.cast(no, ctypes.c_void_p),
-                                ctypes.cast(an, ctypes.c_void_p))
+                                ctypes.cast(an, ctypes.c_void_p),
+                                _lib.TPR_DS_STORE_DEFAULT if budget is None else budget)
         words = ctypes.c_int64(0)
         _lib.check(lib.tpr_attn_plan(ctypes.byref(desc), None, 0, ctypes.byref(words)), "tpr_attn_plan")
         host = torch.empty(int(words.value), dtype=torch.int32)

@@ -30,7 +30,7 @@ from typing import Optional, Tuple
 import torch
 
 from . import _lib
-from .meta import TPRPrefixMeta
+from .meta import TPRPrefixMeta, ds_store_budget_bytes
 
 __all__ = ["TPRPrefixAttention", "tpr_prefix_attention"]
 
@@ -165,16 +165,32 @@ def _check_accumulators(accumulators, prefix_k) -> Tuple[torch.Tensor, torch.Ten
     return accumulators[0], accumulators[1]
 
 
+def _workspace(meta, q, k, budget, ws):
+    """(plan, workspace) of the backward. A plan with a dS store whose
+    workspace cannot be allocated falls back to the plan without one (a few
+    MB), which gives the same gradients with a slower dQ."""
+    plan = meta.plan(q.shape[1], k.shape[1], q.shape[2], q.dtype, q.device, ds_store_budget=budget)
+    if ws is not None or not plan.workspace_bytes:
+        return plan, ws
+    try:
+        return plan, torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=q.device)
+    except torch.OutOfMemoryError:
+        if not plan.dq_from_ds:
+            raise
+    plan = meta.plan(q.shape[1], k.shape[1], q.shape[2], q.dtype, q.device, ds_store_budget=0)
+    ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=q.device) if plan.workspace_bytes else None
+    return plan, ws
+
+
 def _backward(q, k, v, prefix_k, prefix_v, out, lse, dout, meta, scale, *, phases=None, buffers=None,
-              prefix_grad_accumulators=None, recompute_dq=False):
+              prefix_grad_accumulators=None, ds_store_budget=None):
     """Enqueue the backward. ``buffers`` may supply preallocated dq, dk, dv,
     dprefix_k, dprefix_v and delta tensors; ``phases`` is a mask of
     _lib.TPR_BWD_* bits (default: all). With ``prefix_grad_accumulators`` (a
     pair of fp32 tensors shaped like prefix_k) the prefix gradients are added
     into that pair by the kernels (TPR_BWD_ACCUMULATE_PREFIX_F32), which is
-    also what is returned for them. ``recompute_dq`` selects the plan without
-    a dS store (TPRPrefixMeta.plan)."""
-    plan = meta.plan(q.shape[1], k.shape[1], q.shape[2], q.dtype, q.device, recompute_dq=recompute_dq)
+    also what is returned for them. ``ds_store_budget``: the plan's dS store
+    budget in bytes (TPRPrefixMeta.plan; None = the library default)."""
     b = dict(buffers or {})
     dq = b.get("dq") if b.get("dq") is not None else _empty(q)
     dk = b.get("dk") if b.get("dk") is not None else _empty(k)
@@ -194,9 +210,7 @@ def _backward(q, k, v, prefix_k, prefix_v, out, lse, dout, meta, scale, *, phase
             return dq, dk, dv, dpk, dpv
         return dq, dk, dv, dpk.zero_(), dpv.zero_()
     delta = b.get("delta") if b.get("delta") is not None else torch.empty_like(lse)
-    ws = b.get("workspace")
-    if ws is None and plan.workspace_bytes:
-        ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=q.device)
+    plan, ws = _workspace(meta, q, k, ds_store_budget, b.get("workspace"))
     lib = _lib.load()
     params = _lib.TprBwdParams(
         _lib.ABI_VERSION, flags, scale, 0.0,
@@ -211,20 +225,29 @@ def _backward(q, k, v, prefix_k, prefix_v, out, lse, dout, meta, scale, *, phase
 
 
 class TPRPrefixAttention(torch.autograd.Function):
-    """(q, k, v, prefix_k, prefix_v, meta, softmax_scale, prefix_grad_accumulators) -> (out, lse).
+    """(q, k, v, prefix_k, prefix_v, meta, softmax_scale, prefix_grad_accumulators,
+    recompute_dq, ds_store_budget) -> (out, lse).
 
     With ``prefix_grad_accumulators`` = (dK, dV), fp32 tensors shaped like
     prefix_k, the backward adds the prefix gradients into them (the relay of
     prefix_state.py:546-573, in fp32 and inside the kernel) and gives
     prefix_k / prefix_v no autograd gradient; they must then not require one.
-    ``recompute_dq``: the backward uses the plan without a dS store (a small
-    workspace, a slower dQ; see TPRPrefixMeta.plan).
+
+    Memory: the backward's workspace holds, besides a few MB of statistics,
+    the dS store when the plan has one -- 2 bytes per visible (query, key)
+    pair and query head, 6.5 GB at the Qwen3-4B layer shape (prefix 4096 +
+    4 x 4096, GQA 32/8) -- which makes dQ one matrix product instead of three.
+    ``ds_store_budget`` caps it in bytes: None = the library default (8 GiB),
+    0 = no store (``recompute_dq=True`` is the same). If the workspace of a
+    plan with a store cannot be allocated, the backward falls back to the plan
+    without one (same gradients, slower dQ).
     """
 
     @staticmethod
     def forward(ctx, q, k, v, prefix_k, prefix_v, meta, softmax_scale=None, prefix_grad_accumulators=None,
-                recompute_dq=False):
+                recompute_dq=False, ds_store_budget=None):
         scale = validate(q, k, v, prefix_k, prefix_v, meta, softmax_scale)
+        budget = ds_store_budget_bytes(ds_store_budget, recompute_dq)
         if prefix_grad_accumulators is not None:
             if prefix_k.requires_grad or prefix_v.requires_grad:
                 raise ValueError("prefix_k/prefix_v must not require grad when prefix_grad_accumulators is given")
@@ -235,7 +258,7 @@ class TPRPrefixAttention(torch.autograd.Function):
         ctx.meta = meta
         ctx.scale = scale
         ctx.accumulators = prefix_grad_accumulators
-        ctx.recompute_dq = bool(recompute_dq)
+        ctx.ds_store_budget = budget
         ctx.mark_non_differentiable(lse)
         return out, lse
 
@@ -246,17 +269,18 @@ class TPRPrefixAttention(torch.autograd.Function):
             dout = torch.zeros_like(out)
         dout = dout.contiguous()
         dq, dk, dv, dpk, dpv = _backward(q, k, v, prefix_k, prefix_v, out, lse, dout, ctx.meta, ctx.scale,
-                                         prefix_grad_accumulators=ctx.accumulators, recompute_dq=ctx.recompute_dq)
+                                         prefix_grad_accumulators=ctx.accumulators,
+                                         ds_store_budget=ctx.ds_store_budget)
         if ctx.accumulators is not None:
             dpk = dpv = None
-        return dq, dk, dv, dpk, dpv, None, None, None, None
+        return dq, dk, dv, dpk, dpv, None, None, None, None, None
 
 
 def tpr_prefix_attention(q, k, v, prefix_k, prefix_v, meta: TPRPrefixMeta, softmax_scale=None, *,
-                         prefix_grad_accumulators=None, recompute_dq=False):
+                         prefix_grad_accumulators=None, recompute_dq=False, ds_store_budget=None):
     """Functional form of TPRPrefixAttention; returns (out, lse)."""
     return TPRPrefixAttention.apply(q, k, v, prefix_k, prefix_v, meta, softmax_scale, prefix_grad_accumulators,
-                                    recompute_dq)
+                                    recompute_dq, ds_store_budget)
 
 
 def prefix_attention_forward(q, k, v, prefix_k, prefix_v, meta: TPRPrefixMeta, softmax_scale=None):
@@ -268,7 +292,7 @@ def prefix_attention_forward(q, k, v, prefix_k, prefix_v, meta: TPRPrefixMeta, s
 
 def prefix_attention_backward(q, k, v, prefix_k, prefix_v, out, lse, dout, meta: TPRPrefixMeta,
                               softmax_scale=None, *, phases=None, buffers=None, prefix_grad_accumulators=None,
-                              recompute_dq=False):
+                              recompute_dq=False, ds_store_budget=None):
     """Backward only: (dq, dk, dv, dprefix_k, dprefix_v) from saved out/lse.
 
     ``phases`` selects backward phases (mask of TPR_BWD_DELTA / _DKDV / _DQ,
@@ -278,9 +302,12 @@ def prefix_attention_backward(q, k, v, prefix_k, prefix_v, out, lse, dout, meta:
     ``delta`` scratch and the ``workspace``, keyed by name.
     ``prefix_grad_accumulators``: a (dK, dV) pair of fp32 tensors shaped like
     prefix_k into which the prefix gradients are added (and returned).
-    ``recompute_dq``: use the plan without a dS store (TPRPrefixMeta.plan);
-    with a dS store the dQ phase reads what the dK/dV phase wrote."""
+    ``ds_store_budget`` (bytes; None = the library default) or
+    ``recompute_dq=True`` (= budget 0) select the plan (TPRPrefixMeta.plan);
+    with a dS store the dQ phase reads what the dK/dV phase wrote, and a
+    ``workspace`` given in ``buffers`` must be of that plan's size."""
     scale = validate(q, k, v, prefix_k, prefix_v, meta, softmax_scale)
     tensors = [*_inputs(q, k, v, prefix_k, prefix_v), *(t.contiguous() for t in (out, lse, dout))]
     return _backward(*tensors[:7], tensors[7], meta, scale, phases=phases, buffers=buffers,
-                     prefix_grad_accumulators=prefix_grad_accumulators, recompute_dq=recompute_dq)
+                     prefix_grad_accumulators=prefix_grad_accumulators,
+                     ds_store_budget=ds_store_budget_bytes(ds_store_budget, recompute_dq))

@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define TPR_ATTN_ABI_VERSION 4
+#define TPR_ATTN_ABI_VERSION 5
 
 typedef enum TprStatus {
   TPR_OK = 0,
@@ -76,15 +76,27 @@ typedef enum TprDtype {
  * leaves are numbered in DFS order, segment_plan.py:266-275), and a node that
  * appears in a path must appear at the same depth in every path.
  *
- * flags: 0, or TPR_PLAN_RECOMPUTE_DQ. By default a bf16 head_dim-128 or 256
- * plan has the dK/dV kernel store every dS block it computes (bf16, 2 bytes per
- * visible (query, key) pair and query head) in the backward workspace, and
- * the dQ kernel reads them: dQ = scale dS K then costs one matrix product
- * instead of three (the scores S and dP recomputed). The workspace grows by
- * that store; a plan whose store would exceed 32 GiB recomputes instead.
- * TPR_PLAN_RECOMPUTE_DQ asks for the recomputing dQ and the small workspace
- * (needed by tpr_attn_bwd_noalloc for such shapes). Other paths ignore it. */
+ * dS store. A bf16 head_dim-128 or 256 plan may have the dK/dV kernel store
+ * every dS block it computes (bf16, 2 bytes per visible (query, key) pair and
+ * query head) in the backward workspace, and the dQ kernel read them: dQ =
+ * scale dS K then costs one matrix product instead of three (the scores S and
+ * dP recomputed). ds_store_max_bytes is the caller's budget for that store:
+ * the plan has one only when it fits, otherwise dQ recomputes and the
+ * workspace stays small (a few MB: statistics and split-tile partials).
+ *   ds_store_max_bytes = 0                      no store (the zeroed default)
+ *   ds_store_max_bytes = TPR_DS_STORE_DEFAULT   the library's default budget,
+ *                        TPR_DS_STORE_DEFAULT_BYTES (8 GiB): the Qwen3-4B
+ *                        layer shape (prefix 4096 + 4 x 4096, GQA 32/8) needs
+ *                        6.5 GB, prefix 32768 + 8 x 2048 needs 35.5 GB
+ *   ds_store_max_bytes > 0                      at most that many bytes
+ * flags: 0, or TPR_PLAN_RECOMPUTE_DQ, which forces no store whatever the
+ * budget (needed by tpr_attn_bwd_noalloc for shapes whose store would not fit
+ * its scratch). Other paths ignore both. The store's size is
+ * tpr_attn_bwd_workspace_bytes() of the plan minus that of the same tree
+ * planned with budget 0. */
 #define TPR_PLAN_RECOMPUTE_DQ 1
+#define TPR_DS_STORE_DEFAULT (-1)
+#define TPR_DS_STORE_DEFAULT_BYTES (INT64_C(8) << 30)
 typedef struct TprTreeDesc {
   int32_t num_leaves;
   int32_t num_nodes;
@@ -97,6 +109,7 @@ typedef struct TprTreeDesc {
   const int32_t* cu_seqlens_q;
   const int32_t* node_offsets;
   const int32_t* leaf_ancestors;
+  int64_t ds_store_max_bytes; /* dS store budget: 0, TPR_DS_STORE_DEFAULT or > 0 bytes */
 } TprTreeDesc;
 
 /* Forward: out = softmax(scale * q [prefix_k; k]^T + mask) [prefix_v; v], and
@@ -131,7 +144,8 @@ typedef struct TprFwdParams {
  * over every descendant leaf of each node in leaf order (fixed-order
  * reduction, the deterministic counterpart of prefix_state.py:565-573).
  * delta is caller-provided scratch of lse's shape; workspace is caller-provided
- * scratch of tpr_attn_bwd_workspace_bytes() bytes (may be NULL when that is 0).
+ * scratch of at least tpr_attn_bwd_workspace_bytes() bytes, 256-byte aligned
+ * (TPR_ERR_INVALID_ARGUMENT otherwise; may be NULL when that size is 0).
  *
  * flags = TPR_BWD_ACCUMULATE_PREFIX_F32: dprefix_k/dprefix_v are fp32 buffers
  * of [total_prefix, Hkv, D] whatever the dtype, and each node's gradient
@@ -163,8 +177,8 @@ typedef struct TprBwdParams {
   void* dv;
   void* dprefix_k;
   void* dprefix_v;
-  void* workspace;
-  size_t workspace_bytes;
+  void* workspace;        /* 256-byte aligned */
+  size_t workspace_bytes; /* >= tpr_attn_bwd_workspace_bytes(plan_host) */
   /* row strides of q, k and v, as in TprFwdParams (0 = packed); the
    * gradients dq, dk, dv are written packed */
   int64_t q_row_stride;
@@ -218,7 +232,9 @@ int tpr_attn_bwd_phases(const TprBwdParams* params, int phases, void* stream);
  * tpr_attn_bwd_workspace_bytes() exceeds that is rejected with
  * TPR_ERR_UNSUPPORTED. The call allocates and frees nothing; the scratch
  * address is looked up once per device (with that device current) on the
- * first call there. Every call on one GPU shares that GPU's scratch: calls
+ * first call there, which must not be under stream capture (a capturing
+ * first call is refused with TPR_ERR_INVALID_ARGUMENT): make one call per
+ * device before capturing it into a graph. Every call on one GPU shares that GPU's scratch: calls
  * that overlap on one GPU (two streams, two threads) race and must be
  * serialised by the caller. Nothing in the scratch needs to start at zero:
  * each call writes every workspace element it later reads. */

@@ -26,7 +26,7 @@ def _declared_functions():
 
 def test_library_loads_and_reports_abi_version():
     lib = _lib.load()
-    assert lib.tpr_attn_abi_version() == _lib.ABI_VERSION == 4
+    assert lib.tpr_attn_abi_version() == _lib.ABI_VERSION == 5
 
 
 def test_every_declared_symbol_is_exported_and_bound():

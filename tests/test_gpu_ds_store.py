@@ -130,3 +130,35 @@ def test_autograd_backward_follows_the_recompute_flag(recompute, cuda_device):
     torch.cuda.synchronize()
     for name, leaf, ref in zip(("dq", "dk", "dv", "dprefix_k", "dprefix_v"), leaves, direct):
         assert torch.equal(leaf.grad, ref), name
+
+
+def test_backward_falls_back_to_recomputing_dq_when_the_store_does_not_fit_in_memory(cuda_device):
+    """The autograd backward whose dS store workspace cannot be allocated
+    (the allocator capped 160 MB above what it holds, so the 419 MB store
+    fails and the gradients plus the 1 MB recomputing workspace fit) runs the plan
+    without a store: its gradients equal those of recompute_dq=True bitwise."""
+    from bridge_amd import TPRPrefixMeta, tpr_prefix_attention
+    meta, hq, hkv, d = TPRPrefixMeta.shared_prefix(1024, [1024] * 4), 32, 8, 128
+    plan = meta.plan(hq, hkv, d, torch.bfloat16, cuda_device)
+    small = meta.plan(hq, hkv, d, torch.bfloat16, cuda_device, ds_store_budget=0)
+    assert plan.dq_from_ds and plan.workspace_bytes - small.workspace_bytes == 800 * 32 * 16384
+    q, k, v, pk, pv, dout = make_inputs(meta, hq, hkv, d, torch.bfloat16, seed=17, device=cuda_device)
+    grads = {}
+    for label, recompute in (("recompute", True), ("fallback", False)):
+        leaves = [t.clone().requires_grad_(True) for t in (q, k, v, pk, pv)]
+        out, _ = tpr_prefix_attention(*leaves, meta, 0.09, recompute_dq=recompute)
+        torch.cuda.synchronize()
+        total = torch.cuda.get_device_properties(cuda_device).total_memory
+        if label == "fallback":
+            torch.cuda.empty_cache()
+            cap = torch.cuda.memory_reserved(cuda_device) + (160 << 20)
+            torch.cuda.set_per_process_memory_fraction(cap / total, cuda_device)
+        try:
+            out.backward(dout)
+            torch.cuda.synchronize()
+        finally:
+            torch.cuda.set_per_process_memory_fraction(1.0, cuda_device)
+        grads[label] = [t.grad for t in leaves]
+    print(f"fallback: store {plan.workspace_bytes} B, recomputing workspace {small.workspace_bytes} B", flush=True)
+    for a, b in zip(grads["fallback"], grads["recompute"]):
+        assert torch.equal(a, b)

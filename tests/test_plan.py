@@ -7,7 +7,7 @@ from collections import Counter
 import pytest
 import torch
 
-from bridge_amd import TPRPrefixMeta
+from bridge_amd import TPRPrefixMeta, _lib
 
 CPU = torch.device("cpu")
 
@@ -423,27 +423,32 @@ def test_empty_leaves_and_prefixless_trees_plan():
 
 
 def _ds_tables(w):
-    m, n = w[PF["NUM_NODES"]], w[PF["NUM_LEAVES"]]
+    """(base, first): tiles ahead of each segment (nodes, then leaf suffixes)
+    in a query block's dQ walk, and each query block's first slot."""
+    m, n, nq = w[PF["NUM_NODES"]], w[PF["NUM_LEAVES"]], w[PF["N_QBLK"]]
     off = w[PF["OFF_DS"]]
-    first = w[off:off + m + n + 1]
-    tiles = w[off + m + n + 1: off + m + n + 1 + 2 * first[-1]]
-    return first, [(tiles[2 * i], tiles[2 * i + 1]) for i in range(first[-1])]
+    return w[off:off + m + n], w[off + m + n: off + m + n + nq + 1]
 
 
 def _ds_reads_and_writes(meta, hq, hkv, d=128):
     """Emulate the slot arithmetic of the bf16 backward with a dS store: the
-    (slot, query head, wave block) triples every dK/dV stage writes, and those
-    every dQ wave reads (a block wholly past its segment's end is masked, not
-    read). head_dim 128: 128-key tiles of four 32-key wave blocks, dQ
-    workgroups of 8 waves streaming 64-key halves; head_dim 256: 64-key tiles
-    of four 16-key wave blocks, dQ workgroups of 4 waves streaming whole tiles."""
+    (slot, query head, wave block) triples every dK/dV stage writes (slot =
+    first[block] + base[segment] + tile), and those every dQ wave reads (slot =
+    first[block] + position of the tile in the wave's key walk: ancestor nodes
+    root first, then the suffix; a block wholly past its segment's end is
+    masked, not read). head_dim 128: 128-key tiles of four 32-key wave
+    blocks, dQ workgroups of 8 waves streaming 64-key halves; head_dim 256:
+    64-key tiles of four 16-key wave blocks, dQ workgroups of 4 waves
+    streaming whole tiles. Also returns, per dQ wave, the byte offsets of its
+    reads in the [KV head][slot][query head of the group] store."""
     plan = meta.plan(hq, hkv, d, torch.bfloat16, CPU)
     assert plan.dq_from_ds
     kt, wk, waves, step = (128, 32, FWD_WAVES, 64) if d == 128 else (64, 16, 4, 64)
+    head_bytes = kt * 64 * 2
     w, fwd, dkdv, qblk = decode(plan)
     g = hq // hkv
     n_slots = w[PF["DS_SLOTS"]]
-    first, tiles = _ds_tables(w)
+    base, first = _ds_tables(w)
     m = meta.num_nodes
     cu, no = meta.cu_seqlens_q, meta.node_offsets
     leaf_qblk = w[w[PF["OFF_LEAF_QBLK"]]: w[PF["OFF_LEAF_QBLK"]] + meta.num_leaves + 1]
@@ -453,15 +458,15 @@ def _ds_reads_and_writes(meta, hq, hkv, d=128):
 
     writes = Counter()
     for src, seg, key0, kvh, lo, hi, _ in tiles_of(dkdv):
-        t_first, t_lo = tiles[first[seg if src == 0 else m + seg] + key0 // kt]
         for qb in range(lo, hi):
-            slot = t_first + qb - t_lo
-            assert 0 <= slot < n_slots
+            slot = first[qb] + base[seg if src == 0 else m + seg] + key0 // kt
+            assert first[qb] <= slot < first[qb + 1] <= n_slots
             for wv in range(4):
                 if key0 + wk * wv < seg_len(src, seg):  # active waves only
                     for head in range(kvh * g, kvh * g + g):
                         writes[(slot, head, wv)] += 1
     reads = set()
+    wave_offsets = []
     hpw = math.gcd(g, waves)
     tpw = 32 * (waves // hpw)
     for leaf, tok0, qh0, kvh in fwd:
@@ -476,18 +481,22 @@ def _ds_reads_and_writes(meta, hq, hkv, d=128):
             if tw0 >= length:
                 continue
             qb = leaf_qblk[leaf] + tw0 // 64
+            pos, offs = 0, []
             for src, seg, slen, lim in segs:
                 for key0 in range(0, lim, kt):
                     for k0 in range(key0, min(key0 + kt, lim), step):  # the dQ kernel's tiles (halves at 128)
                         if src == 1 and k0 > tw0 + 31:
                             continue
-                        t_first, t_lo = tiles[first[seg if src == 0 else m + seg] + key0 // kt]
-                        slot = t_first + qb - t_lo
-                        assert 0 <= slot < n_slots
+                        slot = first[qb] + pos
+                        assert slot == first[qb] + base[seg if src == 0 else m + seg] + key0 // kt
+                        assert first[qb] <= slot < first[qb + 1]
+                        offs.append(((kvh * n_slots + slot) * g + head - kvh * g) * head_bytes + (k0 - key0) * 128)
                         for wv in range((k0 - key0) // wk, (k0 - key0 + step) // wk):
                             if key0 + wk * wv < slen:
                                 reads.add((slot, head, wv))
-    return n_slots, writes, reads
+                    pos += 1
+            wave_offsets.append(offs)
+    return n_slots, writes, reads, wave_offsets
 
 
 @pytest.mark.parametrize("d", [128, 256])
@@ -503,11 +512,16 @@ def test_ds_store_is_written_once_before_every_dq_read(case, d):
         "mha": (TPRPrefixMeta.shared_prefix(0, [200, 65]), 4, 4),
     }
     meta, hq, hkv = trees[case]
-    n_slots, writes, reads = _ds_reads_and_writes(meta, hq, hkv, d)
+    n_slots, writes, reads, wave_offsets = _ds_reads_and_writes(meta, hq, hkv, d)
     assert set(writes.values()) == {1}  # no block is written twice
     assert reads <= set(writes)         # every read block was written
     # the store holds exactly the visible (tile, query block) pairs: each slot is read
     assert {r[0] for r in reads} == set(range(n_slots))
+    # a dQ wave's reads move forward through the store, one slot of its group per tile
+    head_bytes = (128 if d == 128 else 64) * 64 * 2
+    for offs in wave_offsets:
+        assert offs == sorted(offs)
+        assert all(0 <= o < n_slots * hq * head_bytes for o in offs)
 
 
 def test_ds_store_size_at_the_qwen3_layer_shape():
@@ -530,19 +544,62 @@ def test_ds_store_size_at_the_qwen3_layer_shape():
     assert not meta.plan(32, 8, 128, torch.float32, CPU).dq_from_ds
 
 
-def test_ds_store_falls_back_to_recompute_past_its_cap():
-    """A store over 32 GiB is not planned: prefix 32768 + 8 x 2048 at GQA 32/8
-    would need 256 x 256 + 8 x sum(32 - 2 j, j < 16) = 67,712 slots x 32 heads x
-    16 KiB = 35.5 GB, so its plan keeps the recomputing dQ and the small
-    workspace; with 4 siblings (33,856 slots, 17.7 GB) the store is planned."""
-    cap = 32 << 30
+def test_ds_store_follows_the_byte_budget():
+    """The plan has a dS store only when it fits the budget: at the Qwen3-4B
+    layer shape the store is 12,416 slots x 32 heads x 16 KiB = 6.51 GB, so a
+    budget of one byte less recomputes dQ (small workspace) and one of exactly
+    that size stores; the default budget (8 GiB) stores; prefix 32768 + 8 x
+    2048 (67,712 slots, 35.5 GB) recomputes under the default and stores
+    under a 40 GB budget; budget 0 and recompute_dq=True never store."""
+    from bridge_amd.meta import DS_STORE_DEFAULT_BYTES
+    assert DS_STORE_DEFAULT_BYTES == _lib.TPR_DS_STORE_DEFAULT_BYTES == 8 << 30
+    meta = TPRPrefixMeta.shared_prefix(4096, [4096] * 4)
+    store = 12416 * 32 * 16384
+    small = meta.plan(32, 8, 128, torch.bfloat16, CPU, ds_store_budget=0)
+    assert not small.dq_from_ds and small.host.tolist()[PF["DS_SLOTS"]] == 0
+    assert small.workspace_bytes < 8 << 20  # lse*log2e and -delta rows: 2 x 32 x 16384 floats
+    for budget, stores in ((store - 1, False), (store, True), (None, True), (1 << 40, True)):
+        plan = meta.plan(32, 8, 128, torch.bfloat16, CPU, ds_store_budget=budget)
+        assert plan.dq_from_ds == stores, budget
+        assert plan.workspace_bytes == small.workspace_bytes + (store if stores else 0)
+    assert not meta.plan(32, 8, 128, torch.bfloat16, CPU, recompute_dq=True, ds_store_budget=1 << 40).dq_from_ds
+
     big = TPRPrefixMeta.shared_prefix(32768, [2048] * 8)
     slots = 256 * 256 + 8 * sum(32 - 2 * j for j in range(16))
-    assert slots == 67712 and slots * 32 * 16384 > cap
+    assert slots == 67712 and slots * 32 * 16384 > DS_STORE_DEFAULT_BYTES
     plan = big.plan(32, 8, 128, torch.bfloat16, CPU)
     assert not plan.dq_from_ds and plan.host.tolist()[PF["DS_SLOTS"]] == 0
-    assert plan.workspace_bytes == big.plan(32, 8, 128, torch.bfloat16, CPU, recompute_dq=True).workspace_bytes
-    half = TPRPrefixMeta.shared_prefix(32768, [2048] * 4)
-    hplan = half.plan(32, 8, 128, torch.bfloat16, CPU)
-    hslots = 256 * 128 + 4 * sum(32 - 2 * j for j in range(16))
-    assert hplan.dq_from_ds and hplan.host.tolist()[PF["DS_SLOTS"]] == hslots and hslots * 32 * 16384 <= cap
+    assert plan.workspace_bytes == big.plan(32, 8, 128, torch.bfloat16, CPU, ds_store_budget=0).workspace_bytes
+    large = big.plan(32, 8, 128, torch.bfloat16, CPU, ds_store_budget=40 * 10**9)
+    assert large.dq_from_ds and large.host.tolist()[PF["DS_SLOTS"]] == slots
+    # head_dim 256 (8 KiB per head and slot) under the same rule
+    q35 = meta.plan(8, 2, 256, torch.bfloat16, CPU)
+    assert q35.dq_from_ds
+    need = q35.workspace_bytes - meta.plan(8, 2, 256, torch.bfloat16, CPU, ds_store_budget=0).workspace_bytes
+    assert not meta.plan(8, 2, 256, torch.bfloat16, CPU, ds_store_budget=need - 1).dq_from_ds
+    assert meta.plan(8, 2, 256, torch.bfloat16, CPU, ds_store_budget=need).dq_from_ds
+
+
+@pytest.mark.parametrize("budget", [-1, -5, 1.5, True, "8G"])
+def test_ds_store_budget_rejects_invalid_values(budget):
+    meta = TPRPrefixMeta.shared_prefix(64, [64])
+    with pytest.raises(ValueError, match="ds_store_budget"):
+        meta.plan(4, 1, 128, torch.bfloat16, CPU, ds_store_budget=budget)
+
+
+def test_planner_rejects_negative_store_budgets_other_than_the_default():
+    """Through the C ABI: TPR_DS_STORE_DEFAULT (-1) is the default budget,
+    any other negative value is an invalid argument."""
+    import ctypes
+    lib = _lib.load()
+    cu = (ctypes.c_int32 * 2)(0, 64)
+    no = (ctypes.c_int32 * 2)(0, 64)
+    an = (ctypes.c_int32 * 1)(0)
+    words = ctypes.c_int64(0)
+    for budget, ok in ((_lib.TPR_DS_STORE_DEFAULT, True), (0, True), (1, True), (-2, False)):
+        desc = _lib.TprTreeDesc(1, 1, 1, 4, 1, 128, _lib.TPR_DTYPE_BF16, 0, ctypes.cast(cu, ctypes.c_void_p),
+                                ctypes.cast(no, ctypes.c_void_p), ctypes.cast(an, ctypes.c_void_p), budget)
+        rc = lib.tpr_attn_plan(ctypes.byref(desc), None, 0, ctypes.byref(words))
+        assert (rc == _lib.TPR_OK) == ok, budget
+        if not ok:
+            assert rc == _lib.TPR_ERR_INVALID_ARGUMENT and b"ds_store_max_bytes" in lib.tpr_attn_last_error()

@@ -91,3 +91,46 @@ def test_noalloc_backward_equals_the_workspace_backward(cuda_device):
             assert torch.isfinite(b.float()).all(), label
             assert torch.equal(a, b), f"call {i}: {label} differs"
         print(f"  bitwise equal: delta dq dk dv dprefix_k dprefix_v", flush=True)
+
+
+@pytest.mark.gpu
+def test_noalloc_backward_replays_from_a_captured_graph(cuda_device):
+    """tpr_attn_bwd_noalloc captured into a torch.cuda.CUDAGraph after one call
+    outside capture (which looks up the scratch address): every replay, with
+    eager work and synchronisation between replays, equals tpr_attn_bwd
+    bitwise. The backward's kernels fill every workspace element they read,
+    so no memset node is needed."""
+    lib = _lib.load()
+    meta, hq, hkv, d = TPRPrefixMeta.shared_prefix(200, [100, 37]), 8, 2, 128
+    scale = 1.0 / math.sqrt(d)
+    plan = meta.plan(hq, hkv, d, torch.bfloat16, cuda_device)
+    assert plan.dq_from_ds and plan.workspace_bytes <= lib.tpr_attn_bwd_noalloc_max_workspace_bytes()
+    print(f"[noalloc graph] tq={meta.total_q} tp={meta.total_prefix} workspace_bytes={plan.workspace_bytes}",
+          flush=True)
+    q, k, v, pk, pv, dout = make_inputs(meta, hq, hkv, d, torch.bfloat16, seed=41, device=cuda_device)
+    out, lse = prefix_attention_forward(q, k, v, pk, pv, meta, scale)
+    tensors = (q, k, v, pk, pv, out, lse, dout)
+    ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=cuda_device)
+    ref = _fresh_outputs(q, k, v, pk, pv, lse)
+    p_ref = _bwd_params(plan, scale, tensors, ref, ws)
+    _lib.check(lib.tpr_attn_bwd(ctypes.byref(p_ref), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)),
+               "tpr_attn_bwd")
+    mine = _fresh_outputs(q, k, v, pk, pv, lse)
+    p = _bwd_params(plan, scale, tensors, mine, None)
+    _lib.check(lib.tpr_attn_bwd_noalloc(ctypes.byref(p), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)),
+               "tpr_attn_bwd_noalloc (outside capture)")
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _lib.check(lib.tpr_attn_bwd_noalloc(ctypes.byref(p),
+                                            ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)),
+                   "tpr_attn_bwd_noalloc (captured)")
+    for rep in range(3):
+        for t in mine:
+            t.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for label, a, b in zip(("delta", "dq", "dk", "dv", "dprefix_k", "dprefix_v"), mine, ref):
+            assert torch.equal(a, b), f"replay {rep}: {label} differs"
+        print(f"  replay {rep}: bitwise equal", flush=True)
