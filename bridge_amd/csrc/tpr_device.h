@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #include "tpr_common.h"
+#include "tpr_lanes.h"
 
 namespace tpr {
 
@@ -71,16 +72,7 @@ template <typename T> __device__ __forceinline__ T from_f32(float x);
 template <> __device__ __forceinline__ float from_f32<float>(float x) { return x; }
 template <> __device__ __forceinline__ bf16 from_f32<bf16>(float x) { return static_cast<bf16>(x); }
 
-// 16-byte chunk swizzle of a [rows][128 bf16] LDS tile (256 B rows):
-// physical chunk = logical chunk ^ f(row), with f swapping the two 2-bit
-// fields of row % 16. Rows r..r+15 at one logical chunk land in 16 distinct
-// chunks (conflict-free ds_read_b128 over 16 lanes), and 4 consecutive rows
-// (r % 4 == 0) x 4 consecutive chunks land in 16 distinct chunks
-// (conflict-free ds_read_tr16_b64 over 32 lanes).
-__device__ __forceinline__ int swz_chunk(int row, int chunk) {
-  return chunk ^ (((row & 3) << 2) | ((row >> 2) & 3));
-}
-// byte offset of element (row, col) in a swizzled 256-byte-row tile
+// byte offset of element (row, col) in a swizzled 256-byte-row tile (swz_chunk: tpr_lanes.h)
 __device__ __forceinline__ int swz_off(int row, int col) {
   return row * 256 + (swz_chunk(row, col >> 3) << 4) + ((col & 7) << 1);
 }

@@ -94,13 +94,13 @@ struct DmaLanes {
 
 template <int kWaves>
 __device__ __forceinline__ DmaLanes<kWaves> make_dma_lanes(uint32_t row_bytes, int wave, int lane) {
+  static_assert(kWaves == 4, "the tile4 lane map (tpr_lanes.h) is for 4 waves of 4 blocks");
   DmaLanes<kWaves> p;
 #pragma unroll
   for (int j = 0; j < DmaLanes<kWaves>::kBlocks; j++) {
-    const int row = 4 * (wave * DmaLanes<kWaves>::kBlocks + j) + (lane >> 4);
-    p.row[j] = row;
-    p.cbytes[j] = static_cast<uint32_t>(swz_chunk(row, lane & 15)) * 16u;
-    p.voff[j] = static_cast<uint32_t>(row) * row_bytes + p.cbytes[j];
+    p.row[j] = tile4_row(wave, lane, j);
+    p.cbytes[j] = tile4_chunk_bytes_swz(wave, lane, j);
+    p.voff[j] = tile4_lane_bytes_swz(wave, lane, row_bytes, j);
   }
   return p;
 }
@@ -134,10 +134,10 @@ struct TileLanes4 {
 
 __device__ __forceinline__ TileLanes4 make_tile_lanes4(int wave, int lane, uint32_t row_bytes) {
   TileLanes4 p;
-  p.row0 = static_cast<uint32_t>(16 * wave + (lane >> 4));
-  p.cb0 = static_cast<uint32_t>(16 * ((lane & 15) ^ ((lane >> 4) << 2)));
+  p.row0 = static_cast<uint32_t>(tile4_row(wave, lane, 0));
+  p.cb0 = tile4_chunk_bytes(lane, 0);
 #pragma unroll
-  for (int j = 0; j < 4; j++) p.full[j] = (p.row0 + 4u * j) * row_bytes + (p.cb0 ^ (16u * j));
+  for (int j = 0; j < 4; j++) p.full[j] = tile4_lane_bytes(wave, lane, row_bytes, j);
   return p;
 }
 
@@ -932,10 +932,7 @@ __global__ __launch_bounds__(512) void mfma_dqs(KernelArgs a) {
   // at l (the swizzle is its own inverse)
   uint32_t dsv[4];
 #pragma unroll
-  for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-    for (int qc = 0; qc < 2; qc++)
-      dsv[2 * kb + qc] = kb * 4096 + qc * 1024 + 16 * (lane ^ (8 * (lane >> 5) + 4 * qc));
+  for (int j = 0; j < 4; j++) dsv[j] = dqs_ds_lane_bytes(lane, j);
   // dS^T operand reads (B: lane l gets query l % 32, keys 8 (l / 32) + 0..7
   // of a 16-key step). As a source row of ds_read_tr16_b64, lane l (group
   // g = l / 16, e = (l % 16) / 4, m = l % 4) addresses key 8 (g / 2) + 4 t + e,

@@ -656,7 +656,9 @@ __global__ __launch_bounds__(256) void m16_dqs(KernelArgs a) {
 
   // dS copy: block w (wave block w of the slot, this wave's query half) lands
   // at 1024 w; lane l fetches the chunk that lands at l (the swizzle is its own inverse)
-  const uint32_t dsl = 16u * static_cast<uint32_t>(lane ^ (4 * ((lane >> 4) & 1)));
+  uint32_t dsl[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) dsl[j] = m16_dqs_ds_lane_bytes(lane, j);
   // dS^T operand reads (B: lane l gets query 16 qs + l % 16, keys 32 t + 8 (l / 16) + 0..7).
   // As a source row of ds_read_tr16_b64, lane l (group g, e = (l % 16) / 4,
   // m = l % 4) addresses key 8 g + 4 h + e of the 32-key step (wave block
@@ -730,7 +732,7 @@ __global__ __launch_bounds__(256) void m16_dqs(KernelArgs a) {
                   wave, lane);
     if (vis) {
       const char* src = ds_wave + cpos * ds_tile_bytes;
-      dma_blocks4_nt(src, dsl, 2048 + dsl, 4096 + dsl, 6144 + dsl, lds0 + kDsOff + (b * kM16Waves + wave) * kDsWave);
+      dma_blocks4_nt(src, dsl[0], dsl[1], dsl[2], dsl[3], lds0 + kDsOff + (b * kM16Waves + wave) * kDsWave);
     }
   };
 
