@@ -312,13 +312,19 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
     const char* b = x.suffix ? (is_k ? kbase : vbase) : (is_k ? pkbase : pvbase);
     return b + x.row * static_cast<int64_t>(kv_rb(x, is_k));
   };
-  // group B's copy cursor: the next K tile (tl_k) and the next V tile (tl_v)
-  Cursor dc = cursor_begin(seg);
-  TileLoc tl_k = cursor_tile(dc), tl_v = tl_k;
-  if (grp) dma_tile4_fwd(kv_src(tl_k, true), kv_rb(tl_k, true), tl_k.len, lds0, dl, wave & 3);  // K[0]
+  // Copy cursors. Group B copies K[0], K[1] and V[0] before the tile loop,
+  // then V[j+1] at the start of its softmax phase V(j-1); group A copies
+  // K[j+2] at the end of its MFMA phase M(j), which the other group's
+  // softmax phase outlasts. Both wait for their copies one phase later,
+  // before the barrier ahead of the first M phase that reads them.
+  Cursor dv = cursor_begin(seg);  // B: the next V tile
+  TileLoc tl_v = cursor_tile(dv);
+  if (grp) dma_tile4_fwd(kv_src(tl_v, true), kv_rb(tl_v, true), tl_v.len, lds0, dl, wave & 3);  // K[0]
+  Cursor ka = dv;                 // A: the next K tile (tile 2 when the loop starts); B: tile 1 first
+  TileLoc tl_k = tl_v;
   if (ntiles > 1) {
-    cursor_next(seg, dc);
-    tl_k = cursor_tile(dc);
+    cursor_next(seg, ka);
+    tl_k = cursor_tile(ka);
   }
   // every wave's mask cursor: the tile whose scores the next V phase masks
   Cursor mc = cursor_begin(seg);
@@ -343,19 +349,34 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
   f32x16 s[2];
   bf16x8 pb[2][2];
 
-  // group B, start of iteration j: copy K[j+2] into K buffer j&1 and V[j+1]
-  // into V buffer (j+1)&1
-  auto issue = [&](int j) {
-    if (j + 2 < ntiles)
-      dma_tile4_fwd(kv_src(tl_k, true), kv_rb(tl_k, true), tl_k.len, lds0 + ((j + 2) & 1) * kTileBytes, dl,
-                    wave & 3);
+  // group B before the loop: K[1] into K buffer 1 and V[0] into V buffer 0
+  auto issue_prologue = [&]() {
+    if (ntiles > 1) dma_tile4_fwd(kv_src(tl_k, true), kv_rb(tl_k, true), tl_k.len, lds0 + kTileBytes, dl, wave & 3);
+    dma_tile4_fwd(kv_src(tl_v, false), kv_rb(tl_v, false), tl_v.len, lds0 + 2 * kTileBytes, dl, wave & 3);
+    if (ntiles > 1) {
+      cursor_next(seg, dv);
+      tl_v = cursor_tile(dv);
+    }
+  };
+  // group B, start of iteration j: V[j+1] into V buffer (j+1)&1
+  auto issue_v = [&](int j) {
     if (j + 1 < ntiles)
       dma_tile4_fwd(kv_src(tl_v, false), kv_rb(tl_v, false), tl_v.len, lds0 + (2 + ((j + 1) & 1)) * kTileBytes, dl,
                     wave & 3);
-    tl_v = tl_k;
+    if (j + 2 < ntiles) {
+      cursor_next(seg, dv);
+      tl_v = cursor_tile(dv);
+    }
+  };
+  // group A, end of M(j): K[j+2] into K buffer j&1 (free: K[j] was last read
+  // in group B's M(j-1), before the barrier that opened M(j))
+  auto issue_k = [&](int j) {
+    if (j + 2 < ntiles)
+      dma_tile4_fwd(kv_src(tl_k, true), kv_rb(tl_k, true), tl_k.len, lds0 + ((j + 2) & 1) * kTileBytes, dl,
+                    wave & 3);
     if (j + 3 < ntiles) {
-      cursor_next(seg, dc);
-      tl_k = cursor_tile(dc);
+      cursor_next(seg, ka);
+      tl_k = cursor_tile(ka);
     }
   };
   // M(j): scores of tile j+1 (if with_s) and P[j] V[j] (if with_pv); par = j & 1
@@ -469,10 +490,18 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
   // unrolled by two so that the buffer parity, and with it every LDS address
   // offset, is a compile-time constant.
   if (grp == 0) {
+    if (ntiles > 2) {  // A's K cursor starts at tile 2
+      cursor_next(seg, ka);
+      tl_k = cursor_tile(ka);
+    }
     auto body = [&](auto par, int j) {
       mphase(yes, yes, par);
+      __builtin_amdgcn_sched_barrier(0);
+      issue_k(j);
       phase_barrier();
       vphase(j);
+      __builtin_amdgcn_sched_barrier(0);
+      wait_dma();
       phase_barrier();
     };
     mphase(yes, no, odd);
@@ -491,7 +520,7 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
     phase_barrier();
   } else {
     auto body = [&](auto par, int j) {
-      issue(j);
+      issue_v(j);
       vphase(j - 1);
       phase_barrier();
       mphase(yes, yes, par);
@@ -499,7 +528,7 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
       wait_dma();
       phase_barrier();
     };
-    issue(-1);
+    issue_prologue();
     phase_barrier();
     mphase(yes, no, odd);
     wait_dma();
