@@ -12,7 +12,7 @@ import threading
 
 LIB_NAME = "libtpr_attn.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 TPR_OK = 0
 TPR_ERR_INVALID_ARGUMENT = 1
@@ -24,6 +24,7 @@ TPR_DTYPE_BF16 = 0
 TPR_DTYPE_FP32 = 1
 
 TPR_PLAN_RECOMPUTE_DQ = 1
+TPR_PLAN_MASKED = 2                       # plan for calls with a physical key mask (SIMT kernels)
 TPR_DS_STORE_DEFAULT = -1                 # TprTreeDesc.ds_store_max_bytes: the library's default budget
 TPR_DS_STORE_DEFAULT_BYTES = 8 << 30      # ... which is 8 GiB
 
@@ -85,6 +86,8 @@ class TprFwdParams(ctypes.Structure):
         ("q_row_stride", ctypes.c_int64),
         ("k_row_stride", ctypes.c_int64),
         ("v_row_stride", ctypes.c_int64),
+        ("mask", _p),
+        ("mask_row_stride", ctypes.c_int64),
     ]
 
 
@@ -115,6 +118,8 @@ class TprBwdParams(ctypes.Structure):
         ("q_row_stride", ctypes.c_int64),
         ("k_row_stride", ctypes.c_int64),
         ("v_row_stride", ctypes.c_int64),
+        ("mask", _p),
+        ("mask_row_stride", ctypes.c_int64),
     ]
 
 

@@ -116,6 +116,24 @@ int set_row_strides(KernelArgs& a, const int32_t* ph, int64_t q_rs, int64_t k_rs
   return TPR_OK;
 }
 
+// The key mask: required by a masked plan, refused by any other.
+int set_mask(KernelArgs& a, const int32_t* ph, const uint8_t* mask, int64_t row_stride) {
+  const int64_t cols = ph[PF_MASK_COLS];
+  if (cols == 0) {
+    if (mask) return fail(TPR_ERR_INVALID_ARGUMENT, "a key mask needs a plan built with TPR_PLAN_MASKED");
+    return TPR_OK;
+  }
+  if (!mask && ph[PF_TOTAL_Q] > 0)
+    return fail(TPR_ERR_INVALID_ARGUMENT, "the plan was built with TPR_PLAN_MASKED: mask must not be NULL");
+  const int64_t stride = row_stride == 0 ? cols : row_stride;
+  if (stride < cols)
+    return fail(TPR_ERR_INVALID_ARGUMENT, "mask_row_stride must be 0 or at least %lld bytes (the longest key "
+                "sequence), got %lld", static_cast<long long>(cols), static_cast<long long>(row_stride));
+  a.mask = mask;
+  a.mask_rs = stride;
+  return TPR_OK;
+}
+
 int check_tensor(const void* p, const char* name, bool needed, bool mfma) {
   if (!needed) return TPR_OK;
   if (!p) return fail(TPR_ERR_INVALID_ARGUMENT, "%s must not be NULL", name);
@@ -200,6 +218,7 @@ extern "C" int tpr_attn_fwd(const TprFwdParams* p, void* stream) {
     return rc;
   KernelArgs a = args_from_plan(ph, p->plan_device, p->softmax_scale);
   if ((rc = set_row_strides(a, ph, p->q_row_stride, p->k_row_stride, p->v_row_stride))) return rc;
+  if ((rc = set_mask(a, ph, p->mask, p->mask_row_stride))) return rc;
   a.q = p->q;
   a.k = p->k;
   a.v = p->v;
@@ -260,6 +279,7 @@ int bwd_phases(const TprBwdParams* p, int phases, void* stream, void* workspace,
     return fail(TPR_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
   KernelArgs a = args_from_plan(ph, p->plan_device, p->softmax_scale);
   if ((rc = set_row_strides(a, ph, p->q_row_stride, p->k_row_stride, p->v_row_stride))) return rc;
+  if ((rc = set_mask(a, ph, p->mask, p->mask_row_stride))) return rc;
   a.q = p->q;
   a.k = p->k;
   a.v = p->v;

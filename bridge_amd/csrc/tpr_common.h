@@ -9,7 +9,7 @@
 namespace tpr {
 
 constexpr int32_t kPlanMagic = 0x31525054;  // "TPR1"
-constexpr int32_t kPlanVersion = 4;
+constexpr int32_t kPlanVersion = 5;
 
 // Header word indices.
 enum PlanField : int {
@@ -50,6 +50,8 @@ enum PlanField : int {
                      // suffixes) in the dQ walk of a query block below it, then
                      // [n_qblk + 1] first slot of each query block; slot of (segment, tile t,
                      // block b) = first[b] + base[segment] + t
+  PF_MASK_COLS,      // plan built for a key mask (TPR_PLAN_MASKED): the longest key sequence
+                     // of any leaf (the least mask row length); 0 = not a masked plan
   PF_HEADER_WORDS = 40
 };
 

@@ -64,6 +64,11 @@ struct KernelArgs {
   void* ds;
   int32_t off_ds, off_ds_first, num_nodes;
   int64_t ds_slots;
+  // physical key mask of a masked plan (SIMT kernels): nonzero = hidden; row
+  // = query row of q, column = key position in the row's leaf key sequence
+  // (ancestor nodes root first, then the suffix)
+  const uint8_t* mask;
+  int64_t mask_rs;  // bytes
 };
 
 __device__ __forceinline__ float to_f32(float x) { return x; }

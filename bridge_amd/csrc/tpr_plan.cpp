@@ -97,7 +97,7 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
     return fail(TPR_ERR_UNSUPPORTED, "head_dim must be a multiple of 8 and at most 256, got %d", D);
   if (t->dtype != TPR_DTYPE_BF16 && t->dtype != TPR_DTYPE_FP32)
     return fail(TPR_ERR_INVALID_ARGUMENT, "unknown dtype %d", t->dtype);
-  if (t->flags & ~TPR_PLAN_RECOMPUTE_DQ)
+  if (t->flags & ~(TPR_PLAN_RECOMPUTE_DQ | TPR_PLAN_MASKED))
     return fail(TPR_ERR_INVALID_ARGUMENT, "unknown plan flags 0x%x", static_cast<unsigned>(t->flags));
   if (t->ds_store_max_bytes < 0 && t->ds_store_max_bytes != TPR_DS_STORE_DEFAULT)
     return fail(TPR_ERR_INVALID_ARGUMENT, "ds_store_max_bytes must be 0, TPR_DS_STORE_DEFAULT or positive, got %lld",
@@ -145,7 +145,9 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
                   "descendant leaves of node %d are not contiguous; number leaves in DFS order", n);
   }
 
-  const int path = t->dtype != TPR_DTYPE_BF16 ? PATH_SIMT
+  // a masked plan runs the SIMT kernels, the ones that read a key mask
+  const bool masked = (t->flags & TPR_PLAN_MASKED) != 0;
+  const int path = t->dtype != TPR_DTYPE_BF16 || masked ? PATH_SIMT
                    : D == kMfmaD             ? PATH_MFMA
                    : (D == 64 || D == 256)   ? PATH_MFMA16
                                              : PATH_SIMT;
@@ -157,6 +159,15 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
       int n = anc[s * depth + d];
       if (n >= 0) prefix_len[s] += no[n + 1] - no[n];
     }
+  // a masked plan's least mask row length: the longest key sequence of any leaf
+  int64_t mask_cols = 0;
+  if (masked) {
+    mask_cols = 1;
+    for (int s = 0; s < N; s++) mask_cols = std::max<int64_t>(mask_cols, prefix_len[s] + cu[s + 1] - cu[s]);
+    if (mask_cols > INT32_MAX)
+      return fail(TPR_ERR_UNSUPPORTED, "a masked plan needs key sequences of at most 2^31 - 1 keys, got %lld",
+                  static_cast<long long>(mask_cols));
+  }
 
   // ---- key runs (the MFMA forward / dQ key streams) --------------------------
   // A leaf's ancestors, root first, as runs of rows of prefix_k/v: an ancestor
@@ -226,7 +237,8 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
   for (int s = 0; s < N; s++) {
     const int len = cu[s + 1] - cu[s];
     for (int tok = 0; tok < len; tok += tokens_per_wg) {
-      const int64_t keys = prefix_len[s] + std::min(tok + tokens_per_wg, len);
+      // keys the item streams: under a mask every suffix key may be visible
+      const int64_t keys = prefix_len[s] + (masked ? len : std::min(tok + tokens_per_wg, len));
       for (int qh = 0; qh < Hq; qh += heads_per_wg) {
         Item it;
         it.words = {s, tok, qh, qh / G};
@@ -330,7 +342,9 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
         }
         continue;
       }
-      for (int h = 0; h < Hkv; h++) add_tile(1, s, j * KT, h, first_block(j), leaf_qblk[s + 1]);
+      // causal: the blocks from the tile's own on; under a mask every block of the leaf
+      const int32_t lo = masked ? leaf_qblk[s] : first_block(j);
+      for (int h = 0; h < Hkv; h++) add_tile(1, s, j * KT, h, lo, leaf_qblk[s + 1]);
     }
   }
   int32_t n_dkdv = 0;
@@ -419,6 +433,7 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
   plan[PF_MAX_RUNS] = std::max(max_runs, 1);
   plan[PF_DS_SLOTS] = static_cast<int32_t>(ds_slots);
   plan[PF_OFF_DS] = ds_table.empty() ? 0 : append(ds_table.data(), ds_table.size());
+  plan[PF_MASK_COLS] = static_cast<int32_t>(mask_cols);
   plan[PF_TOTAL_WORDS] = static_cast<int32_t>(plan.size());
   return TPR_OK;
 }

@@ -21,6 +21,16 @@
 //   dq = scale sum_j ds_j k_j, dk_j += scale ds_j q.
 // Key streams: the leaf's own suffix, then its ancestors' key runs (the
 // plan's run table: ancestors root first, rows adjacent in prefix_k/v merged).
+//
+// Masked plans (kMask): a physical key mask replaces the causal rule, as in
+// the reference's custom-mask mode (rectangular_attention.py:112-122): key
+// c of a leaf's sequence cat(ancestors, suffix) is visible to query row r iff
+// mask[r][c] == 0, so every suffix key is streamed, and the dK/dV items of a
+// suffix tile cover every query block of the leaf. The mask bytes of each
+// (query tile, key tile) pair are staged in LDS with the tiles. A row with no
+// visible key ends with l = 0: its output is 0, its lse -inf, and every p of
+// it is 0 in the backward (p is selected by visibility, never computed from
+// that lse).
 
 #include "tpr_device.h"
 
@@ -233,9 +243,35 @@ __device__ __forceinline__ bool key_segment(const KernelArgs& a, int leaf, int s
   return true;
 }
 
+// Stage mask bytes of query rows [row0, row0 + rows) and key columns
+// [col0, col0 + cols) into LDS (rows x cols, row-major); entries of rows at or
+// beyond valid_rows and columns at or beyond valid_cols read as hidden (1).
+__device__ __forceinline__ void stage_mask(uint8_t* ms, const KernelArgs& a, int64_t row0, int rows, int valid_rows,
+                                           int64_t col0, int cols, int valid_cols) {
+  for (int idx = threadIdx.x; idx < rows * cols; idx += blockDim.x) {
+    const int r = idx / cols, c = idx % cols;
+    ms[idx] = r < valid_rows && c < valid_cols ? a.mask[(row0 + r) * a.mask_rs + col0 + c] : uint8_t{1};
+  }
+}
+
+// Mask column of the first key of a segment in a leaf's key sequence: the
+// lengths of the leaf's ancestors ahead of node `node` (all of them for
+// node < 0, i.e. the leaf's own suffix).
+__device__ __forceinline__ int leaf_key_column(const KernelArgs& a, int leaf, int node) {
+  const int32_t* anc = a.plan + a.off_anc + static_cast<int64_t>(leaf) * a.max_depth;
+  const int32_t* no = a.plan + a.off_node_off;
+  int col = 0;
+  for (int i = 0; i < a.max_depth; i++) {
+    const int n = anc[i];
+    if (n < 0 || n == node) break;
+    col += no[n + 1] - no[n];
+  }
+  return col;
+}
+
 // ---------------------------------------------------------------------------
 // Forward: block = kSimtQ queries of one head of one leaf, kL lanes per query.
-template <typename T, int DMAX>
+template <typename T, int DMAX, bool kMask>
 __global__ __launch_bounds__(kSimtQ * DMAX / 32) void simt_fwd(KernelArgs a) {
   constexpr int kL = DMAX / 32, kTile = simt_tile<DMAX>();
   const int32_t* item = a.plan + a.off_fwd + 4 * blockIdx.x;
@@ -254,6 +290,7 @@ __global__ __launch_bounds__(kSimtQ * DMAX / 32) void simt_fwd(KernelArgs a) {
   __shared__ __attribute__((aligned(16))) float Ks[kBf ? 4 : kTile * DMAX];
   __shared__ __attribute__((aligned(16))) bf16 Kb[kBf ? kTile * DMAX : 8];
   __shared__ __attribute__((aligned(16))) float Vs[kTile * DMAX];
+  __shared__ uint8_t Ms[kMask ? kSimtQ * kTile : 4];
 
   const float cs = a.scale * kLog2e;
   f32x4 q[8], o[8];
@@ -265,18 +302,23 @@ __global__ __launch_bounds__(kSimtQ * DMAX / 32) void simt_fwd(KernelArgs a) {
   for (int j = 0; j < 8; j++) o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, l = 0.f;
 
-  const int suffix_keys = min(len, tok0 + kSimtQ);
+  // causal: the suffix keys up to the block's last query; masked: all of them
+  const int suffix_keys = kMask ? len : min(len, tok0 + kSimtQ);
+  const int suffix_col = kMask ? leaf_key_column(a, leaf, -1) : 0;  // mask column of suffix key 0
+  int run_col = 0;                                                  // ... of the current run's key 0
   const T *kb, *vb;
   int64_t ks, vs;
   int seg_len;
   for (int sg = 0; key_segment<T>(a, leaf, sg, suffix_keys, kvh, kb, vb, ks, vs, seg_len); sg++) {
     const bool causal = sg == 0;
+    const int seg_col = sg == 0 ? suffix_col : run_col;
     for (int j0 = 0; j0 < seg_len; j0 += kTile) {
       const int nk = min(kTile, seg_len - j0);
       __syncthreads();
       if constexpr (kBf) stage_tile_bf<DMAX>(Kb, kb, ks, j0, kTile, nk, d);
       else stage_tile<DMAX>(Ks, kb, ks, j0, kTile, nk, d);
       stage_tile<DMAX>(Vs, vb, vs, j0, kTile, nk, d);
+      if constexpr (kMask) stage_mask(Ms, a, row0 + tok0, kSimtQ, len - tok0, seg_col + j0, kTile, nk);
       __syncthreads();
       float s[kTile];
       float mt = m;
@@ -285,7 +327,9 @@ __global__ __launch_bounds__(kSimtQ * DMAX / 32) void simt_fwd(KernelArgs a) {
         float x;
         if constexpr (kBf) x = group_sum<kL>(dot_lds_bf<kL>(qb, Kb + j * DMAX, c)) * cs;
         else x = group_sum<kL>(dot_lds<kL>(q, Ks + j * DMAX, c));
-        const bool vis = j < nk && (!causal || j0 + j <= t);
+        bool vis;
+        if constexpr (kMask) vis = j < nk && !Ms[(t - tok0) * kTile + j];
+        else vis = j < nk && (!causal || j0 + j <= t);
         s[j] = vis ? x : -INFINITY;
         mt = fmaxf(mt, s[j]);
       }
@@ -303,10 +347,14 @@ __global__ __launch_bounds__(kSimtQ * DMAX / 32) void simt_fwd(KernelArgs a) {
       }
       m = mt;
     }
+    if (sg > 0) run_col += seg_len;
   }
   if (!valid) return;
-  store_slice<kL>(static_cast<T*>(a.out) + static_cast<int64_t>(row0 + t) * qs + qh * d, d, c, 1.f / l, o);
-  if (c == 0) a.lse[static_cast<int64_t>(qh) * a.total_q + row0 + t] = (m + log2f(l)) * kLn2;
+  // l == 0 only for a row a mask hides every key of: out 0, lse -inf
+  store_slice<kL>(static_cast<T*>(a.out) + static_cast<int64_t>(row0 + t) * qs + qh * d, d, c,
+                  l > 0.f ? 1.f / l : 0.f, o);
+  if (c == 0)
+    a.lse[static_cast<int64_t>(qh) * a.total_q + row0 + t] = l > 0.f ? (m + log2f(l)) * kLn2 : -INFINITY;
 }
 
 // ---------------------------------------------------------------------------
@@ -326,7 +374,7 @@ __global__ __launch_bounds__(256) void simt_delta(KernelArgs a) {
 
 // ---------------------------------------------------------------------------
 // dQ: block = kSimtQ queries of one head of one leaf (the forward's items).
-template <typename T, int DMAX>
+template <typename T, int DMAX, bool kMask>
 __global__ __launch_bounds__(kSimtQ * DMAX / 32) void simt_dq(KernelArgs a) {
   constexpr int kL = DMAX / 32, kTile = simt_tile<DMAX>();
   const int32_t* item = a.plan + a.off_fwd + 4 * blockIdx.x;
@@ -347,6 +395,7 @@ __global__ __launch_bounds__(kSimtQ * DMAX / 32) void simt_dq(KernelArgs a) {
   __shared__ __attribute__((aligned(16))) float Vs[kBf ? 4 : kTile * DMAX];
   __shared__ __attribute__((aligned(16))) bf16 Kb[kBf ? kTile * DMAX : 8];
   __shared__ __attribute__((aligned(16))) bf16 Vb[kBf ? kTile * DMAX : 8];
+  __shared__ uint8_t Ms[kMask ? kSimtQ * kTile : 4];
 
   const float cs = a.scale * kLog2e;
   f32x4 q[8], g[8], dq[8];
@@ -366,12 +415,15 @@ __global__ __launch_bounds__(kSimtQ * DMAX / 32) void simt_dq(KernelArgs a) {
   const float lse2 = a.lse_in[stat] * kLog2e;
   const float delta = a.delta[stat];
 
-  const int suffix_keys = min(len, tok0 + kSimtQ);
+  const int suffix_keys = kMask ? len : min(len, tok0 + kSimtQ);
+  const int suffix_col = kMask ? leaf_key_column(a, leaf, -1) : 0;
+  int run_col = 0;
   const T *kb, *vb;
   int64_t ks, vs;
   int seg_len;
   for (int sg = 0; key_segment<T>(a, leaf, sg, suffix_keys, kvh, kb, vb, ks, vs, seg_len); sg++) {
     const bool causal = sg == 0;
+    const int seg_col = sg == 0 ? suffix_col : run_col;
     for (int j0 = 0; j0 < seg_len; j0 += kTile) {
       const int nk = min(kTile, seg_len - j0);
       __syncthreads();
@@ -382,6 +434,7 @@ __global__ __launch_bounds__(kSimtQ * DMAX / 32) void simt_dq(KernelArgs a) {
       } else {
         stage_tile<DMAX>(Vs, vb, vs, j0, kTile, nk, d);
       }
+      if constexpr (kMask) stage_mask(Ms, a, row0 + tok0, kSimtQ, len - tok0, seg_col + j0, kTile, nk);
       __syncthreads();
       for (int j = 0; j < nk; j++) {
         float s, dp;
@@ -392,11 +445,14 @@ __global__ __launch_bounds__(kSimtQ * DMAX / 32) void simt_dq(KernelArgs a) {
           s = group_sum<kL>(dot_lds<kL>(q, Ks + j * DMAX, c));
           dp = group_sum<kL>(dot_lds<kL>(g, Vs + j * DMAX, c));
         }
-        const bool vis = !causal || j0 + j <= t;
+        bool vis;
+        if constexpr (kMask) vis = !Ms[(t - tok0) * kTile + j];
+        else vis = !causal || j0 + j <= t;
         const float ds = vis ? exp2f(s - lse2) * (dp - delta) : 0.f;
         axpy_lds<kL>(dq, ds, Ks + j * DMAX, c);
       }
     }
+    if (sg > 0) run_col += seg_len;
   }
   if (!valid) return;
   store_slice<kL>(static_cast<T*>(a.dq) + static_cast<int64_t>(row0 + t) * qs + qh * d, d, c, a.scale, dq);
@@ -408,7 +464,7 @@ __global__ __launch_bounds__(kSimtQ * DMAX / 32) void simt_dq(KernelArgs a) {
 // query head of the group) that sees the keys, in the plan's fixed order, so
 // a prefix node's gradient is summed over its descendant leaves in leaf order
 // without atomics.
-template <typename T, int DMAX>
+template <typename T, int DMAX, bool kMask>
 __global__ __launch_bounds__(kSimtKeys * DMAX / 32) void simt_dkdv(KernelArgs a) {
   constexpr int kL = DMAX / 32, kTile = simt_tile<DMAX>();
   const int32_t* item = a.plan + a.off_dkdv + DK_WORDS * blockIdx.x;
@@ -436,6 +492,7 @@ __global__ __launch_bounds__(kSimtKeys * DMAX / 32) void simt_dkdv(KernelArgs a)
   __shared__ __attribute__((aligned(16))) float Qs[kTile * DMAX];
   __shared__ __attribute__((aligned(16))) float Gs[kTile * DMAX];
   __shared__ float Ls[kTile], Ds[kTile];  // lse * log2e, delta
+  __shared__ uint8_t Ms[kMask ? kTile * kSimtKeys : 4];
 
   f32x4 kr[8], vr[8], dk[8], dv[8];
   load_slice<kL>(kbase + krow * (prefix ? ks : a.k_rs) + kvh * d, d, c, a.scale * kLog2e, kr);
@@ -449,6 +506,8 @@ __global__ __launch_bounds__(kSimtKeys * DMAX / 32) void simt_dkdv(KernelArgs a)
     const int leaf = qblk[2 * qb], tok0 = qblk[2 * qb + 1];
     const int row0 = cu[leaf], len = cu[leaf + 1] - cu[leaf];
     const int nblk = min(kSimtTile, len - tok0);
+    // mask column of the item's first key in this leaf's key sequence
+    const int col0 = kMask ? leaf_key_column(a, leaf, prefix ? seg : -1) + key0 : 0;
     for (int gh = 0; gh < a.group; gh++) {
       const int qh = kvh * a.group + gh;
       for (int sub = 0; sub < nblk; sub += kTile) {
@@ -462,6 +521,7 @@ __global__ __launch_bounds__(kSimtKeys * DMAX / 32) void simt_dkdv(KernelArgs a)
           Ls[i] = a.lse_in[at] * kLog2e;
           Ds[i] = a.delta[at];
         }
+        if constexpr (kMask) stage_mask(Ms, a, r0, kTile, nq, col0, kSimtKeys, seg_len - key0);
         __syncthreads();
         for (int i = 0; i < nq; i++) {
           f32x4 qi[8], gi[8];
@@ -470,7 +530,9 @@ __global__ __launch_bounds__(kSimtKeys * DMAX / 32) void simt_dkdv(KernelArgs a)
           const float s = group_sum<kL>(dot_regs(kr, qi));
           const float dp = group_sum<kL>(dot_regs(vr, gi));
           // causal: key kp is visible to query tok0 + sub + i iff kp <= tok0 + sub + i
-          const bool vis = prefix || kp <= tok0 + sub + i;
+          bool vis;
+          if constexpr (kMask) vis = !Ms[i * kSimtKeys + (kp - key0)];
+          else vis = prefix || kp <= tok0 + sub + i;
           const float p = vis ? exp2f(s - Ls[i]) : 0.f;
           const float ds = p * (dp - Ds[i]);
 #pragma unroll
@@ -502,27 +564,27 @@ __global__ __launch_bounds__(kSimtKeys * DMAX / 32) void simt_dkdv(KernelArgs a)
   store_slice<kL>(static_cast<T*>(prefix ? a.dpv : a.dv) + at, d, c, 1.f, dv);
 }
 
-template <typename T>
+template <typename T, bool kMask>
 int launch_fwd_t(const KernelArgs& a, hipStream_t s) {
   if (a.n_items <= 0) return 0;
-  if (a.d <= 64) hipLaunchKernelGGL((simt_fwd<T, 64>), dim3(a.n_items), dim3(kSimtQ * 2), 0, s, a);
-  else if (a.d <= 128) hipLaunchKernelGGL((simt_fwd<T, 128>), dim3(a.n_items), dim3(kSimtQ * 4), 0, s, a);
-  else hipLaunchKernelGGL((simt_fwd<T, 256>), dim3(a.n_items), dim3(kSimtQ * 8), 0, s, a);
+  if (a.d <= 64) hipLaunchKernelGGL((simt_fwd<T, 64, kMask>), dim3(a.n_items), dim3(kSimtQ * 2), 0, s, a);
+  else if (a.d <= 128) hipLaunchKernelGGL((simt_fwd<T, 128, kMask>), dim3(a.n_items), dim3(kSimtQ * 4), 0, s, a);
+  else hipLaunchKernelGGL((simt_fwd<T, 256, kMask>), dim3(a.n_items), dim3(kSimtQ * 8), 0, s, a);
   return hipGetLastError() == hipSuccess ? 0 : 4;
 }
 
-template <typename T>
+template <typename T, bool kMask>
 int launch_bwd_t(const KernelArgs& a, int n_fwd, int n_dkdv, hipStream_t s) {
   if (n_dkdv > 0) {
-    if (a.d <= 64) hipLaunchKernelGGL((simt_dkdv<T, 64>), dim3(n_dkdv), dim3(kSimtKeys * 2), 0, s, a);
-    else if (a.d <= 128) hipLaunchKernelGGL((simt_dkdv<T, 128>), dim3(n_dkdv), dim3(kSimtKeys * 4), 0, s, a);
-    else hipLaunchKernelGGL((simt_dkdv<T, 256>), dim3(n_dkdv), dim3(kSimtKeys * 8), 0, s, a);
+    if (a.d <= 64) hipLaunchKernelGGL((simt_dkdv<T, 64, kMask>), dim3(n_dkdv), dim3(kSimtKeys * 2), 0, s, a);
+    else if (a.d <= 128) hipLaunchKernelGGL((simt_dkdv<T, 128, kMask>), dim3(n_dkdv), dim3(kSimtKeys * 4), 0, s, a);
+    else hipLaunchKernelGGL((simt_dkdv<T, 256, kMask>), dim3(n_dkdv), dim3(kSimtKeys * 8), 0, s, a);
     if (hipGetLastError() != hipSuccess) return 4;
   }
   if (n_fwd > 0) {
-    if (a.d <= 64) hipLaunchKernelGGL((simt_dq<T, 64>), dim3(n_fwd), dim3(kSimtQ * 2), 0, s, a);
-    else if (a.d <= 128) hipLaunchKernelGGL((simt_dq<T, 128>), dim3(n_fwd), dim3(kSimtQ * 4), 0, s, a);
-    else hipLaunchKernelGGL((simt_dq<T, 256>), dim3(n_fwd), dim3(kSimtQ * 8), 0, s, a);
+    if (a.d <= 64) hipLaunchKernelGGL((simt_dq<T, 64, kMask>), dim3(n_fwd), dim3(kSimtQ * 2), 0, s, a);
+    else if (a.d <= 128) hipLaunchKernelGGL((simt_dq<T, 128, kMask>), dim3(n_fwd), dim3(kSimtQ * 4), 0, s, a);
+    else hipLaunchKernelGGL((simt_dq<T, 256, kMask>), dim3(n_fwd), dim3(kSimtQ * 8), 0, s, a);
     if (hipGetLastError() != hipSuccess) return 4;
   }
   return 0;
@@ -531,7 +593,8 @@ int launch_bwd_t(const KernelArgs& a, int n_fwd, int n_dkdv, hipStream_t s) {
 }  // namespace
 
 int launch_simt_fwd(const KernelArgs& a, bool fp32, hipStream_t s) {
-  return fp32 ? launch_fwd_t<float>(a, s) : launch_fwd_t<bf16>(a, s);
+  if (a.mask) return fp32 ? launch_fwd_t<float, true>(a, s) : launch_fwd_t<bf16, true>(a, s);
+  return fp32 ? launch_fwd_t<float, false>(a, s) : launch_fwd_t<bf16, false>(a, s);
 }
 
 int launch_delta(const KernelArgs& a, bool fp32, hipStream_t s) {
@@ -546,7 +609,9 @@ int launch_delta(const KernelArgs& a, bool fp32, hipStream_t s) {
 }
 
 int launch_simt_bwd(const KernelArgs& a, int n_fwd, int n_dkdv, bool fp32, hipStream_t s) {
-  return fp32 ? launch_bwd_t<float>(a, n_fwd, n_dkdv, s) : launch_bwd_t<bf16>(a, n_fwd, n_dkdv, s);
+  if (a.mask)
+    return fp32 ? launch_bwd_t<float, true>(a, n_fwd, n_dkdv, s) : launch_bwd_t<bf16, true>(a, n_fwd, n_dkdv, s);
+  return fp32 ? launch_bwd_t<float, false>(a, n_fwd, n_dkdv, s) : launch_bwd_t<bf16, false>(a, n_fwd, n_dkdv, s);
 }
 
 }  // namespace tpr

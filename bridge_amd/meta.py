@@ -34,6 +34,7 @@ _PF_N_FWD = 19
 _PF_N_DKDV = 21
 _PF_TOTAL_WORDS = 27
 _PF_DS_SLOTS = 30
+_PF_MASK_COLS = 32
 
 DS_STORE_DEFAULT_BYTES = 8 << 30  # the library's default dS store budget (TPR_DS_STORE_DEFAULT_BYTES)
 
@@ -77,6 +78,12 @@ class LaunchPlan:
         head_dim 128 and 256 when the store fits the plan's dS store budget);
         the workspace then holds the store."""
         return int(self.host[_PF_DS_SLOTS]) > 0
+
+    @property
+    def masked(self) -> bool:
+        """Whether the plan is for calls with a physical key mask (built with
+        ``masked=True``; SIMT kernels, the mask the only visibility rule)."""
+        return int(self.host[_PF_MASK_COLS]) > 0
 
     @property
     def num_forward_items(self) -> int:
@@ -206,6 +213,11 @@ class TPRPrefixMeta:
     def suffix_lengths(self) -> Tuple[int, ...]:
         return tuple(b - a for a, b in zip(self.cu_seqlens_q[:-1], self.cu_seqlens_q[1:]))
 
+    def max_keys(self) -> int:
+        """Longest key sequence of any leaf (ancestor prefix + own suffix):
+        the least column count of a key mask."""
+        return max((self.prefix_length(i) + s for i, s in enumerate(self.suffix_lengths())), default=0)
+
     def visible_pairs(self) -> int:
         """Sum over leaves of S_i * P_i + S_i (S_i + 1) / 2 (per query head)."""
         return sum(s * self.prefix_length(i) + s * (s + 1) // 2 for i, s in enumerate(self.suffix_lengths()))
@@ -213,7 +225,7 @@ class TPRPrefixMeta:
     # ---- launch plan -------------------------------------------------------
     def plan(self, num_q_heads: int, num_kv_heads: int, head_dim: int, dtype: torch.dtype,
              device: torch.device, *, recompute_dq: bool = False,
-             ds_store_budget: Optional[int] = None) -> LaunchPlan:
+             ds_store_budget: Optional[int] = None, masked: bool = False) -> LaunchPlan:
         """Build (once per configuration) the native launch plan and upload it.
 
         ``ds_store_budget``: bytes the backward's dS store may take (bf16
@@ -224,7 +236,12 @@ class TPRPrefixMeta:
         workspace is a few MB. ``None``: the library default,
         ``DS_STORE_DEFAULT_BYTES`` (8 GiB; the Qwen3-4B layer shape, prefix
         4096 + 4 x 4096 at GQA 32/8, needs 6.5 GB); ``0``: no store.
-        ``recompute_dq=True`` is the same as ``ds_store_budget=0``."""
+        ``recompute_dq=True`` is the same as ``ds_store_budget=0``.
+
+        ``masked=True``: the plan for calls that pass a physical key mask,
+        which is then the only visibility rule (the reference's custom-mask
+        mode); it runs the SIMT kernels, for any dtype and head size, with
+        no dS store."""
         if dtype == torch.bfloat16:
             code = _lib.TPR_DTYPE_BF16
         elif dtype == torch.float32:
@@ -232,8 +249,9 @@ class TPRPrefixMeta:
         else:
             raise ValueError(f"prefix attention supports torch.bfloat16 and torch.float32, got {dtype}")
         budget = ds_store_budget_bytes(ds_store_budget, recompute_dq)
-        flags = 0
-        key = (num_q_heads, num_kv_heads, head_dim, code, str(device), budget)
+        masked = bool(masked)
+        flags = _lib.TPR_PLAN_MASKED if masked else 0
+        key = (num_q_heads, num_kv_heads, head_dim, code, str(device), budget, masked)
         cached = self._plans.get(key)
         if cached is not None:
             return cached

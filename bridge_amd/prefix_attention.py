@@ -19,6 +19,13 @@ GPU without atomics.
 For one leaf under one node this equals the reference's
 rectangular_causal_attention(q, cat(prefix_k, k), cat(prefix_v, v))
 (rectangular_attention.py:125-209); see ``bridge_amd.rectangular_attention``.
+
+``attention_mask`` (optional, bool ``[Tq, L]``, True = hidden) replaces the
+causal rule by a physical key mask, the reference's custom-mask mode
+(rectangular_attention.py:112-122): row r is query row r, column c is key c
+of that row's leaf key sequence cat(ancestor nodes root first, own suffix),
+and L is at least ``meta.max_keys()``. Masked calls run on the SIMT kernels.
+A query row that sees no key gets output 0 and zero gradients.
 """
 
 from __future__ import annotations
@@ -130,8 +137,34 @@ def validate(q, k, v, prefix_k, prefix_v, meta: TPRPrefixMeta, softmax_scale):
     return softmax_scale
 
 
-def _forward(q, k, v, prefix_k, prefix_v, meta, scale):
-    plan = meta.plan(q.shape[1], k.shape[1], q.shape[2], q.dtype, q.device)
+def check_mask(attention_mask, q: torch.Tensor, meta: TPRPrefixMeta) -> Optional[torch.Tensor]:
+    """The physical key mask as the kernels read it (uint8 rows, nonzero =
+    hidden), or None. Exception types and wording follow the reference's
+    _validate_attention_mask (rectangular_attention.py:86-109)."""
+    if attention_mask is None:
+        return None
+    if not isinstance(attention_mask, torch.Tensor):
+        raise TypeError(f"attention_mask must be a torch.Tensor or None, got {type(attention_mask).__name__}")
+    if attention_mask.dtype != torch.bool:
+        raise ValueError(f"attention_mask must use torch.bool, got {attention_mask.dtype}")
+    if attention_mask.device != q.device:
+        raise ValueError(f"attention_mask must be on {q.device}, got {attention_mask.device}")
+    keys = meta.max_keys()
+    if attention_mask.ndim != 2 or attention_mask.shape[0] != meta.total_q or attention_mask.shape[1] < keys:
+        raise ValueError(f"attention_mask must have shape [{meta.total_q}, L] with L >= {keys} (query rows, "
+                         f"longest leaf key sequence), got {tuple(attention_mask.shape)}")
+    return attention_mask.contiguous().view(torch.uint8)
+
+
+def _mask_args(mask: Optional[torch.Tensor]) -> Tuple[Optional[int], int]:
+    """(pointer, row stride in bytes) of a checked mask for the ABI."""
+    if mask is None:
+        return None, 0
+    return _ptr(mask), int(mask.shape[1])
+
+
+def _forward(q, k, v, prefix_k, prefix_v, meta, scale, mask=None):
+    plan = meta.plan(q.shape[1], k.shape[1], q.shape[2], q.dtype, q.device, masked=mask is not None)
     out = _empty(q)
     lse = torch.empty((q.shape[1], q.shape[0]), dtype=torch.float32, device=q.device)
     if q.shape[0] == 0:
@@ -141,7 +174,7 @@ def _forward(q, k, v, prefix_k, prefix_v, meta, scale):
         _lib.ABI_VERSION, 0, scale, 0.0,
         plan.host.data_ptr(), plan.device.data_ptr(),
         _ptr(q), _ptr(k), _ptr(v), _ptr(prefix_k), _ptr(prefix_v), _ptr(out), _ptr(lse),
-        _row_stride(q), _row_stride(k), _row_stride(v))
+        _row_stride(q), _row_stride(k), _row_stride(v), *_mask_args(mask))
     _lib.check(lib.tpr_attn_fwd(ctypes.byref(params), ctypes.c_void_p(_stream_handle(q.device))), "tpr_attn_fwd")
     return out, lse
 
@@ -165,11 +198,11 @@ def _check_accumulators(accumulators, prefix_k) -> Tuple[torch.Tensor, torch.Ten
     return accumulators[0], accumulators[1]
 
 
-def _workspace(meta, q, k, budget, ws):
+def _workspace(meta, q, k, budget, ws, masked=False):
     """(plan, workspace) of the backward. A plan with a dS store whose
     workspace cannot be allocated falls back to the plan without one (a few
     MB), which gives the same gradients with a slower dQ."""
-    plan = meta.plan(q.shape[1], k.shape[1], q.shape[2], q.dtype, q.device, ds_store_budget=budget)
+    plan = meta.plan(q.shape[1], k.shape[1], q.shape[2], q.dtype, q.device, ds_store_budget=budget, masked=masked)
     if ws is not None or not plan.workspace_bytes:
         return plan, ws
     try:
@@ -183,14 +216,15 @@ def _workspace(meta, q, k, budget, ws):
 
 
 def _backward(q, k, v, prefix_k, prefix_v, out, lse, dout, meta, scale, *, phases=None, buffers=None,
-              prefix_grad_accumulators=None, ds_store_budget=None):
+              prefix_grad_accumulators=None, ds_store_budget=None, mask=None):
     """Enqueue the backward. ``buffers`` may supply preallocated dq, dk, dv,
     dprefix_k, dprefix_v and delta tensors; ``phases`` is a mask of
     _lib.TPR_BWD_* bits (default: all). With ``prefix_grad_accumulators`` (a
     pair of fp32 tensors shaped like prefix_k) the prefix gradients are added
     into that pair by the kernels (TPR_BWD_ACCUMULATE_PREFIX_F32), which is
     also what is returned for them. ``ds_store_budget``: the plan's dS store
-    budget in bytes (TPRPrefixMeta.plan; None = the library default)."""
+    budget in bytes (TPRPrefixMeta.plan; None = the library default).
+    ``mask``: the forward's key mask as check_mask returns it, or None."""
     b = dict(buffers or {})
     dq = b.get("dq") if b.get("dq") is not None else _empty(q)
     dk = b.get("dk") if b.get("dk") is not None else _empty(k)
@@ -210,14 +244,14 @@ def _backward(q, k, v, prefix_k, prefix_v, out, lse, dout, meta, scale, *, phase
             return dq, dk, dv, dpk, dpv
         return dq, dk, dv, dpk.zero_(), dpv.zero_()
     delta = b.get("delta") if b.get("delta") is not None else torch.empty_like(lse)
-    plan, ws = _workspace(meta, q, k, ds_store_budget, b.get("workspace"))
+    plan, ws = _workspace(meta, q, k, ds_store_budget, b.get("workspace"), masked=mask is not None)
     lib = _lib.load()
     params = _lib.TprBwdParams(
         _lib.ABI_VERSION, flags, scale, 0.0,
         plan.host.data_ptr(), plan.device.data_ptr(),
         _ptr(q), _ptr(k), _ptr(v), _ptr(prefix_k), _ptr(prefix_v), _ptr(out), _ptr(dout), _ptr(lse),
         _ptr(delta), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dpk), _ptr(dpv), _ptr(ws), plan.workspace_bytes,
-        _row_stride(q), _row_stride(k), _row_stride(v))
+        _row_stride(q), _row_stride(k), _row_stride(v), *_mask_args(mask))
     mask = phases if phases is not None else (_lib.TPR_BWD_DELTA | _lib.TPR_BWD_DKDV | _lib.TPR_BWD_DQ)
     _lib.check(lib.tpr_attn_bwd_phases(ctypes.byref(params), int(mask), ctypes.c_void_p(_stream_handle(q.device))),
                "tpr_attn_bwd")
@@ -226,7 +260,7 @@ def _backward(q, k, v, prefix_k, prefix_v, out, lse, dout, meta, scale, *, phase
 
 class TPRPrefixAttention(torch.autograd.Function):
     """(q, k, v, prefix_k, prefix_v, meta, softmax_scale, prefix_grad_accumulators,
-    recompute_dq, ds_store_budget) -> (out, lse).
+    recompute_dq, ds_store_budget, attention_mask) -> (out, lse).
 
     With ``prefix_grad_accumulators`` = (dK, dV), fp32 tensors shaped like
     prefix_k, the backward adds the prefix gradients into them (the relay of
@@ -241,20 +275,25 @@ class TPRPrefixAttention(torch.autograd.Function):
     0 = no store (``recompute_dq=True`` is the same). If the workspace of a
     plan with a store cannot be allocated, the backward falls back to the plan
     without one (same gradients, slower dQ).
+
+    ``attention_mask``: an optional physical key mask (module docstring),
+    which replaces the causal rule.
     """
 
     @staticmethod
     def forward(ctx, q, k, v, prefix_k, prefix_v, meta, softmax_scale=None, prefix_grad_accumulators=None,
-                recompute_dq=False, ds_store_budget=None):
+                recompute_dq=False, ds_store_budget=None, attention_mask=None):
         scale = validate(q, k, v, prefix_k, prefix_v, meta, softmax_scale)
+        mask = check_mask(attention_mask, q, meta)
         budget = ds_store_budget_bytes(ds_store_budget, recompute_dq)
         if prefix_grad_accumulators is not None:
             if prefix_k.requires_grad or prefix_v.requires_grad:
                 raise ValueError("prefix_k/prefix_v must not require grad when prefix_grad_accumulators is given")
             _check_accumulators(prefix_grad_accumulators, prefix_k)
         q, k, v, prefix_k, prefix_v = _inputs(q, k, v, prefix_k, prefix_v)
-        out, lse = _forward(q, k, v, prefix_k, prefix_v, meta, scale)
+        out, lse = _forward(q, k, v, prefix_k, prefix_v, meta, scale, mask)
         ctx.save_for_backward(q, k, v, prefix_k, prefix_v, out, lse)
+        ctx.mask = mask
         ctx.meta = meta
         ctx.scale = scale
         ctx.accumulators = prefix_grad_accumulators
@@ -270,29 +309,32 @@ class TPRPrefixAttention(torch.autograd.Function):
         dout = dout.contiguous()
         dq, dk, dv, dpk, dpv = _backward(q, k, v, prefix_k, prefix_v, out, lse, dout, ctx.meta, ctx.scale,
                                          prefix_grad_accumulators=ctx.accumulators,
-                                         ds_store_budget=ctx.ds_store_budget)
+                                         ds_store_budget=ctx.ds_store_budget, mask=ctx.mask)
         if ctx.accumulators is not None:
             dpk = dpv = None
-        return dq, dk, dv, dpk, dpv, None, None, None, None, None
+        return dq, dk, dv, dpk, dpv, None, None, None, None, None, None
 
 
 def tpr_prefix_attention(q, k, v, prefix_k, prefix_v, meta: TPRPrefixMeta, softmax_scale=None, *,
-                         prefix_grad_accumulators=None, recompute_dq=False, ds_store_budget=None):
+                         prefix_grad_accumulators=None, recompute_dq=False, ds_store_budget=None,
+                         attention_mask=None):
     """Functional form of TPRPrefixAttention; returns (out, lse)."""
     return TPRPrefixAttention.apply(q, k, v, prefix_k, prefix_v, meta, softmax_scale, prefix_grad_accumulators,
-                                    recompute_dq, ds_store_budget)
+                                    recompute_dq, ds_store_budget, attention_mask)
 
 
-def prefix_attention_forward(q, k, v, prefix_k, prefix_v, meta: TPRPrefixMeta, softmax_scale=None):
+def prefix_attention_forward(q, k, v, prefix_k, prefix_v, meta: TPRPrefixMeta, softmax_scale=None, *,
+                             attention_mask=None):
     """Forward only, no autograd graph: (out, lse)."""
     scale = validate(q, k, v, prefix_k, prefix_v, meta, softmax_scale)
+    mask = check_mask(attention_mask, q, meta)
     q, k, v, prefix_k, prefix_v = _inputs(q, k, v, prefix_k, prefix_v)
-    return _forward(q, k, v, prefix_k, prefix_v, meta, scale)
+    return _forward(q, k, v, prefix_k, prefix_v, meta, scale, mask)
 
 
 def prefix_attention_backward(q, k, v, prefix_k, prefix_v, out, lse, dout, meta: TPRPrefixMeta,
                               softmax_scale=None, *, phases=None, buffers=None, prefix_grad_accumulators=None,
-                              recompute_dq=False, ds_store_budget=None):
+                              recompute_dq=False, ds_store_budget=None, attention_mask=None):
     """Backward only: (dq, dk, dv, dprefix_k, dprefix_v) from saved out/lse.
 
     ``phases`` selects backward phases (mask of TPR_BWD_DELTA / _DKDV / _DQ,
@@ -305,9 +347,11 @@ def prefix_attention_backward(q, k, v, prefix_k, prefix_v, out, lse, dout, meta:
     ``ds_store_budget`` (bytes; None = the library default) or
     ``recompute_dq=True`` (= budget 0) select the plan (TPRPrefixMeta.plan);
     with a dS store the dQ phase reads what the dK/dV phase wrote, and a
-    ``workspace`` given in ``buffers`` must be of that plan's size."""
+    ``workspace`` given in ``buffers`` must be of that plan's size.
+    ``attention_mask``: the forward's physical key mask, if it had one."""
     scale = validate(q, k, v, prefix_k, prefix_v, meta, softmax_scale)
+    mask = check_mask(attention_mask, q, meta)
     tensors = [*_inputs(q, k, v, prefix_k, prefix_v), *(t.contiguous() for t in (out, lse, dout))]
     return _backward(*tensors[:7], tensors[7], meta, scale, phases=phases, buffers=buffers,
                      prefix_grad_accumulators=prefix_grad_accumulators,
-                     ds_store_budget=ds_store_budget_bytes(ds_store_budget, recompute_dq))
+                     ds_store_budget=ds_store_budget_bytes(ds_store_budget, recompute_dq), mask=mask)

@@ -8,9 +8,17 @@ the device check names a ROCm GPU where the reference names an NPU.
 
 Key/value carry the external prefix in front of the suffix, exactly as the
 reference's caller builds them (attention.py:150-158): the prefix length is
-``Skv - Sq`` and the mask is right-down causal (key j visible to query i iff
-j <= Skv - Sq + i; the reference's sparse mode 3). The call is one leaf under
-one prefix node of the sibling-batched ``TPRPrefixAttention``.
+``Skv - Sq`` and, without ``attention_mask``, the mask is right-down causal
+(key j visible to query i iff j <= Skv - Sq + i; the reference's sparse mode
+3). The call is one leaf under one prefix node of the sibling-batched
+``TPRPrefixAttention``.
+
+A physical ``attention_mask`` (bool ``[Sq, Skv]``, True = excluded) is the
+sole visibility rule, as in the reference's custom-mask mode (sparse mode 0
+with the token window open, :112-122): it may hide padding rows and columns
+or show more than the causal mask. It runs on the masked (SIMT) kernels,
+except a mask equal to the right-down causal one, which takes the unmasked
+kernels. A query row the mask hides entirely gets output 0 and no gradient.
 """
 
 from __future__ import annotations
@@ -102,8 +110,8 @@ def rectangular_causal_attention(
     query ``[Sq, 1, Hq, D]`` (post-RoPE), key/value ``[Skv, 1, Hkv, D]``
     including the external prefix; returns ``[Sq, 1, Hq * D]``.
     ``inner_precise`` is accepted for signature compatibility (accumulation
-    is always fp32). An ``attention_mask`` is accepted only when it equals the
-    right-down causal mask; other physical masks are not supported here.
+    is always fp32). ``attention_mask``: an optional physical ``[Sq, Skv]``
+    bool mask, True = excluded, which replaces the causal rule.
     """
     query_length, kv_length, query_heads, head_dim = _validate_inputs(query, key, value, dropout_p)
     _validate_attention_mask(attention_mask, query_length=query_length, kv_length=kv_length, device=query.device)
@@ -117,17 +125,19 @@ def rectangular_causal_attention(
         raise ValueError(f"softmax_scale must be finite and positive, got {softmax_scale}")
     if pre_tokens < kv_length:
         raise NotImplementedError("a preceding-token window shorter than the KV length is not supported")
-    if attention_mask is not None:
-        if not torch.equal(attention_mask, _right_down_causal_mask(query_length, kv_length, attention_mask.device)):
-            raise NotImplementedError("only the right-down causal attention mask is supported on MI355X")
+    if attention_mask is not None and torch.equal(
+            attention_mask, _right_down_causal_mask(query_length, kv_length, attention_mask.device)):
+        attention_mask = None  # the causal mask itself: the unmasked kernels
 
     prefix_length = kv_length - query_length
     q = query.squeeze(1)
     k = key.squeeze(1)
     v = value.squeeze(1)
     meta = _single_leaf_meta(prefix_length, query_length)
+    # one leaf: the mask's columns cat(prefix, suffix) are the leaf's key sequence
     output, _ = TPRPrefixAttention.apply(q[:, :, :], k[prefix_length:], v[prefix_length:],
-                                         k[:prefix_length], v[:prefix_length], meta, softmax_scale)
+                                         k[:prefix_length], v[:prefix_length], meta, softmax_scale,
+                                         None, False, None, attention_mask)
     expected_shape = (query_length, query_heads, head_dim)
     if tuple(output.shape) != expected_shape:
         raise RuntimeError(f"unexpected attention output shape: expected {expected_shape}, got {tuple(output.shape)}")

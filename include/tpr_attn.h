@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define TPR_ATTN_ABI_VERSION 5
+#define TPR_ATTN_ABI_VERSION 6
 
 typedef enum TprStatus {
   TPR_OK = 0,
@@ -89,12 +89,21 @@ typedef enum TprDtype {
  *                        layer shape (prefix 4096 + 4 x 4096, GQA 32/8) needs
  *                        6.5 GB, prefix 32768 + 8 x 2048 needs 35.5 GB
  *   ds_store_max_bytes > 0                      at most that many bytes
- * flags: 0, or TPR_PLAN_RECOMPUTE_DQ, which forces no store whatever the
- * budget (needed by tpr_attn_bwd_noalloc for shapes whose store would not fit
- * its scratch). Other paths ignore both. The store's size is
- * tpr_attn_bwd_workspace_bytes() of the plan minus that of the same tree
- * planned with budget 0. */
+ * TPR_PLAN_RECOMPUTE_DQ forces no store whatever the budget (needed by
+ * tpr_attn_bwd_noalloc for shapes whose store would not fit its scratch).
+ * Other paths ignore both. The store's size is tpr_attn_bwd_workspace_bytes()
+ * of the plan minus that of the same tree planned with budget 0.
+ *
+ * Key mask. TPR_PLAN_MASKED builds a plan for calls that pass a physical key
+ * mask (TprFwdParams.mask): the mask is then the only visibility rule, as in
+ * the reference's custom-mask mode (sparse mode 0, rectangular_attention.py:
+ * 112-122) -- the causal rule is not applied on top of it, so a mask may also
+ * show a leaf's later suffix keys. Such a plan always runs the SIMT kernels
+ * (any dtype and head size), with no dS store; every call with it must pass a
+ * mask, and a call with a mask must use such a plan.
+ * flags: 0 or an OR of TPR_PLAN_RECOMPUTE_DQ and TPR_PLAN_MASKED. */
 #define TPR_PLAN_RECOMPUTE_DQ 1
+#define TPR_PLAN_MASKED 2
 #define TPR_DS_STORE_DEFAULT (-1)
 #define TPR_DS_STORE_DEFAULT_BYTES (INT64_C(8) << 30)
 typedef struct TprTreeDesc {
@@ -105,7 +114,7 @@ typedef struct TprTreeDesc {
   int32_t num_kv_heads;
   int32_t head_dim;
   int32_t dtype; /* TprDtype */
-  int32_t flags; /* 0 or TPR_PLAN_RECOMPUTE_DQ */
+  int32_t flags; /* 0, TPR_PLAN_RECOMPUTE_DQ, TPR_PLAN_MASKED */
   const int32_t* cu_seqlens_q;
   const int32_t* node_offsets;
   const int32_t* leaf_ancestors;
@@ -138,6 +147,16 @@ typedef struct TprFwdParams {
   int64_t q_row_stride;
   int64_t k_row_stride;
   int64_t v_row_stride;
+  /* Physical key mask of a TPR_PLAN_MASKED plan (NULL with any other plan):
+   * bytes, nonzero = hidden, one row per query token (the rows of q), row r
+   * at mask + r * mask_row_stride. Column c of a row of leaf s is key c of
+   * that leaf's key sequence cat(ancestor nodes root first, own suffix), the
+   * columns of the reference's [Sq, Skv] bool mask for one leaf. A row reads
+   * only its leaf's columns; mask_row_stride (bytes, 0 = the minimum) must be
+   * at least the longest key sequence of any leaf. A query row that sees no
+   * key gets out = 0, lse = -inf and zero gradients. */
+  const uint8_t* mask;
+  int64_t mask_row_stride;
 } TprFwdParams;
 
 /* Backward: dq, dk, dv for the suffix tokens, and dprefix_k/dprefix_v summed
@@ -184,6 +203,9 @@ typedef struct TprBwdParams {
   int64_t q_row_stride;
   int64_t k_row_stride;
   int64_t v_row_stride;
+  /* the forward's key mask (TprFwdParams.mask) */
+  const uint8_t* mask;
+  int64_t mask_row_stride;
 } TprBwdParams;
 
 /* ABI version compiled into the library (TPR_ATTN_ABI_VERSION). */

@@ -24,6 +24,12 @@ It restates, in fresh code, the reference's fp32 math for the hot path:
   order (kv_stack.py:175-203 split per ancestor slice, prefix_state.py:546-573
   sibling accumulation; here the sum is kept in the compute dtype instead of
   the reference's bf16 ``add_``).
+* ``tree_forward`` / ``tree_backward`` with ``mask`` -- the reference's
+  custom-mask mode (rectangular_attention.py:112-122, sparse mode 0): a
+  physical bool mask [Tq, L] (True = excluded; column c = key c of the
+  row's leaf sequence cat(ancestors, suffix)) is the only visibility rule; a
+  row that sees no key gets out 0, lse -inf and no gradient (the fully-masked
+  padding row of equivalence/test_rectangular_attention_npu.py:149-284).
 * ``tree_autograd`` -- the same tree computed the reference's way: one dense
   ``prefix_attention`` per leaf on freshly concatenated anchors, gradients by
   autograd, anchor gradients split per ancestor and summed in leaf order.
@@ -36,7 +42,12 @@ Parity pins (each is a test in tests/test_oracle.py):
   sibling sum invariants (unit/test_kv_stack.py:79-120), batched-tree ==
   sum of single-leaf runs (unit/test_segment_executor.py:291-325),
   torch scaled_dot_product_attention in fp64 with an explicit mask, and
-  central finite differences of the explicit backward.
+  central finite differences of the explicit backward. The masked forms:
+  scaled_dot_product_attention in fp64 (values and autograd gradients) with
+  random masks that show later suffix keys, the causal mask giving the
+  unmasked result, and the reference's padding equivalence (a masked padding
+  row and column leave the logical rows' results unchanged, the padding
+  gets zero gradient, a fully masked row zero output).
 """
 
 from __future__ import annotations
@@ -241,12 +252,24 @@ def _head_groups(hq, hkv, heads_per_chunk):
         yield h0, min(hkv, h0 + kv_per_chunk)
 
 
+def _visible(tree: Tree, s, plen, mask, device):
+    """[S, plen + S] bool: keys of leaf s each query row sees -- the causal
+    rule j <= plen + i, or the complement of the physical ``mask`` rows."""
+    a, b = tree.leaf_range(s)
+    if mask is not None:
+        return ~mask[a:b, :plen + b - a].to(device)
+    col = torch.arange(plen + b - a, device=device)
+    return col[None, :] <= plen + torch.arange(b - a, device=device)[:, None]
+
+
 def tree_forward(q, k, v, pk, pv, tree: Tree, scale=None, *, compute_dtype=torch.float64,
-                 heads_per_chunk=64):
+                 heads_per_chunk=64, mask=None):
     """Forward over a packed tree. Returns (out [Tq,Hq,D] compute_dtype, lse [Hq,Tq] compute_dtype).
 
     Chunked over leaves and KV-head groups to bound memory; each chunk is the
-    dense masked softmax of prefix_attention.
+    dense masked softmax of prefix_attention. ``mask`` (bool [Tq, L], True =
+    excluded) replaces the causal rule; rows that see no key get out 0 and
+    lse -inf.
     """
     tq, hq, d = q.shape
     hkv = k.shape[1]
@@ -260,9 +283,7 @@ def tree_forward(q, k, v, pk, pv, tree: Tree, scale=None, *, compute_dtype=torch
         if b == a:
             continue
         keys, values, plen = _leaf_kv(tree, s, k, v, pk, pv)
-        length = b - a
-        col = torch.arange(plen + length, device=q.device)
-        visible = col[None, :] <= plen + torch.arange(length, device=q.device)[:, None]
+        visible = _visible(tree, s, plen, mask, q.device)
         for g0, g1 in _head_groups(hq, hkv, heads_per_chunk):
             qs = q[a:b, g0 * group:g1 * group].to(cd).transpose(0, 1)                     # [h,S,D]
             ks = keys[:, g0:g1].to(cd).repeat_interleave(group, 1).permute(1, 2, 0).contiguous()
@@ -270,22 +291,24 @@ def tree_forward(q, k, v, pk, pv, tree: Tree, scale=None, *, compute_dtype=torch
             sc = torch.matmul(qs, ks) * scale
             sc = sc.masked_fill(~visible, float("-inf"))
             m = sc.amax(-1, keepdim=True)
+            m = torch.where(torch.isfinite(m), m, torch.zeros_like(m))  # a row that sees no key: w = 0
             w = torch.exp(sc - m)
             l = w.sum(-1, keepdim=True)
-            o = torch.matmul(w / l, vs)
+            o = torch.matmul(w / torch.where(l > 0, l, torch.ones_like(l)), vs)
             out[a:b, g0 * group:g1 * group] = o.transpose(0, 1)
             lse[g0 * group:g1 * group, a:b] = (m + torch.log(l))[..., 0]
     return out, lse
 
 
 def tree_backward(q, k, v, pk, pv, tree: Tree, dout, scale=None, *, compute_dtype=torch.float64,
-                  heads_per_chunk=64, out=None, lse=None):
+                  heads_per_chunk=64, out=None, lse=None, mask=None):
     """Explicit backward over a packed tree: returns (dq, dk, dv, dpk, dpv) in compute_dtype.
 
     Per (leaf, KV-head group): P = exp(scale*QK^T - lse), dV = P^T dO,
     dP = dO V^T, dS = P * (dP - rowsum(dO*O)), dQ = scale*dS K,
     dK = scale*dS^T Q. Prefix gradients of leaf s are split back to each
-    ancestor node's rows and added in leaf order.
+    ancestor node's rows and added in leaf order. ``mask`` as in
+    tree_forward (P is 0 wherever the key is hidden).
     """
     tq, hq, d = q.shape
     hkv = k.shape[1]
@@ -293,7 +316,8 @@ def tree_backward(q, k, v, pk, pv, tree: Tree, dout, scale=None, *, compute_dtyp
     scale = d ** -0.5 if scale is None else float(scale)
     cd = compute_dtype
     if out is None or lse is None:
-        out, lse = tree_forward(q, k, v, pk, pv, tree, scale, compute_dtype=cd, heads_per_chunk=heads_per_chunk)
+        out, lse = tree_forward(q, k, v, pk, pv, tree, scale, compute_dtype=cd, heads_per_chunk=heads_per_chunk,
+                                mask=mask)
     dq = torch.zeros(tq, hq, d, dtype=cd, device=q.device)
     dk = torch.zeros(k.shape, dtype=cd, device=q.device)
     dv = torch.zeros(v.shape, dtype=cd, device=q.device)
@@ -305,9 +329,7 @@ def tree_backward(q, k, v, pk, pv, tree: Tree, dout, scale=None, *, compute_dtyp
             continue
         keys, values, plen = _leaf_kv(tree, s, k, v, pk, pv)
         rows = torch.tensor(tree.prefix_rows(s), dtype=torch.long, device=q.device)
-        length = b - a
-        col = torch.arange(plen + length, device=q.device)
-        visible = col[None, :] <= plen + torch.arange(length, device=q.device)[:, None]
+        visible = _visible(tree, s, plen, mask, q.device)
         for g0, g1 in _head_groups(hq, hkv, heads_per_chunk):
             hs = slice(g0 * group, g1 * group)
             qs = q[a:b, hs].to(cd).transpose(0, 1)                                            # [h,S,D]

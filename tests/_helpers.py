@@ -26,12 +26,32 @@ def make_inputs(meta, hq, hkv, d, dtype, seed, device):
     return [torch.randn(s, generator=gen).to(dtype).to(device) for s in shapes]
 
 
-def oracle(meta, q, k, v, pk, pv, dout, scale, compute_dtype=torch.float64, device="cpu"):
+def oracle(meta, q, k, v, pk, pv, dout, scale, compute_dtype=torch.float64, device="cpu", mask=None):
     tree = tree_of(meta)
     args = [t.detach().to(device) for t in (q, k, v, pk, pv)]
-    out, lse = tree_forward(*args, tree, scale, compute_dtype=compute_dtype)
-    grads = tree_backward(*args, tree, dout.detach().to(device), scale, compute_dtype=compute_dtype, out=out, lse=lse)
+    if mask is not None:
+        mask = mask.to(device)
+    out, lse = tree_forward(*args, tree, scale, compute_dtype=compute_dtype, mask=mask)
+    grads = tree_backward(*args, tree, dout.detach().to(device), scale, compute_dtype=compute_dtype, out=out, lse=lse,
+                          mask=mask)
     return out, lse, grads
+
+
+def random_key_mask(tree, gen, hidden=0.4, empty_rows=()):
+    """bool [Tq, L] (True = hidden) over each row's leaf key sequence: about
+    ``hidden`` of the keys hidden at random -- so rows see later suffix keys
+    too -- every row keeping at least one key except those in ``empty_rows``,
+    which see none. L is the longest key sequence of any leaf."""
+    lens = [len(tree.prefix_rows(s)) + tree.leaf_range(s)[1] - tree.leaf_range(s)[0]
+            for s in range(tree.num_leaves)]
+    mask = torch.rand(tree.cu_seqlens_q[-1], max(lens), generator=gen) < hidden
+    for s in range(tree.num_leaves):
+        a, b = tree.leaf_range(s)
+        for r in range(a, b):
+            mask[r, torch.randint(0, lens[s], (1,), generator=gen).item()] = False
+    for r in empty_rows:
+        mask[r] = True
+    return mask
 
 
 def max_abs(a, b) -> float:

@@ -26,7 +26,7 @@ def _declared_functions():
 
 def test_library_loads_and_reports_abi_version():
     lib = _lib.load()
-    assert lib.tpr_attn_abi_version() == _lib.ABI_VERSION == 5
+    assert lib.tpr_attn_abi_version() == _lib.ABI_VERSION == 6
 
 
 def test_every_declared_symbol_is_exported_and_bound():
@@ -170,6 +170,41 @@ def test_bad_row_strides_are_rejected_before_any_launch():
         b.k_row_stride = hkv * d - 8
         assert lib.tpr_attn_bwd(ctypes.byref(b), None) != 0
         assert b"k_row_stride" in lib.tpr_attn_last_error() or b"must not be NULL" in lib.tpr_attn_last_error()
+
+
+def test_key_mask_rules_are_checked_before_any_launch():
+    """A key mask needs a TPR_PLAN_MASKED plan, such a plan needs a mask, and
+    the mask rows must hold the longest key sequence (prefix 8 + suffix 4 =
+    12 bytes here). The checks run on the host before anything is enqueued
+    (the pointers below are never dereferenced)."""
+    import torch
+
+    from bridge_amd import TPRPrefixMeta
+    lib = _lib.load()
+    meta = TPRPrefixMeta.shared_prefix(8, [4])
+    plain = meta.plan(4, 2, 128, torch.bfloat16, torch.device("cpu"))
+    masked = meta.plan(4, 2, 128, torch.bfloat16, torch.device("cpu"), masked=True)
+    assert not plain.masked and masked.masked and masked.path == "simt" and masked.workspace_bytes == 0
+    cases = [(plain, 1 << 30, 0, b"TPR_PLAN_MASKED"), (masked, None, 0, b"must not be NULL"),
+             (masked, 1 << 30, 11, b"at least 12")]
+    for plan, mask, stride, words in cases:
+        p = _fake_fwd_params(plan)
+        p.mask, p.mask_row_stride = mask, stride
+        assert lib.tpr_attn_fwd(ctypes.byref(p), None) == _lib.TPR_ERR_INVALID_ARGUMENT
+        assert words in lib.tpr_attn_last_error(), (words, lib.tpr_attn_last_error())
+        b = _lib.TprBwdParams()
+        b.abi_version = _lib.ABI_VERSION
+        b.softmax_scale = 0.1
+        b.plan_host = b.plan_device = plan.host.data_ptr()
+        fake = 1 << 20
+        for name in ("q", "k", "v", "prefix_k", "prefix_v", "out", "dout", "lse", "delta", "dq", "dk", "dv",
+                     "dprefix_k", "dprefix_v", "workspace"):
+            setattr(b, name, fake)
+            fake += 1 << 20
+        b.workspace_bytes = plan.workspace_bytes
+        b.mask, b.mask_row_stride = mask, stride
+        assert lib.tpr_attn_bwd(ctypes.byref(b), None) == _lib.TPR_ERR_INVALID_ARGUMENT
+        assert words in lib.tpr_attn_last_error(), (words, lib.tpr_attn_last_error())
 
 
 def test_fused_projection_views_pass_through_with_their_row_stride():

@@ -110,17 +110,76 @@ def test_explicit_causal_mask_matches_sparse_mode_3_forward_and_backward(cuda_de
             torch.testing.assert_close(mine.float().cpu(), theirs, atol=6e-3, rtol=2e-2)
 
 
-def test_physical_padding_mask_is_refused(cuda_device):
-    """The reference's :149-284 pads Q/KV with one physical row and masks it
-    with a custom mask. The drop-in accepts only the right-down causal mask
-    (the one mask the sibling-batched kernel computes): any other mask raises
-    NotImplementedError before a launch."""
+def test_physical_padding_mask_matches_logical_attention_forward_and_backward(cuda_device):
+    """The reference's :149-284: Q 63 + 1 and KV 127 + 1 physical rows, GQA
+    4/2, D 64, bf16. The padding key is hidden by a custom mask (the padding
+    query sees keys up to position 126), or, with ``inner_precise=2`` there,
+    the padding query row is hidden entirely. Against the logical call (63 x
+    127, causal mask): output within 6e-3 / 1e-2, gradients of the logical
+    rows within 6e-3 / 2e-2, the padding rows' gradients zero, and the fully
+    hidden row's output zero -- the reference's assertions. The masked calls
+    run on the masked SIMT kernels, the logical one on the 16x16x32 MFMA
+    kernels."""
     from bridge_amd import rectangular_causal_attention
-    (q, k, v), _ = _inputs(2027, 64, 128, 4, 2, 64, cuda_device)
+    lq, lkv, hq, hkv, d = 63, 127, 4, 2, 64
+    scale = d ** -0.5
+    g = torch.Generator().manual_seed(2027)
+    logical = [torch.randn(n, 1, h, d, generator=g).bfloat16().to(cuda_device)
+               for n, h in ((lq, hq), (lkv, hkv), (lkv, hkv))]
+    physical = [torch.cat((t, torch.randn(1, *t.shape[1:], generator=g).bfloat16().to(cuda_device))) for t in logical]
+    grad_output = torch.randn(lq, 1, hq * d, generator=g).bfloat16().to(cuda_device)
+    physical_grad_output = torch.cat((grad_output, torch.zeros_like(grad_output[:1])))
     query_positions = torch.arange(64, 128, device=cuda_device).clamp_max(126)
     key_positions = torch.arange(128, device=cuda_device).clamp_max(126)
-    key_valid = torch.arange(128, device=cuda_device) < 127
-    physical_mask = torch.logical_or(~key_valid.unsqueeze(0),
-                                     key_positions.unsqueeze(0) > query_positions.unsqueeze(1))
-    with pytest.raises(NotImplementedError):
-        rectangular_causal_attention(q, k, v, softmax_scale=64 ** -0.5, attention_mask=physical_mask)
+    key_valid = torch.arange(128, device=cuda_device) < lkv
+    physical_mask = torch.logical_or(~key_valid.unsqueeze(0), key_positions.unsqueeze(0) > query_positions.unsqueeze(1))
+    invalid_row_mask = torch.logical_or(physical_mask, (torch.arange(64, device=cuda_device) >= lq).unsqueeze(1))
+
+    la = [t.clone().requires_grad_(True) for t in logical]
+    logical_output = rectangular_causal_attention(*la, softmax_scale=scale,
+                                                  attention_mask=_right_down_mask(lq, lkv, cuda_device))
+    logical_output.backward(grad_output)
+    runs = []
+    for mask, precise in ((physical_mask, 0), (invalid_row_mask, 2)):
+        pa = [t.clone().requires_grad_(True) for t in physical]
+        out = rectangular_causal_attention(*pa, softmax_scale=scale, attention_mask=mask, inner_precise=precise)
+        out.backward(physical_grad_output)
+        runs.append((out, pa))
+    torch.cuda.synchronize()
+    torch.testing.assert_close(runs[0][0][:lq].float(), logical_output.float(), atol=6e-3, rtol=1e-2)
+    for _, inputs in runs:
+        for phys, log in zip(inputs, la):
+            torch.testing.assert_close(phys.grad[:log.shape[0]].float(), log.grad.float(), atol=6e-3, rtol=2e-2)
+            torch.testing.assert_close(phys.grad[log.shape[0]:], torch.zeros_like(phys.grad[log.shape[0]:]))
+    invalid_row_output = runs[1][0]
+    torch.testing.assert_close(invalid_row_output[:lq].float(), logical_output.float(), atol=6e-3, rtol=1e-2)
+    torch.testing.assert_close(invalid_row_output[lq:], torch.zeros_like(invalid_row_output[lq:]))
+
+
+def test_physical_mask_against_the_fp32_oracle(cuda_device):
+    """A physical mask that shows later keys too (not a causal mask), through
+    the drop-in: output and gradients within the reference's bf16 tolerances
+    (6e-3 / 1e-2, grads 6e-3 / 2e-2) of the fp64 oracle with the same mask."""
+    from bridge_amd import TPRPrefixMeta, rectangular_causal_attention
+    from oracle.tpr_oracle import tree_backward, tree_forward
+    from _helpers import random_key_mask, tree_of
+    sq, skv, hq, hkv, d = 40, 100, 4, 2, 64
+    p = skv - sq
+    scale = d ** -0.5
+    (q, k, v), dout = _inputs(2028, sq, skv, hq, hkv, d, cuda_device)
+    tree = tree_of(TPRPrefixMeta.shared_prefix(p, [sq]))
+    mask = random_key_mask(tree, torch.Generator().manual_seed(7))
+    assert mask.shape == (sq, skv)
+    qa, ka, va = (t.clone().requires_grad_(True) for t in (q, k, v))
+    out = rectangular_causal_attention(qa, ka, va, softmax_scale=scale, attention_mask=mask.to(cuda_device))
+    out.backward(dout)
+    torch.cuda.synchronize()
+    qt, kt, vt = (t.double().cpu()[:, 0] for t in (q, k, v))
+    args = (qt, kt[p:], vt[p:], kt[:p], vt[:p], tree)
+    ro, lse = tree_forward(*args, scale, mask=mask)
+    dq, dk, dv, dpk, dpv = tree_backward(*args, dout.double().cpu().view(sq, hq, d), scale, out=ro, lse=lse,
+                                         mask=mask)
+    torch.testing.assert_close(out.double().cpu().view(sq, hq, d), ro, atol=6e-3, rtol=1e-2)
+    for mine, theirs in ((qa.grad[:, 0], dq), (ka.grad[:, 0], torch.cat((dpk, dk))),
+                         (va.grad[:, 0], torch.cat((dpv, dv)))):
+        torch.testing.assert_close(mine.double().cpu(), theirs, atol=6e-3, rtol=2e-2)

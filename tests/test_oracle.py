@@ -6,6 +6,7 @@ import math
 import pytest
 import torch
 
+from _helpers import random_key_mask
 from oracle.tpr_oracle import (
     Tree,
     block_reference,
@@ -270,3 +271,108 @@ def test_visible_pairs_matches_closed_form():
     anc = [[0, 1 + b] for b in range(4) for _ in range(4)]
     tree = Tree([i * leaf for i in range(17)], [0, root] + [root + (b + 1) * branch for b in range(4)], anc)
     assert visible_pairs(tree) == 58728448
+
+
+# ---- masked forms: the custom-mask mode of rectangular_attention.py:112-122 --
+def _sdpa_tree(q, k, v, pk, pv, tree, dout, scale, mask):
+    """Per leaf, torch's scaled_dot_product_attention in fp64 with the mask's
+    complement as attn_mask, gradients by autograd (summed over leaves)."""
+    ins = [t.detach().clone().requires_grad_(True) for t in (q, k, v, pk, pv)]
+    qa, ka, va, pka, pva = ins
+    group = q.shape[1] // k.shape[1]
+    outs = []
+    for s in range(tree.num_leaves):
+        a, b = tree.leaf_range(s)
+        rows = torch.tensor(tree.prefix_rows(s), dtype=torch.long)
+        keys = torch.cat((pka[rows], ka[a:b])).repeat_interleave(group, 1).transpose(0, 1)
+        vals = torch.cat((pva[rows], va[a:b])).repeat_interleave(group, 1).transpose(0, 1)
+        allowed = ~mask[a:b, :keys.shape[1]]
+        outs.append(torch.nn.functional.scaled_dot_product_attention(
+            qa[a:b].transpose(0, 1), keys, vals, attn_mask=allowed, scale=scale).transpose(0, 1))
+    out = torch.cat(outs)
+    (out * dout).sum().backward()
+    return out.detach(), [t.grad for t in ins]
+
+
+@pytest.mark.parametrize("name", sorted(TREES))
+def test_masked_tree_matches_sdpa_fp64_values_and_gradients(name):
+    tree = TREES[name]
+    q, k, v, pk, pv, dout = _random_tree_inputs(31, tree)
+    mask = random_key_mask(tree, torch.Generator().manual_seed(3))
+    # the mask shows some query a later key of its own suffix (not causal)
+    later = [(r, c) for s in range(tree.num_leaves) for r in range(*tree.leaf_range(s))
+             for c in range(len(tree.prefix_rows(s)) + r - tree.leaf_range(s)[0] + 1,
+                            len(tree.prefix_rows(s)) + tree.leaf_range(s)[1] - tree.leaf_range(s)[0])
+             if not mask[r, c]]
+    assert later
+    out, lse = tree_forward(q, k, v, pk, pv, tree, 0.45, mask=mask)
+    grads = tree_backward(q, k, v, pk, pv, tree, dout, 0.45, out=out, lse=lse, mask=mask)
+    ref, ref_grads = _sdpa_tree(q, k, v, pk, pv, tree, dout, 0.45, mask)
+    torch.testing.assert_close(out, ref, atol=1e-12, rtol=1e-12)
+    for mine, theirs in zip(grads, ref_grads):
+        torch.testing.assert_close(mine, theirs, atol=1e-11, rtol=1e-9)
+    # lse: torch.logsumexp of the visible scaled scores
+    for s in range(tree.num_leaves):
+        a, b = tree.leaf_range(s)
+        rows = tree.prefix_rows(s)
+        keys = torch.cat((pk[rows], k[a:b])).repeat_interleave(2, 1)
+        sc = torch.einsum("thd,khd->htk", q[a:b], keys) * 0.45
+        sc = sc.masked_fill(mask[a:b, :keys.shape[0]][None], float("-inf"))
+        torch.testing.assert_close(lse[:, a:b], torch.logsumexp(sc, -1), atol=1e-12, rtol=1e-12)
+
+
+@pytest.mark.parametrize("name", sorted(TREES))
+def test_causal_mask_gives_the_unmasked_tree(name):
+    tree = TREES[name]
+    q, k, v, pk, pv, dout = _random_tree_inputs(32, tree)
+    lens = [len(tree.prefix_rows(s)) + tree.leaf_range(s)[1] - tree.leaf_range(s)[0] for s in range(tree.num_leaves)]
+    mask = torch.ones(tree.cu_seqlens_q[-1], max(lens), dtype=torch.bool)
+    for s in range(tree.num_leaves):
+        a, b = tree.leaf_range(s)
+        plen = len(tree.prefix_rows(s))
+        for i in range(b - a):
+            mask[a + i, :plen + i + 1] = False
+    plain = tree_backward(q, k, v, pk, pv, tree, dout, 0.4)
+    masked = tree_backward(q, k, v, pk, pv, tree, dout, 0.4, mask=mask)
+    for x, y in zip(plain, masked):
+        torch.testing.assert_close(x, y, atol=0, rtol=0)
+    assert torch.equal(tree_forward(q, k, v, pk, pv, tree, 0.4)[1], tree_forward(q, k, v, pk, pv, tree, 0.4,
+                                                                                 mask=mask)[1])
+
+
+def test_physical_padding_mask_equals_logical_attention():
+    """equivalence/test_rectangular_attention_npu.py:149-284 on the oracle, in
+    fp64: Q 63 + 1 padding row and KV 127 + 1 padding row (prefix 64), GQA
+    4/2, D 64. With the padding key hidden (and the padding query seeing keys
+    up to position 126), the logical rows' output and gradients equal the
+    unpadded causal attention, the padding rows get zero gradient (their
+    upstream gradient is zero); with the padding query row hidden entirely its
+    output is 0 and its lse -inf."""
+    gen = torch.Generator().manual_seed(2027)
+    sq, skv, hq, hkv, d = 63, 127, 4, 2, 64
+    p = skv - sq
+    q, k, v = (torch.randn(n, h, d, generator=gen, dtype=torch.float64) for n, h in ((sq, hq), (skv, hkv), (skv, hkv)))
+    dout = torch.randn(sq, hq, d, generator=gen, dtype=torch.float64)
+    pq, pk_, pv_ = (torch.cat((t, torch.randn(1, *t.shape[1:], generator=gen, dtype=torch.float64))) for t in (q, k, v))
+    pdout = torch.cat((dout, torch.zeros(1, hq, d, dtype=torch.float64)))
+    logical = tree_backward(q, k[p:], v[p:], k[:p], v[:p], Tree.single(p, [sq]), dout, d ** -0.5)
+    logical_out, _ = tree_forward(q, k[p:], v[p:], k[:p], v[:p], Tree.single(p, [sq]), d ** -0.5)
+    query_positions = torch.arange(64, 128).clamp_max(126)
+    key_positions = torch.arange(128).clamp_max(126)
+    key_valid = torch.arange(128) < skv
+    physical = ~key_valid[None, :] | (key_positions[None, :] > query_positions[:, None])
+    invalid_row = physical | (torch.arange(64) >= sq)[:, None]
+    tree = Tree.single(p, [sq + 1])
+    for mask in (physical, invalid_row):
+        args = (pq, pk_[p:], pv_[p:], pk_[:p], pv_[:p], tree)
+        out, lse = tree_forward(*args, d ** -0.5, mask=mask)
+        dq, dk, dv, dpk, dpv = tree_backward(*args, pdout, d ** -0.5, out=out, lse=lse, mask=mask)
+        torch.testing.assert_close(out[:sq], logical_out, atol=1e-12, rtol=1e-12)
+        torch.testing.assert_close(dq[:sq], logical[0], atol=1e-12, rtol=1e-12)
+        torch.testing.assert_close(torch.cat((dpk, dk[:sq])), torch.cat((logical[3], logical[1])), atol=1e-12,
+                                   rtol=1e-12)
+        torch.testing.assert_close(torch.cat((dpv, dv[:sq])), torch.cat((logical[4], logical[2])), atol=1e-12,
+                                   rtol=1e-12)
+        for g in (dq[sq:], dk[sq:], dv[sq:]):
+            assert torch.count_nonzero(g) == 0
+    assert torch.count_nonzero(out[sq:]) == 0 and bool(torch.isneginf(lse[:, sq:]).all())

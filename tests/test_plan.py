@@ -15,7 +15,7 @@ CPU = torch.device("cpu")
 PF = dict(MAGIC=0, NUM_LEAVES=2, NUM_NODES=3, MAX_DEPTH=4, TOTAL_Q=5, TOTAL_PREFIX=6, HQ=7, HKV=8, D=9,
           PATH=11, OFF_CU=12, OFF_NODE_OFF=13, OFF_ANC=14, OFF_NODE_LEAF=15, N_QBLK=16, OFF_QBLK=17,
           OFF_LEAF_QBLK=18, N_FWD=19, OFF_FWD=20, N_DKDV=21, OFF_DKDV=22, N_RED=23, TOTAL_WORDS=27,
-          OFF_RUNS=28, MAX_RUNS=29, DS_SLOTS=30, OFF_DS=31)
+          OFF_RUNS=28, MAX_RUNS=29, DS_SLOTS=30, OFF_DS=31, MASK_COLS=32)
 
 FWD_WAVES = 8  # waves per forward / dQ workgroup (kFwdWaves)
 
@@ -366,7 +366,8 @@ def test_planner_rejects_unknown_plan_flags():
     cu = (ctypes.c_int32 * 2)(0, 4)
     no = (ctypes.c_int32 * 2)(0, 8)
     an = (ctypes.c_int32 * 1)(0)
-    for flags, ok in ((0, True), (_lib.TPR_PLAN_RECOMPUTE_DQ, True), (2, False), (-1, False)):
+    for flags, ok in ((0, True), (_lib.TPR_PLAN_RECOMPUTE_DQ, True), (_lib.TPR_PLAN_MASKED, True),
+                      (_lib.TPR_PLAN_MASKED | _lib.TPR_PLAN_RECOMPUTE_DQ, True), (4, False), (-1, False)):
         desc = _lib.TprTreeDesc(1, 1, 1, 4, 2, 128, _lib.TPR_DTYPE_BF16, flags, ctypes.cast(cu, ctypes.c_void_p),
                                 ctypes.cast(no, ctypes.c_void_p), ctypes.cast(an, ctypes.c_void_p))
         words = ctypes.c_int64(0)
@@ -374,6 +375,31 @@ def test_planner_rejects_unknown_plan_flags():
         assert (rc == _lib.TPR_OK) == ok, (flags, rc)
         if not ok:
             assert rc == _lib.TPR_ERR_INVALID_ARGUMENT and b"plan flags" in lib.tpr_attn_last_error()
+
+
+@pytest.mark.parametrize("dtype, d", [(torch.bfloat16, 128), (torch.bfloat16, 64), (torch.float32, 96)])
+def test_masked_plan_runs_simt_items_over_every_suffix_key(dtype, d):
+    """A masked plan (the mask the only visibility rule) runs the SIMT
+    kernels whatever the dtype and head size, records the longest key
+    sequence as the least mask row length, gives every suffix tile's dK/dV
+    item all of its leaf's query blocks (a mask may show later keys), and
+    still covers every key tile once."""
+    meta = TPRPrefixMeta(cu_seqlens_q=(0, 33, 98, 138, 155), node_offsets=(0, 130, 200, 270, 290),
+                         leaf_ancestors=((0, 1), (0, 1), (0, 2), (0, 2)))
+    plan = meta.plan(8, 2, d, dtype, CPU, masked=True)
+    assert plan.path == "simt" and plan.masked and not plan.dq_from_ds and plan.workspace_bytes == 0
+    w, fwd, dkdv, qblk = decode(plan)
+    assert w[PF["MASK_COLS"]] == meta.max_keys() == 200 + 65
+    leaf_qblk = w[w[PF["OFF_LEAF_QBLK"]]: w[PF["OFF_LEAF_QBLK"]] + 5]
+    seen = Counter()
+    for src, seg, key0, kvh, lo, hi, slot in tiles_of(dkdv):
+        seen[(src, seg, key0, kvh)] += 1
+        if src == 1:
+            assert (lo, hi) == (leaf_qblk[seg], leaf_qblk[seg + 1])
+    for s in range(4):
+        length = meta.cu_seqlens_q[s + 1] - meta.cu_seqlens_q[s]
+        assert all(seen[(1, s, k0, h)] == 1 for k0 in range(0, length, 64) for h in range(2))
+    assert not meta.plan(8, 2, d, dtype, CPU).masked
 
 
 def test_segment_tree_lowering_turn_tree():
