@@ -287,6 +287,69 @@ __device__ __forceinline__ TileLoc cursor_tile(const Cursor& c) {
                  c.lt * kTileRows, c.d == 0};
 }
 
+// The same key stream as Cursor, carrying the current tile's K and V source
+// addresses: the step inside a segment is a few scalar adds (no 64-bit
+// multiply per tile), and only a segment change reads the key table. A
+// cursor whose addresses are never read (a mask cursor) compiles to its
+// position fields alone.
+struct KvSources {
+  const char* k;   // suffix K / V of the workgroup's KV head (row 0)
+  const char* v;
+  const char* pk;  // prefix K / V of the KV head (row 0)
+  const char* pv;
+  uint32_t k_rb, v_rb, p_rb;  // row bytes of k, v and the packed prefix
+};
+
+struct KvCursor {
+  const char* k;   // K rows of the current tile (uniform)
+  const char* v;   // V rows of the current tile
+  int64_t kstep, vstep;  // bytes of one tile of the current segment
+  uint32_t krb, vrb;     // row bytes of the current segment
+  int rem;         // rows of the segment from the current tile on (0 past the stream's end)
+  int pos0;        // position of the tile's first key within its segment
+  int d;           // 0 = suffix, 1 + e = key run e
+};
+
+template <typename Keys>
+__device__ __forceinline__ void kv_enter(const Keys& t, const KvSources& s, KvCursor& c) {
+  Cursor seg{c.d, 0, 0, 0};
+  cursor_load(t, seg);
+  const bool suffix = c.d == 0;
+  c.krb = suffix ? s.k_rb : s.p_rb;
+  c.vrb = suffix ? s.v_rb : s.p_rb;
+  c.kstep = static_cast<int64_t>(c.krb) * kTileRows;
+  c.vstep = static_cast<int64_t>(c.vrb) * kTileRows;
+  c.k = (suffix ? s.k : s.pk) + static_cast<int64_t>(seg.row) * c.krb;
+  c.v = (suffix ? s.v : s.pv) + static_cast<int64_t>(seg.row) * c.vrb;
+  c.rem = seg.len;
+  c.pos0 = 0;
+}
+
+template <typename Keys>
+__device__ __forceinline__ KvCursor kv_begin(const Keys& t, const KvSources& s) {
+  KvCursor c;
+  c.d = 0;  // the suffix holds at least one key
+  kv_enter(t, s, c);
+  return c;
+}
+
+// Past the last run the cursor stays at an empty segment (rem 0).
+template <typename Keys>
+__device__ __forceinline__ void kv_next(const Keys& t, const KvSources& s, KvCursor& c) {
+  c.rem -= kTileRows;
+  c.pos0 += kTileRows;
+  c.k += c.kstep;
+  c.v += c.vstep;
+  if (c.rem <= 0) {
+    do {
+      c.d++;
+      kv_enter(t, s, c);
+    } while (c.rem == 0 && c.d < kMfmaRegRuns);
+  }
+}
+
+__device__ __forceinline__ int kv_len(const KvCursor& c) { return min(kTileRows, c.rem); }
+
 // A plan word read through the scalar cache (s_load_dword) at a uniform
 // address, waited for here. The compiler reads plan words it cannot prove
 // unclobbered with vector loads, and its vmcnt(0) wait for one of those also

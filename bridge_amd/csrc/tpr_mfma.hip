@@ -307,28 +307,18 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
 
   const auto seg = load_keys<kRunList>(a, leaf, suffix_keys);
   const int ntiles = seg.ntiles;
-  auto kv_rb = [&](const TileLoc& x, bool is_k) { return x.suffix ? (is_k ? k_rb : v_rb) : p_rb; };
-  auto kv_src = [&](const TileLoc& x, bool is_k) {
-    const char* b = x.suffix ? (is_k ? kbase : vbase) : (is_k ? pkbase : pvbase);
-    return b + x.row * static_cast<int64_t>(kv_rb(x, is_k));
-  };
+  const KvSources src{kbase, vbase, pkbase, pvbase, k_rb, v_rb, p_rb};
   // Copy cursors. Group B copies K[0], K[1] and V[0] before the tile loop,
   // then V[j+1] at the start of its softmax phase V(j-1); group A copies
   // K[j+2] at the end of its MFMA phase M(j), which the other group's
   // softmax phase outlasts. Both wait for their copies one phase later,
   // before the barrier ahead of the first M phase that reads them.
-  Cursor dv = cursor_begin(seg);  // B: the next V tile
-  TileLoc tl_v = cursor_tile(dv);
-  if (grp) dma_tile4_fwd(kv_src(tl_v, true), kv_rb(tl_v, true), tl_v.len, lds0, dl, wave & 3);  // K[0]
-  Cursor ka = dv;                 // A: the next K tile (tile 2 when the loop starts); B: tile 1 first
-  TileLoc tl_k = tl_v;
-  if (ntiles > 1) {
-    cursor_next(seg, ka);
-    tl_k = cursor_tile(ka);
-  }
+  KvCursor dv = kv_begin(seg, src);  // B: the next V tile
+  if (grp) dma_tile4_fwd(dv.k, dv.krb, kv_len(dv), lds0, dl, wave & 3);  // K[0]
+  KvCursor ka = dv;                  // A: the next K tile (tile 2 when the loop starts); B: tile 1 first
+  if (ntiles > 1) kv_next(seg, src, ka);
   // every wave's mask cursor: the tile whose scores the next V phase masks
-  Cursor mc = cursor_begin(seg);
-  TileLoc tl_m = cursor_tile(mc);
+  KvCursor mc = kv_begin(seg, src);
 
   // Q as the B operand of S^T = K Q^T: lane holds Q[t][16c + 8h .. +7]
   bf16x8 qv[8];
@@ -351,33 +341,20 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
 
   // group B before the loop: K[1] into K buffer 1 and V[0] into V buffer 0
   auto issue_prologue = [&]() {
-    if (ntiles > 1) dma_tile4_fwd(kv_src(tl_k, true), kv_rb(tl_k, true), tl_k.len, lds0 + kTileBytes, dl, wave & 3);
-    dma_tile4_fwd(kv_src(tl_v, false), kv_rb(tl_v, false), tl_v.len, lds0 + 2 * kTileBytes, dl, wave & 3);
-    if (ntiles > 1) {
-      cursor_next(seg, dv);
-      tl_v = cursor_tile(dv);
-    }
+    if (ntiles > 1) dma_tile4_fwd(ka.k, ka.krb, kv_len(ka), lds0 + kTileBytes, dl, wave & 3);
+    dma_tile4_fwd(dv.v, dv.vrb, kv_len(dv), lds0 + 2 * kTileBytes, dl, wave & 3);
+    if (ntiles > 1) kv_next(seg, src, dv);
   };
   // group B, start of iteration j: V[j+1] into V buffer (j+1)&1
   auto issue_v = [&](int j) {
-    if (j + 1 < ntiles)
-      dma_tile4_fwd(kv_src(tl_v, false), kv_rb(tl_v, false), tl_v.len, lds0 + (2 + ((j + 1) & 1)) * kTileBytes, dl,
-                    wave & 3);
-    if (j + 2 < ntiles) {
-      cursor_next(seg, dv);
-      tl_v = cursor_tile(dv);
-    }
+    if (j + 1 < ntiles) dma_tile4_fwd(dv.v, dv.vrb, kv_len(dv), lds0 + (2 + ((j + 1) & 1)) * kTileBytes, dl, wave & 3);
+    if (j + 2 < ntiles) kv_next(seg, src, dv);
   };
   // group A, end of M(j): K[j+2] into K buffer j&1 (free: K[j] was last read
   // in group B's M(j-1), before the barrier that opened M(j))
   auto issue_k = [&](int j) {
-    if (j + 2 < ntiles)
-      dma_tile4_fwd(kv_src(tl_k, true), kv_rb(tl_k, true), tl_k.len, lds0 + ((j + 2) & 1) * kTileBytes, dl,
-                    wave & 3);
-    if (j + 3 < ntiles) {
-      cursor_next(seg, ka);
-      tl_k = cursor_tile(ka);
-    }
+    if (j + 2 < ntiles) dma_tile4_fwd(ka.k, ka.krb, kv_len(ka), lds0 + ((j + 2) & 1) * kTileBytes, dl, wave & 3);
+    if (j + 3 < ntiles) kv_next(seg, src, ka);
   };
   // M(j): scores of tile j+1 (if with_s) and P[j] V[j] (if with_pv); par = j & 1
   auto mphase = [&](auto with_s, auto with_pv, auto par) {
@@ -421,9 +398,10 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
     // visibility: key kb*32 + 16*(r/8) + 8*h + r%8 <= lim. A tile entirely in
     // this wave's future gets lim < 0 (nothing visible).
     float mt = s_max;
-    if (tl_m.len < kTileRows || (tl_m.suffix && tl_m.pos0 + kTileRows - 1 > tw0)) {
-      int lim = tl_m.len - 1 - 8 * h;
-      if (tl_m.suffix) lim = min(lim, t - tl_m.pos0 - 8 * h);
+    const bool m_suffix = mc.d == 0;
+    if (mc.rem < kTileRows || (m_suffix && mc.pos0 + kTileRows - 1 > tw0)) {
+      int lim = kv_len(mc) - 1 - 8 * h;
+      if (m_suffix) lim = min(lim, t - mc.pos0 - 8 * h);
 #pragma unroll
       for (int kb = 0; kb < 2; kb++)
 #pragma unroll
@@ -434,10 +412,7 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; r++) mt = fmaxf(mt, s[kb][r]);
     }
-    if (j + 2 < ntiles) {
-      cursor_next(seg, mc);
-      tl_m = cursor_tile(mc);
-    }
+    if (j + 2 < ntiles) kv_next(seg, src, mc);
     // Lanes n and n + 32 hold the same query row (different keys) and share
     // its reference max m. A row outgrew m iff one of its two halves did, so
     // the test needs no exchange; the row max over both halves is formed only
@@ -490,10 +465,7 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
   // unrolled by two so that the buffer parity, and with it every LDS address
   // offset, is a compile-time constant.
   if (grp == 0) {
-    if (ntiles > 2) {  // A's K cursor starts at tile 2
-      cursor_next(seg, ka);
-      tl_k = cursor_tile(ka);
-    }
+    if (ntiles > 2) kv_next(seg, src, ka);  // A's K cursor starts at tile 2
     auto body = [&](auto par, int j) {
       mphase(yes, yes, par);
       __builtin_amdgcn_sched_barrier(0);
