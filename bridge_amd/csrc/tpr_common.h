@@ -9,7 +9,7 @@
 namespace tpr {
 
 constexpr int32_t kPlanMagic = 0x31525054;  // "TPR1"
-constexpr int32_t kPlanVersion = 5;
+constexpr int32_t kPlanVersion = 6;
 
 // Header word indices.
 enum PlanField : int {
@@ -52,6 +52,8 @@ enum PlanField : int {
                      // block b) = first[b] + base[segment] + t
   PF_MASK_COLS,      // plan built for a key mask (TPR_PLAN_MASKED): the longest key sequence
                      // of any leaf (the least mask row length); 0 = not a masked plan
+  PF_N_DQS,          // dQ work items of the head_dim-256 dS-store path (0: dQ takes the forward items)
+  PF_OFF_DQS,        // [n][4] like the forward items, kM16DqsWaves waves of 32 tokens each
   PF_HEADER_WORDS = 40
 };
 
@@ -124,6 +126,7 @@ constexpr int kStatRowsOffset = 64;   // floats before the lse*log2e rows
 // MFMA16 family (bf16, head_dim 64 and 256)
 constexpr int kM16Waves = 4;          // waves per workgroup (all kernels)
 constexpr int kM16Tokens = 32;        // forward / dQ tokens per wave (two 16-query sub-blocks)
+constexpr int kM16DqsWaves = 8;       // waves of the head_dim-256 dQ-from-store workgroup (two per SIMD)
 // dK/dV keys per wave: one 16-key block (at head_dim 256 the accumulators of
 // two would not fit the register file; at 64 two measured no faster)
 constexpr int m16_wave_keys(int /*head_dim*/) { return 16; }

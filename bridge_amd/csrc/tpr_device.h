@@ -64,6 +64,9 @@ struct KernelArgs {
   void* ds;
   int32_t off_ds, off_ds_first, num_nodes;
   int64_t ds_slots;
+  // the head_dim-256 dQ-from-store work items (PF_OFF_DQS) and their query
+  // heads per workgroup
+  int32_t off_dqs, hpw_dqs;
   // physical key mask of a masked plan (SIMT kernels): nonzero = hidden; row
   // = query row of q, column = key position in the row's leaf key sequence
   // (ancestor nodes root first, then the suffix)

@@ -607,23 +607,29 @@ __global__ __launch_bounds__(256) void m16_dq(KernelArgs a) {
 
 // ---------------------------------------------------------------------------
 // dQ from the dS store (head_dim 256): dQ^T += K^T dS^T over the dS blocks
-// the dK/dV kernel stored, instead of recomputing S and dP. Work items and
-// waves as the forward's. The key stream follows the dK/dV tiling: the leaf's
-// ancestor nodes root first, then its suffix, in 64-key tiles, one dS slot
-// each. A slot holds a head's 64 x 64 block as four 2 KiB wave blocks (16
-// keys each) of [32-query half][lane L] x 8 queries, lane L holding key L %
-// 16 and queries 32 t + 8 (L / 16) .. +7. Per tile every wave copies its
-// share of the K rows (read transposed as the A operand) and its own 4 KiB
-// of dS (the four wave blocks' halves of its 32 queries), then runs 64 MFMAs.
-// The copy puts chunk L of each 1 KiB block at L ^ (4 ((L >> 4) & 1)), which
-// spreads every 32-lane pass of the transposed dS reads over all 64 banks.
-// Three buffers keep two tiles in flight behind the one being computed.
+// the dK/dV kernel stored, instead of recomputing S and dP. A workgroup is
+// kM16DqsWaves = 8 waves of 32 tokens of one query head each (the plan's own
+// dQ items, PF_OFF_DQS: twice the forward's tokens), two waves per SIMD, so
+// that every K tile copied to LDS serves twice the queries of a 4-wave
+// workgroup and one wave's copies issue while its partner computes. The key
+// stream follows the dK/dV tiling: the leaf's ancestor nodes root first, then
+// its suffix, in 64-key tiles, one dS slot each. A slot holds a head's 64 x 64
+// block as four 2 KiB wave blocks (16 keys each) of [32-query half][lane L] x
+// 8 queries, lane L holding key L % 16 and queries 32 t + 8 (L / 16) .. +7.
+// Per tile every wave copies its share of the K rows (4 of the tile's 32
+// blocks; read transposed as the A operand) and its own 4 KiB of dS (the four
+// wave blocks' halves of its 32 queries), then runs 64 MFMAs. The copy puts
+// chunk L of each 1 KiB block at L ^ (4 ((L >> 4) & 1)), which spreads every
+// 32-lane pass of the transposed dS reads over all 64 banks. The dS blocks
+// (the HBM stream) are copied two tiles ahead of the one being computed into
+// three buffers, the K rows (mostly L2 hits) one tile ahead into two: 160 KiB.
 // ---------------------------------------------------------------------------
 template <int kD, bool kStrided>
-__global__ __launch_bounds__(256) void m16_dqs(KernelArgs a) {
+__global__ __launch_bounds__(64 * kM16DqsWaves) void m16_dqs(KernelArgs a) {
   using T = Geo<kD>;
   static_assert(kD == 256, "the dS store serves head_dim 256 on this family");
-  const int32_t* item = a.plan + a.off_fwd + 4 * blockIdx.x;
+  constexpr int kW = kM16DqsWaves;
+  const int32_t* item = a.plan + a.off_dqs + 4 * blockIdx.x;
   const int leaf = item[0];
   if (leaf < 0) return;
   const int tok0 = item[1], qh0 = item[2], kvh = item[3];
@@ -632,10 +638,10 @@ __global__ __launch_bounds__(256) void m16_dqs(KernelArgs a) {
   const int row0 = cu[leaf], len = cu[leaf + 1] - cu[leaf];
 
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int hpw = a.hpw;
+  const int hpw = a.hpw_dqs;
   const int head = qh0 + wave % hpw;
   const int tw0 = tok0 + kM16Tokens * (wave / hpw);
-  const int tpw = kM16Tokens * (kM16Waves / hpw);
+  const int tpw = kM16Tokens * (kW / hpw);
   const int suffix_keys = min(len, tok0 + tpw);
   const int i16 = lane & 15, g = lane >> 4;
   const bool wave_ok = tw0 < len;
@@ -647,9 +653,9 @@ __global__ __launch_bounds__(256) void m16_dqs(KernelArgs a) {
   const uint32_t k_rb = kStrided ? static_cast<uint32_t>(a.k_rs) * 2 : p_rb;
   constexpr int kKeys = m16_keys(kD);                 // keys per tile (= per dS slot)
   constexpr int kSlotHead = m16_ds_head_bytes(kD);    // 8 KiB per head per slot
-  constexpr int kBufs = 3, kDsWave = 4096;
-  constexpr int kDsOff = kBufs * T::TB;               // K [buffer] | dS [buffer][wave]
-  __shared__ __attribute__((aligned(1024))) char smem[kBufs * (T::TB + kM16Waves * kDsWave)];
+  constexpr int kKBufs = 2, kDsBufs = 3, kDsWave = 4096;
+  constexpr int kDsOff = kKBufs * T::TB;              // K [buffer] | dS [buffer][wave]
+  __shared__ __attribute__((aligned(1024))) char smem[kKBufs * T::TB + kDsBufs * kW * kDsWave];
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(smem));
   const char* kbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.k) + kvh * kD);
   const char* pkbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.pk) + kvh * kD);
@@ -720,20 +726,34 @@ __global__ __launch_bounds__(256) void m16_dqs(KernelArgs a) {
               jq * 1024;
   }
   const int64_t ds_tile_bytes = static_cast<int64_t>(a.group) * kSlotHead;  // one slot of the group
-  // copy the current tile into buffer b (K: this wave's T::BPW blocks; dS: 4
-  // blocks if the wave reads the tile -- prefix tiles: every wave; suffix
-  // tiles: those not entirely in the wave's future)
-  auto issue = [&](int b, int& rows, bool& vis) __attribute__((always_inline)) {
+
+  // A tile of the stream (uniform): its K rows, their count, whether this
+  // wave reads it (prefix tiles: every wave; suffix tiles: those not entirely
+  // in the wave's future) and its dS position. `more` is false past the end.
+  struct Tile {
+    const char* k;
+    uint32_t rb;
+    int rows, pos;
+    bool vis, more;
+  };
+  auto tile_here = [&]() __attribute__((always_inline)) {
     const bool suffix = cd == depth;
-    rows = min(kKeys, clen - ckey);
-    vis = wave_ok && (!suffix || ckey <= tw0 + kM16Tokens - 1);
-    const uint32_t rb = suffix ? k_rb : p_rb;
-    copy_tile<kD>((suffix ? kbase : pkbase) + static_cast<int64_t>(crow + ckey) * rb, rb, rows, lds0 + b * T::TB,
-                  wave, lane);
-    if (vis) {
-      const char* src = ds_wave + cpos * ds_tile_bytes;
-      dma_blocks4_nt(src, dsl[0], dsl[1], dsl[2], dsl[3], lds0 + kDsOff + (b * kM16Waves + wave) * kDsWave);
-    }
+    Tile t;
+    t.more = clim > 0;
+    t.rb = suffix ? k_rb : p_rb;
+    t.k = (suffix ? kbase : pkbase) + static_cast<int64_t>(crow + ckey) * t.rb;
+    t.rows = min(kKeys, clen - ckey);
+    t.pos = cpos;
+    t.vis = t.more && wave_ok && (!suffix || ckey <= tw0 + kM16Tokens - 1);
+    return t;
+  };
+  auto issue_k = [&](const Tile& t, int kb) __attribute__((always_inline)) {
+    copy_tile<kD, kW>(t.k, t.rb, t.rows, lds0 + kb * T::TB, wave, lane);
+  };
+  auto issue_ds = [&](const Tile& t, int sb) __attribute__((always_inline)) {
+    if (t.vis)
+      dma_blocks4_nt(ds_wave + t.pos * ds_tile_bytes, dsl[0], dsl[1], dsl[2], dsl[3],
+                     lds0 + kDsOff + (sb * kW + wave) * kDsWave);
   };
 
   f32x4 dq[2][T::ND];
@@ -741,10 +761,11 @@ __global__ __launch_bounds__(256) void m16_dqs(KernelArgs a) {
   for (int qs = 0; qs < 2; qs++)
 #pragma unroll
     for (int db = 0; db < T::ND; db++) dq[qs][db] = f32x4{};
-  // 64 MFMAs on buffer b; keys at or past `rows` (the segment's end) read as zero dS
-  auto compute = [&](int b, int rows) __attribute__((always_inline)) {
-    const char* kt = smem + b * T::TB;
-    const char* dt = smem + kDsOff + (b * kM16Waves + wave) * kDsWave;
+  // 64 MFMAs on K buffer kb and dS buffer sb; keys at or past `rows` (the
+  // segment's end) read as zero dS
+  auto compute = [&](int kb, int sb, int rows) __attribute__((always_inline)) {
+    const char* kt = smem + kb * T::TB;
+    const char* dt = smem + kDsOff + (sb * kW + wave) * kDsWave;
     bf16x8 f[2][2];  // [qs][t]
 #pragma unroll
     for (int qs = 0; qs < 2; qs++)
@@ -783,32 +804,37 @@ __global__ __launch_bounds__(256) void m16_dqs(KernelArgs a) {
     });
   };
 
-  // copies complete in issue order: waiting until at most tile i + 1's copies
-  // are outstanding means tile i landed
+  // Tiles i (computed), i + 1 (K and dS in flight) and i + 2 (dS in flight):
+  // K of tile j in K buffer j % 2, dS in dS buffer j % 3. At step i the K rows
+  // of tile i + 1 and the dS of tile i + 2 are issued, in that order; copies
+  // complete in issue order, so waiting until at most the last dS copies are
+  // outstanding means both K and dS of the next tile have landed.
+  static_assert(T::TB / 1024 / kW == 4, "4 K copies per wave per tile");
   next_segment();
-  int rows[kBufs];
-  bool vis[kBufs];
-  issue(0, rows[0], vis[0]);
+  Tile t0 = tile_here();
+  issue_k(t0, 0);
+  issue_ds(t0, 0);
   advance();
-  bool more1 = clim > 0;
-  if (more1) issue(1, rows[1], vis[1]);
-  static_assert(T::BPW == 8, "8 K copies per wave per tile");
-  for (int b = 0;;) {
-    const int b1 = b == kBufs - 1 ? 0 : b + 1, b2 = b1 == kBufs - 1 ? 0 : b1 + 1;
-    if (!more1) wait_dma();
-    else if (vis[b1]) asm volatile("s_waitcnt vmcnt(12)");
-    else asm volatile("s_waitcnt vmcnt(8)");
-    __syncthreads();  // tile i has landed; every wave is done with buffer b2 (tile i - 1)
-    bool more2 = false;
-    if (more1) {
+  Tile t1 = tile_here();
+  if (t1.more) issue_ds(t1, 1);
+  int kb = 0, sb = 0;
+  for (;;) {
+    if (t1.vis) asm volatile("s_waitcnt vmcnt(4)");  // the last issued copies are t1's dS (4 blocks)
+    else asm volatile("s_waitcnt vmcnt(0)");
+    __syncthreads();  // tile i has landed; every wave is done with tile i - 1's buffers
+    Tile t2{};
+    if (t1.more) {
       advance();
-      more2 = clim > 0;
-      if (more2) issue(b2, rows[b2], vis[b2]);
+      t2 = tile_here();
+      issue_k(t1, kb ^ 1);
+      if (t2.more) issue_ds(t2, sb == 0 ? kDsBufs - 1 : sb - 1);  // buffer (i + 2) % 3
     }
-    if (vis[b]) compute(b, rows[b]);
-    if (!more1) break;
-    more1 = more2;
-    b = b1;
+    if (t0.vis) compute(kb, sb, t0.rows);
+    if (!t1.more) break;
+    t0 = t1;
+    t1 = t2;
+    kb ^= 1;
+    sb = sb == kDsBufs - 1 ? 0 : sb + 1;
   }
 
   if (!wave_ok) return;
@@ -1228,9 +1254,9 @@ int launch_dq_d(const KernelArgs& a, int n_fwd, hipStream_t s) {
   if constexpr (kD == 256) {
     if (n_fwd > 0 && a.ds) {  // dQ from the dS store
       if (strided_rows<kD>(a))
-        hipLaunchKernelGGL((m16_dqs<kD, true>), dim3(n_fwd), dim3(64 * kM16Waves), 0, s, a);
+        hipLaunchKernelGGL((m16_dqs<kD, true>), dim3(n_fwd), dim3(64 * kM16DqsWaves), 0, s, a);
       else
-        hipLaunchKernelGGL((m16_dqs<kD, false>), dim3(n_fwd), dim3(64 * kM16Waves), 0, s, a);
+        hipLaunchKernelGGL((m16_dqs<kD, false>), dim3(n_fwd), dim3(64 * kM16DqsWaves), 0, s, a);
       return hipGetLastError() != hipSuccess ? 4 : 0;
     }
   }

@@ -233,23 +233,27 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
                      [&](int x, int y) { return cu[x + 1] - cu[x] > cu[y + 1] - cu[y]; });
     for (int r = 0; r < N; r++) leaf_rank[by_len[r]] = r;
   }
-  std::vector<Item> fwd;
-  for (int s = 0; s < N; s++) {
-    const int len = cu[s + 1] - cu[s];
-    for (int tok = 0; tok < len; tok += tokens_per_wg) {
-      // keys the item streams: under a mask every suffix key may be visible
-      const int64_t keys = prefix_len[s] + (masked ? len : std::min(tok + tokens_per_wg, len));
-      for (int qh = 0; qh < Hq; qh += heads_per_wg) {
-        Item it;
-        it.words = {s, tok, qh, qh / G};
-        it.work = keys + static_cast<int64_t>(N - leaf_rank[s]) * (int64_t{1} << 40);
-        it.kvh = qh / G;
-        fwd.push_back(std::move(it));
+  // items of `heads` query heads x `tokens` tokens of one leaf, dealt to the XCDs
+  auto query_items = [&](int heads, int tokens, int32_t* count) {
+    std::vector<Item> items;
+    for (int s = 0; s < N; s++) {
+      const int len = cu[s + 1] - cu[s];
+      for (int tok = 0; tok < len; tok += tokens) {
+        // keys the item streams: under a mask every suffix key may be visible
+        const int64_t keys = prefix_len[s] + (masked ? len : std::min(tok + tokens, len));
+        for (int qh = 0; qh < Hq; qh += heads) {
+          Item it;
+          it.words = {s, tok, qh, qh / G};
+          it.work = keys + static_cast<int64_t>(N - leaf_rank[s]) * (int64_t{1} << 40);
+          it.kvh = qh / G;
+          items.push_back(std::move(it));
+        }
       }
     }
-  }
+    return order_for_xcds(items, Hkv, 4, count);
+  };
   int32_t n_fwd = 0;
-  std::vector<int32_t> fwd_words = order_for_xcds(fwd, Hkv, 4, &n_fwd);
+  std::vector<int32_t> fwd_words = query_items(heads_per_wg, tokens_per_wg, &n_fwd);
 
   // ---- dK/dV items ---------------------------------------------------------
   // One item per (KV segment tile, KV head). On the MFMA path an item streams
@@ -393,6 +397,17 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
     }
   }
 
+  // ---- dQ items of the head_dim-256 dS store ---------------------------------------
+  // The dQ-from-store kernel at head_dim 256 runs kM16DqsWaves waves of 32
+  // tokens (two per SIMD), twice the forward's, so every K tile it copies
+  // serves twice the queries.
+  int32_t n_dqs = 0;
+  std::vector<int32_t> dqs_words;
+  if (path == PATH_MFMA16 && D == 256 && ds_slots > 0) {
+    const int heads = gcd_int(G, kM16DqsWaves);
+    dqs_words = query_items(heads, kM16Tokens * (kM16DqsWaves / heads), &n_dqs);
+  }
+
   // ---- assemble ----------------------------------------------------------------
   plan.assign(PF_HEADER_WORDS, 0);
   auto append = [&](const int32_t* src, size_t count) {
@@ -434,6 +449,8 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
   plan[PF_DS_SLOTS] = static_cast<int32_t>(ds_slots);
   plan[PF_OFF_DS] = ds_table.empty() ? 0 : append(ds_table.data(), ds_table.size());
   plan[PF_MASK_COLS] = static_cast<int32_t>(mask_cols);
+  plan[PF_N_DQS] = n_dqs;
+  plan[PF_OFF_DQS] = dqs_words.empty() ? 0 : append(dqs_words.data(), dqs_words.size());
   plan[PF_TOTAL_WORDS] = static_cast<int32_t>(plan.size());
   return TPR_OK;
 }

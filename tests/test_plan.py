@@ -15,7 +15,7 @@ CPU = torch.device("cpu")
 PF = dict(MAGIC=0, NUM_LEAVES=2, NUM_NODES=3, MAX_DEPTH=4, TOTAL_Q=5, TOTAL_PREFIX=6, HQ=7, HKV=8, D=9,
           PATH=11, OFF_CU=12, OFF_NODE_OFF=13, OFF_ANC=14, OFF_NODE_LEAF=15, N_QBLK=16, OFF_QBLK=17,
           OFF_LEAF_QBLK=18, N_FWD=19, OFF_FWD=20, N_DKDV=21, OFF_DKDV=22, N_RED=23, TOTAL_WORDS=27,
-          OFF_RUNS=28, MAX_RUNS=29, DS_SLOTS=30, OFF_DS=31, MASK_COLS=32)
+          OFF_RUNS=28, MAX_RUNS=29, DS_SLOTS=30, OFF_DS=31, MASK_COLS=32, N_DQS=33, OFF_DQS=34)
 
 FWD_WAVES = 8  # waves per forward / dQ workgroup (kFwdWaves)
 
@@ -469,9 +469,11 @@ def _ds_reads_and_writes(meta, hq, hkv, d=128):
     reads in the [KV head][slot][query head of the group] store."""
     plan = meta.plan(hq, hkv, d, torch.bfloat16, CPU)
     assert plan.dq_from_ds
-    kt, wk, waves, step = (128, 32, FWD_WAVES, 64) if d == 128 else (64, 16, 4, 64)
+    kt, wk, waves, step = (128, 32, FWD_WAVES, 64) if d == 128 else (64, 16, 8, 64)
     head_bytes = kt * 64 * 2
     w, fwd, dkdv, qblk = decode(plan)
+    if d == 256:  # the head_dim-256 dQ kernel's own items (8 waves)
+        fwd = [tuple(w[w[PF["OFF_DQS"]] + 4 * i: w[PF["OFF_DQS"]] + 4 * i + 4]) for i in range(w[PF["N_DQS"]])]
     g = hq // hkv
     n_slots = w[PF["DS_SLOTS"]]
     base, first = _ds_tables(w)
@@ -523,6 +525,43 @@ def _ds_reads_and_writes(meta, hq, hkv, d=128):
                     pos += 1
             wave_offsets.append(offs)
     return n_slots, writes, reads, wave_offsets
+
+
+@pytest.mark.parametrize("hq,hkv", [(8, 2), (16, 2), (32, 8), (6, 2), (4, 4), (16, 1)])
+def test_head_dim_256_dq_items_cover_every_query_row_once(hq, hkv):
+    """The dS-store dQ kernel at head_dim 256 takes the plan's own work items
+    (PF_N_DQS / PF_OFF_DQS): 8 waves of 32 tokens of one query head, hpw =
+    gcd(group, 8) heads per item, so 32 * 8 / hpw tokens. Every (leaf, token,
+    query head) is in exactly one item, items of one KV head only; the list
+    exists only on that path (head_dim 256 with a dS store)."""
+    meta = TPRPrefixMeta(cu_seqlens_q=(0, 100, 163, 163, 420), node_offsets=(0, 64, 200),
+                         leaf_ancestors=((0, 1), (0, 1), (0,), (0,)))
+    plan = meta.plan(hq, hkv, 256, torch.bfloat16, CPU)
+    assert plan.path == "mfma" and plan.dq_from_ds
+    w = plan.host.tolist()
+    n, off = w[PF["N_DQS"]], w[PF["OFF_DQS"]]
+    assert n > 0 and off > 0
+    items = [tuple(w[off + 4 * i: off + 4 * i + 4]) for i in range(n)]
+    g = hq // hkv
+    hpw = math.gcd(g, 8)
+    tpw = 32 * (8 // hpw)
+    covered = Counter()
+    for leaf, tok0, qh0, kvh in items:
+        if leaf < 0:
+            continue
+        assert kvh == qh0 // g and qh0 % hpw == 0 and tok0 % tpw == 0
+        length = meta.cu_seqlens_q[leaf + 1] - meta.cu_seqlens_q[leaf]
+        assert 0 <= tok0 < length
+        for h in range(qh0, qh0 + hpw):
+            for t in range(tok0, min(tok0 + tpw, length)):
+                covered[(leaf, t, h)] += 1
+    expected = {(s, t, h) for s in range(4) for t in range(meta.cu_seqlens_q[s + 1] - meta.cu_seqlens_q[s])
+                for h in range(hq)}
+    assert set(covered) == expected and set(covered.values()) == {1}
+    # no list where dQ takes the forward's items
+    for d, kw in ((256, dict(recompute_dq=True)), (128, {}), (64, {})):
+        other = meta.plan(hq, hkv, d, torch.bfloat16, CPU, **kw).host.tolist()
+        assert other[PF["N_DQS"]] == 0 and other[PF["OFF_DQS"]] == 0
 
 
 @pytest.mark.parametrize("d", [128, 256])
