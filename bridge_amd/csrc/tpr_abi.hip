@@ -89,6 +89,8 @@ KernelArgs args_from_plan(const int32_t* ph, const int32_t* pd, float scale) {
   a.off_runs = ph[PF_OFF_RUNS];
   a.max_runs = ph[PF_MAX_RUNS];
   a.off_dqs = ph[PF_OFF_DQS];
+  // query heads per dQ-from-store workgroup (8 waves in both families)
+  static_assert(kFwdWaves == kM16DqsWaves, "one dQ-from-store item layout");
   a.hpw_dqs = 1;
   for (int g = kM16DqsWaves; g >= 1; g--)
     if (a.group % g == 0 && kM16DqsWaves % g == 0) { a.hpw_dqs = g; break; }
@@ -311,7 +313,7 @@ int bwd_phases(const TprBwdParams* p, int phases, void* stream, void* workspace,
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int n_dkdv = (phases & (TPR_BWD_DKDV | TPR_BWD_DKDV_TILES)) ? ph[PF_N_DKDV] : 0;
   const int n_red = (phases & (TPR_BWD_DKDV | TPR_BWD_DKDV_REDUCE)) ? ph[PF_N_RED] : 0;  // 0 on the SIMT path
-  // dQ work items: the forward's, or the head_dim-256 store path's own list
+  // dQ work items: the forward's, or a dS-store plan's own list
   const int n_dq = (phases & TPR_BWD_DQ) ? (ph[PF_N_DQS] > 0 ? ph[PF_N_DQS] : ph[PF_N_FWD]) : 0;
   if (phases & TPR_BWD_DELTA)
     rc = path == PATH_MFMA ? launch_mfma_delta(a, s) : path == PATH_MFMA16 ? launch_m16_delta(a, s)

@@ -9,7 +9,7 @@
 namespace tpr {
 
 constexpr int32_t kPlanMagic = 0x31525054;  // "TPR1"
-constexpr int32_t kPlanVersion = 6;
+constexpr int32_t kPlanVersion = 7;
 
 // Header word indices.
 enum PlanField : int {
@@ -52,8 +52,9 @@ enum PlanField : int {
                      // block b) = first[b] + base[segment] + t
   PF_MASK_COLS,      // plan built for a key mask (TPR_PLAN_MASKED): the longest key sequence
                      // of any leaf (the least mask row length); 0 = not a masked plan
-  PF_N_DQS,          // dQ work items of the head_dim-256 dS-store path (0: dQ takes the forward items)
-  PF_OFF_DQS,        // [n][4] like the forward items, kM16DqsWaves waves of 32 tokens each
+  PF_N_DQS,          // dQ work items of a dS-store plan (0: dQ takes the forward items)
+  PF_OFF_DQS,        // [n][4] like the forward items: 8 waves of kDqsTokens (head_dim 128) or
+                     // kM16Tokens (head_dim 256) tokens each
   PF_HEADER_WORDS = 40
 };
 
@@ -101,6 +102,7 @@ constexpr int kSimtTile = 32;   // keys (fwd/dQ) or queries (dK/dV) staged per L
 constexpr int kMfmaD = 128;
 constexpr int kFwdWaves = 8;          // waves per forward / dQ workgroup
 constexpr int kFwdTokens = 32;        // tokens per wave (one query head per wave)
+constexpr int kDqsTokens = 64;        // tokens per wave of the dQ-from-store kernel (one query block)
 constexpr int kFwdKeys = 64;          // keys per LDS tile
 constexpr int kDkdvWaves = 4;         // waves per dK/dV workgroup
 constexpr int kDkdvKeys = 32 * kDkdvWaves;  // keys per dK/dV workgroup (32 per wave)

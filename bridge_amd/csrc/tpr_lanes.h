@@ -54,16 +54,18 @@ TPR_HD uint32_t tile4_lane_bytes(int wave, int lane, uint32_t row_bytes, int j) 
          tile4_chunk_bytes(lane, j);
 }
 
-// dS store, head_dim 128: a dQ wave's 4 KiB block of one 64-key half is the
-// slot's wave blocks kb = 0, 1 (4 KiB apart) x 16-query quarters qc = 0, 1
-// (1 KiB apart) of its 32-query half; copy block j = 2 kb + qc, and lane l
-// fetches the chunk that lands at l after the swizzle l ^ (8 (l / 32) + 4 qc).
+// dS store, head_dim 128: one 32-query half of a dQ wave's 8 KiB block of a
+// 64-key half is the slot's wave blocks kb = 0, 1 (4 KiB apart) x 16-query
+// quarters qc = 0, 1 (1 KiB apart) of that 32-query half; copy block j =
+// 2 kb + qc, and lane l fetches the chunk that lands at l after the swizzle
+// l ^ (8 (l / 32) + 4 qc). The wave copies its two 32-query halves from
+// sources 2 KiB apart.
 TPR_HD uint32_t dqs_ds_lane_bytes(int lane, int j) {
   const int kb = j >> 1, qc = j & 1;
   return static_cast<uint32_t>(kb * 4096 + qc * 1024 + 16 * (lane ^ (8 * (lane >> 5) + 4 * qc)));
 }
-// the half's blocks lie at most 8 KiB (the second half) plus 2 KiB (the
-// second 32-query half) into the slot's 16 KiB head block
+// the copies' sources lie at most 8 KiB (the second 64-key half) plus 2 KiB
+// (the second 32-query half) into the slot's 16 KiB head block
 constexpr int kDqsDsSpanBytes = 8192 + 2048;
 
 // dS store, head_dim 256: a slot's 64-key tile of one head is four 2 KiB

@@ -875,25 +875,28 @@ __global__ __launch_bounds__(512) void mfma_dq(KernelArgs a) {
 // dQ from the dS store: dQ^T = K^T dS^T, times scale -- the forward's P V
 // product with V -> K and P -> dS, the dS blocks read from what the dK/dV
 // kernel stored instead of recomputed from Q, K, dO and V. Work items are the
-// forward's. The key stream follows the dK/dV kernel's tiling: the leaf's
+// plan's own (PF_OFF_DQS): 8 waves, two per SIMD, each one whole 64-query
+// block of one query head, so every K^T operand a wave reads from LDS feeds
+// two MFMAs (its two 32-query sub-blocks) and every K row copied serves 512
+// query rows. The key stream follows the dK/dV kernel's tiling: the leaf's
 // ancestor nodes root first, then its suffix, each in 128-key tiles of two
 // 64-key halves, so every half lies in one dS slot. Per half: every wave
 // copies two 1 KiB blocks of the K rows (swizzled like the forward's V tile,
-// read column-wise as the A operand) and its own 64 x 32 dS block (4 KiB),
-// then runs 16 MFMAs.
+// read column-wise as the A operand) and its own 64 x 64 dS block (8 KiB),
+// then runs 32 MFMAs.
 // A slot holds a head's 128 x 64 block as four 4 KiB wave blocks of 32 keys,
 // each [32-query half j][16-query quarter qc][lane L] x 8 queries, lane L
 // holding key L % 32 and queries 32 j + 16 qc + 8 (L / 32) .. +7 (the dK/dV
 // kernel's register order). The copy puts chunk L of each 1 KiB block at
 // L ^ (8 (L / 32) + 4 qc), which spreads every 32-lane pass of the
-// transposed operand reads over all 64 banks. The kernel streams 2 bytes of
-// dS per MFMA multiply-add pair from HBM, so it is bound by memory latency
-// and bandwidth: three buffers keep two halves in flight behind the one
-// being computed.
+// transposed operand reads over all 64 banks. K and dS are double-buffered
+// (two halves of K and of every wave's dS: 160 KiB of LDS): the next half's
+// copies are issued right after the barrier that frees their buffers and
+// land while the current half is computed.
 // ---------------------------------------------------------------------------
 template <bool kStrided>
 __global__ __launch_bounds__(512) void mfma_dqs(KernelArgs a) {
-  const int32_t* item = a.plan + a.off_fwd + 4 * blockIdx.x;
+  const int32_t* item = a.plan + a.off_dqs + 4 * blockIdx.x;
   const int leaf = item[0];
   if (leaf < 0) return;
   const int tok0 = item[1], qh0 = item[2], kvh = item[3];
@@ -902,25 +905,25 @@ __global__ __launch_bounds__(512) void mfma_dqs(KernelArgs a) {
   const int row0 = cu[leaf], len = cu[leaf + 1] - cu[leaf];
 
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int hpw = a.hpw;
+  const int hpw = a.hpw_dqs;
   const int head = qh0 + wave % hpw;
-  const int tw0 = tok0 + kFwdTokens * (wave / hpw);  // first token of this wave
-  const int tpw = kFwdTokens * (kFwdWaves / hpw);
+  const int tw0 = tok0 + kDqsTokens * (wave / hpw);  // first token of this wave (a query block's first)
+  const int tpw = kDqsTokens * (kFwdWaves / hpw);
   const int suffix_keys = min(len, tok0 + tpw);
   const bool wave_ok = tw0 < len;
   const int qb = a.plan[a.off_leaf_qblk + leaf] + tw0 / kDkdvQ;  // the wave's query block
-  const int jq = (tw0 / kFwdTokens) & 1;                          // and its 32-query half of it
   const int h = lane >> 5;
+  static_assert(kDqsTokens == kDkdvQ, "a dQ wave is one query block of the dS slots");
 
   const int64_t qstride = static_cast<int64_t>(a.hq) * kMfmaD;
   const uint32_t p_rb = static_cast<uint32_t>(a.hkv) * kMfmaD * 2;
   const uint32_t k_rb = kStrided ? static_cast<uint32_t>(a.k_rs) * 2 : p_rb;
 
-  constexpr int kBufs = 3;
-  constexpr int kDsWave = 4096;                   // one wave's dS block per half
+  constexpr int kBufs = 2;
+  constexpr int kDsWave = 8192;                   // one wave's dS block per half
   constexpr int kDsOff = kBufs * kTileBytes;      // K [buffer] | dS [buffer][wave]
   __shared__ __attribute__((aligned(1024))) char smem[kBufs * (kTileBytes + kFwdWaves * kDsWave)];
-  static_assert(sizeof(smem) >= kFwdWaves * 8192, "the output rows are staged in the tile buffers");
+  static_assert(sizeof(smem) >= kFwdWaves * 2 * 8192, "the output rows are staged in the tile buffers");
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(smem));
 
   const char* kbase = reinterpret_cast<const char*>(static_cast<const bf16*>(a.k) + kvh * kMfmaD);
@@ -929,8 +932,8 @@ __global__ __launch_bounds__(512) void mfma_dqs(KernelArgs a) {
   const uint32_t krow0 = static_cast<uint32_t>(8 * wave + (lane >> 4));
   const uint32_t kcb0 = static_cast<uint32_t>(16 * ((lane & 15) ^ ((lane >> 4) << 2)));
   const FwdLdsOffsets lo = make_fwd_lds_offsets(lane);
-  // dS copy, block (kb, qc) = 2 kb + qc: lane l fetches the chunk that lands
-  // at l (the swizzle is its own inverse)
+  // dS copy of one 32-query half, block (kb, qc) = 2 kb + qc: lane l fetches
+  // the chunk that lands at l (the swizzle is its own inverse)
   uint32_t dsv[4];
 #pragma unroll
   for (int j = 0; j < 4; j++) dsv[j] = dqs_ds_lane_bytes(lane, j);
@@ -993,60 +996,78 @@ __global__ __launch_bounds__(512) void mfma_dqs(KernelArgs a) {
       if (ckey >= clim) next_segment();
     }
   };
-  // this wave's dS blocks: its query block's first slot, its head, its 32-query half
+  // this wave's dS blocks: its query block's first slot, its head
   const char* ds_wave = nullptr;
   if (wave_ok) {
     const int first = plan_word(a.plan + a.off_ds_first + qb);
     ds_wave = static_cast<const char*>(a.ds) +
-              ((static_cast<int64_t>(kvh) * a.ds_slots + first) * a.group + (head - kvh * a.group)) * kDsHeadBytes +
-              jq * 2048;
+              ((static_cast<int64_t>(kvh) * a.ds_slots + first) * a.group + (head - kvh * a.group)) * kDsHeadBytes;
   }
   const int64_t ds_tile_bytes = static_cast<int64_t>(a.group) * kDsHeadBytes;  // one slot of the group
-  // copy the current half into buffer b; returns its rows, and whether this
+
+  // A half of the stream (uniform): its K rows, their count, whether this
   // wave reads it (prefix halves: every wave; suffix halves: those not
-  // entirely in the wave's future). A wave issues 2 copies for K and 4 for
-  // its dS block (if it reads the half).
-  auto issue = [&](int b, int& rows, bool& vis) __attribute__((always_inline)) {
+  // entirely in the wave's future) and its dS source. `more` is false past
+  // the end.
+  struct Half {
+    const char* k;
+    const char* ds;
+    uint32_t rb;
+    int rows;
+    bool vis, more;
+  };
+  auto half_here = [&]() __attribute__((always_inline)) {
     const int k0 = ckey + kTileRows * chalf;
     const bool suffix = cd == depth;
-    rows = min(kTileRows, clen - k0);
-    vis = wave_ok && (!suffix || k0 <= tw0 + kFwdTokens - 1);
-    {
-      const uint32_t rb = suffix ? k_rb : p_rb;
-      const char* src = (suffix ? kbase : pkbase) + static_cast<int64_t>(crow + k0) * rb;
-      const uint32_t last = static_cast<uint32_t>(rows - 1);
+    Half t;
+    t.more = clim > 0;
+    t.rb = suffix ? k_rb : p_rb;
+    t.k = (suffix ? kbase : pkbase) + static_cast<int64_t>(crow + k0) * t.rb;
+    t.ds = ds_wave + cpos * ds_tile_bytes + 2 * chalf * 4096;
+    t.rows = min(kTileRows, clen - k0);
+    t.vis = t.more && wave_ok && (!suffix || k0 <= tw0 + kDqsTokens - 1);
+    return t;
+  };
+  // copy a half into buffer b: 2 K blocks per wave, and the wave's 8 KiB of
+  // dS (two 32-query halves of 4 blocks each) if it reads the half
+  auto issue = [&](const Half& t, int b) __attribute__((always_inline)) {
+    const uint32_t last = static_cast<uint32_t>(t.rows - 1);
 #pragma unroll
-      for (int j = 0; j < 2; j++)  // block 2w + j: rows 8w + 4j + l / 16; the swizzle's row term is (2w + j) % 4
-        dma16s(src, min(krow0 + 4u * j, last) * rb + (kcb0 ^ (16u * ((2 * wave + j) & 3))),
-               lds0 + b * kTileBytes + (2 * wave + j) * 1024);
-    }
-    if (vis) {
-      const char* src = ds_wave + cpos * ds_tile_bytes + 2 * chalf * 4096;
-      dma_blocks4_nt(src, dsv[0], dsv[1], dsv[2], dsv[3], lds0 + kDsOff + (b * kFwdWaves + wave) * kDsWave);
+    for (int j = 0; j < 2; j++)  // block 2w + j: rows 8w + 4j + l / 16; the swizzle's row term is (2w + j) % 4
+      dma16s(t.k, min(krow0 + 4u * j, last) * t.rb + (kcb0 ^ (16u * ((2 * wave + j) & 3))),
+             lds0 + b * kTileBytes + (2 * wave + j) * 1024);
+    if (t.vis) {
+      const uint32_t dst = lds0 + kDsOff + (b * kFwdWaves + wave) * kDsWave;
+      dma_blocks4_nt(t.ds, dsv[0], dsv[1], dsv[2], dsv[3], dst);
+      dma_blocks4_nt(t.ds + 2048, dsv[0], dsv[1], dsv[2], dsv[3], dst + 4096);
     }
   };
 
-  f32x16 dq[4];
+  f32x16 dq[2][4];
 #pragma unroll
-  for (int i = 0; i < 4; i++) dq[i] = f32x16{};
-  // 16 MFMAs on buffer b: key step (kb, kc) covers keys 32 kb + 16 kc ..
+  for (int j = 0; j < 2; j++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) dq[j][i] = f32x16{};
+  // 32 MFMAs on buffer b: key step st = (kb, kc) covers keys 32 kb + 16 kc ..
   // +15; keys at or past `rows` (the segment's end) read as zero dS
   auto compute = [&](int b, int rows) __attribute__((always_inline)) {
     const char* kt = smem + b * kTileBytes;
     const char* dt = smem + kDsOff + (b * kFwdWaves + wave) * kDsWave;
-    bf16x8 f[4];  // dS^T operands of the four key steps
+    bf16x8 f[2][4];  // dS^T operands of the two 32-query halves and four key steps
 #pragma unroll
-    for (int st = 0; st < 4; st++) {
-      const int kb = st >> 1, kc = st & 1;
-      f[st] = lds_col8_at(dt + kb * 2048 + kc * 256, dso[0], dso[1]);
-      if (rows < kTileRows) {
+    for (int j = 0; j < 2; j++)
 #pragma unroll
-        for (int i = 0; i < 8; i++)
-          if (32 * kb + 16 * kc + 8 * h + i >= rows) f[st][i] = static_cast<bf16>(0.f);
+      for (int st = 0; st < 4; st++) {
+        const int kb = st >> 1, kc = st & 1;
+        f[j][st] = lds_col8_at(dt + j * 4096 + kb * 2048 + kc * 256, dso[0], dso[1]);
+        if (rows < kTileRows) {
+#pragma unroll
+          for (int i = 0; i < 8; i++)
+            if (32 * kb + 16 * kc + 8 * h + i >= rows) f[j][st][i] = static_cast<bf16>(0.f);
+        }
       }
-    }
     // one fenced slot per (key step st, head-dim block db): the K^T operand,
-    // read kRead slots ahead, and its MFMA
+    // read kRead slots ahead, and its two MFMAs
     constexpr int kRead = 4, kRing = kRead + 1;
     bf16x8 ra[kRing];
     auto read_slot = [&](auto ic) __attribute__((always_inline)) {
@@ -1057,43 +1078,41 @@ __global__ __launch_bounds__(512) void mfma_dqs(KernelArgs a) {
     static_for<16>([&](auto ic) {
       constexpr int i = decltype(ic)::value;
       if constexpr (i + kRead < 16) read_slot(std::integral_constant<int, i + kRead>{});
-      dq[i % 4] = mfma(ra[i % kRing], f[i / 4], dq[i % 4]);
+#pragma unroll
+      for (int j = 0; j < 2; j++) dq[j][i % 4] = mfma(ra[i % kRing], f[j][i / 4], dq[j][i % 4]);
       __builtin_amdgcn_sched_barrier(0);
     });
   };
 
-  // halves i (computed), i + 1 and i + 2 (in flight) sit in buffers i % 3,
-  // (i + 1) % 3, (i + 2) % 3; loads complete in issue order, so waiting
-  // until at most half i + 1's copies are outstanding means half i landed
+  // half i (computed) sits in buffer i % 2, half i + 1 (in flight) in the
+  // other; at the top of step i only half i's copies are outstanding
   next_segment();
-  int rows[kBufs];
-  bool vis[kBufs];
-  issue(0, rows[0], vis[0]);
+  Half t0 = half_here();
+  issue(t0, 0);
   advance();
-  bool more1 = clim > 0;  // half i + 1 exists
-  if (more1) issue(1, rows[1], vis[1]);
-  for (int b = 0;;) {
-    const int b1 = b == kBufs - 1 ? 0 : b + 1, b2 = b1 == kBufs - 1 ? 0 : b1 + 1;
-    if (!more1) wait_dma();
-    else if (vis[b1]) asm volatile("s_waitcnt vmcnt(6)");
-    else asm volatile("s_waitcnt vmcnt(2)");
-    __syncthreads();  // half i has landed; every wave is done with buffer b2 (half i - 1)
-    bool more2 = false;
-    if (more1) {
+  Half t1 = half_here();
+  int b = 0;
+  for (;;) {
+    wait_dma();
+    __syncthreads();  // half i has landed; every wave is done with the other buffer (half i - 1)
+    if (t1.more) {
+      issue(t1, b ^ 1);
       advance();
-      more2 = clim > 0;
-      if (more2) issue(b2, rows[b2], vis[b2]);
     }
-    if (vis[b]) compute(b, rows[b]);
-    if (!more1) break;
-    more1 = more2;
-    b = b1;
+    if (t0.vis) compute(b, t0.rows);
+    if (!t1.more) break;
+    t0 = t1;
+    t1 = half_here();
+    b ^= 1;
   }
   __syncthreads();  // every LDS read is done: the buffers are free for the row staging
   if (!wave_ok) return;
-  store_tile_rows(smem + wave * 8192, dq, a.scale,
-                  static_cast<bf16*>(a.dq) + static_cast<int64_t>(row0 + tw0) * qstride + head * kMfmaD, qstride,
-                  len - tw0, lane);
+#pragma unroll
+  for (int j = 0; j < 2; j++)
+    if (tw0 + 32 * j < len)
+      store_tile_rows(smem + (2 * wave + j) * 8192, dq[j], a.scale,
+                      static_cast<bf16*>(a.dq) + static_cast<int64_t>(row0 + tw0 + 32 * j) * qstride + head * kMfmaD,
+                      qstride, len - tw0 - 32 * j, lane);
 }
 
 // ---------------------------------------------------------------------------

@@ -397,15 +397,17 @@ static int build_plan(const TprTreeDesc* t, std::vector<int32_t>& plan) {
     }
   }
 
-  // ---- dQ items of the head_dim-256 dS store ---------------------------------------
-  // The dQ-from-store kernel at head_dim 256 runs kM16DqsWaves waves of 32
-  // tokens (two per SIMD), twice the forward's, so every K tile it copies
+  // ---- dQ items of the dS store -------------------------------------------------
+  // The dQ-from-store kernels run 8 waves (two per SIMD) of kDqsTokens tokens
+  // at head_dim 128 (a whole query block per wave) and kM16Tokens at head_dim
+  // 256, twice the forward's tokens per workgroup, so every K tile they copy
   // serves twice the queries.
   int32_t n_dqs = 0;
   std::vector<int32_t> dqs_words;
-  if (path == PATH_MFMA16 && D == 256 && ds_slots > 0) {
+  if (ds_slots > 0) {
     const int heads = gcd_int(G, kM16DqsWaves);
-    dqs_words = query_items(heads, kM16Tokens * (kM16DqsWaves / heads), &n_dqs);
+    const int tokens = (path == PATH_MFMA ? kDqsTokens : kM16Tokens) * (kM16DqsWaves / heads);
+    dqs_words = query_items(heads, tokens, &n_dqs);
   }
 
   // ---- assemble ----------------------------------------------------------------

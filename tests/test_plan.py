@@ -462,18 +462,21 @@ def _ds_reads_and_writes(meta, hq, hkv, d=128):
     first[block] + base[segment] + tile), and those every dQ wave reads (slot =
     first[block] + position of the tile in the wave's key walk: ancestor nodes
     root first, then the suffix; a block wholly past its segment's end is
-    masked, not read). head_dim 128: 128-key tiles of four 32-key wave
-    blocks, dQ workgroups of 8 waves streaming 64-key halves; head_dim 256:
-    64-key tiles of four 16-key wave blocks, dQ workgroups of 4 waves
-    streaming whole tiles. Also returns, per dQ wave, the byte offsets of its
-    reads in the [KV head][slot][query head of the group] store."""
+    masked, not read). Both take the plan's own dQ items (8 waves). head_dim
+    128: 128-key tiles of four 32-key wave blocks, dQ waves of 64 tokens
+    streaming 64-key halves; head_dim 256: 64-key tiles of four 16-key wave
+    blocks, dQ waves of 32 tokens streaming whole tiles. Also returns, per dQ
+    wave, the byte offsets of its reads in the [KV head][slot][query head of
+    the group] store."""
     plan = meta.plan(hq, hkv, d, torch.bfloat16, CPU)
     assert plan.dq_from_ds
-    kt, wk, waves, step = (128, 32, FWD_WAVES, 64) if d == 128 else (64, 16, 8, 64)
+    kt, wk, wt, step = (128, 32, 64, 64) if d == 128 else (64, 16, 32, 64)
+    waves = 8
     head_bytes = kt * 64 * 2
     w, fwd, dkdv, qblk = decode(plan)
-    if d == 256:  # the head_dim-256 dQ kernel's own items (8 waves)
-        fwd = [tuple(w[w[PF["OFF_DQS"]] + 4 * i: w[PF["OFF_DQS"]] + 4 * i + 4]) for i in range(w[PF["N_DQS"]])]
+    # the dQ kernel's own items
+    fwd = [tuple(w[w[PF["OFF_DQS"]] + 4 * i: w[PF["OFF_DQS"]] + 4 * i + 4]) for i in range(w[PF["N_DQS"]])]
+    assert fwd
     g = hq // hkv
     n_slots = w[PF["DS_SLOTS"]]
     base, first = _ds_tables(w)
@@ -496,7 +499,7 @@ def _ds_reads_and_writes(meta, hq, hkv, d=128):
     reads = set()
     wave_offsets = []
     hpw = math.gcd(g, waves)
-    tpw = 32 * (waves // hpw)
+    tpw = wt * (waves // hpw)
     for leaf, tok0, qh0, kvh in fwd:
         if leaf < 0:
             continue
@@ -505,7 +508,7 @@ def _ds_reads_and_writes(meta, hq, hkv, d=128):
                 if no[nd + 1] > no[nd]]
         segs.append((1, leaf, length, min(length, tok0 + tpw)))
         for wave in range(waves):
-            head, tw0 = qh0 + wave % hpw, tok0 + 32 * (wave // hpw)
+            head, tw0 = qh0 + wave % hpw, tok0 + wt * (wave // hpw)
             if tw0 >= length:
                 continue
             qb = leaf_qblk[leaf] + tw0 // 64
@@ -513,7 +516,7 @@ def _ds_reads_and_writes(meta, hq, hkv, d=128):
             for src, seg, slen, lim in segs:
                 for key0 in range(0, lim, kt):
                     for k0 in range(key0, min(key0 + kt, lim), step):  # the dQ kernel's tiles (halves at 128)
-                        if src == 1 and k0 > tw0 + 31:
+                        if src == 1 and k0 > tw0 + wt - 1:
                             continue
                         slot = first[qb] + pos
                         assert slot == first[qb] + base[seg if src == 0 else m + seg] + key0 // kt
@@ -527,16 +530,18 @@ def _ds_reads_and_writes(meta, hq, hkv, d=128):
     return n_slots, writes, reads, wave_offsets
 
 
+@pytest.mark.parametrize("d", [128, 256])
 @pytest.mark.parametrize("hq,hkv", [(8, 2), (16, 2), (32, 8), (6, 2), (4, 4), (16, 1)])
-def test_head_dim_256_dq_items_cover_every_query_row_once(hq, hkv):
-    """The dS-store dQ kernel at head_dim 256 takes the plan's own work items
-    (PF_N_DQS / PF_OFF_DQS): 8 waves of 32 tokens of one query head, hpw =
-    gcd(group, 8) heads per item, so 32 * 8 / hpw tokens. Every (leaf, token,
-    query head) is in exactly one item, items of one KV head only; the list
-    exists only on that path (head_dim 256 with a dS store)."""
+def test_dq_from_store_items_cover_every_query_row_once(hq, hkv, d):
+    """The dS-store dQ kernels take the plan's own work items (PF_N_DQS /
+    PF_OFF_DQS): 8 waves of one query head each, 64 tokens (one query block)
+    at head_dim 128 and 32 at head_dim 256, hpw = gcd(group, 8) heads per
+    item, so 8 / hpw times a wave's tokens per item. Every (leaf, token,
+    query head) is in exactly one item, items of one KV head only, and an
+    item's tokens start a query block; the list exists only with a dS store."""
     meta = TPRPrefixMeta(cu_seqlens_q=(0, 100, 163, 163, 420), node_offsets=(0, 64, 200),
                          leaf_ancestors=((0, 1), (0, 1), (0,), (0,)))
-    plan = meta.plan(hq, hkv, 256, torch.bfloat16, CPU)
+    plan = meta.plan(hq, hkv, d, torch.bfloat16, CPU)
     assert plan.path == "mfma" and plan.dq_from_ds
     w = plan.host.tolist()
     n, off = w[PF["N_DQS"]], w[PF["OFF_DQS"]]
@@ -544,7 +549,7 @@ def test_head_dim_256_dq_items_cover_every_query_row_once(hq, hkv):
     items = [tuple(w[off + 4 * i: off + 4 * i + 4]) for i in range(n)]
     g = hq // hkv
     hpw = math.gcd(g, 8)
-    tpw = 32 * (8 // hpw)
+    tpw = (64 if d == 128 else 32) * (8 // hpw)
     covered = Counter()
     for leaf, tok0, qh0, kvh in items:
         if leaf < 0:
@@ -558,9 +563,9 @@ def test_head_dim_256_dq_items_cover_every_query_row_once(hq, hkv):
     expected = {(s, t, h) for s in range(4) for t in range(meta.cu_seqlens_q[s + 1] - meta.cu_seqlens_q[s])
                 for h in range(hq)}
     assert set(covered) == expected and set(covered.values()) == {1}
-    # no list where dQ takes the forward's items
-    for d, kw in ((256, dict(recompute_dq=True)), (128, {}), (64, {})):
-        other = meta.plan(hq, hkv, d, torch.bfloat16, CPU, **kw).host.tolist()
+    # no list where dQ recomputes and takes the forward's items
+    for dd, kw in ((d, dict(recompute_dq=True)), (64, {})):
+        other = meta.plan(hq, hkv, dd, torch.bfloat16, CPU, **kw).host.tolist()
         assert other[PF["N_DQS"]] == 0 and other[PF["OFF_DQS"]] == 0
 
 
