@@ -1028,14 +1028,17 @@ __global__ __launch_bounds__(512) void mfma_dqs(KernelArgs a) {
     t.vis = t.more && wave_ok && (!suffix || k0 <= tw0 + kDqsTokens - 1);
     return t;
   };
-  // copy a half into buffer b: 2 K blocks per wave, and the wave's 8 KiB of
-  // dS (two 32-query halves of 4 blocks each) if it reads the half
-  auto issue = [&](const Half& t, int b) __attribute__((always_inline)) {
+  // copy a half's K rows into K buffer b (2 blocks per wave), and the wave's
+  // 8 KiB of its dS (two 32-query halves of 4 blocks each) into dS buffer b
+  // if it reads the half
+  auto issue_k = [&](const Half& t, int b) __attribute__((always_inline)) {
     const uint32_t last = static_cast<uint32_t>(t.rows - 1);
 #pragma unroll
     for (int j = 0; j < 2; j++)  // block 2w + j: rows 8w + 4j + l / 16; the swizzle's row term is (2w + j) % 4
       dma16s(t.k, min(krow0 + 4u * j, last) * t.rb + (kcb0 ^ (16u * ((2 * wave + j) & 3))),
              lds0 + b * kTileBytes + (2 * wave + j) * 1024);
+  };
+  auto issue_ds = [&](const Half& t, int b) __attribute__((always_inline)) {
     if (t.vis) {
       const uint32_t dst = lds0 + kDsOff + (b * kFwdWaves + wave) * kDsWave;
       dma_blocks4_nt(t.ds, dsv[0], dsv[1], dsv[2], dsv[3], dst);
@@ -1049,23 +1052,27 @@ __global__ __launch_bounds__(512) void mfma_dqs(KernelArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; i++) dq[j][i] = f32x16{};
   // 32 MFMAs on buffer b: key step st = (kb, kc) covers keys 32 kb + 16 kc ..
-  // +15; keys at or past `rows` (the segment's end) read as zero dS
-  auto compute = [&](int b, int rows) __attribute__((always_inline)) {
+  // +15; keys at or past `rows` (the segment's end) read as zero dS. Once the
+  // dS operands are in registers the wave's dS buffer b is free, and the dS
+  // of half `next` is copied into it before the MFMAs.
+  auto compute = [&](int b, int rows, const Half& next) __attribute__((always_inline)) {
     const char* kt = smem + b * kTileBytes;
     const char* dt = smem + kDsOff + (b * kFwdWaves + wave) * kDsWave;
     bf16x8 f[2][4];  // dS^T operands of the two 32-query halves and four key steps
 #pragma unroll
     for (int j = 0; j < 2; j++)
 #pragma unroll
-      for (int st = 0; st < 4; st++) {
-        const int kb = st >> 1, kc = st & 1;
-        f[j][st] = lds_col8_at(dt + j * 4096 + kb * 2048 + kc * 256, dso[0], dso[1]);
-        if (rows < kTileRows) {
+      for (int st = 0; st < 4; st++)
+        f[j][st] = lds_col8_at(dt + j * 4096 + (st >> 1) * 2048 + (st & 1) * 256, dso[0], dso[1]);
+    if (rows < kTileRows) {  // a segment's last half only
+#pragma unroll
+      for (int j = 0; j < 2; j++)
+#pragma unroll
+        for (int st = 0; st < 4; st++)
 #pragma unroll
           for (int i = 0; i < 8; i++)
-            if (32 * kb + 16 * kc + 8 * h + i >= rows) f[j][st][i] = static_cast<bf16>(0.f);
-        }
-      }
+            if (16 * st + 8 * h + i >= rows) f[j][st][i] = static_cast<bf16>(0.f);
+    }
     // one fenced slot per (key step st, head-dim block db): the K^T operand,
     // read kRead slots ahead, and its two MFMAs
     constexpr int kRead = 4, kRing = kRead + 1;
@@ -1075,6 +1082,9 @@ __global__ __launch_bounds__(512) void mfma_dqs(KernelArgs a) {
       ra[i % kRing] = lds_col8_at(kt + (32 * (st >> 1) + 16 * (st & 1)) * 256, lo.v[db][0], lo.v[db][1]);
     };
     static_for<kRead>([&](auto ic) { read_slot(ic); });
+    // every LDS read of the buffer has returned before a copy may overwrite it
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    issue_ds(next, b);
     static_for<16>([&](auto ic) {
       constexpr int i = decltype(ic)::value;
       if constexpr (i + kRead < 16) read_slot(std::integral_constant<int, i + kRead>{});
@@ -1084,25 +1094,36 @@ __global__ __launch_bounds__(512) void mfma_dqs(KernelArgs a) {
     });
   };
 
-  // half i (computed) sits in buffer i % 2, half i + 1 (in flight) in the
-  // other; at the top of step i only half i's copies are outstanding
+  // Half j sits in K buffer and dS buffer j % 2. At step i the K rows of
+  // half i + 1 are copied after the barrier (every wave is then done with
+  // half i - 1's K buffer), and the dS of half i + 2 as soon as the wave holds
+  // half i's dS operands in registers, so the dS stream runs two halves
+  // ahead. Copies complete in issue order: at the top of step i the last
+  // ones issued are half i + 1's dS (8 blocks), and waiting until at most
+  // those are outstanding means half i's K rows and dS have landed.
   next_segment();
   Half t0 = half_here();
-  issue(t0, 0);
+  issue_k(t0, 0);
+  issue_ds(t0, 0);
   advance();
   Half t1 = half_here();
+  if (t1.more) issue_ds(t1, 1);
   int b = 0;
   for (;;) {
-    wait_dma();
-    __syncthreads();  // half i has landed; every wave is done with the other buffer (half i - 1)
+    if (t1.vis) asm volatile("s_waitcnt vmcnt(8)");
+    else wait_dma();
+    __syncthreads();  // half i has landed; every wave is done with the other K buffer (half i - 1)
+    Half t2{};
     if (t1.more) {
-      issue(t1, b ^ 1);
+      issue_k(t1, b ^ 1);
       advance();
+      t2 = half_here();
     }
-    if (t0.vis) compute(b, t0.rows);
+    if (t0.vis) compute(b, t0.rows, t2);
+    else issue_ds(t2, b);  // the wave did not copy half i's dS: its buffer is free
     if (!t1.more) break;
     t0 = t1;
-    t1 = half_here();
+    t1 = t2;
     b ^= 1;
   }
   __syncthreads();  // every LDS read is done: the buffers are free for the row staging
