@@ -778,13 +778,17 @@ __global__ __launch_bounds__(64 * kM16DqsWaves) void m16_dqs(KernelArgs a) {
         bf16x8 r;
         r[0] = l4[0]; r[1] = l4[1]; r[2] = l4[2]; r[3] = l4[3];
         r[4] = h4[0]; r[5] = h4[1]; r[6] = h4[2]; r[7] = h4[3];
-        if (rows < kKeys) {
-#pragma unroll
-          for (int i = 0; i < 8; i++)
-            if (32 * t + 8 * g + i >= rows) r[i] = static_cast<bf16>(0.f);
-        }
         f[qs][t] = r;
       }
+    if (rows < kKeys) {  // a segment's last tile only
+#pragma unroll
+      for (int qs = 0; qs < 2; qs++)
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+          for (int i = 0; i < 8; i++)
+            if (32 * t + 8 * g + i >= rows) f[qs][t][i] = static_cast<bf16>(0.f);
+    }
     // one fenced slot per (key step t, head-dim block db): the K^T operand
     // (head dims 16 db.., keys 32 t..), read kRead slots ahead, and two MFMAs
     constexpr int kSlots = 2 * T::ND;
