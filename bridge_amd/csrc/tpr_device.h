@@ -50,7 +50,7 @@ struct KernelArgs {
   int32_t off_runs, max_runs;  // key-run table [N][max_runs][2]
   int32_t n_items;
   float* ws;       // fp32 partial dK/dV slots of split tiles
-  float* stat_ws;  // MFMA backward: [0] = +inf, [1] = 0, then lse*log2e rows from kStatRowsOffset
+  float* stat_ws;  // MFMA backward: [0] = -inf, [1] = 0, then -lse*log2e rows from kStatRowsOffset
   float* ndelta_ws;  // MFMA backward: -delta rows [Hq, Tq] (the dK/dV kernel's dP accumulator start)
   // token (row) strides of q, k and v in elements (the packed Hq*D / Hkv*D
   // unless the caller reads them out of a wider buffer); every other tensor
