@@ -912,7 +912,6 @@ __global__ __launch_bounds__(512) void mfma_dqs(KernelArgs a) {
   const int suffix_keys = min(len, tok0 + tpw);
   const bool wave_ok = tw0 < len;
   const int qb = a.plan[a.off_leaf_qblk + leaf] + tw0 / kDkdvQ;  // the wave's query block
-  const int h = lane >> 5;
   static_assert(kDqsTokens == kDkdvQ, "a dQ wave is one query block of the dS slots");
 
   const int64_t qstride = static_cast<int64_t>(a.hq) * kMfmaD;
@@ -1052,27 +1051,36 @@ __global__ __launch_bounds__(512) void mfma_dqs(KernelArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; i++) dq[j][i] = f32x16{};
   // 32 MFMAs on buffer b: key step st = (kb, kc) covers keys 32 kb + 16 kc ..
-  // +15; keys at or past `rows` (the segment's end) read as zero dS. Once the
-  // dS operands are in registers the wave's dS buffer b is free, and the dS
-  // of half `next` is copied into it before the MFMAs.
+  // +15. The dS operands of key step st are read with the K^T operands, four
+  // slots ahead of their first MFMA, so the MFMAs start after three reads.
+  // LDS reads return in issue order: once slot 12's MFMAs (the first to use
+  // key step 3) have issued, every read of the wave's dS buffer has returned
+  // and the dS of half `next` may be copied into it.
   auto compute = [&](int b, int rows, const Half& next) __attribute__((always_inline)) {
     const char* kt = smem + b * kTileBytes;
     const char* dt = smem + kDsOff + (b * kFwdWaves + wave) * kDsWave;
+    if (rows < kTileRows) {
+      // a segment's last half: zero the dS of keys at or past `rows` in the
+      // wave's buffer (its copy has landed), lane l the chunk it copied for
+      // key 32 kb + l % 32 of each 1 KiB block
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++)
+        if (32 * kb + (lane & 31) >= rows) {
+#pragma unroll
+          for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int qc = 0; qc < 2; qc++)
+              *reinterpret_cast<bf16x8*>(const_cast<char*>(dt) + j * 4096 + kb * 2048 + qc * 1024 +
+                                         16 * (lane ^ (8 * (lane >> 5) + 4 * qc))) = bf16x8{};
+        }
+    }
     bf16x8 f[2][4];  // dS^T operands of the two 32-query halves and four key steps
-#pragma unroll
-    for (int j = 0; j < 2; j++)
-#pragma unroll
-      for (int st = 0; st < 4; st++)
-        f[j][st] = lds_col8_at(dt + j * 4096 + (st >> 1) * 2048 + (st & 1) * 256, dso[0], dso[1]);
-    if (rows < kTileRows) {  // a segment's last half only
+    auto read_f = [&](auto sc) __attribute__((always_inline)) {
+      constexpr int st = decltype(sc)::value;
 #pragma unroll
       for (int j = 0; j < 2; j++)
-#pragma unroll
-        for (int st = 0; st < 4; st++)
-#pragma unroll
-          for (int i = 0; i < 8; i++)
-            if (16 * st + 8 * h + i >= rows) f[j][st][i] = static_cast<bf16>(0.f);
-    }
+        f[j][st] = lds_col8_at(dt + j * 4096 + (st >> 1) * 2048 + (st & 1) * 256, dso[0], dso[1]);
+    };
     // one fenced slot per (key step st, head-dim block db): the K^T operand,
     // read kRead slots ahead, and its two MFMAs
     constexpr int kRead = 4, kRing = kRead + 1;
@@ -1081,13 +1089,15 @@ __global__ __launch_bounds__(512) void mfma_dqs(KernelArgs a) {
       constexpr int i = decltype(ic)::value, st = i / 4, db = i % 4;
       ra[i % kRing] = lds_col8_at(kt + (32 * (st >> 1) + 16 * (st & 1)) * 256, lo.v[db][0], lo.v[db][1]);
     };
+    read_f(std::integral_constant<int, 0>{});
     static_for<kRead>([&](auto ic) { read_slot(ic); });
-    // every LDS read of the buffer has returned before a copy may overwrite it
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    issue_ds(next, b);
     static_for<16>([&](auto ic) {
       constexpr int i = decltype(ic)::value;
-      if constexpr (i + kRead < 16) read_slot(std::integral_constant<int, i + kRead>{});
+      if constexpr (i == 13) issue_ds(next, b);
+      if constexpr (i + kRead < 16) {
+        if constexpr ((i + kRead) % 4 == 0) read_f(std::integral_constant<int, (i + kRead) / 4>{});
+        read_slot(std::integral_constant<int, i + kRead>{});
+      }
 #pragma unroll
       for (int j = 0; j < 2; j++) dq[j][i % 4] = mfma(ra[i % kRing], f[j][i / 4], dq[j][i % 4]);
       __builtin_amdgcn_sched_barrier(0);
