@@ -532,33 +532,55 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// delta[h][t] = sum_d dout[t][h][d] * out[t][h][d] (head_dim 128): 16 lanes per
-// (t, h) row, one 16-byte load of each tensor per lane. Also fills the stat
-// area of the workspace that the dK/dV kernel copies per query block:
-// lse[h][t] * log2e and the two constants for rows past a block's end.
+// delta[h][t] = sum_d dout[t][h][d] * out[t][h][d] (head_dim 128). A workgroup
+// takes 64 tokens of one head: 16 lanes per (t, h) row, one 16-byte load of
+// each tensor per lane and row, four rows per 16-lane group (eight loads in
+// flight per lane). The row sums meet in LDS so that the per-head outputs --
+// delta, and the stat rows the dK/dV kernel copies per query block
+// (-lse*log2e, -delta) -- are written 64 consecutive floats at a time. Also
+// the two constants for rows past a block's end.
 // ---------------------------------------------------------------------------
+constexpr int kDeltaTokens = 64;
+
 __global__ __launch_bounds__(256) void mfma_delta(KernelArgs a) {
-  const int64_t rows = static_cast<int64_t>(a.total_q) * a.hq;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 16 + (threadIdx.x >> 4);
-  const int c = threadIdx.x & 15;
-  float s = 0.f;
-  if (row < rows) {
-    const bf16x8 o = *reinterpret_cast<const bf16x8*>(static_cast<const bf16*>(a.out_in) + row * kMfmaD + 8 * c);
-    const bf16x8 g = *reinterpret_cast<const bf16x8*>(static_cast<const bf16*>(a.dout) + row * kMfmaD + 8 * c);
+  const int head = blockIdx.y;
+  const int t0 = blockIdx.x * kDeltaTokens;
+  const int c = threadIdx.x & 15, r = threadIdx.x >> 4;
+  __shared__ float sums[kDeltaTokens];
+  bf16x8 o[4], g[4];
 #pragma unroll
-    for (int i = 0; i < 8; i++) s = fmaf(static_cast<float>(o[i]), static_cast<float>(g[i]), s);
+  for (int k = 0; k < 4; k++) {
+    const int t = t0 + 16 * k + r;
+    if (t < a.total_q) {
+      const int64_t at = (static_cast<int64_t>(t) * a.hq + head) * kMfmaD + 8 * c;
+      o[k] = *reinterpret_cast<const bf16x8*>(static_cast<const bf16*>(a.out_in) + at);
+      g[k] = *reinterpret_cast<const bf16x8*>(static_cast<const bf16*>(a.dout) + at);
+    } else {
+      o[k] = bf16x8{};
+      g[k] = bf16x8{};
+    }
   }
-  s += __shfl_xor(s, 8);
-  s += __shfl_xor(s, 4);
-  s += __shfl_xor(s, 2);
-  s += __shfl_xor(s, 1);
-  if (c == 0 && row < rows) {
-    const int64_t at = (row % a.hq) * a.total_q + row / a.hq;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) s = fmaf(static_cast<float>(o[k][i]), static_cast<float>(g[k][i]), s);
+    s += __shfl_xor(s, 8);
+    s += __shfl_xor(s, 4);
+    s += __shfl_xor(s, 2);
+    s += __shfl_xor(s, 1);
+    if (c == 0) sums[16 * k + r] = s;
+  }
+  __syncthreads();
+  const int i = threadIdx.x;
+  if (i < kDeltaTokens && t0 + i < a.total_q) {
+    const int64_t at = static_cast<int64_t>(head) * a.total_q + t0 + i;
+    const float s = sums[i];
     a.delta[at] = s;
     a.stat_ws[kStatRowsOffset + at] = -(a.lse_in[at] * kLog2e);  // the dK/dV kernel copies these rows
     a.ndelta_ws[at] = -s;
   }
-  if (blockIdx.x == 0 && threadIdx.x == 0) {
+  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) {
     a.stat_ws[0] = -INFINITY;  // -lse*log2e of a query past a block's end: P = 0
     a.stat_ws[1] = 0.f;       // its -delta
   }
@@ -1738,9 +1760,8 @@ int launch_mfma_fwd(const KernelArgs& a, hipStream_t s) {
 }
 
 int launch_mfma_delta(const KernelArgs& a, hipStream_t s) {
-  const int64_t rows = static_cast<int64_t>(a.total_q) * a.hq;
-  const int blocks = static_cast<int>((rows + 15) / 16);
-  if (blocks > 0) hipLaunchKernelGGL(mfma_delta, dim3(blocks), dim3(256), 0, s, a);
+  const int blocks = (a.total_q + kDeltaTokens - 1) / kDeltaTokens;
+  if (blocks > 0 && a.hq > 0) hipLaunchKernelGGL(mfma_delta, dim3(blocks, a.hq), dim3(256), 0, s, a);
   return hipGetLastError() == hipSuccess ? 0 : 4;
 }
 
