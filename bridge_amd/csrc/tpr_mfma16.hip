@@ -235,14 +235,25 @@ __global__ __launch_bounds__(64 * m16_fwd_waves(kD)) void m16_fwd(KernelArgs a) 
   wait_dma();
   __syncthreads();
 
+  // With two waves per SIMD (8 waves: w and w + 4 share one), the upper four
+  // issue their share of the next tile's copies after the S slots instead of
+  // before them, so that each wave's copy issue runs beside its SIMD
+  // partner's MFMAs.
+  const bool copy_late = kFW == 8 && wave >= 4;
   for (int j = 0; j < ntiles; j++) {
     const int buf = j & 1;
-    if (j + 1 < ntiles) {  // copy tile j+1 into the other buffer (read by tile j-1, released by the last barrier)
+    if (j + 1 < ntiles) {
       cursor_next(seg, cc);
       tl_c = cursor_tile(cc);
-      copy_tile<kD, kFW>(kv_src(tl_c, true), kv_rb(tl_c, true), tl_c.len, lds0 + (1 - buf) * T::TB, wave, lane);
-      copy_tile<kD, kFW>(kv_src(tl_c, false), kv_rb(tl_c, false), tl_c.len, lds0 + (3 - buf) * T::TB, wave, lane);
     }
+    // copy tile j+1 into the other buffer (read by tile j-1, released by the last barrier)
+    auto issue_next = [&]() __attribute__((always_inline)) {
+      if (j + 1 < ntiles) {
+        copy_tile<kD, kFW>(kv_src(tl_c, true), kv_rb(tl_c, true), tl_c.len, lds0 + (1 - buf) * T::TB, wave, lane);
+        copy_tile<kD, kFW>(kv_src(tl_c, false), kv_rb(tl_c, false), tl_c.len, lds0 + (3 - buf) * T::TB, wave, lane);
+      }
+    };
+    if (!copy_late) issue_next();
     const char* kt = smem + buf * T::TB;
     const char* vt = smem + (2 + buf) * T::TB;
 
@@ -332,6 +343,9 @@ __global__ __launch_bounds__(64 * m16_fwd_waves(kD)) void m16_fwd(KernelArgs a) 
     static_for<kSlots>([&](auto ic) {
       constexpr int i = decltype(ic)::value;
       if constexpr (i + kRead < kSlots) read_slot(std::integral_constant<int, i + kRead>{});
+      if constexpr (i == kS) {
+        if (copy_late) issue_next();
+      }
       if constexpr (i < kS) {
         constexpr int b = i % 4, s = i / 4;
 #pragma unroll
