@@ -293,6 +293,16 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
   const uint32_t k_rb = kStrided ? static_cast<uint32_t>(a.k_rs) * 2 : p_rb;
   const uint32_t v_rb = kStrided ? static_cast<uint32_t>(a.v_rs) * 2 : p_rb;
   const int64_t q_rs = kStrided ? a.q_rs : qstride;
+  // Q as the B operand of S^T = K Q^T: lane holds Q[t][16c + 8h .. +7]. Issued
+  // first, so that its latency runs under the key-table loads and the first
+  // tile's copy.
+  bf16x8 qv[8];
+  {
+    const bf16* qp = static_cast<const bf16*>(a.q) + static_cast<int64_t>(row0 + min(t, len - 1)) * q_rs +
+                     head * kMfmaD + 8 * h;
+#pragma unroll
+    for (int c = 0; c < 8; c++) qv[c] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(qp + 16 * c));
+  }
 
   __shared__ __attribute__((aligned(1024))) char smem[4 * kTileBytes];  // K0 K1 V0 V1
   static_assert(sizeof(smem) >= kFwdWaves * 8192, "the output rows are staged in the tile buffers");
@@ -320,14 +330,6 @@ __global__ __launch_bounds__(512) void mfma_fwd(KernelArgs a) {
   // every wave's mask cursor: the tile whose scores the next V phase masks
   KvCursor mc = kv_begin(seg, src);
 
-  // Q as the B operand of S^T = K Q^T: lane holds Q[t][16c + 8h .. +7]
-  bf16x8 qv[8];
-  {
-    const bf16* qp = static_cast<const bf16*>(a.q) + static_cast<int64_t>(row0 + min(t, len - 1)) * q_rs +
-                     head * kMfmaD + 8 * h;
-#pragma unroll
-    for (int c = 0; c < 8; c++) qv[c] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(qp + 16 * c));
-  }
 
   f32x16 o[4];
 #pragma unroll
