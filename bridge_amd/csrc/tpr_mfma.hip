@@ -914,9 +914,10 @@ __global__ __launch_bounds__(512) void mfma_dq(KernelArgs a) {
 // kernel's register order). The copy puts chunk L of each 1 KiB block at
 // L ^ (8 (L / 32) + 4 qc), which spreads every 32-lane pass of the
 // transposed operand reads over all 64 banks. K and dS are double-buffered
-// (two halves of K and of every wave's dS: 160 KiB of LDS): the next half's
-// copies are issued right after the barrier that frees their buffers and
-// land while the current half is computed.
+// (two halves of K and of every wave's dS: 160 KiB of LDS). The next half's
+// K rows are copied right after the barrier that frees their buffer; a
+// wave's dS buffer is its own, so the dS two halves ahead is copied into it
+// as soon as the wave's reads of the current half's dS have returned.
 // ---------------------------------------------------------------------------
 template <bool kStrided>
 __global__ __launch_bounds__(512) void mfma_dqs(KernelArgs a) {
