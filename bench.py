@@ -97,8 +97,8 @@ def cpu_model() -> str:
 
 def cpu_threads() -> int:
     """Host threads the CPU baseline may use: the CPUs this process may run on,
-    capped by OMP_NUM_THREADS when the environment sets it (the GPU box gives a
-    job a share of the host's cores)."""
+    capped by OMP_NUM_THREADS when the environment sets it (a shared GPU host
+    may give a job only a share of its cores)."""
     try:
         usable = len(os.sched_getaffinity(0))
     except AttributeError:
