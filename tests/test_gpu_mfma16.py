@@ -67,23 +67,24 @@ def _cases():
     }
 
 
-def _run(meta, q, k, v, pk, pv, dout, scale):
+def _run(meta, q, k, v, pk, pv, dout, scale, recompute_dq=False):
     from bridge_amd import TPRPrefixAttention
     tensors = [t.clone().requires_grad_(True) for t in (q, k, v, pk, pv)]
-    out, lse = TPRPrefixAttention.apply(*tensors, meta, scale)
+    out, lse = TPRPrefixAttention.apply(*tensors, meta, scale, None, recompute_dq)
     out.backward(dout)
     torch.cuda.synchronize()
     return out.detach(), lse.detach(), [t.grad for t in tensors]
 
 
-def _check(tag, meta, hq, hkv, d, seed, device):
+def _check(tag, meta, hq, hkv, d, seed, device, recompute_dq=False):
     scale = 1.0 / math.sqrt(d)
-    plan = meta.plan(hq, hkv, d, torch.bfloat16, device)
+    plan = meta.plan(hq, hkv, d, torch.bfloat16, device, recompute_dq=recompute_dq)
     print(f"[mfma16 {tag}] d={d} hq={hq} hkv={hkv} tq={meta.total_q} tp={meta.total_prefix} "
-          f"path={plan.path} mfma={plan.mfma_shape} slots={int(plan.host[25])}", flush=True)
+          f"path={plan.path} mfma={plan.mfma_shape} slots={int(plan.host[25])} recompute_dq={recompute_dq}",
+          flush=True)
     assert plan.path == "mfma" and plan.mfma_shape == "16x16x32"
     q, k, v, pk, pv, dout = make_inputs(meta, hq, hkv, d, torch.bfloat16, seed=seed, device=device)
-    out, lse, grads = _run(meta, q, k, v, pk, pv, dout, scale)
+    out, lse, grads = _run(meta, q, k, v, pk, pv, dout, scale, recompute_dq)
     ro, rl, rg = oracle(meta, q, k, v, pk, pv, dout, scale)
     print(f"  out max_abs={max_abs(out, ro):.3e} cos={cosine(out, ro):.6f} lse max_abs={max_abs(lse, rl):.3e}",
           flush=True)
@@ -112,6 +113,14 @@ def test_mfma16_matches_oracle(name, d, cuda_device):
     grads = _check(name, meta, hq, hkv, d, seed=5, device=cuda_device)
     if name == "unused_node":
         assert torch.count_nonzero(grads[3][10:]) == 0 and torch.count_nonzero(grads[4][10:]) == 0
+
+
+@pytest.mark.parametrize("name", list(_cases()))
+def test_mfma16_head_dim_256_recomputing_dq_matches_oracle(name, cuda_device):
+    """The same cases at head_dim 256 with the recomputing dQ plan (m16_dq
+    instead of the dS store and m16_dqs; head_dim 64 always recomputes)."""
+    meta, hq, hkv = _cases()[name]
+    _check(name, meta, hq, hkv, 256, seed=5, device=cuda_device, recompute_dq=True)
 
 
 @pytest.mark.parametrize("d", [64, 256])

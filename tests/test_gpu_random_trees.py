@@ -58,10 +58,10 @@ def random_meta(seed: int, deep: bool = False):
     return TPRPrefixMeta(meta.cu_seqlens_q, tuple(offsets), ancestors)
 
 
-def _run(meta, q, k, v, pk, pv, dout, scale):
+def _run(meta, q, k, v, pk, pv, dout, scale, recompute_dq=False):
     from bridge_amd import TPRPrefixAttention
     tensors = [t.clone().requires_grad_(True) for t in (q, k, v, pk, pv)]
-    out, lse = TPRPrefixAttention.apply(*tensors, meta, scale)
+    out, lse = TPRPrefixAttention.apply(*tensors, meta, scale, None, recompute_dq)
     out.backward(dout)
     torch.cuda.synchronize()
     return out.detach(), lse.detach(), [t.grad for t in tensors]
@@ -76,17 +76,22 @@ def _describe(meta, plan):
 HEADS = [(8, 2), (4, 4), (6, 2), (4, 1)]
 
 
+@pytest.mark.parametrize("recompute_dq", [False, True], ids=["ds_store", "recompute"])
 @pytest.mark.parametrize("seed", range(10))
-def test_random_tree_mfma_bf16(seed, cuda_device):
+def test_random_tree_mfma_bf16(seed, recompute_dq, cuda_device):
+    """Both dQ plans: from the dS store, and recomputing S and dP; seeds 8
+    and 9 are deep trees whose leaves have more key runs than the kernels
+    hold in registers (the run-list instances)."""
     meta = random_meta(seed, deep=seed >= 8)
     hq, hkv = HEADS[seed % len(HEADS)]
     d = 128
     scale = 1.0 / math.sqrt(d)
-    plan = meta.plan(hq, hkv, d, torch.bfloat16, cuda_device)
-    print(f"[random mfma seed={seed}] hq={hq} hkv={hkv} {_describe(meta, plan)}", flush=True)
-    assert plan.path == "mfma"
+    plan = meta.plan(hq, hkv, d, torch.bfloat16, cuda_device, recompute_dq=recompute_dq)
+    print(f"[random mfma seed={seed} recompute_dq={recompute_dq}] hq={hq} hkv={hkv} {_describe(meta, plan)}",
+          flush=True)
+    assert plan.path == "mfma" and plan.dq_from_ds == (not recompute_dq)
     q, k, v, pk, pv, dout = make_inputs(meta, hq, hkv, d, torch.bfloat16, seed=100 + seed, device=cuda_device)
-    out, lse, grads = _run(meta, q, k, v, pk, pv, dout, scale)
+    out, lse, grads = _run(meta, q, k, v, pk, pv, dout, scale, recompute_dq)
     ro, rl, rg = oracle(meta, q, k, v, pk, pv, dout, scale)
     print(f"  out max_abs={max_abs(out, ro):.3e} cos={cosine(out, ro):.6f} lse max_abs={max_abs(lse, rl):.3e}",
           flush=True)
