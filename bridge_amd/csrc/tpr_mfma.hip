@@ -233,10 +233,11 @@ __device__ __forceinline__ void store_tile_rows(char* stage, const f32x16 (&acc)
 //   M(j): S[j+1] = K[j+1] Q^T and O += P[j] V[j]   (MFMA, LDS reads)
 //   V(j): P[j+1] = softmax(S[j+1]), rescaling O     (VALU only)
 // Group B runs one phase behind group A, so on every SIMD one wave's MFMAs
-// overlap the other wave's softmax. Group B also copies the K/V tiles: it
-// issues K[j+2] and V[j+1] at the start of its V(j-1) phase and waits for them
-// at the end of its M(j) phase, two barriers before group A reads them. K runs
-// one tile ahead of V; two K and two V buffers (64 KiB) suffice.
+// overlap the other wave's softmax. The K/V tile copies are split between the
+// groups: group A issues K[j+2] at the end of its M(j) phase, group B V[j+1]
+// at the start of its V(j-1) phase; each group waits for its own copies before
+// the barrier ahead of their first reader. K runs one tile ahead of V; two K
+// and two V buffers (64 KiB) suffice.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ void qk_tile(const char* kt, const bf16x8 (&qv)[8], const FwdLdsOffsets& lo,
                                         f32x16 (&s)[2]) {
