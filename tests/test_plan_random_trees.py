@@ -5,7 +5,8 @@ segment trees with empty nodes and leaves, relabelled node ids (so a leaf's
 ancestors form anywhere from one key run to one run per node), and deep
 chains with side branches.
 
-- Forward items: every (leaf, token, query head) in exactly one item.
+- Forward items (head_dim 64, 128, 256), and the dQ items of a dS-store
+  plan: every (leaf, token, query head) in exactly one item.
 - dK/dV items: every (segment, key tile, KV head) present, its query blocks
   exactly those that see it (every query block of the leaves under a prefix
   node; a suffix tile's blocks from its diagonal to the leaf's end), split
@@ -40,7 +41,7 @@ def _leaf_len(meta, s):
     return meta.cu_seqlens_q[s + 1] - meta.cu_seqlens_q[s]
 
 
-@pytest.mark.parametrize("d", [128, 256])
+@pytest.mark.parametrize("d", [64, 128, 256])
 @pytest.mark.parametrize("seed", SEEDS)
 def test_forward_items_cover_every_query_row_once(seed, d):
     meta, hq, hkv = _case(seed)
@@ -48,8 +49,8 @@ def test_forward_items_cover_every_query_row_once(seed, d):
     assert plan.path == "mfma"
     _, fwd, _, _ = decode(plan)
     g = hq // hkv
-    # head_dim 128: 8 waves of 32 tokens; head_dim 256: 128-row items of
-    # 32 tokens x 4 / hpw heads
+    # head_dim 128: 8 waves of 32 tokens; head_dim 64 and 256: 128-row items
+    # of 32 tokens x 4 / hpw heads
     waves = 8 if d == 128 else 4
     hpw = math.gcd(g, waves)
     tpw = 32 * (waves // hpw)
@@ -65,7 +66,7 @@ def test_forward_items_cover_every_query_row_once(seed, d):
     assert set(covered) == expected and set(covered.values()) <= {1}
 
 
-@pytest.mark.parametrize("d,kt", [(128, 128), (256, 64)])
+@pytest.mark.parametrize("d,kt", [(64, 64), (128, 128), (256, 64)])
 @pytest.mark.parametrize("seed", SEEDS)
 def test_dkdv_tiles_stream_exactly_the_query_blocks_that_see_them(seed, d, kt):
     meta, hq, hkv = _case(seed)
@@ -106,6 +107,35 @@ def test_dkdv_tiles_stream_exactly_the_query_blocks_that_see_them(seed, d, kt):
         assert set(got.values()) <= {1}, tile
         if blocks:
             assert all(qblk[b][0] in ([tile[1]] if tile[0] == 1 else range(n_leaves)) for b in blocks)
+
+
+@pytest.mark.parametrize("d", [128, 256])
+@pytest.mark.parametrize("seed", SEEDS)
+def test_dq_from_store_items_cover_every_query_row_once(seed, d):
+    """The dS-store dQ kernels' own items: 8 waves of one query head, 64
+    tokens each at head_dim 128 and 32 at 256, gcd(group, 8) heads per item."""
+    meta, hq, hkv = _case(seed)
+    plan = meta.plan(hq, hkv, d, torch.bfloat16, CPU)
+    w = plan.host.tolist()
+    n, off = w[PF["N_DQS"]], w[PF["OFF_DQS"]]
+    if meta.total_q == 0:
+        assert not plan.dq_from_ds
+        return
+    assert plan.dq_from_ds and n > 0
+    g = hq // hkv
+    hpw = math.gcd(g, 8)
+    tpw = (64 if d == 128 else 32) * (8 // hpw)
+    covered = Counter()
+    for i in range(n):
+        leaf, tok0, qh0, kvh = w[off + 4 * i: off + 4 * i + 4]
+        if leaf < 0:
+            continue
+        assert kvh == qh0 // g and qh0 % hpw == 0 and tok0 % tpw == 0 and 0 <= tok0 < _leaf_len(meta, leaf)
+        for h in range(qh0, qh0 + hpw):
+            for t in range(tok0, min(tok0 + tpw, _leaf_len(meta, leaf))):
+                covered[(leaf, t, h)] += 1
+    expected = {(s, t, h) for s in range(meta.num_leaves) for t in range(_leaf_len(meta, s)) for h in range(hq)}
+    assert set(covered) == expected and set(covered.values()) <= {1}
 
 
 @pytest.mark.parametrize("d", [128, 256])
