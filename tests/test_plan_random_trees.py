@@ -12,6 +12,9 @@ chains with side branches.
   node; a suffix tile's blocks from its diagonal to the leaf's end), split
   tiles as disjoint chunks whose union is that range, each fp32 partial slot
   used once.
+- Key runs (the forward's and dQ's key stream over the prefix): each leaf's
+  runs, expanded, are its ancestors' prefix_k/v rows root first, with no two
+  runs adjacent in prefix_k/v and no empty run.
 - dS store (bf16 head_dim 128 and 256): every block dQ reads was written
   exactly once by dK/dV, every slot is read, each dQ wave's reads move
   forward through the store.
@@ -24,7 +27,7 @@ import pytest
 import torch
 
 from test_gpu_random_trees import random_meta
-from test_plan import PF, _ds_reads_and_writes, decode, tiles_of
+from test_plan import PF, _ds_reads_and_writes, decode, key_runs, tiles_of
 
 CPU = torch.device("cpu")
 HEADS = [(32, 8), (8, 2), (6, 2), (4, 4), (16, 2)]
@@ -152,3 +155,16 @@ def test_ds_store_is_written_once_before_every_dq_read(seed, d):
     for offs in wave_offsets:
         assert offs == sorted(offs)
         assert all(0 <= o < n_slots * hq * head_bytes for o in offs)
+
+
+@pytest.mark.parametrize("seed", SEEDS)
+def test_key_runs_list_each_leafs_ancestor_rows_root_first(seed):
+    meta, hq, hkv = _case(seed)
+    width, runs = key_runs(meta.plan(hq, hkv, 128, torch.bfloat16, CPU))
+    no = meta.node_offsets
+    assert width == max([len(r) for r in runs] + [0])
+    for leaf, leaf_runs in enumerate(runs):
+        rows = [r for a in meta.leaf_ancestors[leaf] for r in range(no[a], no[a + 1])]
+        assert [r for row, ln in leaf_runs for r in range(row, row + ln)] == rows
+        # maximal: a run never starts where the previous one ends
+        assert all(r0 + l0 != r1 for (r0, l0), (r1, _) in zip(leaf_runs, leaf_runs[1:]))
