@@ -7,7 +7,8 @@ ratios 1, 2, 3, 4 and 8 (1, 2 and 4 query heads per forward workgroup), no
 prefix, tile-aligned and ragged lengths, a depth-3 tree, an unused node, empty
 leaves, a 12-level chain as one key run and as 12 separate runs (the run-list
 variant), split prefix tiles (fp32 partials + ordered reduction), seeded
-random trees, and determinism."""
+random trees (also the relabelled and deep ones of the head_dim-128 suite,
+at head_dim 256 with both dQ plans), and determinism."""
 
 from __future__ import annotations
 
@@ -152,6 +153,23 @@ def test_mfma16_random_trees(seed, cuda_device):
     d = (64, 256)[seed % 2]
     hq, hkv = [(8, 2), (4, 4), (6, 2), (4, 1)][seed]
     _check(f"random{seed}", _random_meta(300 + seed), hq, hkv, d, seed=400 + seed, device=cuda_device)
+
+
+@pytest.mark.parametrize("plan", ["d64", "d256_ds_store", "d256_recompute"])
+@pytest.mark.parametrize("seed", range(4))
+def test_mfma16_relabelled_random_trees(seed, plan, cuda_device):
+    """The head_dim-128 suite's random trees on the 16-wide kernels: node ids
+    relabelled (a leaf's ancestors form one to many key runs in prefix_k/v),
+    seeds 2 and 3 deep chains whose 11 and 9 runs take the run-list kernels;
+    head_dim 64, and 256 with both dQ plans."""
+    from test_gpu_random_trees import random_meta
+    meta = random_meta(500 + seed, deep=seed >= 2)
+    d = 64 if plan == "d64" else 256
+    hq, hkv = [(8, 2), (4, 1), (6, 2), (4, 4)][seed]
+    runs = int(meta.plan(hq, hkv, d, torch.bfloat16, torch.device("cpu")).host[29])
+    assert (runs > 8) == (seed >= 2)
+    _check(f"relabelled{seed}", meta, hq, hkv, d, seed=600 + seed, device=cuda_device,
+           recompute_dq=plan == "d256_recompute")
 
 
 @pytest.mark.parametrize("d", [64, 256])
