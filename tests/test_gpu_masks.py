@@ -5,7 +5,8 @@ fp64 oracle (oracle/tpr_oracle.py tree_forward / tree_backward with ``mask``).
 
 Masks are random (about 40% of each row's keys hidden, so rows also see later
 keys of their own suffix) with a few rows that see no key at all, which must
-come out as output 0, lse -inf and zero gradient."""
+come out as output 0, lse -inf and zero gradient. The trees are fixed cases
+and the relabelled (and deep) random trees of the head_dim-128 suite."""
 
 from __future__ import annotations
 
@@ -51,10 +52,27 @@ KINDS = [(torch.float32, 64), (torch.float32, 96), (torch.bfloat16, 64), (torch.
 @pytest.mark.parametrize("dtype, d", KINDS, ids=[f"{str(t).split('.')[1]}_d{d}" for t, d in KINDS])
 @pytest.mark.parametrize("name", ["single_leaf_gqa2", "siblings_empty_leaf", "depth3_tree", "no_prefix"])
 def test_masked_kernels_match_oracle(name, dtype, d, cuda_device):
-    from bridge_amd import tpr_prefix_attention
     meta, hq, hkv, empty = _cases()[name]
+    _check_masked(name, meta, hq, hkv, empty, dtype, d, d + len(name), cuda_device)
+
+
+@pytest.mark.parametrize("dtype, d", [(torch.float32, 64), (torch.bfloat16, 128)], ids=["float32_d64", "bfloat16_d128"])
+@pytest.mark.parametrize("seed", range(3))
+def test_masked_kernels_on_relabelled_random_trees(seed, dtype, d, cuda_device):
+    """The head_dim-128 suite's random trees (node ids relabelled, seed 2 a
+    deep chain with side branches) under random masks, the first and last
+    query rows seeing no key."""
+    from test_gpu_random_trees import random_meta
+    meta = random_meta(800 + seed, deep=seed == 2)
+    assert meta.total_q > 1
+    _check_masked(f"random{seed}", meta, (4, 8, 6)[seed], 2, (0, meta.total_q - 1), dtype, d, 900 + seed,
+                  cuda_device)
+
+
+def _check_masked(name, meta, hq, hkv, empty, dtype, d, mask_seed, cuda_device):
+    from bridge_amd import tpr_prefix_attention
     scale = 1.0 / math.sqrt(d)
-    mask = random_key_mask(tree_of(meta), torch.Generator().manual_seed(d + len(name)), empty_rows=empty)
+    mask = random_key_mask(tree_of(meta), torch.Generator().manual_seed(mask_seed), empty_rows=empty)
     plan = meta.plan(hq, hkv, d, dtype, cuda_device, masked=True)
     assert plan.path == "simt" and plan.masked
     q, k, v, pk, pv, dout = make_inputs(meta, hq, hkv, d, dtype, seed=17, device=cuda_device)
