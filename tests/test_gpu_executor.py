@@ -1,8 +1,10 @@
 """GPU: the sibling-batched executor through the kernel against the reference's
 per-sibling schedule on the oracle.
 
-A two-layer model (bf16, GQA 8/2, head_dim 128: the MFMA kernels) runs a
-3-level ragged segment tree with ``BatchedLeafExecutor``: one launch per layer
+A two-layer model (bf16, GQA 8/2) runs a 3-level ragged segment tree at
+head_dim 128 (the 32x32x16 MFMA kernels), and a 5-deep chain ending in five
+sibling leaves at head_dim 256 (the 16x16x32 kernels), with
+``BatchedLeafExecutor``: one launch per layer
 for each run of sibling leaves, RoPE positions from the parent's end, the
 path gradient added in-kernel into the PrefixKVStack's fp32 rows, and Pop
 recomputes that inject it. The reference flow -- one leaf visit at a time
@@ -26,27 +28,39 @@ from _toy_model import ToyModel
 
 pytestmark = pytest.mark.gpu
 
-PARENTS = {0: None, 1: 0, 2: 0, 3: 2, 4: 2, 5: 2, 6: 5, 7: 5, 8: 0, 9: 0, 10: 0, 11: 10}
-LENGTHS = {0: 300, 1: 200, 2: 150, 3: 90, 4: 170, 5: 64, 6: 33, 7: 100, 8: 256, 9: 77, 10: 40, 11: 129}
+TREES = {
+    # name: (parents, lengths, head_dim, sibling runs the batched schedule visits, relayed nodes)
+    "ragged_depth3": ({0: None, 1: 0, 2: 0, 3: 2, 4: 2, 5: 2, 6: 5, 7: 5, 8: 0, 9: 0, 10: 0, 11: 10},
+                      {0: 300, 1: 200, 2: 150, 3: 90, 4: 170, 5: 64, 6: 33, 7: 100, 8: 256, 9: 77, 10: 40, 11: 129},
+                      128, [(1,), (3, 4), (6, 7), (8, 9), (11,)], {0, 2, 5, 10}),
+    # a 5-deep chain ending in five sibling leaves, a side branch with a leaf
+    # before an internal sibling, at head_dim 256 (the 16x16x32 kernels)
+    "deep_wide_d256": ({0: None, 1: 0, 2: 1, 3: 2, 4: 3, 5: 4, 6: 4, 7: 4, 8: 4, 9: 4, 10: 2, 11: 2, 12: 11},
+                       {0: 130, 1: 64, 2: 97, 3: 40, 4: 128, 5: 70, 6: 150, 7: 33, 8: 64, 9: 101, 10: 58, 11: 80,
+                        12: 66},
+                       256, [(5, 6, 7, 8, 9), (10,), (12,)], {0, 1, 2, 3, 4, 11}),
+}
 
 
-def test_batched_tree_schedule_matches_per_sibling_oracle(cuda_device):
+@pytest.mark.parametrize("name", list(TREES))
+def test_batched_tree_schedule_matches_per_sibling_oracle(name, cuda_device):
+    parents, lengths, d, want_visits, want_relayed = TREES[name]
     gen = torch.Generator(device="cpu").manual_seed(11)
-    tokens = {s: torch.randint(0, 64, (n,), generator=gen) for s, n in LENGTHS.items()}
-    segs = build_segments(PARENTS, LENGTHS)
-    base = ToyModel(hq=8, hkv=2, d=128, hidden=256, layers=2, seed=5, dtype=torch.bfloat16)
+    tokens = {s: torch.randint(0, 64, (n,), generator=gen) for s, n in lengths.items()}
+    segs = build_segments(parents, lengths)
+    base = ToyModel(hq=8, hkv=2, d=d, hidden=256, layers=2, seed=5, dtype=torch.bfloat16)
 
     gpu = base.clone_to(torch.bfloat16, cuda_device)
-    ex = BatchedLeafExecutor(segs, gpu.forward_fn(tokens), PrefixKVStack(sum(LENGTHS.values())),
+    ex = BatchedLeafExecutor(segs, gpu.forward_fn(tokens), PrefixKVStack(sum(lengths.values())),
                              device=cuda_device)
     mine = ex.run(batch=True)
     torch.cuda.synchronize()
     visits = [st.segment_ids for st in mine.steps if st.kind is ExecutionKind.VISIT_LEAVES]
-    print(f"[executor] batched visits {visits}", flush=True)
-    assert visits == [(1,), (3, 4), (6, 7), (8, 9), (11,)]
+    print(f"[executor {name}] batched visits {visits}", flush=True)
+    assert visits == want_visits
 
     ref_model = base.clone_to(torch.float64, "cpu")
-    ref_ex = BatchedLeafExecutor(segs, ref_model.forward_fn(tokens), PrefixKVStack(sum(LENGTHS.values())),
+    ref_ex = BatchedLeafExecutor(segs, ref_model.forward_fn(tokens), PrefixKVStack(sum(lengths.values())),
                                  backend_factory=OracleStackBackend)
     ref = ref_ex.run(batch=False)
     assert mine.leaf_trace() == ref.leaf_trace()
@@ -60,7 +74,7 @@ def test_batched_tree_schedule_matches_per_sibling_oracle(cuda_device):
     loss_ref = sum(v.item() for v in ref.losses.values())
     print(f"  loss {loss_mine:.4f} vs {loss_ref:.4f}", flush=True)
     assert abs(loss_mine - loss_ref) <= 1e-2 * abs(loss_ref)
-    assert set(mine.relayed) == set(ref.relayed) == {0, 2, 5, 10}
+    assert set(mine.relayed) == set(ref.relayed) == want_relayed
     for seg, layers in ref.relayed.items():
         for layer, (rk, rv) in layers.items():
             gk, gv = mine.relayed[seg][layer]
